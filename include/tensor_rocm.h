@@ -1,0 +1,242 @@
+/*
+ * tensor_rocm.h — C ABI of libtensor_ops_rocm.so, the MI355X (gfx950) int8
+ * quantized-linear backend for Inference-PIO.
+ *
+ * Two layers, both extern "C", plain pointers and sizes only:
+ *
+ *  1. Drop-in `Tensor*` layer. Same struct, same calling convention as the
+ *     reference ABI (src/inference_pio/plugins/common/tensor.h:19-69): inputs
+ *     first, caller-allocated `out` last, `void` return. A Python binding written
+ *     for the reference (src/inference_pio/core/engine/backend.py:46-160) can
+ *     load this library unchanged. Errors never abort the process: the `void`
+ *     entry points record a message readable through tensor_last_error(), and
+ *     every new op also has an `int`-returning `*_status` twin.
+ *
+ *  2. Raw-pointer layer (`pio_*`). Device pointers, explicit element types,
+ *     explicit stream (NULL = the library's current stream). The drop-in layer
+ *     is a thin wrapper over it; tests and the benchmark drive it directly with
+ *     device memory they own.
+ *
+ * Data layout (all row-major, innermost dimension contiguous):
+ *   weights   W   int8  [N, K]   one row per output channel (reference Linear
+ *                                layout, backend.py:698; tensor_ops.c:316)
+ *   w scales  s_w fp32  [N]      per output channel
+ *   act.      x   fp32|fp16 [M, K]
+ *   quant act q   int8  [M, K],  s_a fp32 [M]  (per token, symmetric)
+ *   outputs   y   fp32|fp16 [M, N]
+ * Non-fp32 data rides in `Tensor.data` byte-packed, as the reference does for
+ * int8 (tensor_ops.c:227-228).
+ */
+#ifndef INFERENCE_PIO_TENSOR_ROCM_H
+#define INFERENCE_PIO_TENSOR_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Reference struct, field for field: tensor.h:19-25; Python mirror CTensor,
+ * backend.py:37-44. `size` is the element count; device_id -1 = host, >=0 = GPU. */
+typedef struct {
+    float* data;
+    int* shape;
+    int ndim;
+    int size;
+    int device_id;
+} Tensor;
+
+/* Element types for the typed allocator and the raw layer. */
+enum {
+    PIO_F32 = 0,
+    PIO_F16 = 1,
+    PIO_I8 = 2,
+    PIO_I32 = 3,
+};
+
+/* Status codes returned by every `int` entry point. */
+enum {
+    PIO_OK = 0,
+    PIO_ERR_INVALID = -1,   /* bad shape / dtype / null pointer / device mismatch */
+    PIO_ERR_HIP = -2,       /* a HIP runtime call failed                           */
+    PIO_ERR_OOM = -3,       /* device or pool allocation failed                    */
+    PIO_ERR_UNSUPPORTED = -4,
+};
+
+/* ---------------------------------------------------------------------------
+ * Drop-in: memory and data movement. Required unconditionally by the reference
+ * binding (backend.py:49-55, 67-68).
+ * ------------------------------------------------------------------------- */
+
+/* tensor.h:28; tensor_ops.c:95-133. fp32 elements (4 B each); device_id >= 0
+ * allocates in HBM through the caching allocator / pool, -1 on the host. */
+Tensor* create_tensor(int* shape, int ndim, int device_id);
+/* tensor.h:29; tensor_ops.c:135-162. Pool-owned memory is returned to the pool,
+ * never handed to hipFree. */
+void free_tensor(Tensor* t);
+/* tensor.h:32; tensor_ops.c:280-283. */
+void tensor_fill(Tensor* t, float value);
+/* tensor.h:33-34; tensor_ops.c:287-288. `size` counts 4-byte words, exactly as
+ * the reference (an int8 [N,K] tensor is loaded as ceil(N*K/4) "floats"). */
+void tensor_load_data(Tensor* t, float* buffer, int size);
+void tensor_get_data(Tensor* t, float* buffer, int size);
+/* tensor.h:37-38; tensor_ops.c:289-296 (elementwise fp32). */
+void tensor_add(Tensor* a, Tensor* b, Tensor* out);
+void tensor_mul(Tensor* a, Tensor* b, Tensor* out);
+
+/* New: typed allocation (no reference counterpart: the reference has no dtype
+ * and over-allocates int8 at 4 B/elem). Allocates size*elem_bytes(dtype). */
+Tensor* create_tensor_typed(int* shape, int ndim, int device_id, int dtype);
+int tensor_dtype(Tensor* t);
+/* New: byte-count loaders next to the float-count ones (tensor_ops.c:287-288). */
+void tensor_load_bytes(Tensor* t, const void* src, size_t nbytes);
+void tensor_get_bytes(Tensor* t, void* dst, size_t nbytes);
+int tensor_load_bytes_status(Tensor* t, const void* src, size_t nbytes);
+int tensor_get_bytes_status(Tensor* t, void* dst, size_t nbytes);
+
+/* ---------------------------------------------------------------------------
+ * Drop-in: allocator (tensor_ops.c:69-93; bound at backend.py:88-91, 150-154,
+ * used by UnifiedMemoryManager.malloc_pinned, unified_manager.py:16-28).
+ * ------------------------------------------------------------------------- */
+
+/* tensor_ops.c:74-89: reserve one HBM arena on the current device; later
+ * device tensors are bump-allocated from it (256 B aligned) until it is full,
+ * then fall back to the caching allocator. Second call is a no-op. */
+void init_memory_pool(size_t size_bytes);
+/* tensor_ops.c:91-93: rewind the arena. Tensors still pointing into it become
+ * dangling, exactly as in the reference. */
+void reset_memory_pool(void);
+/* backend.py:150-154 (pinned host memory, hipHostMalloc). */
+void* allocate_pinned_memory(size_t size);
+void free_pinned_memory(void* ptr);
+/* New: stats[0]=bytes hipMalloc'd, [1]=bytes in live tensors, [2]=bytes cached
+ * for reuse, [3]=peak live bytes, [4]=hipMalloc calls, [5]=arena size,
+ * [6]=arena bytes used. */
+void tensor_pool_stats(size_t* stats7);
+/* New: hipFree every cached (not live) block. */
+void tensor_empty_cache(void);
+
+/* ---------------------------------------------------------------------------
+ * Drop-in: streams and graphs (probed by hasattr at backend.py:82-87, 139-149;
+ * CUDAGraph wrapper backend.py:801-810). One in-order HIP stream per device is
+ * the library default; set_current_stream(NULL) restores it.
+ * ------------------------------------------------------------------------- */
+void* create_stream(void);
+void destroy_stream(void* stream);
+void stream_synchronize(void* stream);
+void set_current_stream(void* stream);
+void* get_current_stream(void);
+void device_synchronize(void);
+void begin_capture(void);
+void end_capture(void);
+void replay_graph(void);
+
+/* New: error channel (the reference has none; its CUDA path exit()s,
+ * tensor_ops_cuda.cu:10-18). Message of the last failed call on this thread,
+ * "" if none; tensor_clear_error() resets it. */
+const char* tensor_last_error(void);
+void tensor_clear_error(void);
+
+/* ---------------------------------------------------------------------------
+ * Drop-in: int8 path.
+ * ------------------------------------------------------------------------- */
+
+/* tensor_ops.c:217-246, identical semantics: A [..,M,K] int8, B [..,K,N] int8
+ * (N contiguous), out fp32 [..,M,N] = (float) int32 sum; batch = out->size/(M*N),
+ * A and B both offset per batch. */
+void tensor_matmul_int8(Tensor* a, Tensor* b, Tensor* out);
+int tensor_matmul_int8_status(Tensor* a, Tensor* b, Tensor* out);
+/* Same, int32 accumulators written raw (out must be PIO_I32 or fp32-sized). */
+void tensor_matmul_int8_i32(Tensor* a, Tensor* b, Tensor* out);
+int tensor_matmul_int8_i32_status(Tensor* a, Tensor* b, Tensor* out);
+
+/* tensor_ops_cuda.cu:923-929 / tensor_ops_opencl.c:1429-1438 (per-tensor
+ * scale, scale->size == 1), extended to per-row scales when scale->size equals
+ * the row count of a 2-D int8 input: out[r,c] = float(q[r,c]) * scale[r]. */
+void tensor_dequantize(Tensor* q, Tensor* scale, Tensor* out);
+int tensor_dequantize_status(Tensor* q, Tensor* scale, Tensor* out);
+
+/* W8 per-output-channel dequant linear (replaces tensor_linear, tensor_ops.c:
+ * 323-335, for int8 weights): out[m,n] = s_w[n] * sum_k x[m,k]*W[n,k] + bias[n].
+ * x fp32|fp16 [..,K]; W int8 [N,K]; s_w fp32 [N]; bias fp32 [N] or NULL;
+ * out fp32|fp16 [..,N]. Decode (small M) runs the HBM-streaming GEMV. */
+void tensor_linear_w8(Tensor* x, Tensor* w, Tensor* s_w, Tensor* bias, Tensor* out);
+int tensor_linear_w8_status(Tensor* x, Tensor* w, Tensor* s_w, Tensor* bias, Tensor* out);
+
+/* Per-token symmetric activation quantizer (no reference counterpart):
+ * amax = max_k |x[m,k]|; s[m] = amax/127 (IEEE division; s=1 when amax==0);
+ * q[m,k] = clamp(rint(x[m,k]/s[m]), -127, 127), round-half-even.
+ * x fp32|fp16 [..,K]; q int8 [..,K]; s fp32 [..]. */
+void tensor_quantize_per_token(Tensor* x, Tensor* q, Tensor* s);
+int tensor_quantize_per_token_status(Tensor* x, Tensor* q, Tensor* s);
+
+/* W8A8 linear: acc = sum_k q[m,k]*W[n,k] (int32, bit-exact vs tensor_ops.c:
+ * 217-246); out[m,n] = cvt(float(acc)*s_a[m]*s_w[n] (+ bias[n])).
+ * out fp32|fp16 [..,N]. Runs on int8 MFMA. */
+void tensor_linear_w8a8(Tensor* q, Tensor* s_a, Tensor* w, Tensor* s_w, Tensor* bias, Tensor* out);
+int tensor_linear_w8a8_status(Tensor* q, Tensor* s_a, Tensor* w, Tensor* s_w, Tensor* bias, Tensor* out);
+
+/* Int8 MoE expert layer (replaces Qwen3Coder30BMoE.forward, ip/models/
+ * qwen3_coder_30b/model.py:308-353, with a deterministic combine):
+ *   p = softmax(logits) (tensor_ops.c:351-368); top_k by tensor_topk's rule
+ *   (tensor_ops.c:719-738, strict '>' so ties keep the lower expert id);
+ *   weights = top-k probabilities, divided by their sum when renorm != 0;
+ *   per (token, slot): h = silu(g)*u of the W8A8 gate_up output (fp32),
+ *   requantized per row, then the W8A8 down projection;
+ *   out[t] = sum over slots in order k = 0..top_k-1 of w[t,k] * down(t,k).
+ * x fp32|fp16 [T,H]; logits fp32 [T,E]; w_gu int8 [E,2I,H] (gate rows first,
+ * then up rows); s_gu fp32 [E,2I]; w_down int8 [E,H,I]; s_down fp32 [E,H];
+ * out fp32|fp16 [T,H]. Device scratch comes from the caching allocator. */
+void tensor_moe_w8a8(Tensor* x, Tensor* logits, Tensor* w_gu, Tensor* s_gu, Tensor* w_down,
+                     Tensor* s_down, int top_k, int renorm, Tensor* out);
+int tensor_moe_w8a8_status(Tensor* x, Tensor* logits, Tensor* w_gu, Tensor* s_gu, Tensor* w_down,
+                           Tensor* s_down, int top_k, int renorm, Tensor* out);
+
+/* ---------------------------------------------------------------------------
+ * Raw-pointer layer. All pointers are device pointers; `stream` is a
+ * hipStream_t (NULL = library current stream). Return PIO_OK or an error code.
+ * ------------------------------------------------------------------------- */
+
+/* y[m,n] = s_w[n]*sum_k x[m,k]*W[n,k] (+bias[n]); x_dtype, y_dtype in {F32,F16}.
+ * Requirements: K % 16 == 0, pointers 16-byte aligned. Any M >= 1. */
+int pio_gemv_w8(const void* x, int x_dtype, const int8_t* w, const float* s_w, const float* bias,
+                void* y, int y_dtype, int M, int N, int K, void* stream);
+
+/* Per-token quantizer as tensor_quantize_per_token. Any K >= 1. */
+int pio_quantize_per_token(const void* x, int x_dtype, int8_t* q, float* s, int M, int K,
+                           void* stream);
+
+/* W8A8 GEMM as tensor_linear_w8a8; y_dtype in {F32,F16,I32}. With y_dtype ==
+ * PIO_I32 the raw int32 accumulators are written and s_a/s_w/bias are ignored.
+ * Requirements: K % 16 == 0, pointers 16-byte aligned. */
+int pio_gemm_w8a8(const int8_t* q, const float* s_a, const int8_t* w, const float* s_w,
+                  const float* bias, void* y, int y_dtype, int M, int N, int K, void* stream);
+
+/* tensor_matmul_int8 semantics on raw pointers (B is [K,N]); `out_i32` != 0
+ * writes int32 instead of fp32. `workspace` needs pio_matmul_int8_workspace()
+ * bytes (B is repacked to [N,K] there). */
+size_t pio_matmul_int8_workspace(int batch, int M, int K, int N);
+int pio_matmul_int8(const int8_t* a, const int8_t* b, void* c, int out_i32, int batch, int M,
+                    int K, int N, void* workspace, void* stream);
+
+/* Router: probs = softmax(logits[T,E]) (reference formula), top-k selection
+ * (strict '>'), optional renormalization. topk_w fp32 [T,k], topk_id int32 [T,k]. */
+int pio_moe_route(const float* logits, float* topk_w, int32_t* topk_id, int T, int E, int top_k,
+                  int renorm, void* stream);
+
+/* Full MoE layer on raw pointers; workspace needs pio_moe_workspace() bytes. */
+size_t pio_moe_workspace(int T, int H, int I, int E, int top_k);
+int pio_moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* w_gu,
+                 const float* s_gu, const int8_t* w_down, const float* s_down, void* out,
+                 int out_dtype, int T, int H, int I, int E, int top_k, int renorm, void* workspace,
+                 void* stream);
+
+/* Library version string and the gfx target it was built for. */
+const char* pio_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* INFERENCE_PIO_TENSOR_ROCM_H */

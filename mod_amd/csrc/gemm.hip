@@ -1,0 +1,254 @@
+// W8A8 int8 GEMM on gfx950 MFMA (dense prefill linears and tensor_matmul_int8).
+//   acc[m,n] = sum_k A[m,k] * B[n,k]          int32, exact (|acc| < 2^31 for K < 133144)
+//   C[m,n]   = cvt(float(acc) * s_a[m] * s_w[n] (+ bias[n]))   or raw acc / float(acc)
+// A int8 [M,K] (quantized activations, optionally row-gathered through an index
+// list for MoE groups), B int8 [N,K] (weights, K contiguous), both "K-major", so
+// one v_mfma_i32_16x16x64_i8 consumes 16 contiguous bytes per lane from each.
+//
+// Block tile 128x128, K step 64, 256 threads = 4 waves in a 2x2 grid, each wave
+// owning a 64x64 sub-tile = 4x4 MFMA tiles (64 int32 accumulators per lane).
+// Operand tiles are staged through LDS (row stride padded 64 -> 80 B so the 16
+// lanes of one ds_read_b128 phase hit distinct banks), double buffered, with the
+// next K step's global loads issued before the current step's MFMAs.
+//
+// MFMA operand layout used (16x16xK): lane l supplies A row (l % 16) and B
+// column (l % 16), K bytes [16*(l/16), 16*(l/16)+16) of the 64-wide K step.
+// A and B use the same per-lane K assignment, so whatever internal K order the
+// instruction uses, every A[m,k] meets B[n,k] exactly once. Result layout:
+// lane l holds D[4*(l/16) + v][l % 16], v = 0..3.
+#include "gemm_core.hpp"
+
+namespace pio {
+
+enum { OUT_F32 = 0, OUT_F16 = 1, OUT_I32 = 2, OUT_F32_RAW = 3 };
+
+struct GemmParams {
+    const int8_t* A;
+    int64_t lda, a_batch;
+    const int8_t* B;
+    int64_t ldb, b_batch;
+    const float* s_a;
+    const float* s_w;
+    const float* bias;
+    void* C;
+    int64_t ldc, c_batch;
+    int M, N, K;
+};
+
+// Dense tiles: blockIdx.x = N tile, blockIdx.y = M tile, blockIdx.z = batch.
+template <int OUT>
+__global__ __launch_bounds__(256, 2) void gemm_i8_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(16))) int8_t lds[TILE_LDS_BYTES];
+    const int m0 = blockIdx.y * TM, n0 = blockIdx.x * TN, z = blockIdx.z;
+    TileSrc s;
+    s.A = p.A + z * p.a_batch + (int64_t)m0 * p.lda;
+    s.a_rows = nullptr;
+    s.lda = p.lda;
+    s.m_rem = p.M - m0;
+    s.B = p.B + z * p.b_batch + (int64_t)n0 * p.ldb;
+    s.ldb = p.ldb;
+    s.n_rem = p.N - n0;
+    s.K = p.K;
+    v4i acc[4][4];
+    mma_tile_128(s, lds, acc);
+
+    char* C = (char*)p.C;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int n = n0 + acc_col(j);
+        if (n >= p.N) continue;
+        float sw = 0.f, bn = 0.f;
+        if (OUT == OUT_F32 || OUT == OUT_F16) {
+            sw = p.s_w[n];
+            if (p.bias) bn = p.bias[n];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int m = m0 + acc_row(i, v);
+                if (m >= p.M) continue;
+                const int64_t off = z * p.c_batch + (int64_t)m * p.ldc + n;
+                const int a = acc[i][j][v];
+                if (OUT == OUT_I32) {
+                    ((int32_t*)C)[off] = a;
+                } else if (OUT == OUT_F32_RAW) {
+                    ((float*)C)[off] = (float)a;
+                } else {
+                    float val = (float)a * p.s_a[m] * sw;
+                    if (p.bias) val += bn;
+                    if (OUT == OUT_F32) ((float*)C)[off] = val;
+                    else ((_Float16*)C)[off] = (_Float16)val;
+                }
+            }
+        }
+    }
+}
+
+int launch_gemm(const GemmParams& p, int out_mode, int batch, hipStream_t st) {
+    dim3 grid(ceil_div(p.N, TN), ceil_div(p.M, TM), batch), block(256);
+    switch (out_mode) {
+    case OUT_F32: gemm_i8_kernel<OUT_F32><<<grid, block, 0, st>>>(p); break;
+    case OUT_F16: gemm_i8_kernel<OUT_F16><<<grid, block, 0, st>>>(p); break;
+    case OUT_I32: gemm_i8_kernel<OUT_I32><<<grid, block, 0, st>>>(p); break;
+    case OUT_F32_RAW: gemm_i8_kernel<OUT_F32_RAW><<<grid, block, 0, st>>>(p); break;
+    default: return set_error(PIO_ERR_INVALID, "gemm: bad output mode");
+    }
+    PIO_LAUNCHED();
+    return PIO_OK;
+}
+
+int gemm_w8a8(const int8_t* q, const float* s_a, const int8_t* w, const float* s_w,
+              const float* bias, void* y, int y_dtype, int M, int N, int K, hipStream_t st) {
+    PIO_REQUIRE(q && w && y, "gemm_w8a8: null pointer");
+    PIO_REQUIRE(M >= 0 && N >= 0 && K >= 0, "gemm_w8a8: negative shape");
+    PIO_REQUIRE(K % 16 == 0, "gemm_w8a8: K=%d must be a multiple of 16", K);
+    PIO_REQUIRE(aligned16(q) && aligned16(w), "gemm_w8a8: operands must be 16-byte aligned");
+    int mode;
+    if (y_dtype == PIO_I32) mode = OUT_I32;
+    else if (y_dtype == PIO_F32) mode = OUT_F32;
+    else if (y_dtype == PIO_F16) mode = OUT_F16;
+    else return set_error(PIO_ERR_INVALID, "gemm_w8a8: bad output dtype %d", y_dtype);
+    if (mode != OUT_I32) PIO_REQUIRE(s_a && s_w, "gemm_w8a8: null scales");
+    if (M == 0 || N == 0) return PIO_OK;
+    GemmParams p{};
+    p.A = q; p.lda = K;
+    p.B = w; p.ldb = K;
+    p.s_a = s_a; p.s_w = s_w; p.bias = bias;
+    p.C = y; p.ldc = N;
+    p.M = M; p.N = N; p.K = K;
+    return launch_gemm(p, mode, 1, st);
+}
+
+// [K,N] -> [N,K] int8 transpose through a 64x64 LDS tile (per batch z).
+__global__ __launch_bounds__(256) void transpose_i8_kernel(const int8_t* __restrict__ src,
+                                                           int8_t* __restrict__ dst, int K, int N,
+                                                           int Kp, int64_t sbatch,
+                                                           int64_t dbatch) {
+    __shared__ int8_t t[64][65];
+    const int k0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    src += blockIdx.z * sbatch;
+    dst += blockIdx.z * dbatch;
+    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+        const int r = i / 64, c = i % 64;   // r: k, c: n
+        const int k = k0 + r, n = n0 + c;
+        t[r][c] = (k < K && n < N) ? src[(int64_t)k * N + n] : (int8_t)0;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+        const int r = i / 64, c = i % 64;   // r: n, c: k
+        const int n = n0 + r, k = k0 + c;
+        if (n < N && k < Kp) dst[(int64_t)n * Kp + k] = t[c][r];
+    }
+}
+
+static int padded_k(int K) { return (K + 15) / 16 * 16; }
+
+}  // namespace pio
+
+using namespace pio;
+
+PIO_EXPORT int pio_gemm_w8a8(const int8_t* q, const float* s_a, const int8_t* w, const float* s_w,
+                             const float* bias, void* y, int y_dtype, int M, int N, int K,
+                             void* stream) {
+    return gemm_w8a8(q, s_a, w, s_w, bias, y, y_dtype, M, N, K, pick_stream(stream));
+}
+
+// Workspace: B repacked to [batch][N][Kp] (Kp = K rounded up to 16, zero
+// padded) and, when K % 16 != 0, A repacked to [batch][M][Kp].
+static size_t matmul_ws(int batch, int M, int K, int N) {
+    const size_t Kp = padded_k(K);
+    size_t b = (size_t)batch * N * Kp;
+    size_t a = (K % 16) ? (size_t)batch * M * Kp : 0;
+    return (b + 255) / 256 * 256 + a;
+}
+
+PIO_EXPORT size_t pio_matmul_int8_workspace(int batch, int M, int K, int N) {
+    return matmul_ws(batch, M, K, N);
+}
+
+// Row copy of A [M,K] into [M,Kp] with zero padding (only when K % 16 != 0).
+__global__ void pad_rows_i8_kernel(const int8_t* __restrict__ src, int8_t* __restrict__ dst, int M,
+                                   int K, int Kp) {
+    const int64_t n = (int64_t)M * Kp;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / Kp, c = i % Kp;
+        dst[i] = c < K ? src[r * K + c] : (int8_t)0;
+    }
+}
+
+static int matmul_int8_impl(const int8_t* a, const int8_t* b, void* c, int out_i32, int batch,
+                            int M, int K, int N, void* ws, hipStream_t st) {
+    PIO_REQUIRE(a && b && c, "matmul_int8: null pointer");
+    PIO_REQUIRE(batch >= 1 && M >= 0 && K >= 0 && N >= 0, "matmul_int8: bad shape");
+    if (M == 0 || N == 0) return PIO_OK;
+    const int Kp = padded_k(K);
+    Scratch own;
+    if (!ws) {
+        PIO_TRY(own.get(matmul_ws(batch, M, K, N)));
+        ws = own.ptr;
+    }
+    int8_t* bt = (int8_t*)ws;
+    const size_t bt_bytes = ((size_t)batch * N * Kp + 255) / 256 * 256;
+    dim3 tg(ceil_div(N, 64), ceil_div(Kp > 0 ? Kp : 1, 64), batch);
+    transpose_i8_kernel<<<tg, 256, 0, st>>>(b, bt, K, N, Kp, (int64_t)K * N, (int64_t)N * Kp);
+    PIO_LAUNCHED();
+    const int8_t* ap = a;
+    if (K % 16) {
+        int8_t* apad = bt + bt_bytes;
+        for (int z = 0; z < batch; z++) {
+            pad_rows_i8_kernel<<<256, 256, 0, st>>>(a + (int64_t)z * M * K,
+                                                    apad + (int64_t)z * M * Kp, M, K, Kp);
+            PIO_LAUNCHED();
+        }
+        ap = apad;
+    }
+    if (!aligned16(ap)) {
+        // Unaligned A (a sub-view): repack through the workspace path.
+        return set_error(PIO_ERR_INVALID, "matmul_int8: A must be 16-byte aligned");
+    }
+    GemmParams p{};
+    p.A = ap; p.lda = Kp; p.a_batch = (int64_t)M * Kp;
+    p.B = bt; p.ldb = Kp; p.b_batch = (int64_t)N * Kp;
+    p.C = c; p.ldc = N; p.c_batch = (int64_t)M * N;
+    p.M = M; p.N = N; p.K = Kp;
+    int rc = launch_gemm(p, out_i32 ? OUT_I32 : OUT_F32_RAW, batch, st);
+    return rc;
+}
+
+PIO_EXPORT int pio_matmul_int8(const int8_t* a, const int8_t* b, void* c, int out_i32, int batch,
+                               int M, int K, int N, void* workspace, void* stream) {
+    return matmul_int8_impl(a, b, c, out_i32, batch, M, K, N, workspace, pick_stream(stream));
+}
+
+static int matmul_int8_tensor(Tensor* a, Tensor* b, Tensor* out, int out_i32) {
+    PIO_TRY(check_device_tensor(a, "matmul_int8 a"));
+    PIO_TRY(check_device_tensor(b, "matmul_int8 b"));
+    PIO_TRY(check_device_tensor(out, "matmul_int8 out"));
+    PIO_REQUIRE(a->ndim >= 2 && b->ndim >= 2, "matmul_int8: operands must be >= 2-D");
+    const int M = a->shape[a->ndim - 2], K = a->shape[a->ndim - 1];
+    const int Kb = b->shape[b->ndim - 2], N = b->shape[b->ndim - 1];
+    PIO_REQUIRE(K == Kb, "matmul_int8: inner dims differ (%d vs %d)", K, Kb);
+    PIO_REQUIRE(M > 0 && N > 0, "matmul_int8: empty operand");
+    const int batch = out->size / (M * N);   // tensor_ops.c:223
+    PIO_REQUIRE(batch >= 1 && (int64_t)batch * M * N == out->size,
+                "matmul_int8: out size %d is not a multiple of M*N", out->size);
+    PIO_REQUIRE((int64_t)a->size >= (int64_t)batch * M * K && (int64_t)b->size >= (int64_t)batch * K * N,
+                "matmul_int8: operands too small for batch %d", batch);
+    return matmul_int8_impl((const int8_t*)a->data, (const int8_t*)b->data, out->data, out_i32,
+                            batch, M, K, N, nullptr, current_stream());
+}
+
+PIO_EXPORT int tensor_matmul_int8_status(Tensor* a, Tensor* b, Tensor* out) {
+    return matmul_int8_tensor(a, b, out, 0);
+}
+PIO_EXPORT void tensor_matmul_int8(Tensor* a, Tensor* b, Tensor* out) {
+    matmul_int8_tensor(a, b, out, 0);
+}
+PIO_EXPORT int tensor_matmul_int8_i32_status(Tensor* a, Tensor* b, Tensor* out) {
+    return matmul_int8_tensor(a, b, out, 1);
+}
+PIO_EXPORT void tensor_matmul_int8_i32(Tensor* a, Tensor* b, Tensor* out) {
+    matmul_int8_tensor(a, b, out, 1);
+}

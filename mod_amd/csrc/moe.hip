@@ -1,0 +1,390 @@
+// Int8 MoE expert layer. Replaces the reference's per-expert Python loop
+// (Qwen3Coder30BMoE.forward, ip/models/qwen3_coder_30b/model.py:308-353: a
+// D2H sync per slot, one gather/MLP/scatter call chain per expert, an atomic
+// and therefore order-dependent scatter-add) with six launches and a
+// deterministic combine:
+//
+//  1. route:   p = softmax(logits) exactly as tensor_softmax (tensor_ops.c:351-368:
+//              max seeded with -1e9, exp(x - max), multiply by 1/sum); top-k by
+//              tensor_topk's rule (tensor_ops.c:719-738: strict '>', so equal
+//              probabilities keep the lower expert id first); weights = the top-k
+//              probabilities, optionally renormalized to sum 1.
+//  2. group:   (token, slot) pairs are sorted by expert, tokens ascending inside
+//              an expert (a counting sort over a token x expert bitmap in LDS), so
+//              every expert's rows are one contiguous run of an index list.
+//  3. quant:   x is quantized per token once (the rows are shared by all 8 slots).
+//  4. gate_up: grouped W8A8 GEMM, one block per (expert, 128-column tile); the
+//              block walks its expert's row tiles, so each weight tile is read
+//              from HBM once. fp32 output.
+//  5. swiglu:  h = silu(g) * u (tensor_ops.c:588-604 formula) and per-row requant.
+//  6. down:    grouped W8A8 GEMM over the contiguous h rows, fp32 output.
+//  7. combine: out[t] = sum_{k=0..top_k-1} w[t,k] * down[pos(t,k)], in k order.
+#include "gemm_core.hpp"
+
+namespace pio {
+
+int quantize_per_token(const void* x, int x_dtype, int8_t* q, float* s, int M, int K,
+                       hipStream_t st);
+
+// ------------------------------------------------------------------ route ---
+// One wave per token, 4 tokens per block; the token's E probabilities live in LDS.
+constexpr int ROUTE_MAX_E = 1024;
+
+__global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict__ logits,
+                                                        float* __restrict__ topk_w,
+                                                        int32_t* __restrict__ topk_id, int T,
+                                                        int E, int top_k, int renorm) {
+    __shared__ float sp[4][ROUTE_MAX_E];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int t = blockIdx.x * 4 + w;
+    if (t >= T) return;
+    const float* lr = logits + (int64_t)t * E;
+    float* p = sp[w];
+
+    float mx = -1e9f;
+    for (int e = lane; e < E; e += 64) {
+        p[e] = lr[e];
+        mx = fmaxf(mx, p[e]);
+    }
+    mx = wave_max(mx);
+    float sum = 0.f;
+    for (int e = lane; e < E; e += 64) {
+        float v = expf(p[e] - mx);
+        p[e] = v;
+        sum += v;
+    }
+    sum = wave_sum(sum);
+    const float inv = 1.0f / sum;
+    for (int e = lane; e < E; e += 64) p[e] *= inv;
+
+    // k rounds of (max value, then min index) selection; chosen entries are
+    // retired by setting them to -inf (probabilities are >= 0).
+    float wsum = 0.f;
+    float myw = 0.f;
+    int myid = 0;
+    for (int kk = 0; kk < top_k; kk++) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+        for (int e = lane; e < E; e += 64) {
+            const float v = p[e];
+            if (v > bv) { bv = v; bi = e; }
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int oi = __shfl_xor(bi, o, 64);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        if (lane == kk) { myw = bv; myid = bi; }
+        wsum += bv;
+        if (lane == (bi & 63)) p[bi] = -INFINITY;
+    }
+    if (lane < top_k) {
+        topk_w[(int64_t)t * top_k + lane] = renorm ? myw / wsum : myw;
+        topk_id[(int64_t)t * top_k + lane] = myid;
+    }
+}
+
+// ------------------------------------------------------------------ group ---
+// Single block. bitmap[t][e/32] marks (t, e) pairs; thread e counts column e,
+// an exclusive scan gives expert offsets, then thread e lays out its rows in
+// token order. Limits: T * ceil(E/32) <= GROUP_LDS_WORDS (56 KB of LDS).
+constexpr int GROUP_LDS_WORDS = 14336;
+
+__global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t* __restrict__ topk_id,
+                                                         int T, int E, int top_k,
+                                                         int32_t* __restrict__ offsets,
+                                                         int32_t* __restrict__ row_token,
+                                                         int32_t* __restrict__ pos_of_pair) {
+    __shared__ uint32_t bm[GROUP_LDS_WORDS];
+    __shared__ int32_t cnt[ROUTE_MAX_E + 1];
+    const int words = (E + 31) / 32;
+    for (int i = threadIdx.x; i < T * words; i += blockDim.x) bm[i] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < T * top_k; i += blockDim.x) {
+        const int t = i / top_k, e = topk_id[i];
+        atomicOr(&bm[t * words + (e >> 5)], 1u << (e & 31));
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+        int c = 0;
+        for (int t = 0; t < T; t++) c += (bm[t * words + (e >> 5)] >> (e & 31)) & 1;
+        cnt[e] = c;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int run = 0;
+        for (int e = 0; e < E; e++) {
+            const int c = cnt[e];
+            cnt[e] = run;
+            offsets[e] = run;
+            run += c;
+        }
+        cnt[E] = run;
+        offsets[E] = run;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+        int pos = cnt[e];
+        for (int t = 0; t < T; t++) {
+            if ((bm[t * words + (e >> 5)] >> (e & 31)) & 1) {
+                int kk = 0;
+                while (kk < top_k && topk_id[t * top_k + kk] != e) kk++;
+                row_token[pos] = t;
+                pos_of_pair[t * top_k + kk] = pos;
+                pos++;
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------- grouped W8A8 GEMM ---
+struct GroupedParams {
+    const int8_t* A;          // quantized activations, lda = K
+    const int32_t* a_rows;    // gathered row ids (gate_up) or nullptr (down: rows = positions)
+    const float* s_a;         // per A row (indexed by gathered id, or by position)
+    const int8_t* W;          // [E][N][K]
+    const float* s_w;         // [E][N]
+    const int32_t* offsets;   // [E+1]
+    float* C;                 // [rows][N], row = position
+    int N, K;
+};
+
+__global__ __launch_bounds__(256, 2) void moe_grouped_gemm_kernel(GroupedParams p) {
+    __shared__ __attribute__((aligned(16))) int8_t lds[TILE_LDS_BYTES];
+    const int e = blockIdx.y, n0 = blockIdx.x * TN;
+    const int beg = p.offsets[e], cnt = p.offsets[e + 1] - beg;
+    const int8_t* W = p.W + (int64_t)e * p.N * p.K;
+    const float* sw = p.s_w + (int64_t)e * p.N;
+    for (int m0 = 0; m0 < cnt; m0 += TM) {
+        TileSrc s;
+        if (p.a_rows) {
+            s.A = p.A;
+            s.a_rows = p.a_rows + beg + m0;
+        } else {
+            s.A = p.A + (int64_t)(beg + m0) * p.K;
+            s.a_rows = nullptr;
+        }
+        s.lda = p.K;
+        s.m_rem = cnt - m0;
+        s.B = W + (int64_t)n0 * p.K;
+        s.ldb = p.K;
+        s.n_rem = p.N - n0;
+        s.K = p.K;
+        v4i acc[4][4];
+        mma_tile_128(s, lds, acc);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int n = n0 + acc_col(j);
+            if (n >= p.N) continue;
+            const float swn = sw[n];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int r = m0 + acc_row(i, v);
+                    if (r >= cnt) continue;
+                    const int pos = beg + r;
+                    const float sa = p.s_a[p.a_rows ? p.a_rows[pos] : pos];
+                    p.C[(int64_t)pos * p.N + n] = (float)acc[i][j][v] * sa * swn;
+                }
+        }
+    }
+}
+
+// ------------------------------------------------------ swiglu + requant ---
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    return g * (1.0f / (1.0f + expf(-g))) * u;
+}
+
+__global__ __launch_bounds__(256) void moe_swiglu_quant_kernel(const float* __restrict__ gu,
+                                                               int8_t* __restrict__ q,
+                                                               float* __restrict__ s, int rows,
+                                                               int I) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const float* g = gu + (int64_t)r * 2 * I;
+    float amax = 0.f;
+    for (int i = lane; i < I; i += 64) amax = fmaxf(amax, fabsf(silu_mul(g[i], g[I + i])));
+    amax = wave_max(amax);
+    const float sc = amax == 0.f ? 1.f : amax / 127.0f;
+    if (lane == 0) s[r] = sc;
+    for (int i = lane; i < I; i += 64) {
+        float v = __builtin_rintf(silu_mul(g[i], g[I + i]) / sc);
+        v = fminf(fmaxf(v, -127.f), 127.f);
+        q[(int64_t)r * I + i] = (int8_t)(int)v;
+    }
+}
+
+// ---------------------------------------------------------------- combine ---
+template <typename OT>
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ d,
+                                                          const float* __restrict__ topk_w,
+                                                          const int32_t* __restrict__ pos_of_pair,
+                                                          OT* __restrict__ out, int T, int H,
+                                                          int top_k) {
+    const int t = blockIdx.y;
+    for (int n = blockIdx.x * 256 + threadIdx.x; n < H; n += gridDim.x * 256) {
+        float acc = 0.f;
+        for (int kk = 0; kk < top_k; kk++) {
+            const int pr = t * top_k + kk;
+            acc += topk_w[pr] * d[(int64_t)pos_of_pair[pr] * H + n];
+        }
+        out[(int64_t)t * H + n] = from_f32<OT>(acc);
+    }
+}
+
+// --------------------------------------------------------------- workspace ---
+struct MoeWs {
+    float* topk_w;
+    int32_t* topk_id;
+    int32_t* offsets;
+    int32_t* row_token;
+    int32_t* pos_of_pair;
+    int8_t* qx;
+    float* sx;
+    float* gu;
+    int8_t* qh;
+    float* sh;
+    float* d;
+    size_t total;
+};
+
+static size_t al(size_t b) { return (b + 255) / 256 * 256; }
+
+static MoeWs moe_layout(char* base, int T, int H, int I, int E, int k) {
+    MoeWs w{};
+    const size_t P = (size_t)T * k;
+    size_t o = 0;
+    auto take = [&](size_t bytes) { char* p = base ? base + o : nullptr; o += al(bytes); return p; };
+    w.topk_w = (float*)take(P * 4);
+    w.topk_id = (int32_t*)take(P * 4);
+    w.offsets = (int32_t*)take((size_t)(E + 1) * 4);
+    w.row_token = (int32_t*)take(P * 4);
+    w.pos_of_pair = (int32_t*)take(P * 4);
+    w.qx = (int8_t*)take((size_t)T * H);
+    w.sx = (float*)take((size_t)T * 4);
+    w.gu = (float*)take(P * 2 * I * 4);
+    w.qh = (int8_t*)take(P * I);
+    w.sh = (float*)take(P * 4);
+    w.d = (float*)take(P * H * 4);
+    w.total = o;
+    return w;
+}
+
+int moe_route(const float* logits, float* topk_w, int32_t* topk_id, int T, int E, int top_k,
+              int renorm, hipStream_t st) {
+    PIO_REQUIRE(logits && topk_w && topk_id, "moe_route: null pointer");
+    PIO_REQUIRE(T >= 0 && E >= 1 && E <= ROUTE_MAX_E, "moe_route: need 1 <= E <= %d", ROUTE_MAX_E);
+    PIO_REQUIRE(top_k >= 1 && top_k <= E && top_k <= 64, "moe_route: bad top_k %d", top_k);
+    if (T == 0) return PIO_OK;
+    moe_route_kernel<<<ceil_div(T, 4), 256, 0, st>>>(logits, topk_w, topk_id, T, E, top_k, renorm);
+    PIO_LAUNCHED();
+    return PIO_OK;
+}
+
+int moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* w_gu,
+             const float* s_gu, const int8_t* w_down, const float* s_down, void* out,
+             int out_dtype, int T, int H, int I, int E, int top_k, int renorm, void* ws,
+             hipStream_t st) {
+    PIO_REQUIRE(x && logits && w_gu && s_gu && w_down && s_down && out, "moe: null pointer");
+    PIO_REQUIRE(T >= 0 && H > 0 && I > 0, "moe: bad shape");
+    PIO_REQUIRE(H % 16 == 0 && I % 16 == 0, "moe: H=%d and I=%d must be multiples of 16", H, I);
+    PIO_REQUIRE(out_dtype == PIO_F32 || out_dtype == PIO_F16, "moe: out must be fp32 or fp16");
+    PIO_REQUIRE((int64_t)T * ((E + 31) / 32) <= GROUP_LDS_WORDS,
+                "moe: T*ceil(E/32) = %lld exceeds the grouping limit %d",
+                (long long)T * ((E + 31) / 32), GROUP_LDS_WORDS);
+    PIO_REQUIRE(aligned16(w_gu) && aligned16(w_down), "moe: weights must be 16-byte aligned");
+    if (T == 0) return PIO_OK;
+    Scratch own;
+    if (!ws) {
+        PIO_TRY(own.get(moe_layout(nullptr, T, H, I, E, top_k).total));
+        ws = own.ptr;
+    }
+    MoeWs w = moe_layout((char*)ws, T, H, I, E, top_k);
+    const int P = T * top_k;
+
+    PIO_TRY(moe_route(logits, w.topk_w, w.topk_id, T, E, top_k, renorm, st));
+    moe_group_kernel<<<1, 1024, 0, st>>>(w.topk_id, T, E, top_k, w.offsets, w.row_token,
+                                         w.pos_of_pair);
+    PIO_LAUNCHED();
+    PIO_TRY(quantize_per_token(x, x_dtype, w.qx, w.sx, T, H, st));
+
+    GroupedParams g{};
+    g.A = w.qx; g.a_rows = w.row_token; g.s_a = w.sx;
+    g.W = w_gu; g.s_w = s_gu; g.offsets = w.offsets; g.C = w.gu;
+    g.N = 2 * I; g.K = H;
+    moe_grouped_gemm_kernel<<<dim3(ceil_div(2 * I, TN), E), 256, 0, st>>>(g);
+    PIO_LAUNCHED();
+
+    moe_swiglu_quant_kernel<<<ceil_div(P, 4), 256, 0, st>>>(w.gu, w.qh, w.sh, P, I);
+    PIO_LAUNCHED();
+
+    GroupedParams d{};
+    d.A = w.qh; d.a_rows = nullptr; d.s_a = w.sh;
+    d.W = w_down; d.s_w = s_down; d.offsets = w.offsets; d.C = w.d;
+    d.N = H; d.K = I;
+    moe_grouped_gemm_kernel<<<dim3(ceil_div(H, TN), E), 256, 0, st>>>(d);
+    PIO_LAUNCHED();
+
+    dim3 cg(ceil_div(H, 256), T);
+    if (out_dtype == PIO_F32)
+        moe_combine_kernel<float><<<cg, 256, 0, st>>>(w.d, w.topk_w, w.pos_of_pair, (float*)out, T, H, top_k);
+    else
+        moe_combine_kernel<_Float16><<<cg, 256, 0, st>>>(w.d, w.topk_w, w.pos_of_pair, (_Float16*)out, T, H, top_k);
+    PIO_LAUNCHED();
+    return PIO_OK;
+}
+
+}  // namespace pio
+
+using namespace pio;
+
+PIO_EXPORT size_t pio_moe_workspace(int T, int H, int I, int E, int top_k) {
+    return moe_layout(nullptr, T, H, I, E, top_k).total;
+}
+
+PIO_EXPORT int pio_moe_route(const float* logits, float* topk_w, int32_t* topk_id, int T, int E,
+                             int top_k, int renorm, void* stream) {
+    return moe_route(logits, topk_w, topk_id, T, E, top_k, renorm, pick_stream(stream));
+}
+
+PIO_EXPORT int pio_moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* w_gu,
+                            const float* s_gu, const int8_t* w_down, const float* s_down, void* out,
+                            int out_dtype, int T, int H, int I, int E, int top_k, int renorm,
+                            void* workspace, void* stream) {
+    return moe_w8a8(x, x_dtype, logits, w_gu, s_gu, w_down, s_down, out, out_dtype, T, H, I, E,
+                    top_k, renorm, workspace, pick_stream(stream));
+}
+
+PIO_EXPORT int tensor_moe_w8a8_status(Tensor* x, Tensor* logits, Tensor* w_gu, Tensor* s_gu,
+                                      Tensor* w_down, Tensor* s_down, int top_k, int renorm,
+                                      Tensor* out) {
+    PIO_TRY(check_device_tensor(x, "moe x"));
+    PIO_TRY(check_device_tensor(logits, "moe logits"));
+    PIO_TRY(check_device_tensor(w_gu, "moe w_gu"));
+    PIO_TRY(check_device_tensor(s_gu, "moe s_gu"));
+    PIO_TRY(check_device_tensor(w_down, "moe w_down"));
+    PIO_TRY(check_device_tensor(s_down, "moe s_down"));
+    PIO_TRY(check_device_tensor(out, "moe out"));
+    PIO_REQUIRE(w_gu->ndim == 3 && w_down->ndim == 3, "moe: expert weights must be 3-D");
+    const int E = w_gu->shape[0], I2 = w_gu->shape[1], H = w_gu->shape[2];
+    PIO_REQUIRE(I2 % 2 == 0, "moe: gate_up rows must be even");
+    const int I = I2 / 2;
+    PIO_REQUIRE(w_down->shape[0] == E && w_down->shape[1] == H && w_down->shape[2] == I,
+                "moe: w_down must be [%d,%d,%d]", E, H, I);
+    PIO_REQUIRE(s_gu->size == E * I2 && s_down->size == E * H, "moe: scale sizes mismatch");
+    PIO_REQUIRE(last_dim(x) == H, "moe: x last dim must be %d", H);
+    const int T = x->size / H;
+    PIO_REQUIRE(logits->size == T * E, "moe: logits must be [%d,%d]", T, E);
+    PIO_REQUIRE(out->size == T * H, "moe: out must be [%d,%d]", T, H);
+    return moe_w8a8(x->data, tensor_dtype_of(x), logits->data, (const int8_t*)w_gu->data,
+                    s_gu->data, (const int8_t*)w_down->data, s_down->data, out->data,
+                    tensor_dtype_of(out), T, H, I, E, top_k, renorm, nullptr, current_stream());
+}
+PIO_EXPORT void tensor_moe_w8a8(Tensor* x, Tensor* logits, Tensor* w_gu, Tensor* s_gu,
+                                Tensor* w_down, Tensor* s_down, int top_k, int renorm,
+                                Tensor* out) {
+    tensor_moe_w8a8_status(x, logits, w_gu, s_gu, w_down, s_down, top_k, renorm, out);
+}

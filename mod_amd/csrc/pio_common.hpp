@@ -1,0 +1,110 @@
+// Internal helpers shared by the HIP translation units of libtensor_ops_rocm.so.
+// gfx950 only: wave64, int8 MFMA, 160 KB LDS per CU.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stddef.h>
+#include <stdarg.h>
+
+#include "tensor_rocm.h"
+
+#define PIO_EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace pio {
+
+// ---- error channel -------------------------------------------------------
+// Records a printf-style message for tensor_last_error() and returns `code`.
+int set_error(int code, const char* fmt, ...);
+void clear_error();
+
+// Wraps a HIP call; on failure records the HIP error string and returns.
+#define PIO_HIP(call)                                                                      \
+    do {                                                                                   \
+        hipError_t _e = (call);                                                            \
+        if (_e != hipSuccess)                                                              \
+            return ::pio::set_error(PIO_ERR_HIP, "%s failed: %s (%s:%d)", #call,           \
+                                    hipGetErrorString(_e), __FILE__, __LINE__);            \
+    } while (0)
+
+#define PIO_REQUIRE(cond, ...)                                                             \
+    do {                                                                                   \
+        if (!(cond)) return ::pio::set_error(PIO_ERR_INVALID, __VA_ARGS__);                \
+    } while (0)
+
+// Propagates a non-OK status.
+#define PIO_TRY(expr)                                                                      \
+    do {                                                                                   \
+        int _s = (expr);                                                                   \
+        if (_s != PIO_OK) return _s;                                                       \
+    } while (0)
+
+// Checks the launch status of the kernel just issued.
+#define PIO_LAUNCHED() PIO_HIP(hipGetLastError())
+
+// ---- streams -------------------------------------------------------------
+// The stream raw entry points run on when given NULL: the one set by
+// set_current_stream(), else the library's own in-order stream for the
+// current device (created on first use, default priority).
+hipStream_t current_stream();
+inline hipStream_t pick_stream(void* s) { return s ? (hipStream_t)s : current_stream(); }
+
+// ---- dtypes --------------------------------------------------------------
+inline size_t dtype_bytes(int dt) {
+    switch (dt) {
+    case PIO_F32: return 4;
+    case PIO_F16: return 2;
+    case PIO_I8: return 1;
+    case PIO_I32: return 4;
+    default: return 0;
+    }
+}
+
+// ---- device allocation (caching allocator, runtime.hip) -------------------
+int device_alloc(void** p, size_t bytes);   // on the current device
+void device_free(void* p);                  // back to the cache (or no-op for pool memory)
+
+// Scoped device scratch from the caching allocator.
+struct Scratch {
+    void* ptr = nullptr;
+    ~Scratch() { if (ptr) device_free(ptr); }
+    int get(size_t bytes) { return bytes ? device_alloc(&ptr, bytes) : PIO_OK; }
+};
+
+// ---- Tensor metadata -------------------------------------------------------
+// Element type the tensor was created with (PIO_F32 for create_tensor and for
+// tensors this library did not create).
+int tensor_dtype_of(const Tensor* t);
+inline int64_t numel(const Tensor* t) { return t ? (int64_t)t->size : 0; }
+inline int last_dim(const Tensor* t) { return t->shape[t->ndim - 1]; }
+
+// Validates a device tensor argument.
+int check_device_tensor(const Tensor* t, const char* what);
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// ---- device helpers --------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+template <typename T> __device__ __forceinline__ float to_f32(T v);
+template <> __device__ __forceinline__ float to_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ float to_f32<_Float16>(_Float16 v) { return (float)v; }
+
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+// v_cvt_f16_f32 under the default round-to-nearest-even mode.
+template <> __device__ __forceinline__ _Float16 from_f32<_Float16>(float v) { return (_Float16)v; }
+
+inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+}  // namespace pio

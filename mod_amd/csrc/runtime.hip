@@ -1,0 +1,537 @@
+// Runtime half of libtensor_ops_rocm.so: error channel, streams, graphs, the
+// HBM allocator and the reference's required Tensor* exports.
+//
+// Allocator. The reference CPU backend owns one bump arena (tensor_ops.c:69-133)
+// and falls back to aligned malloc; its Python layer allocates every op output
+// (backend.py:463), so a decode step creates and frees hundreds of tensors. On a
+// GPU each hipMalloc/hipFree is a driver call (hipFree also synchronizes), so
+// here device memory goes through a caching allocator: sizes are rounded (256 B
+// granules up to 1 MiB, 2 MiB granules above), freed blocks go to an exact-size
+// free list and are reused by the next request of that size. init_memory_pool()
+// adds the reference's arena on top: while it has room, device tensors are
+// bump-allocated from it and freeing them is a no-op (tensor_ops.c:135-162).
+// Everything is ordered on one in-order stream per device, so a block freed
+// after its last kernel was enqueued can be handed out again immediately.
+#include "pio_common.hpp"
+
+#include <mutex>
+#include <map>
+#include <unordered_map>
+#include <vector>
+#include <string.h>
+#include <stdio.h>
+#include <stdlib.h>
+
+namespace pio {
+
+// ---------------------------------------------------------------- errors ---
+static thread_local char t_err[1024];
+
+int set_error(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(t_err, sizeof(t_err), fmt, ap);
+    va_end(ap);
+    if (getenv("PIO_VERBOSE")) fprintf(stderr, "[tensor_ops_rocm] %s\n", t_err);
+    return code;
+}
+void clear_error() { t_err[0] = 0; }
+
+// --------------------------------------------------------------- streams ---
+static std::mutex g_mu;
+static hipStream_t g_user_stream = nullptr;
+static std::map<int, hipStream_t> g_dev_stream;
+
+hipStream_t current_stream() {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_user_stream) return g_user_stream;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    auto it = g_dev_stream.find(dev);
+    if (it != g_dev_stream.end()) return it->second;
+    hipStream_t s = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    g_dev_stream[dev] = s;
+    return s;
+}
+
+// ------------------------------------------------------------- allocator ---
+struct Arena {
+    char* base = nullptr;
+    size_t size = 0;
+    size_t used = 0;
+};
+
+struct Alloc {
+    std::mutex mu;
+    std::unordered_map<void*, std::pair<size_t, int>> live;   // ptr -> (rounded bytes, device)
+    std::unordered_map<void*, int> arena_live;                // ptr -> device
+    std::map<std::pair<int, size_t>, std::vector<void*>> free_lists;
+    std::map<int, Arena> arenas;
+    size_t reserved = 0, in_use = 0, cached = 0, peak = 0, n_malloc = 0;
+};
+static Alloc& A() {
+    static Alloc* a = new Alloc();   // never destroyed: frees after exit are no-ops
+    return *a;
+}
+
+static size_t round_bytes(size_t b) {
+    if (b == 0) b = 1;
+    const size_t small = 256, big = size_t(2) << 20;
+    return b <= (size_t(1) << 20) ? (b + small - 1) / small * small : (b + big - 1) / big * big;
+}
+
+static void empty_cache_locked(Alloc& a) {
+    for (auto& kv : a.free_lists) {
+        for (void* p : kv.second) {
+            int cur = 0;
+            (void)hipGetDevice(&cur);
+            (void)hipSetDevice(kv.first.first);
+            (void)hipFree(p);
+            (void)hipSetDevice(cur);
+            a.reserved -= kv.first.second;
+            a.cached -= kv.first.second;
+        }
+    }
+    a.free_lists.clear();
+}
+
+int device_alloc(void** out, size_t bytes) {
+    *out = nullptr;
+    int dev = 0;
+    PIO_HIP(hipGetDevice(&dev));
+    Alloc& a = A();
+    std::lock_guard<std::mutex> lk(a.mu);
+    size_t r = round_bytes(bytes);
+    auto ait = a.arenas.find(dev);
+    if (ait != a.arenas.end() && ait->second.base) {
+        Arena& ar = ait->second;
+        size_t off = (ar.used + 255) / 256 * 256;
+        if (off + r <= ar.size) {
+            *out = ar.base + off;
+            ar.used = off + r;
+            a.arena_live[*out] = dev;
+            return PIO_OK;
+        }
+    }
+    auto fit = a.free_lists.find({dev, r});
+    if (fit != a.free_lists.end() && !fit->second.empty()) {
+        *out = fit->second.back();
+        fit->second.pop_back();
+        a.cached -= r;
+    } else {
+        void* p = nullptr;
+        hipError_t e = hipMalloc(&p, r);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            empty_cache_locked(a);
+            e = hipMalloc(&p, r);
+        }
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return set_error(PIO_ERR_OOM, "hipMalloc(%zu) failed on device %d: %s", r, dev,
+                             hipGetErrorString(e));
+        }
+        a.reserved += r;
+        a.n_malloc++;
+        *out = p;
+    }
+    a.live[*out] = {r, dev};
+    a.in_use += r;
+    if (a.in_use > a.peak) a.peak = a.in_use;
+    return PIO_OK;
+}
+
+void device_free(void* p) {
+    if (!p) return;
+    Alloc& a = A();
+    std::lock_guard<std::mutex> lk(a.mu);
+    if (a.arena_live.erase(p)) return;   // pool memory: reclaimed by reset_memory_pool
+    auto it = a.live.find(p);
+    if (it == a.live.end()) return;
+    size_t r = it->second.first;
+    int dev = it->second.second;
+    a.live.erase(it);
+    a.in_use -= r;
+    a.cached += r;
+    a.free_lists[{dev, r}].push_back(p);
+}
+
+// ------------------------------------------------------ tensor metadata ---
+struct Meta {
+    int dtype;
+    size_t bytes;
+};
+static std::mutex g_meta_mu;
+static std::unordered_map<const Tensor*, Meta> g_meta;
+
+int tensor_dtype_of(const Tensor* t) {
+    std::lock_guard<std::mutex> lk(g_meta_mu);
+    auto it = g_meta.find(t);
+    return it == g_meta.end() ? PIO_F32 : it->second.dtype;
+}
+static size_t tensor_bytes_of(const Tensor* t) {
+    std::lock_guard<std::mutex> lk(g_meta_mu);
+    auto it = g_meta.find(t);
+    return it == g_meta.end() ? (size_t)t->size * 4 : it->second.bytes;
+}
+
+int check_device_tensor(const Tensor* t, const char* what) {
+    if (!t) return set_error(PIO_ERR_INVALID, "%s: null tensor", what);
+    if (!t->data && t->size > 0) return set_error(PIO_ERR_INVALID, "%s: null data", what);
+    if (t->device_id < 0)
+        return set_error(PIO_ERR_INVALID, "%s: tensor is on the host (device_id=%d)", what,
+                         t->device_id);
+    if (t->ndim < 1 || !t->shape) return set_error(PIO_ERR_INVALID, "%s: ndim < 1", what);
+    return PIO_OK;
+}
+
+// --------------------------------------------------------- small kernels ---
+template <typename T>
+__global__ void fill_kernel(T* p, int64_t n, T v) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+__global__ void binary_kernel(const float* a, const float* b, float* o, int64_t n, int op) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        o[i] = op == 0 ? a[i] + b[i] : a[i] * b[i];
+}
+
+static int grid_for(int64_t n) {
+    int64_t g = (n + 255) / 256;
+    if (g < 1) g = 1;
+    if (g > 8192) g = 8192;
+    return (int)g;
+}
+
+}  // namespace pio
+
+using namespace pio;
+
+// ======================================================== exported C ABI ===
+
+PIO_EXPORT const char* tensor_last_error(void) { return t_err; }
+PIO_EXPORT void tensor_clear_error(void) { clear_error(); }
+
+PIO_EXPORT const char* pio_version(void) {
+    return "libtensor_ops_rocm 0.1 (gfx950, int8 quantized-linear path)";
+}
+
+static Tensor* make_tensor(const int* shape, int ndim, int device_id, int dtype) {
+    if (ndim < 0 || (ndim > 0 && !shape)) {
+        set_error(PIO_ERR_INVALID, "create_tensor: bad ndim %d", ndim);
+        return nullptr;
+    }
+    size_t eb = dtype_bytes(dtype);
+    if (!eb) {
+        set_error(PIO_ERR_INVALID, "create_tensor: bad dtype %d", dtype);
+        return nullptr;
+    }
+    int64_t n = 1;
+    for (int i = 0; i < ndim; i++) {
+        if (shape[i] < 0) {
+            set_error(PIO_ERR_INVALID, "create_tensor: negative dim");
+            return nullptr;
+        }
+        n *= shape[i];
+    }
+    if (n > INT32_MAX) {
+        set_error(PIO_ERR_INVALID, "create_tensor: %lld elements exceed the int size field",
+                  (long long)n);
+        return nullptr;
+    }
+    Tensor* t = (Tensor*)calloc(1, sizeof(Tensor));
+    if (!t) return nullptr;
+    t->ndim = ndim;
+    t->shape = (int*)malloc(sizeof(int) * (ndim > 0 ? ndim : 1));
+    if (!t->shape) {
+        free(t);
+        return nullptr;
+    }
+    for (int i = 0; i < ndim; i++) t->shape[i] = shape[i];
+    t->size = (int)n;
+    t->device_id = device_id;
+    size_t bytes = (size_t)n * eb;
+    if (device_id >= 0) {
+        int cur = 0;
+        (void)hipGetDevice(&cur);
+        if (cur != device_id && hipSetDevice(device_id) != hipSuccess) {
+            set_error(PIO_ERR_INVALID, "create_tensor: no device %d", device_id);
+            free(t->shape);
+            free(t);
+            return nullptr;
+        }
+        void* p = nullptr;
+        if (device_alloc(&p, bytes) != PIO_OK) {
+            free(t->shape);
+            free(t);
+            return nullptr;
+        }
+        t->data = (float*)p;
+    } else {
+        size_t hb = (bytes + 63) / 64 * 64;
+        t->data = (float*)aligned_alloc(64, hb ? hb : 64);
+        if (!t->data) {
+            set_error(PIO_ERR_OOM, "create_tensor: host alloc of %zu bytes failed", bytes);
+            free(t->shape);
+            free(t);
+            return nullptr;
+        }
+    }
+    {
+        std::lock_guard<std::mutex> lk(g_meta_mu);
+        g_meta[t] = Meta{dtype, bytes};
+    }
+    return t;
+}
+
+PIO_EXPORT Tensor* create_tensor(int* shape, int ndim, int device_id) {
+    return make_tensor(shape, ndim, device_id, PIO_F32);
+}
+PIO_EXPORT Tensor* create_tensor_typed(int* shape, int ndim, int device_id, int dtype) {
+    return make_tensor(shape, ndim, device_id, dtype);
+}
+PIO_EXPORT int tensor_dtype(Tensor* t) { return tensor_dtype_of(t); }
+
+PIO_EXPORT void free_tensor(Tensor* t) {
+    if (!t) return;
+    bool ours;
+    {
+        std::lock_guard<std::mutex> lk(g_meta_mu);
+        ours = g_meta.erase(t) > 0;
+    }
+    if (ours && t->data) {
+        if (t->device_id >= 0) device_free(t->data);
+        else free(t->data);
+    }
+    if (ours) {
+        free(t->shape);
+        free(t);
+    }
+}
+
+static int fill_impl(Tensor* t, float v) {
+    if (!t) return set_error(PIO_ERR_INVALID, "tensor_fill: null tensor");
+    int dt = tensor_dtype_of(t);
+    int64_t n = t->size;
+    if (t->device_id < 0) {
+        for (int64_t i = 0; i < n; i++) {
+            if (dt == PIO_F32) t->data[i] = v;
+            else return set_error(PIO_ERR_UNSUPPORTED, "tensor_fill: host fill needs fp32");
+        }
+        return PIO_OK;
+    }
+    if (n == 0) return PIO_OK;
+    hipStream_t s = current_stream();
+    switch (dt) {
+    case PIO_F32: fill_kernel<float><<<grid_for(n), 256, 0, s>>>(t->data, n, v); break;
+    case PIO_F16:
+        fill_kernel<_Float16><<<grid_for(n), 256, 0, s>>>((_Float16*)t->data, n, (_Float16)v);
+        break;
+    case PIO_I8: {
+        float c = v > 127.f ? 127.f : (v < -128.f ? -128.f : v);
+        fill_kernel<int8_t><<<grid_for(n), 256, 0, s>>>((int8_t*)t->data, n, (int8_t)(int)c);
+        break;
+    }
+    case PIO_I32:
+        fill_kernel<int32_t><<<grid_for(n), 256, 0, s>>>((int32_t*)t->data, n, (int32_t)v);
+        break;
+    default: return set_error(PIO_ERR_INVALID, "tensor_fill: bad dtype");
+    }
+    PIO_LAUNCHED();
+    return PIO_OK;
+}
+PIO_EXPORT void tensor_fill(Tensor* t, float value) { fill_impl(t, value); }
+
+static int binary_impl(Tensor* a, Tensor* b, Tensor* o, int op) {
+    const char* nm = op == 0 ? "tensor_add" : "tensor_mul";
+    PIO_REQUIRE(a && b && o, "%s: null tensor", nm);
+    PIO_REQUIRE(a->size >= o->size && b->size >= o->size, "%s: operands smaller than out", nm);
+    if (o->device_id < 0) {
+        PIO_REQUIRE(a->device_id < 0 && b->device_id < 0, "%s: device mismatch", nm);
+        for (int i = 0; i < o->size; i++)
+            o->data[i] = op == 0 ? a->data[i] + b->data[i] : a->data[i] * b->data[i];
+        return PIO_OK;
+    }
+    PIO_REQUIRE(a->device_id == o->device_id && b->device_id == o->device_id,
+                "%s: device mismatch", nm);
+    if (o->size == 0) return PIO_OK;
+    binary_kernel<<<grid_for(o->size), 256, 0, current_stream()>>>(a->data, b->data, o->data,
+                                                                    o->size, op);
+    PIO_LAUNCHED();
+    return PIO_OK;
+}
+PIO_EXPORT void tensor_add(Tensor* a, Tensor* b, Tensor* out) { binary_impl(a, b, out, 0); }
+PIO_EXPORT void tensor_mul(Tensor* a, Tensor* b, Tensor* out) { binary_impl(a, b, out, 1); }
+
+static int copy_bytes(Tensor* t, void* host, size_t nbytes, bool h2d) {
+    PIO_REQUIRE(t && (host || nbytes == 0), "tensor copy: null argument");
+    size_t cap = tensor_bytes_of(t);
+    PIO_REQUIRE(nbytes <= cap, "tensor copy: %zu bytes exceed the tensor's %zu", nbytes, cap);
+    if (nbytes == 0) return PIO_OK;
+    if (t->device_id < 0) {
+        if (h2d) memcpy(t->data, host, nbytes);
+        else memcpy(host, t->data, nbytes);
+        return PIO_OK;
+    }
+    hipStream_t s = current_stream();
+    if (h2d) PIO_HIP(hipMemcpyAsync(t->data, host, nbytes, hipMemcpyHostToDevice, s));
+    else PIO_HIP(hipMemcpyAsync(host, t->data, nbytes, hipMemcpyDeviceToHost, s));
+    PIO_HIP(hipStreamSynchronize(s));
+    return PIO_OK;
+}
+
+PIO_EXPORT void tensor_load_data(Tensor* t, float* buffer, int size) {
+    copy_bytes(t, buffer, size > 0 ? (size_t)size * 4 : 0, true);
+}
+PIO_EXPORT void tensor_get_data(Tensor* t, float* buffer, int size) {
+    copy_bytes(t, buffer, size > 0 ? (size_t)size * 4 : 0, false);
+}
+PIO_EXPORT int tensor_load_bytes_status(Tensor* t, const void* src, size_t nbytes) {
+    return copy_bytes(t, (void*)src, nbytes, true);
+}
+PIO_EXPORT int tensor_get_bytes_status(Tensor* t, void* dst, size_t nbytes) {
+    return copy_bytes(t, dst, nbytes, false);
+}
+PIO_EXPORT void tensor_load_bytes(Tensor* t, const void* src, size_t nbytes) {
+    tensor_load_bytes_status(t, src, nbytes);
+}
+PIO_EXPORT void tensor_get_bytes(Tensor* t, void* dst, size_t nbytes) {
+    tensor_get_bytes_status(t, dst, nbytes);
+}
+
+// ------------------------------------------------------------ pool / stats ---
+PIO_EXPORT void init_memory_pool(size_t size_bytes) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        set_error(PIO_ERR_HIP, "init_memory_pool: no device");
+        return;
+    }
+    Alloc& a = A();
+    std::lock_guard<std::mutex> lk(a.mu);
+    Arena& ar = a.arenas[dev];
+    if (ar.base) return;   // already initialised (tensor_ops.c:75)
+    void* p = nullptr;
+    if (hipMalloc(&p, size_bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        set_error(PIO_ERR_OOM, "init_memory_pool: hipMalloc(%zu) failed", size_bytes);
+        return;
+    }
+    ar.base = (char*)p;
+    ar.size = size_bytes;
+    ar.used = 0;
+}
+
+PIO_EXPORT void reset_memory_pool(void) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    Alloc& a = A();
+    std::lock_guard<std::mutex> lk(a.mu);
+    auto it = a.arenas.find(dev);
+    if (it == a.arenas.end()) return;
+    it->second.used = 0;
+    for (auto i = a.arena_live.begin(); i != a.arena_live.end();)
+        i = i->second == dev ? a.arena_live.erase(i) : std::next(i);
+}
+
+PIO_EXPORT void tensor_pool_stats(size_t* s) {
+    if (!s) return;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    Alloc& a = A();
+    std::lock_guard<std::mutex> lk(a.mu);
+    s[0] = a.reserved;
+    s[1] = a.in_use;
+    s[2] = a.cached;
+    s[3] = a.peak;
+    s[4] = a.n_malloc;
+    auto it = a.arenas.find(dev);
+    s[5] = it == a.arenas.end() ? 0 : it->second.size;
+    s[6] = it == a.arenas.end() ? 0 : it->second.used;
+}
+
+PIO_EXPORT void tensor_empty_cache(void) {
+    Alloc& a = A();
+    std::lock_guard<std::mutex> lk(a.mu);
+    empty_cache_locked(a);
+}
+
+PIO_EXPORT void* allocate_pinned_memory(size_t size) {
+    void* p = nullptr;
+    if (hipHostMalloc(&p, size ? size : 1, hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        set_error(PIO_ERR_OOM, "allocate_pinned_memory(%zu) failed", size);
+        return nullptr;
+    }
+    return p;
+}
+PIO_EXPORT void free_pinned_memory(void* ptr) {
+    if (ptr) (void)hipHostFree(ptr);
+}
+
+// ---------------------------------------------------------------- streams ---
+PIO_EXPORT void* create_stream(void) {
+    hipStream_t s = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) {
+        set_error(PIO_ERR_HIP, "create_stream failed");
+        return nullptr;
+    }
+    return (void*)s;
+}
+PIO_EXPORT void destroy_stream(void* s) {
+    if (!s) return;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        if (g_user_stream == (hipStream_t)s) g_user_stream = nullptr;
+    }
+    (void)hipStreamDestroy((hipStream_t)s);
+}
+PIO_EXPORT void stream_synchronize(void* s) {
+    (void)hipStreamSynchronize(s ? (hipStream_t)s : current_stream());
+}
+PIO_EXPORT void set_current_stream(void* s) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_user_stream = (hipStream_t)s;
+}
+PIO_EXPORT void* get_current_stream(void) { return (void*)current_stream(); }
+PIO_EXPORT void device_synchronize(void) { (void)hipDeviceSynchronize(); }
+
+// ----------------------------------------------------------------- graphs ---
+// One captured graph per process, matching the reference wrapper's
+// begin_capture/end_capture/replay_graph (backend.py:801-810).
+static hipGraph_t g_graph = nullptr;
+static hipGraphExec_t g_graph_exec = nullptr;
+static hipStream_t g_capture_stream = nullptr;
+
+PIO_EXPORT void begin_capture(void) {
+    g_capture_stream = current_stream();
+    if (hipStreamBeginCapture(g_capture_stream, hipStreamCaptureModeRelaxed) != hipSuccess)
+        set_error(PIO_ERR_HIP, "begin_capture failed");
+}
+PIO_EXPORT void end_capture(void) {
+    if (!g_capture_stream) return;
+    if (g_graph_exec) {
+        (void)hipGraphExecDestroy(g_graph_exec);
+        g_graph_exec = nullptr;
+    }
+    if (g_graph) {
+        (void)hipGraphDestroy(g_graph);
+        g_graph = nullptr;
+    }
+    if (hipStreamEndCapture(g_capture_stream, &g_graph) != hipSuccess) {
+        set_error(PIO_ERR_HIP, "end_capture failed");
+        return;
+    }
+    if (hipGraphInstantiate(&g_graph_exec, g_graph, nullptr, nullptr, 0) != hipSuccess)
+        set_error(PIO_ERR_HIP, "hipGraphInstantiate failed");
+}
+PIO_EXPORT void replay_graph(void) {
+    if (!g_graph_exec) {
+        set_error(PIO_ERR_INVALID, "replay_graph: nothing captured");
+        return;
+    }
+    if (hipGraphLaunch(g_graph_exec, g_capture_stream) != hipSuccess)
+        set_error(PIO_ERR_HIP, "hipGraphLaunch failed");
+}

@@ -1,0 +1,141 @@
+"""CPU-only checks of the C-ABI library: it loads, exports every symbol the
+header declares plus the ones the reference binding requires unconditionally,
+and rejects malformed calls before touching a GPU."""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "tensor_rocm.h"
+
+
+def header_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"^[A-Za-z_][\w\s\*]*?\b([A-Za-z_]\w*)\s*\([^;{]*\)\s*;", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_header_parses():
+    names = header_functions()
+    assert "create_tensor" in names and "pio_gemv_w8" in names and len(names) > 40
+
+
+def test_library_exports_every_declared_symbol():
+    from mod_amd import ops
+    missing = [n for n in header_functions() if not hasattr(ops.lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    # The Python signature table covers exactly the header.
+    assert sorted(ops.SIGNATURES) == header_functions()
+
+
+def test_reference_required_symbols_exported():
+    """backend.py:49-55, 67-68 set argtypes on these without hasattr."""
+    from mod_amd import ops
+    for n in ("create_tensor", "free_tensor", "tensor_fill", "tensor_add", "tensor_mul",
+              "tensor_load_data", "tensor_get_data"):
+        assert hasattr(ops.lib, n), n
+
+
+def test_no_unexpected_dynamic_exports():
+    from mod_amd import ops
+    out = subprocess.run(["nm", "-D", "--defined-only", str(ops.LIB_FILE)], capture_output=True,
+                         text=True, check=True).stdout
+    syms = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    extra = sorted(s for s in syms if s not in set(header_functions()))
+    assert not extra, f"exported but not declared: {extra}"
+
+
+def test_ctensor_layout_matches_reference_struct():
+    from mod_amd.ops import CTensor
+    assert [f[0] for f in CTensor._fields_] == ["data", "shape", "ndim", "size", "device_id"]
+    assert ctypes.sizeof(CTensor) == 32
+
+
+def test_product_never_imports_oracle():
+    for p in (ROOT / "mod_amd").rglob("*.py"):
+        src = p.read_text()
+        assert not re.search(r"^\s*(from|import)\s+oracle\b", src, flags=re.M), p
+
+
+def test_build_flags_disable_packed_fp32():
+    from mod_amd import build_ops
+    flags = " ".join(build_ops.HIP_FLAGS)
+    assert "-Xclang -target-feature -Xclang -packed-fp32-ops" in flags
+    assert "--offload-arch=gfx950" in flags
+
+
+# Invalid arguments are rejected before any HIP call. A non-null stream value
+# is passed so the library does not create its own stream; it is never used.
+FAKE_STREAM = 1
+
+
+def test_gemv_rejects_bad_k_without_gpu():
+    from mod_amd import ops
+    rc = ops.lib.pio_gemv_w8(16, ops.F32, 16, 16, None, 16, ops.F32, 1, 8, 15, FAKE_STREAM)
+    assert rc == ops.ERR_INVALID
+    assert "multiple of 16" in ops.last_error()
+
+
+def test_gemm_rejects_bad_dtype_and_null():
+    from mod_amd import ops
+    rc = ops.lib.pio_gemm_w8a8(16, 16, 16, 16, None, 16, 7, 4, 4, 16, FAKE_STREAM)
+    assert rc == ops.ERR_INVALID and "dtype" in ops.last_error()
+    rc = ops.lib.pio_gemm_w8a8(None, 16, 16, 16, None, 16, ops.F16, 4, 4, 16, FAKE_STREAM)
+    assert rc == ops.ERR_INVALID and "null" in ops.last_error()
+
+
+def test_quantizer_and_moe_reject_bad_args():
+    from mod_amd import ops
+    assert ops.lib.pio_quantize_per_token(16, 9, 16, 16, 4, 16, FAKE_STREAM) == ops.ERR_INVALID
+    assert ops.lib.pio_moe_route(16, 16, 16, 4, 2000, 8, 0, FAKE_STREAM) == ops.ERR_INVALID
+    assert ops.lib.pio_moe_w8a8(16, ops.F32, 16, 16, 16, 16, 16, 16, ops.F32, 8, 30, 16, 8, 2, 0,
+                                None, FAKE_STREAM) == ops.ERR_INVALID
+    assert "multiples of 16" in ops.last_error()
+
+
+def test_tensor_layer_rejects_host_tensors_and_nulls():
+    from mod_amd import ops
+    rc = ops.lib.tensor_linear_w8_status(None, None, None, None, None)
+    assert rc == ops.ERR_INVALID and "null" in ops.last_error()
+    # A host tensor (device_id -1) is refused by the GPU ops.
+    shape = (ctypes.c_int * 2)(2, 16)
+    t = ops.lib.create_tensor(shape, 2, -1)
+    assert t
+    try:
+        assert ops.lib.tensor_quantize_per_token_status(t, t, t) == ops.ERR_INVALID
+        assert "host" in ops.last_error()
+    finally:
+        ops.lib.free_tensor(t)
+
+
+def test_host_tensor_roundtrip_without_gpu():
+    """create_tensor(device_id=-1) behaves like the reference CPU tensor."""
+    import numpy as np
+    from mod_amd import ops
+    shape = (ctypes.c_int * 2)(2, 3)
+    t = ops.lib.create_tensor(shape, 2, -1)
+    try:
+        data = np.arange(6, dtype=np.float32)
+        ops.lib.tensor_load_data(t, data.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), 6)
+        ops.lib.tensor_fill  # exported
+        out = np.zeros(6, np.float32)
+        ops.lib.tensor_get_data(t, out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), 6)
+        assert np.array_equal(out, data)
+        assert t.contents.size == 6 and t.contents.device_id == -1
+        ops.lib.tensor_add(t, t, t)
+        ops.lib.tensor_get_data(t, out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), 6)
+        assert np.array_equal(out, 2 * data)
+        # Loading more bytes than the tensor holds is refused, not written.
+        big = np.zeros(100, np.float32)
+        assert ops.lib.tensor_load_bytes_status(t, big.ctypes.data, 400) == ops.ERR_INVALID
+    finally:
+        ops.lib.free_tensor(t)
+
+
+def test_version_string():
+    from mod_amd import ops
+    assert "gfx950" in ops.version()

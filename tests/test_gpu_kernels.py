@@ -1,0 +1,276 @@
+"""GPU parity of the HIP kernels against the CPU oracle, through the C ABI.
+
+Tolerances (from the path's correctness bar): int32 accumulators, quantized
+bytes and scales are bit-exact; fp32 outputs within rel 1e-3, fp16 outputs
+within rel 1e-2 (elementwise, floor 1e-2 * rms; see conftest.assert_rel).
+Inputs: numpy default_rng(seed); weights randint(-127, 127) (exclusive upper
+bound, so [-127, 126]), scales U(0.001, 0.02), activations N(0, 1).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import assert_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def env(torch_dev):
+    import torch
+    from mod_amd import ops
+    return torch, ops, torch_dev
+
+
+def dev(torch, a, device):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+def sync(torch):
+    torch.cuda.synchronize()
+
+
+def stream(torch):
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _inputs(seed, M, N, K, x_dtype=np.float32):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((M, K), dtype=np.float32).astype(x_dtype)
+    W = rng.integers(-127, 127, size=(N, K), dtype=np.int8)
+    s = rng.uniform(0.001, 0.02, size=N).astype(np.float32)
+    return x, W, s
+
+
+# -------------------------------------------------------------------- GEMV
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_gemv_c1_fp32(env, seed):
+    torch, ops, d = env
+    M, N, K = 1, 3072, 1024
+    _say(f"gemv C1 seed={seed}")
+    x, W, s = _inputs(seed, M, N, K)
+    y = torch.empty((M, N), dtype=torch.float32, device=d)
+    ops.gemv_w8(dev(torch, x, d), dev(torch, W, d), dev(torch, s, d), None, y, M, N, K, stream(torch))
+    sync(torch)
+    assert_rel(host(y), oracle.gemv_w8(x, W, s), 1e-3, "gemv C1")
+
+
+@pytest.mark.parametrize("M,N,K,xdt,ydt,bias", [
+    (1, 4096, 1024, np.float32, np.float32, True),     # qkv (bias=True in the reference)
+    (1, 1024, 2048, np.float32, np.float32, False),    # o_proj
+    (1, 1024, 3072, np.float32, np.float32, False),    # down
+    (1, 4000, 1040, np.float32, np.float32, True),     # K tail (not a multiple of 1024)
+    (2, 77, 64, np.float32, np.float16, False),        # tiny N, fp16 out
+    (3, 12288, 4096, np.float16, np.float16, False),   # Qwen3-8B gate/up, fp16 act
+    (4, 4096, 12288, np.float16, np.float16, False),   # Qwen3-8B down
+    (16, 1000, 256, np.float16, np.float32, True),
+    (64, 512, 512, np.float16, np.float16, False),
+])
+def test_gemv_shapes(env, M, N, K, xdt, ydt, bias):
+    torch, ops, d = env
+    _say(f"gemv M={M} N={N} K={K}")
+    x, W, s = _inputs(M * 7 + N, M, N, K, xdt)
+    b = np.random.default_rng(1).standard_normal(N, dtype=np.float32) if bias else None
+    y = torch.empty((M, N), dtype=torch.float16 if ydt == np.float16 else torch.float32, device=d)
+    ops.gemv_w8(dev(torch, x, d), dev(torch, W, d), dev(torch, s, d),
+                None if b is None else dev(torch, b, d), y, M, N, K, stream(torch))
+    sync(torch)
+    ref = oracle.gemv_w8(x, W, s, b, out_dtype=ydt)
+    assert_rel(host(y).astype(np.float64), ref.astype(np.float64),
+               1e-2 if (ydt == np.float16 or xdt == np.float16) else 1e-3, "gemv")
+
+
+def test_gemv_extreme_weights(env):
+    torch, ops, d = env
+    M, N, K = 1, 64, 2048
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    W = np.full((N, K), 127, np.int8)
+    W[1::2] = -128
+    s = np.full(N, 0.01, np.float32)
+    y = torch.empty((M, N), dtype=torch.float32, device=d)
+    ops.gemv_w8(dev(torch, x, d), dev(torch, W, d), dev(torch, s, d), None, y, M, N, K)
+    sync(torch)
+    assert_rel(host(y), oracle.gemv_w8(x, W, s), 1e-3, "gemv extremes")
+
+
+# --------------------------------------------------------------- quantizer
+@pytest.mark.parametrize("M,K,xdt", [(2048, 1024, np.float16), (2048, 3072, np.float16),
+                                     (17, 1000, np.float32), (5, 13, np.float32),
+                                     (512, 2048, np.float16), (3, 12288, np.float32)])
+def test_quant_bitexact(env, M, K, xdt):
+    torch, ops, d = env
+    _say(f"quant M={M} K={K}")
+    rng = np.random.default_rng(M + K)
+    x = (rng.standard_normal((M, K), dtype=np.float32) * rng.uniform(0.1, 10, (M, 1)).astype(np.float32)).astype(xdt)
+    x[0] = 0
+    q = torch.empty((M, K), dtype=torch.int8, device=d)
+    s = torch.empty((M,), dtype=torch.float32, device=d)
+    ops.quantize_per_token(dev(torch, x, d), q, s, M, K, stream(torch))
+    sync(torch)
+    qr, sr = oracle.quant_per_token(x)
+    assert np.array_equal(host(s).view(np.uint32), sr.view(np.uint32))
+    assert np.array_equal(host(q), qr)
+
+
+def test_quant_golden_ties(env):
+    torch, ops, d = env
+    from pathlib import Path
+    g = np.load(Path(__file__).parent / "golden" / "quant_tok.npz")
+    x = g["x"]
+    M, K = x.shape
+    q = torch.empty((M, K), dtype=torch.int8, device=d)
+    s = torch.empty((M,), dtype=torch.float32, device=d)
+    ops.quantize_per_token(dev(torch, x, d), q, s, M, K)
+    sync(torch)
+    assert np.array_equal(host(q), g["q"]) and np.array_equal(host(s), g["s"])
+
+
+# -------------------------------------------------------------------- GEMM
+@pytest.mark.parametrize("M,N,K", [(2048, 3072, 1024), (2048, 1024, 3072), (2048, 2048, 1024),
+                                   (1, 64, 16), (130, 200, 80), (257, 129, 1040), (64, 4096, 4096)])
+def test_gemm_int32_bitexact(env, M, N, K):
+    torch, ops, d = env
+    _say(f"gemm i32 M={M} N={N} K={K}")
+    rng = np.random.default_rng(M + N + K)
+    q = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    W = rng.integers(-127, 127, size=(N, K), dtype=np.int8)
+    c = torch.empty((M, N), dtype=torch.int32, device=d)
+    ops.gemm_w8a8(dev(torch, q, d), None, dev(torch, W, d), None, None, c, M, N, K, stream(torch))
+    sync(torch)
+    assert np.array_equal(host(c), oracle.matmul_nt_i32(q, W))
+
+
+@pytest.mark.parametrize("K,N", [(1024, 3072), (3072, 1024), (1024, 2048)])
+def test_gemm_c3_fp16_pipeline(env, K, N):
+    """C3: x fp16 -> per-token quant -> W8A8 GEMM -> fp16, vs the oracle."""
+    torch, ops, d = env
+    M = 2048
+    _say(f"C3 K={K} N={N}")
+    rng = np.random.default_rng(K + N)
+    x = rng.standard_normal((M, K), dtype=np.float32).astype(np.float16)
+    W = rng.integers(-127, 127, size=(N, K), dtype=np.int8)
+    sw = rng.uniform(0.001, 0.02, size=N).astype(np.float32)
+    q = torch.empty((M, K), dtype=torch.int8, device=d)
+    sa = torch.empty((M,), dtype=torch.float32, device=d)
+    y = torch.empty((M, N), dtype=torch.float16, device=d)
+    acc = torch.empty((M, N), dtype=torch.int32, device=d)
+    wd = dev(torch, W, d)
+    swd = dev(torch, sw, d)
+    ops.quantize_per_token(dev(torch, x, d), q, sa, M, K)
+    ops.gemm_w8a8(q, sa, wd, swd, None, y, M, N, K)
+    ops.gemm_w8a8(q, None, wd, None, None, acc, M, N, K)
+    sync(torch)
+    qr, sr = oracle.quant_per_token(x)
+    assert np.array_equal(host(q), qr)
+    assert np.array_equal(host(acc), oracle.matmul_nt_i32(qr, W))
+    yr = oracle.w8a8(qr, sr, W, sw, out="f16")
+    got = host(y)
+    assert_rel(got.astype(np.float64), yr.astype(np.float64), 1e-2, "C3 fp16")
+    # same formula and rounding on both sides: expect byte equality
+    assert np.array_equal(got.view(np.uint16), yr.view(np.uint16))
+
+
+def test_gemm_fp32_bias(env):
+    torch, ops, d = env
+    M, N, K = 100, 300, 512
+    rng = np.random.default_rng(5)
+    q = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    W = rng.integers(-127, 127, size=(N, K), dtype=np.int8)
+    sa = rng.uniform(0.001, 0.05, M).astype(np.float32)
+    sw = rng.uniform(0.001, 0.02, N).astype(np.float32)
+    b = rng.standard_normal(N, dtype=np.float32)
+    y = torch.empty((M, N), dtype=torch.float32, device=d)
+    ops.gemm_w8a8(dev(torch, q, d), dev(torch, sa, d), dev(torch, W, d), dev(torch, sw, d),
+                  dev(torch, b, d), y, M, N, K)
+    sync(torch)
+    assert_rel(host(y), oracle.w8a8(q, sa, W, sw, b, out="f32"), 1e-5, "gemm f32 bias")
+
+
+# ------------------------------------------------- tensor_matmul_int8 (a1)
+@pytest.mark.parametrize("batch,M,K,N", [(1, 1, 1024, 3072), (2, 5, 37, 7), (3, 64, 1023, 65),
+                                         (1, 128, 256, 128)])
+def test_matmul_int8_matches_reference_semantics(env, batch, M, K, N):
+    torch, ops, d = env
+    _say(f"matmul_int8 b={batch} M={M} K={K} N={N}")
+    rng = np.random.default_rng(batch * 1000 + K)
+    a = rng.integers(-127, 127, size=(batch, M, K), dtype=np.int8)
+    b = rng.integers(-127, 127, size=(batch, K, N), dtype=np.int8)
+    c = torch.empty((batch, M, N), dtype=torch.float32, device=d)
+    ci = torch.empty((batch, M, N), dtype=torch.int32, device=d)
+    ad, bd = dev(torch, a, d), dev(torch, b, d)
+    ops.matmul_int8(ad, bd, c, batch, M, K, N, out_i32=False)
+    ops.matmul_int8(ad, bd, ci, batch, M, K, N, out_i32=True)
+    sync(torch)
+    ref = oracle.matmul_int8(a, b)
+    assert np.array_equal(host(c).view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(host(ci), oracle.matmul_int8(a, b, out_i32=True))
+    if oracle.ref_available():
+        assert np.array_equal(host(c), oracle.ref_matmul_int8(a, b).reshape(c.shape))
+
+
+# --------------------------------------------------------------------- MoE
+def test_moe_route_matches_oracle(env):
+    torch, ops, d = env
+    T, E, k = 512, 128, 8
+    rng = np.random.default_rng(21)
+    lg = rng.standard_normal((T, E), dtype=np.float32)
+    lg[0, :] = 0.5          # all-equal row: ids 0..7
+    lg[1, 3] = lg[1, 9] = 9.0
+    for renorm in (False, True):
+        w = torch.empty((T, k), dtype=torch.float32, device=d)
+        i = torch.empty((T, k), dtype=torch.int32, device=d)
+        ops.moe_route(dev(torch, lg, d), w, i, T, E, k, renorm)
+        sync(torch)
+        wr, ir = oracle.moe_route(lg, k, renorm)
+        assert np.array_equal(host(i), ir)
+        assert_rel(host(w), wr, 1e-5, "route weights")
+    assert list(host(i)[0]) == list(range(8))
+
+
+@pytest.mark.parametrize("T,H,I,E,k,xdt", [(16, 32, 16, 8, 2, np.float32),
+                                           (64, 256, 128, 16, 4, np.float16),
+                                           (512, 2048, 768, 128, 8, np.float16)])
+def test_moe_layer_matches_oracle(env, T, H, I, E, k, xdt):
+    torch, ops, d = env
+    _say(f"moe T={T} H={H} I={I} E={E} k={k}")
+    rng = np.random.default_rng(T + E)
+    x = rng.standard_normal((T, H), dtype=np.float32).astype(xdt)
+    lg = rng.standard_normal((T, E), dtype=np.float32)
+    wgu = rng.integers(-127, 127, size=(E, 2 * I, H), dtype=np.int8)
+    sgu = rng.uniform(0.001, 0.02, size=(E, 2 * I)).astype(np.float32)
+    wd = rng.integers(-127, 127, size=(E, H, I), dtype=np.int8)
+    sd = rng.uniform(0.001, 0.02, size=(E, H)).astype(np.float32)
+    out = torch.empty((T, H), dtype=torch.float32, device=d)
+    ops.moe_w8a8(dev(torch, x, d), dev(torch, lg, d), dev(torch, wgu, d), dev(torch, sgu, d),
+                 dev(torch, wd, d), dev(torch, sd, d), out, T, H, I, E, k, False)
+    sync(torch)
+    ref = oracle.moe_w8a8(x, lg, wgu, sgu, wd, sd, k)
+    # silu's expf differs by ulps between libm and the GPU, which can move a
+    # requantized byte by one; the fp16-level bar covers that.
+    assert_rel(host(out), ref, 1e-2, "moe")
+
+
+def test_moe_tiny_golden(env):
+    torch, ops, d = env
+    from pathlib import Path
+    g = np.load(Path(__file__).parent / "golden" / "moe_tiny.npz")
+    T, H = g["x"].shape
+    E, I2, _ = g["w_gu"].shape
+    out = torch.empty((T, H), dtype=torch.float32, device=d)
+    ops.moe_w8a8(dev(torch, g["x"], d), dev(torch, g["logits"], d), dev(torch, g["w_gu"], d),
+                 dev(torch, g["s_gu"], d), dev(torch, g["w_down"], d), dev(torch, g["s_down"], d),
+                 out, T, H, I2 // 2, E, 2, False)
+    sync(torch)
+    assert_rel(host(out), g["y"], 1e-2, "moe golden")

@@ -1,0 +1,344 @@
+"""Pins the CPU oracle (oracle/int8_ref.c) before it is trusted as the checker.
+
+Each oracle function is checked against something independent of its own
+formula: the reference library itself (compiled from the reference sources by
+oracle/Makefile), exact integer / float64 closed forms, brute force on tiny
+inputs, invariants, and the golden fixtures under tests/golden/.
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+
+GOLD = Path(__file__).resolve().parent / "golden"
+needs_ref = pytest.mark.skipif(not oracle.ref_available(), reason="oracle/_ref not built")
+
+
+# ------------------------------------------------------------------- fp16
+def test_f16_conversion_matches_numpy():
+    rng = np.random.default_rng(0)
+    specials = np.array([0.0, -0.0, 1.0, -1.0, 65504.0, 65519.99, 65520.0, 1e6, -1e6, np.inf,
+                         -np.inf, 6.1035156e-05, 6.1035152e-05, 5.9604645e-08, 2.9802322e-08,
+                         2.9802326e-08, 8.940697e-08, 1e-10, 0.33333334, 2049.0, 2051.0, 2050.0,
+                         1025.5, 1024.5], dtype=np.float32)
+    r = np.concatenate([
+        specials,
+        rng.standard_normal(200000).astype(np.float32) * 100,
+        (rng.standard_normal(100000) * 1e-5).astype(np.float32),
+        rng.uniform(-70000, 70000, 50000).astype(np.float32),
+    ])
+    got = oracle.f32_to_f16_bits(r)
+    exp = r.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, exp)
+    # exact half-way points between neighbouring halves round to even
+    h = np.arange(0, 0x7bff, dtype=np.uint16).view(np.float16).astype(np.float32)
+    mid = ((h[:-1].astype(np.float64) + h[1:].astype(np.float64)) / 2).astype(np.float32)
+    assert np.array_equal(oracle.f32_to_f16_bits(mid), mid.astype(np.float16).view(np.uint16))
+
+
+def test_f16_nan_stays_nan():
+    got = oracle.f32_to_f16_bits(np.array([np.nan], np.float32))
+    assert np.isnan(got.view(np.float16)[0])
+
+
+# ------------------------------------------------------------ int8 matmul
+@needs_ref
+@pytest.mark.parametrize("shape", [(1, 1, 64, 3072), (1, 7, 33, 5), (2, 4, 1023, 9),
+                                   (3, 2, 1025, 17), (1, 16, 256, 64)])
+def test_matmul_int8_bitwise_vs_reference(shape):
+    batch, m, k, n = shape
+    rng = np.random.default_rng(sum(shape))
+    a = rng.integers(-127, 127, size=(batch, m, k), dtype=np.int8)
+    b = rng.integers(-127, 127, size=(batch, k, n), dtype=np.int8)
+    ours = oracle.matmul_int8(a, b)
+    ref = oracle.ref_matmul_int8(a, b)
+    assert ours.dtype == np.float32
+    assert np.array_equal(ours.view(np.uint32), ref.reshape(ours.shape).view(np.uint32))
+
+
+@needs_ref
+def test_matmul_int8_both_reference_builds_agree():
+    rng = np.random.default_rng(9)
+    a = rng.integers(-127, 127, size=(2, 8, 100), dtype=np.int8)
+    b = rng.integers(-127, 127, size=(2, 100, 12), dtype=np.int8)
+    r1 = oracle.ref_matmul_int8(a, b)
+    r2 = oracle.ref_matmul_int8(a, b, lib_=oracle.ref_lib(buildops_flags=True))
+    assert np.array_equal(r1, r2)
+
+
+def test_matmul_int8_closed_form_and_extremes():
+    rng = np.random.default_rng(1)
+    for (m, k, n) in [(1, 1024, 32), (5, 1041, 7), (3, 4096, 3)]:
+        a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+        b = rng.integers(-128, 128, size=(k, n), dtype=np.int8)
+        exact = a.astype(np.int64) @ b.astype(np.int64)
+        assert np.array_equal(oracle.matmul_int8(a, b, out_i32=True)[0], exact)
+        assert np.array_equal(oracle.matmul_int8(a, b)[0], exact.astype(np.float32))
+    # all -127 (sum = 16129*K), mixed +-127, K tail 1025
+    k = 1025
+    a = np.full((2, k), -127, np.int8)
+    b = np.full((k, 3), -127, np.int8)
+    b[:, 1] = 127
+    out = oracle.matmul_int8(a, b, out_i32=True)[0]
+    assert out[0, 0] == 16129 * k and out[0, 1] == -16129 * k
+    # zero operand
+    assert not oracle.matmul_int8(np.zeros((3, 8), np.int8), b[:8], out_i32=True).any()
+
+
+def test_matmul_nt_equals_transposed_reference_loop():
+    rng = np.random.default_rng(2)
+    a = rng.integers(-127, 127, size=(9, 77), dtype=np.int8)
+    w = rng.integers(-127, 127, size=(13, 77), dtype=np.int8)
+    nt = oracle.matmul_nt_i32(a, w)
+    kn = oracle.matmul_int8(a, np.ascontiguousarray(w.T), out_i32=True)[0]
+    assert np.array_equal(nt, kn)
+
+
+def test_golden_mm_i8_small():
+    g = np.load(GOLD / "mm_i8_small.npz")
+    assert np.array_equal(oracle.matmul_int8(g["a"], g["b"]), g["c"])
+
+
+# -------------------------------------------------------------------- GEMV
+@needs_ref
+def test_linear_f32_restatement_vs_reference():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((3, 96), dtype=np.float32)
+    W = rng.standard_normal((40, 96), dtype=np.float32)
+    b = rng.standard_normal(40, dtype=np.float32)
+    ours = oracle.linear_f32(x, W, b)
+    ref = oracle.ref_linear(x, W, b)
+    np.testing.assert_allclose(ours, ref, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_gemv_golden_c1_and_reference_linear(seed):
+    """The W8 GEMV equals the reference fp32 tensor_linear on per-channel
+    dequantized weights (what the model runs today) and the float64 closed form."""
+    g = np.load(GOLD / f"gemv_c1_seed{seed}.npz")
+    y = oracle.gemv_w8(g["x"], g["W"], g["s"])
+    np.testing.assert_allclose(y, g["y_f64"], rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(y, g["y_ref_linear"], rtol=2e-4, atol=2e-4)
+
+
+def test_gemv_special_cases():
+    rng = np.random.default_rng(6)
+    k, n = 64, 16
+    x = rng.standard_normal((2, k), dtype=np.float32)
+    # e_j rows pick x[:, j] * s_w[j] exactly
+    W = np.zeros((n, k), np.int8)
+    W[np.arange(n), np.arange(n) * 3] = 1
+    s = rng.uniform(0.001, 0.02, n).astype(np.float32)
+    y = oracle.gemv_w8(x, W, s)
+    exp = (x[:, np.arange(n) * 3].astype(np.float64) * s.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(y, exp)
+    # bias adds, scaling s_w by 2^3 scales y exactly, linearity in x
+    W = rng.integers(-127, 127, size=(n, k), dtype=np.int8)
+    b = rng.standard_normal(n, dtype=np.float32)
+    y0 = oracle.gemv_w8(x, W, s)
+    yb = oracle.gemv_w8(x, W, s, b)
+    np.testing.assert_allclose(yb - y0, np.broadcast_to(b, y0.shape), rtol=1e-5, atol=1e-5)
+    assert np.array_equal(oracle.gemv_w8(x, W, s * 8), y0 * 8)
+    x2 = rng.standard_normal((2, k), dtype=np.float32)
+    np.testing.assert_allclose(oracle.gemv_w8(x + x2, W, s), y0 + oracle.gemv_w8(x2, W, s),
+                               rtol=1e-4, atol=1e-4)
+    # fp16 activations: identical to fp32 activations holding the same values
+    xh = x.astype(np.float16)
+    assert np.array_equal(oracle.gemv_w8(xh, W, s), oracle.gemv_w8(xh.astype(np.float32), W, s))
+    yh = oracle.gemv_w8(x, W, s, out_dtype=np.float16)
+    assert np.array_equal(yh, y0.astype(np.float16))
+
+
+# --------------------------------------------------------------- quantizer
+def test_quant_golden_ties():
+    g = np.load(GOLD / "quant_tok.npz")
+    q, s = oracle.quant_per_token(g["x"])
+    assert np.array_equal(q, g["q"])
+    assert np.array_equal(s, g["s"])
+
+
+def _brute_quant_row(x):
+    amax = np.float32(np.max(np.abs(x))) if x.size else np.float32(0)
+    s = np.float32(1.0) if amax == 0 else np.float32(amax / np.float32(127.0))
+    out = []
+    for v in x:
+        t = np.float32(v / s)  # IEEE fp32 division
+        best = None
+        for j in range(-127, 128):
+            d = abs(float(t) - j)
+            if best is None or d < best[0] - 1e-12 or (abs(d - best[0]) <= 1e-12 and j % 2 == 0):
+                best = (d, j)
+        out.append(best[1])
+    return np.array(out, np.int8), s
+
+
+def test_quant_brute_force_small():
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((6, 23), dtype=np.float32) * rng.uniform(0.01, 100, (6, 1)).astype(np.float32)
+    q, s = oracle.quant_per_token(x)
+    for i in range(x.shape[0]):
+        qb, sb = _brute_quant_row(x[i])
+        assert s[i] == sb
+        assert np.array_equal(q[i], qb)
+
+
+def test_quant_invariants():
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((64, 1000), dtype=np.float32) * 3
+    x[5] = 0
+    q, s = oracle.quant_per_token(x)
+    assert np.abs(q.astype(np.int32)).max() <= 127
+    nz = np.abs(x).max(1) > 0
+    assert np.all(np.abs(q[nz].astype(np.int32)).max(1) == 127)
+    assert not q[5].any() and s[5] == 1.0
+    err = np.abs(x - q.astype(np.float32) * s[:, None])
+    assert np.all(err <= s[:, None] * (0.5 + 1e-5))
+    assert np.all(np.sign(q[np.abs(x) > s[:, None]]) == np.sign(x[np.abs(x) > s[:, None]]))
+    # fp16 input == fp32 input of the same values
+    xh = x.astype(np.float16)
+    q1, s1 = oracle.quant_per_token(xh)
+    q2, s2 = oracle.quant_per_token(xh.astype(np.float32))
+    assert np.array_equal(q1, q2) and np.array_equal(s1, s2)
+
+
+# -------------------------------------------------------------------- W8A8
+def test_w8a8_int_core_and_epilogue():
+    rng = np.random.default_rng(10)
+    m, n, k = 9, 21, 160
+    q = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
+    W = rng.integers(-127, 127, size=(n, k), dtype=np.int8)
+    sa = rng.uniform(0.001, 0.05, m).astype(np.float32)
+    sw = rng.uniform(0.001, 0.02, n).astype(np.float32)
+    acc = oracle.w8a8(q, sa, W, sw, out="i32")
+    assert np.array_equal(acc, q.astype(np.int64) @ W.astype(np.int64).T)
+    y32 = oracle.w8a8(q, sa, W, sw, out="f32")
+    exact = acc.astype(np.float64) * sa[:, None].astype(np.float64) * sw[None].astype(np.float64)
+    np.testing.assert_allclose(y32, exact, rtol=1e-6)
+    y16 = oracle.w8a8(q, sa, W, sw, out="f16")
+    assert np.array_equal(y16, y32.astype(np.float16))
+    b = rng.standard_normal(n, dtype=np.float32)
+    np.testing.assert_allclose(oracle.w8a8(q, sa, W, sw, b, out="f32"), y32 + b, rtol=1e-6, atol=1e-6)
+
+
+# --------------------------------------------------------------------- MoE
+@needs_ref
+def test_softmax_topk_bitwise_vs_reference():
+    g = np.load(GOLD / "route_tiny.npz")
+    p = oracle.softmax(g["logits"])
+    assert np.array_equal(p, g["probs"])
+    v, i = oracle.topk(p, 2)
+    assert np.array_equal(v, g["topv"]) and np.array_equal(i, g["topi"])
+    # and live against the reference library on a larger case
+    rng = np.random.default_rng(11)
+    lg = rng.standard_normal((64, 128), dtype=np.float32)
+    p = oracle.softmax(lg)
+    assert np.array_equal(p, oracle.ref_softmax(lg))
+    v, i = oracle.topk(p, 8)
+    rv, ri = oracle.ref_topk(p, 8)
+    assert np.array_equal(v, rv) and np.array_equal(i, ri)
+
+
+def test_topk_ties_keep_lower_index_bruteforce():
+    g = np.load(GOLD / "route_tiny.npz")
+    p = g["probs"]
+    for k in (1, 2, 5, 8):
+        _, i = oracle.topk(p, k)
+        exp = np.argsort(-p, axis=1, kind="stable")[:, :k]
+        assert np.array_equal(i, exp)
+    _, i = oracle.topk(p, 3)
+    assert list(i[1]) == [0, 1, 2]  # all-equal row
+
+
+def test_route_renorm():
+    rng = np.random.default_rng(12)
+    lg = rng.standard_normal((32, 16), dtype=np.float32)
+    w, i = oracle.moe_route(lg, 4, renorm=False)
+    p = oracle.softmax(lg)
+    assert np.array_equal(w, np.take_along_axis(p, i, 1))
+    wr, ir = oracle.moe_route(lg, 4, renorm=True)
+    assert np.array_equal(i, ir)
+    np.testing.assert_allclose(wr.sum(1), 1.0, rtol=1e-6)
+
+
+def test_group_matches_reference_moe_dispatch_known_answer():
+    """tests/test_moe_dispatch.py:10-86 of the reference: tokens [0,1,0,1] ->
+    expert 0 gets tokens 0 and 2, expert 1 tokens 1 and 3; adding 10 and
+    scatter-adding back gives [11,11,0,0,13,13,0,0] for expert 0."""
+    ids = np.array([[0], [1], [0], [1]], np.int32)
+    off, rows, pos = oracle.moe_group(ids, 2)
+    assert list(off) == [0, 2, 4]
+    assert list(rows[off[0]:off[1]]) == [0, 2]
+    assert list(rows[off[1]:off[2]]) == [1, 3]
+    data = np.array([[1, 1], [2, 2], [3, 3], [4, 4]], np.float32)
+    out = np.zeros_like(data)
+    for r in range(off[0], off[1]):
+        out[rows[r]] += data[rows[r]] + 10
+    assert out.ravel().tolist() == [11, 11, 0, 0, 13, 13, 0, 0]
+    for t in range(4):
+        assert rows[pos[t]] == t
+
+
+def test_group_bruteforce():
+    rng = np.random.default_rng(13)
+    T, E, k = 50, 12, 3
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    off, rows, pos = oracle.moe_group(ids, E)
+    for e in range(E):
+        toks = sorted(t for t in range(T) if e in ids[t])
+        assert list(rows[off[e]:off[e + 1]]) == toks
+    for t in range(T):
+        for kk in range(k):
+            p = pos[t * k + kk]
+            assert rows[p] == t and off[ids[t, kk]] <= p < off[ids[t, kk] + 1]
+
+
+def _numpy_moe(x, logits, wgu, sgu, wd, sd, k, renorm=False):
+    """Independent numpy composition of the MoE definition (float64 epilogues
+    rounded to fp32 at the same points as the definition)."""
+    T, H = x.shape
+    E, I2, _ = wgu.shape
+    I = I2 // 2
+    w, ids = oracle.moe_route(logits, k, renorm)
+    qx, sx = oracle.quant_per_token(x)
+    out = np.zeros((T, H), np.float32)
+    for t in range(T):
+        acc_o = np.zeros(H, np.float32)
+        for kk in range(k):
+            e = ids[t, kk]
+            acc = qx[t].astype(np.int64) @ wgu[e].astype(np.int64).T
+            gu = (acc.astype(np.float32) * sx[t]) * sgu[e]
+            g, u = gu[:I], gu[I:]
+            h = (g * (np.float32(1) / (np.float32(1) + np.exp(-g)))) * u
+            qh, sh = oracle.quant_per_token(h[None].astype(np.float32))
+            acc2 = qh[0].astype(np.int64) @ wd[e].astype(np.int64).T
+            d = (acc2.astype(np.float32) * sh[0]) * sd[e]
+            acc_o = acc_o + w[t, kk] * d
+        out[t] = acc_o
+    return out
+
+
+def test_moe_oracle_vs_numpy_composition_and_golden():
+    g = np.load(GOLD / "moe_tiny.npz")
+    y = oracle.moe_w8a8(g["x"], g["logits"], g["w_gu"], g["s_gu"], g["w_down"], g["s_down"], 2)
+    assert np.array_equal(y, g["y"])
+    yn = _numpy_moe(g["x"], g["logits"], g["w_gu"], g["s_gu"], g["w_down"], g["s_down"], 2)
+    np.testing.assert_allclose(y, yn, rtol=2e-3, atol=2e-3 * np.abs(yn).max())
+
+
+def test_moe_identical_experts_invariant():
+    """With every expert identical and renormalized weights the layer equals
+    one expert MLP, whatever the routing."""
+    rng = np.random.default_rng(14)
+    T, H, I, E, k = 8, 32, 16, 6, 3
+    x = rng.standard_normal((T, H), dtype=np.float32)
+    lg = rng.standard_normal((T, E), dtype=np.float32)
+    wgu1 = rng.integers(-127, 127, size=(1, 2 * I, H), dtype=np.int8)
+    sgu1 = rng.uniform(0.001, 0.02, (1, 2 * I)).astype(np.float32)
+    wd1 = rng.integers(-127, 127, size=(1, H, I), dtype=np.int8)
+    sd1 = rng.uniform(0.001, 0.02, (1, H)).astype(np.float32)
+    rep = lambda a: np.repeat(a, E, axis=0)  # noqa: E731
+    y = oracle.moe_w8a8(x, lg, rep(wgu1), rep(sgu1), rep(wd1), rep(sd1), k, renorm=True)
+    single = oracle.moe_w8a8(x, np.zeros((T, 1), np.float32), wgu1, sgu1, wd1, sd1, 1, renorm=True)
+    np.testing.assert_allclose(y, single, rtol=1e-5, atol=1e-5 * np.abs(single).max())

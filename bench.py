@@ -1,0 +1,411 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X int8 quantized-linear path (one JSON line on stdout).
+
+Headline (BASELINE.json metric, config 2): greedy int8 decode tok/s of a
+Qwen3-0.6B-shaped decoder (28 layers, hidden 1024, 16/8 heads, head_dim 128,
+SwiGLU 3072, vocab 151936, int8 lm_head), batch 1, 128-token random prompt then
+256 generated tokens. A "step" is one generated token. Random-init int8 weights
+(no checkpoint is available offline) and random prompt ids; every input is
+resident in HBM before the timed region; the timed region is exactly `--steps`
+decode steps (captured-graph replays) bracketed by device synchronization.
+
+Also in the same line:
+  roofline      the dominant kernel (the per-layer W8 GEMV, 112 launches per
+                token) replayed alone from a graph and timed with HIP events on
+                its stream: algorithmic bytes per launch / average launch time.
+  cpu_baseline  the reference CPU path (oracle/_ref/libtensor_ops_ref.so, built
+                from the reference's own tensor_ops.c): its fp32 tensor_linear on
+                per-channel-dequantized weights over every linear of one decode
+                token, on the host cores, extrapolated per token.
+  kernels       the other BASELINE configs' kernels: C1 GEMV, C3 W8A8 GEMMs +
+                quantizer, C4 skinny-M sweep and lm_head, C5 MoE layer.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA, TOP/s
+METRIC = "int8 GEMV % HBM peak; W8A8 GEMM % int8 MFMA peak; Qwen3-0.6B decode tok/s"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------ timing
+class Timer:
+    """Graph-captured repetitions timed with events on the capture stream."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.stream = torch.cuda.Stream()
+
+    def graph(self, fn, reps):
+        torch = self.torch
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(self.stream):
+            fn(self.stream.cuda_stream)           # warm (untimed, outside the graph)
+            self.stream.synchronize()
+            with torch.cuda.graph(g, stream=self.stream):
+                for _ in range(reps):
+                    fn(self.stream.cuda_stream)
+        return g
+
+    def time_graph(self, g, replays=3):
+        torch = self.torch
+        with torch.cuda.stream(self.stream):
+            g.replay()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record(self.stream)
+            for _ in range(replays):
+                g.replay()
+            e1.record(self.stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / replays   # seconds per replay
+
+
+# ------------------------------------------------------------------ decode
+def bench_decode(torch, args):
+    import numpy as np
+    from mod_amd.qwen3 import Qwen3Config, Qwen3Int8Decoder, random_weights
+
+    P = 128
+    cfg = Qwen3Config(max_seq=max(384, P + args.steps))
+    t0 = time.time()
+    w = random_weights(cfg, seed=0)
+    log(f"[decode] random weights built in {time.time() - t0:.1f}s")
+    st = torch.cuda.Stream()
+    dec = Qwen3Int8Decoder(cfg, w, stream=st.cuda_stream)
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab, size=P).astype(np.int32)
+
+    # Warmup: capture the step graph and run W decode steps (untimed).
+    dec.reset(prompt)
+    dec.run(P - 1 + min(args.warmup, cfg.max_seq - P + 1), use_graph=True)
+    torch.cuda.synchronize()
+
+    # Timed: the exact config-2 run. Prefill (P-1 prompt steps) is timed apart.
+    dec.reset(prompt)
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    torch.cuda.synchronize()
+    e[0].record(st)
+    dec.run(P - 1, use_graph=True)
+    e[1].record(st)
+    dec.run(args.steps, use_graph=True)
+    e[2].record(st)
+    e[2].synchronize()
+    torch.cuda.synchronize()
+    prefill_s = e[0].elapsed_time(e[1]) * 1e-3
+    decode_s = e[1].elapsed_time(e[2]) * 1e-3
+    ids = dec.read(P + args.steps)
+    assert np.array_equal(ids[:P], prompt)
+
+    wb = cfg.weight_bytes()
+    mean_ctx = P + (args.steps - 1) / 2.0
+    bytes_tok = wb["int8"] + wb["scales"] + wb["bias_norms"] + cfg.kv_bytes_per_pos() * mean_ctx
+    res = {
+        "tok_s": args.steps / decode_s,
+        "ms_per_token": decode_s / args.steps * 1e3,
+        "prefill_ms": prefill_s * 1e3,
+        "prefill_tok_s": (P - 1) / prefill_s,
+        "bytes_per_token": bytes_tok,
+        "hbm_frac": bytes_tok * args.steps / decode_s / (HBM_PEAK_GBS * 1e9),
+        "ceiling_tok_s": HBM_PEAK_GBS * 1e9 / bytes_tok,
+        "generated_head": ids[P:P + 8].tolist(),
+    }
+    return cfg, w, dec, st, res
+
+
+def bench_decode_gemv(torch, timer, cfg, dec):
+    """Dominant kernel: the 112 per-layer GEMVs of one token, replayed from a
+    graph over the decoder's own weights (plus lm_head separately)."""
+    from mod_amd import ops
+    H, D, I = cfg.hidden, cfg.head_dim, cfg.intermediate
+    nqkv = (cfg.n_heads + 2 * cfg.n_kv_heads) * D
+    x = torch.randn(max(H, I, cfg.n_heads * D), device="cuda")
+    y = torch.empty(max(nqkv, 2 * I, cfg.vocab), device="cuda")
+    layers = dec._layers_c
+    shapes = []
+    for l in range(cfg.n_layers):
+        L = layers[l]
+        shapes += [(L.w_qkv, L.s_qkv, L.b_qkv, nqkv, H), (L.w_o, L.s_o, None, H, cfg.n_heads * D),
+                   (L.w_gu, L.s_gu, None, 2 * I, H), (L.w_down, L.s_down, None, H, I)]
+
+    def layer_gemvs(s):
+        for (wp, sp, bp, n, k) in shapes:
+            ops.gemv_w8(x, wp, sp, bp, y, 1, n, k, s)
+
+    g = timer.graph(layer_gemvs, 1)
+    t = timer.time_graph(g, replays=5)
+    nbytes = sum(n * k + 4 * n + 4 * k + 4 * n + (4 * n if b else 0) for (_, _, b, n, k) in shapes)
+    per_launch_bytes = nbytes / len(shapes)
+    per_launch_s = t / len(shapes)
+
+    def lm(s):
+        ops.gemv_w8(x, dec._lm, dec._slm, None, y, 1, cfg.vocab, H, s)
+    g2 = timer.graph(lm, 4)
+    tl = timer.time_graph(g2, replays=5) / 4
+    lm_bytes = cfg.vocab * H + 8 * cfg.vocab + 4 * H
+    return {
+        "layer_gemv_launches": len(shapes),
+        "layer_gemv_us_per_launch": per_launch_s * 1e6,
+        "layer_gemv_bytes_per_launch": per_launch_bytes,
+        "layer_gemv_GBs": per_launch_bytes / per_launch_s / 1e9,
+        "lm_head_us": tl * 1e6,
+        "lm_head_GBs": lm_bytes / tl / 1e9,
+    }
+
+
+# ----------------------------------------------------------------- kernels
+def bench_kernels(torch, timer):
+    from mod_amd import ops
+    out = {}
+    dev = "cuda"
+
+    # C1: GEMV [1,1024] x int8 [3072,1024], rotating over 160 distinct weights
+    # (> 256 MB Infinity Cache) so every launch streams from HBM.
+    M, N, K = 1, 3072, 1024
+    pool = 160
+    Ws = torch.randint(-127, 127, (pool, N, K), dtype=torch.int8, device=dev)
+    ss = torch.rand((pool, N), device=dev) * 0.019 + 0.001
+    x = torch.randn((M, K), device=dev)
+    y = torch.empty((M, N), device=dev)
+
+    def c1(s):
+        for i in range(pool):
+            ops.gemv_w8(x, Ws[i], ss[i], None, y, M, N, K, s)
+    t = timer.time_graph(timer.graph(c1, 1)) / pool
+    b = N * K + 4 * N + 4 * K + 4 * N
+    out["c1_gemv"] = {"us": t * 1e6, "GBs": b / t / 1e9, "hbm_frac": b / t / 1e9 / HBM_PEAK_GBS,
+                      "bytes": b}
+    del Ws, ss
+
+    # C3: per-token quant + W8A8 GEMM, M=2048, fp16 in/out.
+    c3 = {}
+    for (K, N) in [(1024, 3072), (3072, 1024), (1024, 2048)]:
+        M = 2048
+        xh = torch.randn((M, K), device=dev).half()
+        q = torch.empty((M, K), dtype=torch.int8, device=dev)
+        sa = torch.empty((M,), device=dev)
+        W = torch.randint(-127, 127, (N, K), dtype=torch.int8, device=dev)
+        sw = torch.rand((N,), device=dev) * 0.019 + 0.001
+        yh = torch.empty((M, N), dtype=torch.float16, device=dev)
+        reps = 20
+        tq = timer.time_graph(timer.graph(lambda s: ops.quantize_per_token(xh, q, sa, M, K, s), reps)) / reps
+        tg = timer.time_graph(timer.graph(lambda s: ops.gemm_w8a8(q, sa, W, sw, None, yh, M, N, K, s), reps)) / reps
+        tops = 2 * M * N * K / tg / 1e12
+        c3[f"K{K}_N{N}"] = {"gemm_us": tg * 1e6, "TOPS": tops, "mfma_frac": tops / INT8_PEAK_TOPS,
+                            "quant_us": tq * 1e6, "quant_GBs": (3 * M * K + 4 * M) / tq / 1e9}
+    out["c3_w8a8"] = c3
+
+    # C4: Qwen3-8B linears, GEMV across M (skinny) + lm_head [151936, 4096].
+    c4 = {}
+    for (N, K) in [(12288, 4096), (4096, 12288)]:
+        reps_w = 6   # 6 x 50 MB > Infinity Cache
+        Wp = torch.randint(-127, 127, (reps_w, N, K), dtype=torch.int8, device=dev)
+        sw = torch.rand((N,), device=dev) * 0.019 + 0.001
+        for M in (1, 4, 16, 64):
+            xh = torch.randn((M, K), device=dev).half()
+            yh = torch.empty((M, N), dtype=torch.float16, device=dev)
+
+            def f(s):
+                for i in range(reps_w):
+                    ops.gemv_w8(xh, Wp[i], sw, None, yh, M, N, K, s)
+            t = timer.time_graph(timer.graph(f, 1)) / reps_w
+            b = N * K + 4 * N + 2 * M * K + 2 * M * N
+            c4[f"gemv_N{N}_K{K}_M{M}"] = {"us": t * 1e6, "GBs": b / t / 1e9,
+                                          "hbm_frac": b / t / 1e9 / HBM_PEAK_GBS}
+            # MFMA alternative at the same M: per-token quant + W8A8 GEMM.
+            q = torch.empty((M, K), dtype=torch.int8, device=dev)
+            sa = torch.empty((M,), device=dev)
+
+            def f2(s):
+                for i in range(reps_w):
+                    ops.quantize_per_token(xh, q, sa, M, K, s)
+                    ops.gemm_w8a8(q, sa, Wp[i], sw, None, yh, M, N, K, s)
+            t2 = timer.time_graph(timer.graph(f2, 1)) / reps_w
+            c4[f"w8a8_N{N}_K{K}_M{M}"] = {"us": t2 * 1e6, "GBs": b / t2 / 1e9}
+        del Wp
+    N, K = 151936, 4096
+    Wl = torch.randint(-127, 127, (N, K), dtype=torch.int8, device=dev)
+    sl = torch.rand((N,), device=dev) * 0.019 + 0.001
+    xh = torch.randn((1, K), device=dev).half()
+    yh = torch.empty((1, N), dtype=torch.float16, device=dev)
+    t = timer.time_graph(timer.graph(lambda s: ops.gemv_w8(xh, Wl, sl, None, yh, 1, N, K, s), 4)) / 4
+    b = N * K + 4 * N + 2 * K + 2 * N
+    c4["lm_head_8b_M1"] = {"us": t * 1e6, "GBs": b / t / 1e9, "hbm_frac": b / t / 1e9 / HBM_PEAK_GBS}
+    del Wl
+    out["c4_skinny"] = c4
+
+    # C5: MoE expert layer (128 experts, top-8, 512 tokens, H 2048, I 768).
+    T, H, I, E, k = 512, 2048, 768, 128, 8
+    xm = torch.randn((T, H), device=dev).half()
+    lg = torch.randn((T, E), device=dev)
+    wgu = torch.randint(-127, 127, (E, 2 * I, H), dtype=torch.int8, device=dev)
+    sgu = torch.rand((E, 2 * I), device=dev) * 0.019 + 0.001
+    wdn = torch.randint(-127, 127, (E, H, I), dtype=torch.int8, device=dev)
+    sdn = torch.rand((E, H), device=dev) * 0.019 + 0.001
+    om = torch.empty((T, H), dtype=torch.float16, device=dev)
+    ws = torch.empty((ops.moe_workspace_bytes(T, H, I, E, k),), dtype=torch.uint8, device=dev)
+    t = timer.time_graph(timer.graph(
+        lambda s: ops.moe_w8a8(xm, lg, wgu, sgu, wdn, sdn, om, T, H, I, E, k, False, ws, s), 2)) / 2
+    wbytes = E * (2 * I * H + H * I) + 4 * E * (2 * I + H)
+    ops_ = T * k * (2 * H * 2 * I + 2 * I * H)
+    out["c5_moe"] = {"us": t * 1e6, "weight_GBs": wbytes / t / 1e9,
+                     "hbm_frac": wbytes / t / 1e9 / HBM_PEAK_GBS, "TOPS": ops_ / t / 1e12}
+    return out
+
+
+# ------------------------------------------------------------ CPU baseline
+def cpu_baseline(cfg, w, budget_s=20.0):
+    """The reference CPU path on the host: tensor_linear (fp32, tensor_ops.c:
+    323-335) over one decode token's linears, weights dequantized per channel."""
+    import numpy as np
+    import oracle
+    if not oracle.ref_available():
+        return None
+    L = oracle.ref_lib()
+    H, D, I = cfg.hidden, cfg.head_dim, cfg.intermediate
+    nqkv = (cfg.n_heads + 2 * cfg.n_kv_heads) * D
+    x = {k: oracle.RefTensor((1, k), np.random.default_rng(k).standard_normal((1, k)).astype(np.float32))
+         for k in {H, cfg.n_heads * D, I}}
+    outs = {n: oracle.RefTensor((1, n)) for n in {nqkv, H, 2 * I, cfg.vocab}}
+    mats = []
+    t_build = time.time()
+    for l, Lw in enumerate(w["layers"]):
+        for (wk, sk, bk, n, k) in (("w_qkv", "s_qkv", "b_qkv", nqkv, H),
+                                   ("w_o", "s_o", None, H, cfg.n_heads * D),
+                                   ("w_gu", "s_gu", None, 2 * I, H),
+                                   ("w_down", "s_down", None, H, I)):
+            deq = Lw[wk].astype(np.float32) * Lw[sk][:, None]
+            mats.append((oracle.RefTensor((n, k), deq),
+                         oracle.RefTensor((n,), Lw[bk]) if bk and Lw.get(bk) is not None else None,
+                         n, k))
+    mats.append((oracle.RefTensor((cfg.vocab, H), w["lm_head"].astype(np.float32) * w["s_lm_head"][:, None]),
+                 None, cfg.vocab, H))
+    log(f"[cpu] dequantized reference weights in {time.time() - t_build:.1f}s")
+
+    def one_token():
+        for (tw, tb, n, k) in mats:
+            L.tensor_linear(x[k].h, tw.h, tb.h if tb else None, outs[n].h)
+
+    one_token()    # warm
+    times = []
+    t_start = time.time()
+    while len(times) < 5 and (time.time() - t_start) < budget_s:
+        t0 = time.perf_counter()
+        one_token()
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {
+        "value": 1.0 / med,
+        "unit": "tok/s",
+        "cores": 1,
+        "kind": "reference",
+        "sample": (f"reference tensor_linear (fp32, tensor_ops.c:301-335, built from the reference "
+                   f"source with Makefile:15 flags) over one decode token's {len(mats)} linears of "
+                   f"the config-2 model (weights dequantized per channel), median of {len(times)} "
+                   f"tokens; attention/norm ops excluded. The reference parallelizes over batch "
+                   f"only (tensor_ops.c:306), so at batch 1 one core works "
+                   f"(OMP_NUM_THREADS={os.environ.get('OMP_NUM_THREADS', 'default')}, "
+                   f"host cores={os.cpu_count()})."),
+        "ms_per_token": med * 1e3,
+    }
+
+
+# -------------------------------------------------------------------- main
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--no-kernels", action="store_true", help="skip the C1/C3/C4/C5 kernel suite")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only: the int8 path has no multi-GPU component in this "
+              f"build (asked for --gpus {args.gpus}).", file=sys.stderr)
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 2
+    from mod_amd import ops
+    log(f"[bench] {ops.version()}  lib={ops.LIB_FILE}")
+    timer = Timer(torch)
+
+    cfg, w, dec, st, dres = bench_decode(torch, args)
+    log(f"[decode] {dres['tok_s']:.1f} tok/s ({dres['ms_per_token']:.3f} ms/token), "
+        f"prefill {dres['prefill_ms']:.1f} ms")
+    g = bench_decode_gemv(torch, timer, cfg, dec)
+    log(f"[gemv] layer GEMV {g['layer_gemv_us_per_launch']:.2f} us/launch "
+        f"{g['layer_gemv_GBs']:.0f} GB/s; lm_head {g['lm_head_us']:.1f} us {g['lm_head_GBs']:.0f} GB/s")
+    kern = {}
+    if not args.no_kernels:
+        kern = bench_kernels(torch, timer)
+        log("[kernels] " + json.dumps(kern))
+    cpu = None
+    if not args.no_cpu:
+        try:
+            cpu = cpu_baseline(cfg, w)
+        except Exception as e:  # the GPU result stands without the baseline
+            log(f"[cpu] baseline failed: {e!r}")
+        if cpu:
+            log(f"[cpu] {cpu['value']:.3f} tok/s ({cpu['ms_per_token']:.1f} ms/token)")
+
+    achieved = g["layer_gemv_GBs"]
+    line = {
+        "metric": METRIC,
+        "value": round(dres["tok_s"], 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dres["ms_per_token"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 weights, fp32 activations/accumulate",
+        "data": "synthetic: random-init int8 weights (seed 0), random 128-token prompt",
+        "config": {
+            "workload": "BASELINE config 2: Qwen3-0.6B-shaped int8 greedy decode, batch 1, "
+                        "128-token prompt + 256 generated tokens (steps = generated tokens)",
+            "global_batch": 1, "seq_len": 128 + args.steps, "layers": cfg.n_layers,
+            "hidden": cfg.hidden, "heads": f"{cfg.n_heads}q/{cfg.n_kv_heads}kv",
+            "head_dim": cfg.head_dim, "intermediate": cfg.intermediate, "vocab": cfg.vocab,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "gemv_w8_kernel (per-layer decode GEMVs: qkv, o, gate_up, down)",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": round(g["layer_gemv_bytes_per_launch"]),
+            "us_per_launch": round(g["layer_gemv_us_per_launch"], 3),
+        },
+        "cpu_baseline": cpu and {k: (round(v, 4) if isinstance(v, float) else v)
+                                 for k, v in cpu.items()},
+        "decode": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in dres.items()},
+        "decode_gemv": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in g.items()},
+        "kernels": kern,
+    }
+    print(json.dumps(line), flush=True)
+    dec.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -232,6 +232,56 @@ int pio_moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* 
                  int out_dtype, int T, int H, int I, int E, int top_k, int renorm, void* workspace,
                  void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Int8 Qwen3-style decoder (greedy decode at batch 1). Replaces the decode
+ * loop of Qwen3ForCausalLM.generate / Qwen3DecoderLayer.forward
+ * (ip/models/qwen3_0_6b/architecture.py:124-221) with one device-driven step:
+ *   x = embed[id[pos]]; per layer: h = rmsnorm(x)*w_in; qkv = W8(h) + b_qkv;
+ *   rotate-half RoPE on q and k at `pos` (tensor_ops.c:384-415 formula);
+ *   k, v -> cache; causal GQA attention over positions 0..pos; x += W8_o(attn);
+ *   h = rmsnorm(x)*w_post; x += W8_down(silu(g)*u) with [g|u] = W8_gate_up(h);
+ *   logits = W8_lm_head(rmsnorm(x)*w_final); id[pos+1] = argmax (first max,
+ *   tensor_ops.c:649-662) unless pos+1 is still inside the prompt; pos += 1.
+ * Position and token ids live in device memory, so a step is replayable as a
+ * captured HIP graph. The handle owns activations, KV cache (fp32,
+ * [layer][kv_head][max_seq][head_dim]) and the RoPE table; weights are the
+ * caller's device pointers and must outlive the handle.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    int n_layers, hidden, n_heads, n_kv_heads, head_dim, intermediate, vocab, max_seq;
+    float rms_eps, rope_theta;
+} pio_qwen3_config;
+
+typedef struct {
+    const float* in_norm;    /* [hidden]                                        */
+    const int8_t* w_qkv;     /* [(n_heads + 2*n_kv_heads)*head_dim, hidden]      */
+    const float* s_qkv;      /* [rows of w_qkv]                                  */
+    const float* b_qkv;      /* [rows of w_qkv] or NULL                          */
+    const int8_t* w_o;       /* [hidden, n_heads*head_dim]                       */
+    const float* s_o;        /* [hidden]                                         */
+    const float* post_norm;  /* [hidden]                                         */
+    const int8_t* w_gu;      /* [2*intermediate, hidden]  (gate rows, then up)   */
+    const float* s_gu;       /* [2*intermediate]                                 */
+    const int8_t* w_down;    /* [hidden, intermediate]                           */
+    const float* s_down;     /* [hidden]                                         */
+} pio_qwen3_layer;
+
+/* Creates a decoder on the current device. `layers` is a host array of
+ * cfg->n_layers entries. Returns NULL on error (see tensor_last_error). */
+void* pio_qwen3_create(const pio_qwen3_config* cfg, const float* embed, const float* final_norm,
+                       const int8_t* lm_head, const float* s_lm_head,
+                       const pio_qwen3_layer* layers, void* stream);
+void pio_qwen3_destroy(void* dec);
+/* Loads `ids` (host, prompt_len tokens) and rewinds to position 0. */
+int pio_qwen3_reset(void* dec, const int32_t* ids, int prompt_len);
+/* Enqueues n decode steps; use_graph != 0 replays one captured step graph. */
+int pio_qwen3_run(void* dec, int n_steps, int use_graph);
+/* Waits for the stream, then copies out ids[0..n) and, if logits != NULL, the
+ * last step's logits [vocab]. */
+int pio_qwen3_read(void* dec, int32_t* ids, int n, float* logits);
+/* Device pointer of the last step's logits ([vocab] fp32). */
+const float* pio_qwen3_logits(void* dec);
+
 /* Library version string and the gfx target it was built for. */
 const char* pio_version(void);
 

@@ -1,0 +1,338 @@
+"""Python mirror of the reference Tensor/Module/Linear API for ``rocm:N`` devices.
+
+The reference engine's Python front end (ip/core/engine/backend.py:201-702) is
+torch-free: a ``Tensor`` owns a C ``Tensor*`` created by a backend library and
+every op allocates its output and calls one C entry point. This module keeps
+that contract on top of libtensor_ops_rocm.so, so model code written against
+``Tensor``/``Linear`` runs unchanged, and adds the int8 layers of this path:
+
+* ``W8Linear``   -- weight-only int8 (per-output-channel scales), decode GEMV;
+* ``W8A8Linear`` -- per-token int8 activations x int8 weights on MFMA;
+* ``MoEW8A8``    -- routed int8 expert layer (replaces Qwen3Coder30BMoE).
+
+Differences from the reference, on purpose:
+* tensors free through the library that created them (the reference frees
+  every tensor through ``_lib_cpu``, backend.py:266-272);
+* failed C calls raise ``RocmError`` instead of being ignored;
+* tensors carry a dtype (float32 / float16 / int8 / int32).
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import List, Optional, Sequence, Tuple, Union
+
+import numpy as np
+
+from . import ops
+from .ops import CTensor, RocmError, check, lib
+
+_NP = {"float32": np.float32, "float16": np.float16, "int8": np.int8, "int32": np.int32}
+_CODE = {"float32": ops.F32, "float16": ops.F16, "int8": ops.I8, "int32": ops.I32}
+
+
+def _device_id(device: str) -> int:
+    if device == "cpu":
+        return -1
+    if not device.startswith("rocm"):
+        raise ValueError(f"libtensor_ops_rocm serves 'rocm:N' and 'cpu' devices, not {device!r}")
+    return int(device.split(":")[1]) if ":" in device else 0
+
+
+class Tensor:
+    """A library-owned tensor. ``data`` may be a list or a numpy array."""
+
+    __slots__ = ("device", "dtype", "_handle", "__weakref__")
+
+    def __init__(self, shape: Sequence[int], data=None, device: str = "rocm:0",
+                 dtype: str = "float32", _handle=None):
+        self.device = device
+        self.dtype = dtype
+        if _handle is not None:
+            self._handle = _handle
+        else:
+            if dtype not in _CODE:
+                raise ValueError(f"unsupported dtype {dtype}")
+            c_shape = (ctypes.c_int * len(shape))(*[int(s) for s in shape])
+            h = lib.create_tensor_typed(c_shape, len(shape), _device_id(device), _CODE[dtype])
+            if not h:
+                raise RocmError(f"create_tensor failed: {ops.last_error()}")
+            self._handle = h
+        if data is not None:
+            self.load(data)
+
+    # ------------------------------------------------------------ lifetime
+    def __del__(self):
+        h = getattr(self, "_handle", None)
+        if h is not None:
+            try:
+                lib.free_tensor(h)
+            except Exception:
+                pass
+            self._handle = None
+
+    # ---------------------------------------------------------- properties
+    @property
+    def shape(self) -> Tuple[int, ...]:
+        c = self._handle.contents
+        return tuple(c.shape[i] for i in range(c.ndim))
+
+    @property
+    def ndim(self) -> int:
+        return self._handle.contents.ndim
+
+    @property
+    def size(self) -> int:
+        return self._handle.contents.size
+
+    def data_ptr(self) -> int:
+        return ctypes.cast(self._handle.contents.data, ctypes.c_void_p).value or 0
+
+    @property
+    def nbytes(self) -> int:
+        return self.size * np.dtype(_NP[self.dtype]).itemsize
+
+    # ------------------------------------------------------- data movement
+    def load(self, data) -> None:
+        arr = np.ascontiguousarray(np.asarray(data, dtype=_NP[self.dtype]))
+        if arr.size != self.size:
+            raise ValueError(f"load: {arr.size} elements for a tensor of {self.size}")
+        check(lib.tensor_load_bytes_status(self._handle, arr.ctypes.data, arr.nbytes),
+              "tensor_load_bytes")
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, dtype=_NP[self.dtype])
+        check(lib.tensor_get_bytes_status(self._handle, out.ctypes.data, out.nbytes),
+              "tensor_get_bytes")
+        return out
+
+    def to_list(self) -> List[float]:
+        return self.numpy().ravel().tolist()
+
+    @classmethod
+    def from_numpy(cls, arr: np.ndarray, device: str = "rocm:0") -> "Tensor":
+        name = str(arr.dtype)
+        if name not in _CODE:
+            raise ValueError(f"unsupported dtype {arr.dtype}")
+        return cls(arr.shape, arr, device=device, dtype=name)
+
+    # ----------------------------------------------------------------- ops
+    def _new(self, shape, dtype=None) -> "Tensor":
+        return Tensor(shape, device=self.device, dtype=dtype or self.dtype)
+
+    def fill(self, value: float) -> None:
+        lib.tensor_clear_error()
+        lib.tensor_fill(self._handle, ctypes.c_float(value))
+        _raise_if_error("tensor_fill")
+
+    def add(self, other: "Tensor") -> "Tensor":
+        out = self._new(self.shape)
+        lib.tensor_clear_error()
+        lib.tensor_add(self._handle, other._handle, out._handle)
+        _raise_if_error("tensor_add")
+        return out
+
+    def mul(self, other: "Tensor") -> "Tensor":
+        out = self._new(self.shape)
+        lib.tensor_clear_error()
+        lib.tensor_mul(self._handle, other._handle, out._handle)
+        _raise_if_error("tensor_mul")
+        return out
+
+    __add__ = add
+    __mul__ = mul
+
+    def matmul_int8(self, other: "Tensor", out_dtype: str = "float32") -> "Tensor":
+        """tensor_matmul_int8 semantics (tensor_ops.c:217-246): self [..,M,K],
+        other [..,K,N], both int8."""
+        m, k = self.shape[-2:]
+        n = other.shape[-1]
+        out = self._new(list(self.shape[:-2]) + [m, n], out_dtype)
+        fn = lib.tensor_matmul_int8_i32_status if out_dtype == "int32" else lib.tensor_matmul_int8_status
+        check(fn(self._handle, other._handle, out._handle), "tensor_matmul_int8")
+        return out
+
+    def dequantize(self, scale: "Tensor") -> "Tensor":
+        out = self._new(self.shape, "float32")
+        check(lib.tensor_dequantize_status(self._handle, scale._handle, out._handle),
+              "tensor_dequantize")
+        return out
+
+    def quantize_per_token(self) -> Tuple["Tensor", "Tensor"]:
+        q = self._new(self.shape, "int8")
+        s = self._new(list(self.shape[:-1]) or [1], "float32")
+        check(lib.tensor_quantize_per_token_status(self._handle, q._handle, s._handle),
+              "tensor_quantize_per_token")
+        return q, s
+
+    def linear_w8(self, weight: "Tensor", scale: "Tensor", bias: Optional["Tensor"] = None,
+                  out_dtype: Optional[str] = None) -> "Tensor":
+        n = weight.shape[0]
+        out = self._new(list(self.shape[:-1]) + [n], out_dtype or self.dtype)
+        check(lib.tensor_linear_w8_status(self._handle, weight._handle, scale._handle,
+                                          bias._handle if bias is not None else None,
+                                          out._handle), "tensor_linear_w8")
+        return out
+
+    def linear_w8a8(self, s_a: "Tensor", weight: "Tensor", scale: "Tensor",
+                    bias: Optional["Tensor"] = None, out_dtype: str = "float16") -> "Tensor":
+        n = weight.shape[0]
+        out = self._new(list(self.shape[:-1]) + [n], out_dtype)
+        check(lib.tensor_linear_w8a8_status(self._handle, s_a._handle, weight._handle,
+                                            scale._handle,
+                                            bias._handle if bias is not None else None,
+                                            out._handle), "tensor_linear_w8a8")
+        return out
+
+
+def _raise_if_error(what: str) -> None:
+    msg = ops.last_error()
+    if msg:
+        raise RocmError(f"{what} failed: {msg}")
+
+
+# ---------------------------------------------------------------- modules
+class Module:
+    """Same surface as the reference Module (backend.py:656-693)."""
+
+    def __init__(self):
+        self._parameters = {}
+        self._modules = {}
+        self.training = False
+
+    def __call__(self, *a, **k):
+        return self.forward(*a, **k)
+
+    def forward(self, *a, **k):
+        raise NotImplementedError
+
+    def register_parameter(self, name: str, p):
+        self._parameters[name] = p
+
+    def parameters(self):
+        for p in self._parameters.values():
+            if p is not None:
+                yield p
+        for m in self._modules.values():
+            yield from m.parameters()
+
+    def state_dict(self, prefix: str = "", destination=None):
+        destination = {} if destination is None else destination
+        for n, p in self._parameters.items():
+            if p is not None:
+                destination[prefix + n] = p
+        for n, m in self._modules.items():
+            m.state_dict(prefix + n + ".", destination)
+        return destination
+
+
+def quantize_weight_per_channel(w: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
+    """Offline per-output-channel symmetric quantization of an fp weight [N,K]:
+    s = amax_row / 127 (1 for all-zero rows), q = clamp(rint(w / s), -127, 127)."""
+    w = np.asarray(w, dtype=np.float32)
+    amax = np.abs(w).max(axis=1)
+    s = np.where(amax == 0, np.float32(1), amax / np.float32(127)).astype(np.float32)
+    q = np.clip(np.rint(w / s[:, None]), -127, 127).astype(np.int8)
+    return q, s
+
+
+class W8Linear(Module):
+    """Drop-in for the reference Linear (backend.py:695-702) with int8 weights
+    [out, in] and per-output-channel fp32 scales; forward(x) = x.linear_w8(...)."""
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = True,
+                 device: str = "rocm:0"):
+        super().__init__()
+        self.weight = Tensor([out_features, in_features], device=device, dtype="int8")
+        self.weight_scale = Tensor([out_features], device=device)
+        self.bias = Tensor([out_features], device=device) if bias else None
+        self.register_parameter("weight", self.weight)
+        self.register_parameter("weight_scale", self.weight_scale)
+        if bias:
+            self.register_parameter("bias", self.bias)
+
+    def load_quantized(self, q: np.ndarray, s: np.ndarray, b: Optional[np.ndarray] = None):
+        self.weight.load(q)
+        self.weight_scale.load(s)
+        if b is not None:
+            if self.bias is None:
+                raise ValueError("layer was created without bias")
+            self.bias.load(b)
+
+    def load_float(self, w: np.ndarray, b: Optional[np.ndarray] = None):
+        q, s = quantize_weight_per_channel(w)
+        self.load_quantized(q, s, b)
+
+    def forward(self, x: Tensor) -> Tensor:
+        return x.linear_w8(self.weight, self.weight_scale, self.bias)
+
+
+class W8A8Linear(W8Linear):
+    """Prefill / expert linear: per-token int8 activations on int8 MFMA."""
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = True,
+                 device: str = "rocm:0", out_dtype: str = "float16"):
+        super().__init__(in_features, out_features, bias, device)
+        self.out_dtype = out_dtype
+
+    def forward(self, x: Tensor) -> Tensor:
+        q, s = x.quantize_per_token()
+        return q.linear_w8a8(s, self.weight, self.weight_scale, self.bias, self.out_dtype)
+
+
+class MoEW8A8(Module):
+    """Routed int8 expert layer: forward(x [T,H], router_logits [T,E]) -> [T,H]."""
+
+    def __init__(self, hidden: int, intermediate: int, num_experts: int, top_k: int,
+                 renormalize: bool = False, device: str = "rocm:0", out_dtype: str = "float32"):
+        super().__init__()
+        self.top_k, self.renormalize, self.out_dtype = top_k, renormalize, out_dtype
+        E, H, I = num_experts, hidden, intermediate
+        self.w_gate_up = Tensor([E, 2 * I, H], device=device, dtype="int8")
+        self.s_gate_up = Tensor([E, 2 * I], device=device)
+        self.w_down = Tensor([E, H, I], device=device, dtype="int8")
+        self.s_down = Tensor([E, H], device=device)
+        for n in ("w_gate_up", "s_gate_up", "w_down", "s_down"):
+            self.register_parameter(n, getattr(self, n))
+
+    def forward(self, x: Tensor, router_logits: Tensor) -> Tensor:
+        out = Tensor(list(x.shape), device=x.device, dtype=self.out_dtype)
+        check(lib.tensor_moe_w8a8_status(x._handle, router_logits._handle, self.w_gate_up._handle,
+                                         self.s_gate_up._handle, self.w_down._handle,
+                                         self.s_down._handle, self.top_k,
+                                         int(self.renormalize), out._handle), "tensor_moe_w8a8")
+        return out
+
+
+# ------------------------------------------------- allocator and streams
+def init_memory_pool(size_mb: int = 1024) -> None:
+    """Reserve the HBM arena (reference: backend.py:792-799, CPU arena)."""
+    lib.init_memory_pool(size_mb * 1024 * 1024)
+
+
+def reset_memory_pool() -> None:
+    lib.reset_memory_pool()
+
+
+def allocate_pinned(size_bytes: int):
+    return lib.allocate_pinned_memory(size_bytes)
+
+
+def free_pinned(ptr) -> None:
+    lib.free_pinned_memory(ptr)
+
+
+def synchronize() -> None:
+    lib.stream_synchronize(None)
+
+
+class HIPGraph:
+    """Mirror of the reference CUDAGraph wrapper (backend.py:801-810)."""
+
+    def capture_begin(self):
+        lib.begin_capture()
+
+    def capture_end(self):
+        lib.end_capture()
+
+    def replay(self):
+        lib.replay_graph()

@@ -56,8 +56,8 @@ __global__ __launch_bounds__(256) void gemv_w8_kernel(const XT* __restrict__ x,
                                                       const int8_t* __restrict__ W,
                                                       const float* __restrict__ s_w,
                                                       const float* __restrict__ bias,
-                                                      YT* __restrict__ y, int N, int K,
-                                                      int ldy) {
+                                                      const float* residual,
+                                                      YT* y, int N, int K, int ldy) {
     const int lane = threadIdx.x & 63;
     const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
     if (n0 >= N) return;
@@ -98,43 +98,48 @@ __global__ __launch_bounds__(256) void gemv_w8_kernel(const XT* __restrict__ x,
             if (lane == m * R + r && n0 + r < N) {
                 float v = acc[m][r] * s_w[n0 + r];
                 if (bias) v += bias[n0 + r];
+                // residual may alias y (in-place x += W x'): same lane reads then writes.
+                if (residual) v += residual[(int64_t)m * ldy + n0 + r];
                 y[(int64_t)m * ldy + n0 + r] = from_f32<YT>(v);
             }
         }
 }
 
 template <int R, int MT, typename XT, typename YT>
-static void launch_gemv(const XT* x, const int8_t* w, const float* s_w, const float* bias, YT* y,
-                        int N, int K, hipStream_t st) {
+static void launch_gemv(const XT* x, const int8_t* w, const float* s_w, const float* bias,
+                        const float* res, YT* y, int N, int K, hipStream_t st) {
     dim3 grid(ceil_div(N, 4 * R)), block(256);
-    gemv_w8_kernel<R, MT, XT, YT><<<grid, block, 0, st>>>(x, w, s_w, bias, y, N, K, N);
+    gemv_w8_kernel<R, MT, XT, YT><<<grid, block, 0, st>>>(x, w, s_w, bias, res, y, N, K, N);
 }
 
 template <int R, typename XT, typename YT>
-static void launch_rows(const XT* x, const int8_t* w, const float* s_w, const float* bias, YT* y,
-                        int M, int N, int K, hipStream_t st) {
+static void launch_rows(const XT* x, const int8_t* w, const float* s_w, const float* bias,
+                        const float* res, YT* y, int M, int N, int K, hipStream_t st) {
     // x rows are processed in launches of up to 8; each launch re-streams W.
     for (int m0 = 0; m0 < M;) {
         const int left = M - m0;
         const XT* xm = x + (int64_t)m0 * K;
         YT* ym = y + (int64_t)m0 * N;
-        if (left >= 8) { launch_gemv<R, 8>(xm, w, s_w, bias, ym, N, K, st); m0 += 8; }
-        else if (left >= 4) { launch_gemv<R, 4>(xm, w, s_w, bias, ym, N, K, st); m0 += 4; }
-        else if (left >= 2) { launch_gemv<R, 2>(xm, w, s_w, bias, ym, N, K, st); m0 += 2; }
-        else { launch_gemv<R, 1>(xm, w, s_w, bias, ym, N, K, st); m0 += 1; }
+        const float* rm = res ? res + (int64_t)m0 * N : nullptr;
+        if (left >= 8) { launch_gemv<R, 8>(xm, w, s_w, bias, rm, ym, N, K, st); m0 += 8; }
+        else if (left >= 4) { launch_gemv<R, 4>(xm, w, s_w, bias, rm, ym, N, K, st); m0 += 4; }
+        else if (left >= 2) { launch_gemv<R, 2>(xm, w, s_w, bias, rm, ym, N, K, st); m0 += 2; }
+        else { launch_gemv<R, 1>(xm, w, s_w, bias, rm, ym, N, K, st); m0 += 1; }
     }
 }
 
 template <typename XT, typename YT>
-static void dispatch_r(const XT* x, const int8_t* w, const float* s_w, const float* bias, YT* y,
-                       int M, int N, int K, hipStream_t st) {
+static void dispatch_r(const XT* x, const int8_t* w, const float* s_w, const float* bias,
+                       const float* res, YT* y, int M, int N, int K, hipStream_t st) {
     // Few rows -> fewer rows per wave so the grid still spreads over 256 CUs.
-    if (N >= 32768) launch_rows<4>(x, w, s_w, bias, y, M, N, K, st);
-    else launch_rows<2>(x, w, s_w, bias, y, M, N, K, st);
+    if (N >= 32768) launch_rows<4>(x, w, s_w, bias, res, y, M, N, K, st);
+    else launch_rows<2>(x, w, s_w, bias, res, y, M, N, K, st);
 }
 
-int gemv_w8(const void* x, int x_dtype, const int8_t* w, const float* s_w, const float* bias,
-            void* y, int y_dtype, int M, int N, int K, hipStream_t st) {
+// GEMV with an optional fp32 residual added in the epilogue (y may alias it;
+// y must then be fp32).
+int gemv_w8_res(const void* x, int x_dtype, const int8_t* w, const float* s_w, const float* bias,
+                const float* res, void* y, int y_dtype, int M, int N, int K, hipStream_t st) {
     PIO_REQUIRE(x && w && s_w && y, "gemv_w8: null pointer");
     PIO_REQUIRE(M >= 0 && N >= 0 && K >= 0, "gemv_w8: negative shape");
     PIO_REQUIRE(K % 16 == 0, "gemv_w8: K=%d must be a multiple of 16", K);
@@ -143,14 +148,19 @@ int gemv_w8(const void* x, int x_dtype, const int8_t* w, const float* s_w, const
     PIO_REQUIRE(y_dtype == PIO_F32 || y_dtype == PIO_F16, "gemv_w8: y must be fp32 or fp16");
     if (M == 0 || N == 0) return PIO_OK;
     if (x_dtype == PIO_F32) {
-        if (y_dtype == PIO_F32) dispatch_r((const float*)x, w, s_w, bias, (float*)y, M, N, K, st);
-        else dispatch_r((const float*)x, w, s_w, bias, (_Float16*)y, M, N, K, st);
+        if (y_dtype == PIO_F32) dispatch_r((const float*)x, w, s_w, bias, res, (float*)y, M, N, K, st);
+        else dispatch_r((const float*)x, w, s_w, bias, res, (_Float16*)y, M, N, K, st);
     } else {
-        if (y_dtype == PIO_F32) dispatch_r((const _Float16*)x, w, s_w, bias, (float*)y, M, N, K, st);
-        else dispatch_r((const _Float16*)x, w, s_w, bias, (_Float16*)y, M, N, K, st);
+        if (y_dtype == PIO_F32) dispatch_r((const _Float16*)x, w, s_w, bias, res, (float*)y, M, N, K, st);
+        else dispatch_r((const _Float16*)x, w, s_w, bias, res, (_Float16*)y, M, N, K, st);
     }
     PIO_LAUNCHED();
     return PIO_OK;
+}
+
+int gemv_w8(const void* x, int x_dtype, const int8_t* w, const float* s_w, const float* bias,
+            void* y, int y_dtype, int M, int N, int K, hipStream_t st) {
+    return gemv_w8_res(x, x_dtype, w, s_w, bias, nullptr, y, y_dtype, M, N, K, st);
 }
 
 }  // namespace pio

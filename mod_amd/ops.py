@@ -95,6 +95,12 @@ SIGNATURES: dict[str, tuple] = {
     "pio_moe_workspace": (_sz, [_i, _i, _i, _i, _i]),
     "pio_moe_w8a8": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i,
                           _vp, _vp]),
+    "pio_qwen3_create": (_vp, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "pio_qwen3_destroy": (None, [_vp]),
+    "pio_qwen3_reset": (_i, [_vp, _vp, _i]),
+    "pio_qwen3_run": (_i, [_vp, _i, _i]),
+    "pio_qwen3_read": (_i, [_vp, _vp, _i, _vp]),
+    "pio_qwen3_logits": (_vp, [_vp]),
     "pio_version": (ctypes.c_char_p, []),
 }
 

@@ -1,0 +1,168 @@
+"""Host side of the int8 Qwen3-style decoder (BASELINE config 2 shape).
+
+``Qwen3Int8Decoder`` uploads int8 weights (numpy) into library-owned HBM
+tensors and drives the native decoder (pio_qwen3_* in libtensor_ops_rocm.so):
+one device-driven decode step, captured once as a HIP graph and replayed per
+token. Replaces Qwen3ForCausalLM.generate (ip/models/qwen3_0_6b/architecture.py:
+183-221), whose loop makes ~30 ctypes calls and allocations per layer per token.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import asdict, dataclass
+from typing import Dict, List, Optional
+
+import numpy as np
+
+from . import ops
+from .backend import Tensor
+from .ops import RocmError, check, lib
+
+
+@dataclass
+class Qwen3Config:
+    """Defaults = BASELINE config 2 (Qwen3-0.6B shape, head_dim 128)."""
+    n_layers: int = 28
+    hidden: int = 1024
+    n_heads: int = 16
+    n_kv_heads: int = 8
+    head_dim: int = 128
+    intermediate: int = 3072
+    vocab: int = 151936
+    max_seq: int = 384
+    rms_eps: float = 1e-6
+    rope_theta: float = 10000.0
+
+    def weight_bytes(self) -> Dict[str, int]:
+        """Int8 weight and fp32 scale bytes streamed per decode token."""
+        H, D, I = self.hidden, self.head_dim, self.intermediate
+        nqkv = (self.n_heads + 2 * self.n_kv_heads) * D
+        per_layer = nqkv * H + H * self.n_heads * D + 2 * I * H + H * I
+        scales_layer = 4 * (nqkv + H + 2 * I + H)
+        return {
+            "int8": self.n_layers * per_layer + self.vocab * H,
+            "scales": self.n_layers * scales_layer + 4 * self.vocab,
+            "bias_norms": self.n_layers * 4 * (nqkv + 2 * H) + 4 * H,
+        }
+
+    def kv_bytes_per_pos(self) -> int:
+        """fp32 K and V bytes read per cached position per token."""
+        return self.n_layers * 2 * self.n_kv_heads * self.head_dim * 4
+
+
+class _CConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("n_layers", "hidden", "n_heads", "n_kv_heads",
+                                              "head_dim", "intermediate", "vocab", "max_seq")] + \
+               [("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_float)]
+
+
+class _CLayer(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("in_norm", "w_qkv", "s_qkv", "b_qkv", "w_o", "s_o",
+                                                 "post_norm", "w_gu", "s_gu", "w_down", "s_down")]
+
+
+LAYER_KEYS = ("in_norm", "w_qkv", "s_qkv", "b_qkv", "w_o", "s_o", "post_norm", "w_gu", "s_gu",
+              "w_down", "s_down")
+
+
+def random_weights(cfg: Qwen3Config, seed: int = 0, qkv_bias: bool = True) -> dict:
+    """Random-init int8 weights of the config's architecture (numpy, host).
+    int8 weights ~ randint(-127, 127); scales ~ U(0.001, 0.02) scaled by
+    1/sqrt(K/1024) so activations stay O(1) through the layers; norms ~ 1."""
+    rng = np.random.default_rng(seed)
+    H, D, I, V = cfg.hidden, cfg.head_dim, cfg.intermediate, cfg.vocab
+    nqkv = (cfg.n_heads + 2 * cfg.n_kv_heads) * D
+
+    def lin(n, k):
+        w = rng.integers(-127, 127, size=(n, k), dtype=np.int8)
+        s = (rng.uniform(0.001, 0.02, size=n) * np.sqrt(1024.0 / k) * 0.1).astype(np.float32)
+        return w, s
+
+    layers = []
+    for _ in range(cfg.n_layers):
+        L = {}
+        L["in_norm"] = (1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+        L["w_qkv"], L["s_qkv"] = lin(nqkv, H)
+        L["b_qkv"] = (0.1 * rng.standard_normal(nqkv)).astype(np.float32) if qkv_bias else None
+        L["w_o"], L["s_o"] = lin(H, cfg.n_heads * D)
+        L["post_norm"] = (1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+        L["w_gu"], L["s_gu"] = lin(2 * I, H)
+        L["w_down"], L["s_down"] = lin(H, I)
+        layers.append(L)
+    embed = rng.standard_normal((V, H), dtype=np.float32)
+    lm, s_lm = lin(V, H)
+    return {"embed": embed, "final_norm": np.ones(H, np.float32), "lm_head": lm,
+            "s_lm_head": (s_lm * 10).astype(np.float32), "layers": layers}
+
+
+class Qwen3Int8Decoder:
+    """Native greedy decoder over library-owned device weights."""
+
+    def __init__(self, cfg: Qwen3Config, weights: dict, device: str = "rocm:0",
+                 stream: Optional[int] = None):
+        self.cfg = cfg
+        self._keep: List[Tensor] = []
+
+        def up(a):
+            if a is None:
+                return None
+            t = Tensor.from_numpy(np.ascontiguousarray(a), device)
+            self._keep.append(t)
+            return t.data_ptr()
+
+        self._embed = up(weights["embed"])
+        self._final = up(weights["final_norm"])
+        self._lm = up(weights["lm_head"])
+        self._slm = up(weights["s_lm_head"])
+        layers = (_CLayer * cfg.n_layers)()
+        for i, L in enumerate(weights["layers"]):
+            for k in LAYER_KEYS:
+                setattr(layers[i], k, up(L.get(k)))
+        c = _CConfig(**{k: v for k, v in asdict(cfg).items()})
+        self._cfg_c, self._layers_c = c, layers
+        self._h = lib.pio_qwen3_create(ctypes.addressof(c), self._embed, self._final, self._lm,
+                                       self._slm, ctypes.addressof(layers), stream)
+        if not self._h:
+            raise RocmError(f"pio_qwen3_create failed: {ops.last_error()}")
+        self.prompt_len = 0
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib.pio_qwen3_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def reset(self, ids) -> None:
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        check(lib.pio_qwen3_reset(self._h, ids.ctypes.data, ids.size), "pio_qwen3_reset")
+        self.prompt_len = int(ids.size)
+
+    def run(self, n_steps: int, use_graph: bool = True) -> None:
+        check(lib.pio_qwen3_run(self._h, n_steps, int(use_graph)), "pio_qwen3_run")
+
+    def read(self, n: int, with_logits: bool = False):
+        ids = np.zeros(n, np.int32)
+        logits = np.empty(self.cfg.vocab, np.float32) if with_logits else None
+        check(lib.pio_qwen3_read(self._h, ids.ctypes.data, n,
+                                 None if logits is None else logits.ctypes.data),
+              "pio_qwen3_read")
+        return (ids, logits) if with_logits else ids
+
+    def generate(self, prompt, n_new: int, use_graph: bool = True) -> np.ndarray:
+        """Greedy decode: prompt (P ids) -> P + n_new ids. The prompt is consumed
+        one position per step (P-1 steps), then n_new steps generate."""
+        self.reset(prompt)
+        P = len(prompt)
+        self.run(P - 1 + n_new, use_graph)
+        return self.read(P + n_new)
+
+    def teacher_forced_logits(self, ids, use_graph: bool = False) -> np.ndarray:
+        """Logits after each position of a fixed id sequence ([len-1, vocab])."""
+        self.reset(ids)
+        out = []
+        for _ in range(len(ids) - 1):
+            self.run(1, use_graph)
+            out.append(self.read(0, with_logits=True)[1].copy())
+        return np.stack(out)

@@ -1,0 +1,118 @@
+"""numpy restatement of the int8 Qwen3-style decode step -- TEST INFRASTRUCTURE ONLY.
+
+Follows the reference model structure (ip/models/qwen3_0_6b/architecture.py:
+21-221: fused qkv with bias, rotate-half RoPE, GQA, pre-norm block, fused
+gate_up + SwiGLU, lm_head, greedy argmax) at the BASELINE config-2 shape
+(head_dim 128), with the reference's kernel defects fixed as documented in
+mod_amd/csrc/decode.hip: causal attention over the cache, no dropped residual,
+RoPE applied per head count.
+
+Every linear is the W8 per-channel GEMV: y = s_w * (W_int8 @ x) (+ bias).
+Computation runs in float64 (``dtype=np.float64``) or float32 for the
+full-size config where float64 dequantized weights would not fit comfortably.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+
+@dataclass
+class Qwen3Config:
+    n_layers: int = 28
+    hidden: int = 1024
+    n_heads: int = 16
+    n_kv_heads: int = 8
+    head_dim: int = 128
+    intermediate: int = 3072
+    vocab: int = 151936
+    max_seq: int = 384
+    rms_eps: float = 1e-6
+    rope_theta: float = 10000.0
+
+
+def rope_tables(cfg: Qwen3Config, dtype=np.float64):
+    half = cfg.head_dim // 2
+    j = np.arange(half, dtype=np.float64)
+    inv = cfg.rope_theta ** (-(2 * j) / cfg.head_dim)
+    ang = np.arange(cfg.max_seq, dtype=np.float64)[:, None] * inv[None]
+    return np.cos(ang).astype(dtype), np.sin(ang).astype(dtype)
+
+
+def _lin(x, W, s, b, dt):
+    y = (W.astype(dt) @ x.astype(dt)) * s.astype(dt)
+    if b is not None:
+        y = y + b.astype(dt)
+    return y
+
+
+def _rms(x, w, eps, dt):
+    x = x.astype(dt)
+    return x * (1.0 / np.sqrt(np.mean(x * x) + eps)) * w.astype(dt)
+
+
+def _rope(v, c, s):
+    half = v.shape[-1] // 2
+    r, im = v[..., :half], v[..., half:]
+    return np.concatenate([r * c - im * s, r * s + im * c], axis=-1)
+
+
+class Qwen3Ref:
+    """Incremental decoder with a KV cache; step(id) returns the logits."""
+
+    def __init__(self, cfg: Qwen3Config, w: dict, dtype=np.float64):
+        self.cfg, self.w, self.dt = cfg, w, dtype
+        self.cos, self.sin = rope_tables(cfg, dtype)
+        L, nkv, D = cfg.n_layers, cfg.n_kv_heads, cfg.head_dim
+        self.kc = np.zeros((L, cfg.max_seq, nkv, D), dtype)
+        self.vc = np.zeros((L, cfg.max_seq, nkv, D), dtype)
+        self.pos = 0
+
+    def step(self, tok: int) -> np.ndarray:
+        c, w, dt, pos = self.cfg, self.w, self.dt, self.pos
+        H, D, nq, nkv = c.hidden, c.head_dim, c.n_heads, c.n_kv_heads
+        x = w["embed"][tok].astype(dt)
+        for l, Lw in enumerate(w["layers"]):
+            h = _rms(x, Lw["in_norm"], c.rms_eps, dt)
+            qkv = _lin(h, Lw["w_qkv"], Lw["s_qkv"], Lw.get("b_qkv"), dt)
+            q = qkv[: nq * D].reshape(nq, D)
+            k = qkv[nq * D: (nq + nkv) * D].reshape(nkv, D)
+            v = qkv[(nq + nkv) * D:].reshape(nkv, D)
+            q = _rope(q, self.cos[pos], self.sin[pos])
+            k = _rope(k, self.cos[pos], self.sin[pos])
+            self.kc[l, pos] = k
+            self.vc[l, pos] = v
+            K = self.kc[l, : pos + 1]            # [t, nkv, D]
+            V = self.vc[l, : pos + 1]
+            grp = nq // nkv
+            out = np.empty((nq, D), dt)
+            for hh in range(nq):
+                kv = hh // grp
+                sc = (K[:, kv, :] @ q[hh]) / np.sqrt(D)
+                p = np.exp(sc - sc.max())
+                p = p / p.sum()
+                out[hh] = p @ V[:, kv, :]
+            x = x + _lin(out.reshape(-1), Lw["w_o"], Lw["s_o"], None, dt)
+            h = _rms(x, Lw["post_norm"], c.rms_eps, dt)
+            gu = _lin(h, Lw["w_gu"], Lw["s_gu"], None, dt)
+            g, u = gu[: c.intermediate], gu[c.intermediate:]
+            a = g / (1.0 + np.exp(-g)) * u
+            x = x + _lin(a, Lw["w_down"], Lw["s_down"], None, dt)
+        h = _rms(x, w["final_norm"], c.rms_eps, dt)
+        logits = _lin(h, w["lm_head"], w["s_lm_head"], None, dt)
+        self.pos += 1
+        return logits
+
+
+def greedy(cfg: Qwen3Config, w: dict, prompt, n_new: int, dtype=np.float64):
+    """Greedy decode: returns (ids, logits of every step)."""
+    ref = Qwen3Ref(cfg, w, dtype)
+    ids = list(prompt)
+    all_logits = []
+    for pos in range(len(prompt) + n_new - 1):
+        lg = ref.step(ids[pos])
+        all_logits.append(lg)
+        if pos + 1 >= len(prompt):
+            ids.append(int(np.argmax(lg)))
+    return ids, all_logits

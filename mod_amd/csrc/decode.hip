@@ -4,9 +4,9 @@
 // the position and the token ids -- live in device memory, so the whole step is
 // captured once as a HIP graph and replayed per token with no host round trip:
 //
-//   embed -> L x [ rmsnorm -> W8 qkv(+bias) -> rope+kv-write -> attention ->
-//                  W8 o(+residual) -> rmsnorm -> W8 gate_up -> swiglu ->
-//                  W8 down(+residual) ] -> rmsnorm -> W8 lm_head -> argmax -> finish
+//   embed -> L x [ rmsnorm+W8 qkv+bias+RoPE+kv-write -> attention ->
+//                  W8 o(+residual) -> rmsnorm+W8 gate_up+SwiGLU -> W8 down(+residual) ]
+//         -> rmsnorm+W8 lm_head+block argmax -> finish (argmax, next id, pos += 1)
 //
 // The W8 GEMVs are the HBM-bound kernels (596 MB of int8 weights per token at
 // the Qwen3-0.6B shape); everything else is latency. Semantics follow the
@@ -22,190 +22,312 @@
 
 namespace pio {
 
-int gemv_w8_res(const void* x, int x_dtype, const int8_t* w, const float* s_w, const float* bias,
-                const float* res, void* y, int y_dtype, int M, int N, int K, hipStream_t st);
-
 constexpr int DEC_MAX_SEQ = 8192;
 
-__device__ __forceinline__ float block_sum(float v, float* red) {
-    v = wave_sum(v);
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    __syncthreads();
-    if (lane == 0) red[w] = v;
-    __syncthreads();
-    float t = 0.f;
-    for (int i = 0; i < nw; i++) t += red[i];
-    return t;
-}
-__device__ __forceinline__ float block_max(float v, float* red) {
-    v = wave_max(v);
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    __syncthreads();
-    if (lane == 0) red[w] = v;
-    __syncthreads();
-    float t = -INFINITY;
-    for (int i = 0; i < nw; i++) t = fmaxf(t, red[i]);
-    return t;
-}
-
 // x = embed[ids[pos]] (an out-of-range id reads row 0, as tensor_embed,
-// tensor_ops.c:663-671); also clears the argmax key for this step.
+// tensor_ops.c:663-671).
 __global__ void dec_embed_kernel(const float* __restrict__ embed, const int32_t* __restrict__ ids,
                                  const int32_t* __restrict__ state, float* __restrict__ x, int H,
-                                 int V, int max_seq, unsigned long long* key) {
+                                 int V, int max_seq) {
     const int pos = state[0];
     if (pos >= max_seq) return;
     int id = ids[pos];
     if (id < 0 || id >= V) id = 0;
     for (int i = threadIdx.x; i < H; i += blockDim.x) x[i] = embed[(int64_t)id * H + i];
-    if (threadIdx.x == 0) *key = 0ull;
 }
 
-// out = x * (1/sqrt(mean(x^2) + eps)) * w   (tensor_ops.c:369-383)
-__global__ __launch_bounds__(1024) void dec_rmsnorm_kernel(const float* __restrict__ x,
-                                                           const float* __restrict__ w,
-                                                           float* __restrict__ out, int H,
-                                                           float eps) {
-    __shared__ float red[16];
-    float ss = 0.f;
-    for (int i = threadIdx.x; i < H; i += blockDim.x) ss += x[i] * x[i];
-    ss = block_sum(ss, red);
-    const float sc = 1.0f / sqrtf(ss / (float)H + eps);
-    for (int i = threadIdx.x; i < H; i += blockDim.x) out[i] = x[i] * sc * w[i];
+// ----------------------------------------------------------- fused GEMV ---
+// One kernel template for every decode linear: y = W8(x) with
+//   prologue  optional RMSNorm: x' = x * g, and the row sum of x^2 -- each wave
+//             covers all of x, so the norm costs one extra wave reduction;
+//             the scale 1/sqrt(mean(x^2)+eps) is applied to the dot products
+//             (tensor_ops.c:369-383 applies it to x first; same value up to rounding);
+//   epilogue  PLAIN y = v; RESID y += v (y is the residual stream);
+//             ROPE   rows (n, n+D/2) of one head: bias, rotate-half RoPE at pos
+//                    (tensor_ops.c:384-415 formula), q -> q_out, k/v -> cache row pos;
+//             SWIGLU rows (i, i+I): act[i] = silu(g)*u (tensor_ops.c:588-604);
+//             LOGITS y = v and a per-block argmax key (value, lowest index).
+// A wave owns R rows; paired modes give it R/2 pairs (n, n+half).
+enum { EPI_PLAIN = 0, EPI_RESID = 1, EPI_ROPE = 2, EPI_SWIGLU = 3, EPI_LOGITS = 4 };
+
+struct DecGemv {
+    const float* x;
+    const float* norm_w;   // RMSNorm weight or nullptr
+    float eps;
+    const int8_t* W;
+    const float* s_w;
+    const float* bias;
+    int N, K, half;
+    float* y;
+    const float* cos_t;
+    const float* sin_t;
+    const int32_t* state;
+    float* q_out;
+    float* kc;
+    float* vc;
+    int nq, nkv, max_seq;
+    unsigned long long* part_keys;
+};
+
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float dot16i8(const float (&x)[16], v4i_t w, float acc) {
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        const int u = w[d];
+        acc = fmaf(x[4 * d + 0], (float)(int8_t)(u), acc);
+        acc = fmaf(x[4 * d + 1], (float)(int8_t)(u >> 8), acc);
+        acc = fmaf(x[4 * d + 2], (float)(int8_t)(u >> 16), acc);
+        acc = fmaf(x[4 * d + 3], (float)(int8_t)(u >> 24), acc);
+    }
+    return acc;
 }
 
-// Rotate-half RoPE on q (nq heads) and k (nkv heads) at `pos`, q -> q_out,
-// k and v -> the cache row `pos` ([kv_head][max_seq][D] layout).
-__global__ void dec_rope_cache_kernel(const float* __restrict__ qkv, const float* __restrict__ cos_t,
-                                      const float* __restrict__ sin_t,
-                                      const int32_t* __restrict__ state, float* __restrict__ q_out,
-                                      float* __restrict__ kc, float* __restrict__ vc, int nq,
-                                      int nkv, int D, int max_seq) {
-    const int pos = state[0];
-    if (pos >= max_seq) return;
-    const int half = D / 2;
-    const float* c = cos_t + (int64_t)pos * half;
-    const float* s = sin_t + (int64_t)pos * half;
-    const int pairs = (nq + nkv) * half;
-    for (int i = threadIdx.x + blockIdx.x * blockDim.x; i < pairs; i += blockDim.x * gridDim.x) {
-        const int h = i / half, j = i % half;
-        const float* src = qkv + (int64_t)h * D;   // q heads then k heads, contiguous
-        const float r = src[j], im = src[j + half];
-        const float o0 = r * c[j] - im * s[j];
-        const float o1 = r * s[j] + im * c[j];
-        if (h < nq) {
-            q_out[(int64_t)h * D + j] = o0;
-            q_out[(int64_t)h * D + j + half] = o1;
-        } else {
-            float* dst = kc + ((int64_t)(h - nq) * max_seq + pos) * D;
-            dst[j] = o0;
-            dst[j + half] = o1;
-        }
-    }
-    const float* vsrc = qkv + (int64_t)(nq + nkv) * D;
-    for (int i = threadIdx.x + blockIdx.x * blockDim.x; i < nkv * D; i += blockDim.x * gridDim.x) {
-        const int h = i / D, d = i % D;
-        vc[((int64_t)h * max_seq + pos) * D + d] = vsrc[i];
-    }
-}
-
-// Causal GQA attention for one query position: block = one q head, 256 threads.
-__global__ __launch_bounds__(256) void dec_attn_kernel(const float* __restrict__ q,
-                                                       const float* __restrict__ kc,
-                                                       const float* __restrict__ vc,
-                                                       const int32_t* __restrict__ state,
-                                                       float* __restrict__ out, int nq, int nkv,
-                                                       int D, int max_seq, float scale) {
-    __shared__ float sc[DEC_MAX_SEQ];
-    __shared__ float red[16];
-    __shared__ float part[256];
-    const int pos = state[0];
-    if (pos >= max_seq) return;
-    const int L = pos + 1;
-    const int h = blockIdx.x, kvh = h / (nq / nkv);
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const float* qh = q + (int64_t)h * D;
-    const float* kb = kc + (int64_t)kvh * max_seq * D;
-    const float* vb = vc + (int64_t)kvh * max_seq * D;
-
-    for (int t = w; t < L; t += 4) {
-        float dot = 0.f;
-        for (int d = lane; d < D; d += 64) dot += qh[d] * kb[(int64_t)t * D + d];
-        dot = wave_sum(dot);
-        if (lane == 0) sc[t] = dot * scale;
-    }
-    __syncthreads();
-    float mx = -INFINITY;
-    for (int t = threadIdx.x; t < L; t += blockDim.x) mx = fmaxf(mx, sc[t]);
-    mx = block_max(mx, red);
-    float sum = 0.f;
-    for (int t = threadIdx.x; t < L; t += blockDim.x) {
-        const float e = expf(sc[t] - mx);
-        sc[t] = e;
-        sum += e;
-    }
-    sum = block_sum(sum, red);
-    const float inv = 1.0f / sum;
-    __syncthreads();
-    // out[d] = sum_t p[t] * v[t][d]; the block's threads split (t-slices x d).
-    const int slices = blockDim.x / D > 0 ? blockDim.x / D : 1;
-    const int d = threadIdx.x % D, sl = threadIdx.x / D;
-    float acc = 0.f;
-    if (sl < slices)
-        for (int t = sl; t < L; t += slices) acc += sc[t] * vb[(int64_t)t * D + d];
-    part[threadIdx.x] = acc;
-    __syncthreads();
-    if (threadIdx.x < D) {
-        float o = 0.f;
-        for (int i = 0; i < slices; i++) o += part[i * D + threadIdx.x];
-        out[(int64_t)h * D + threadIdx.x] = o * inv;
-    }
-}
-
-// a[i] = silu(g[i]) * u[i] with [g | u] = gu  (tensor_ops.c:588-604)
-__global__ void dec_swiglu_kernel(const float* __restrict__ gu, float* __restrict__ a, int I) {
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < I; i += gridDim.x * blockDim.x) {
-        const float g = gu[i], u = gu[I + i];
-        a[i] = g * (1.0f / (1.0f + expf(-g))) * u;
-    }
-}
-
-// Argmax with the reference tie rule (strict '>', the first maximum wins,
-// tensor_ops.c:649-662): each block reduces to (value, lowest index), then one
-// 64-bit atomicMax on (order-preserving value bits << 32 | ~index).
 __device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
     uint32_t b = __float_as_uint(v);
     b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
     return ((unsigned long long)b << 32) | (unsigned long long)(0xffffffffu - (uint32_t)i);
 }
-__global__ __launch_bounds__(256) void dec_argmax_kernel(const float* __restrict__ logits, int V,
-                                                         unsigned long long* key) {
-    unsigned long long best = 0ull;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < V; i += gridDim.x * blockDim.x) {
-        const unsigned long long k = argmax_key(logits[i], i);
-        best = k > best ? k : best;
+
+template <int EPI, int R>
+__global__ __launch_bounds__(256) void dec_gemv_kernel(DecGemv p) {
+    constexpr bool PAIRED = (EPI == EPI_ROPE || EPI == EPI_SWIGLU);
+    const int lane = threadIdx.x & 63;
+    const int g = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int K = p.K, N = p.N;
+
+    int row[R];
+    bool ok[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        int n;
+        if (PAIRED) {
+            const int pi = g * (R / 2) + r / 2;
+            n = (pi / p.half) * 2 * p.half + (pi % p.half) + (r & 1) * p.half;
+        } else {
+            n = g * R + r;
+        }
+        ok[r] = n < N;
+        row[r] = ok[r] ? n : N - 1;
     }
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.f;
+    float ss = 0.f;
+    for (int k = lane * 16; k < K; k += 1024) {
+        v4i_t w[R];
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            w[r] = __builtin_nontemporal_load((const v4i_t*)(p.W + (int64_t)row[r] * K + k));
+        float xv[16];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 a = *(const float4*)(p.x + k + 4 * i);
+            xv[4 * i] = a.x; xv[4 * i + 1] = a.y; xv[4 * i + 2] = a.z; xv[4 * i + 3] = a.w;
+        }
+        if (p.norm_w) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 gw = *(const float4*)(p.norm_w + k + 4 * i);
+                ss += xv[4 * i] * xv[4 * i] + xv[4 * i + 1] * xv[4 * i + 1] +
+                      xv[4 * i + 2] * xv[4 * i + 2] + xv[4 * i + 3] * xv[4 * i + 3];
+                xv[4 * i] *= gw.x; xv[4 * i + 1] *= gw.y; xv[4 * i + 2] *= gw.z; xv[4 * i + 3] *= gw.w;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] = dot16i8(xv, w[r], acc[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
+    float nscale = 1.f;
+    if (p.norm_w) nscale = 1.0f / sqrtf(wave_sum(ss) / (float)K + p.eps);
+
+    float v[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        v[r] = acc[r] * p.s_w[row[r]] * nscale;
+        if (p.bias) v[r] += p.bias[row[r]];
+    }
+
+    if (EPI == EPI_PLAIN || EPI == EPI_RESID || EPI == EPI_LOGITS) {
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            if (lane == r && ok[r]) {
+                if (EPI == EPI_RESID) p.y[row[r]] += v[r];
+                else p.y[row[r]] = v[r];
+            }
+    }
+    if (EPI == EPI_LOGITS) {
+        unsigned long long best = 0ull;
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            if (ok[r]) {
+                const unsigned long long kk = argmax_key(v[r], row[r]);
+                best = kk > best ? kk : best;
+            }
+        __shared__ unsigned long long wbest[4];
+        if (lane == 0) wbest[threadIdx.x >> 6] = best;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (int i = 1; i < 4; i++) best = wbest[i] > best ? wbest[i] : best;
+            p.part_keys[blockIdx.x] = best;
+        }
+    }
+    if (EPI == EPI_SWIGLU) {
+#pragma unroll
+        for (int j = 0; j < R / 2; j++)
+            if (lane == j && ok[2 * j]) {
+                const float gg = v[2 * j], u = v[2 * j + 1];
+                p.y[row[2 * j]] = gg * (1.0f / (1.0f + expf(-gg))) * u;
+            }
+    }
+    if (EPI == EPI_ROPE) {
+        const int pos = p.state[0];
+        if (pos >= p.max_seq) return;
+        const int D = 2 * p.half;
+#pragma unroll
+        for (int j = 0; j < R / 2; j++) {
+            if (lane != j || !ok[2 * j]) continue;
+            const int n0 = row[2 * j];
+            const int head = n0 / D, i = n0 % D;
+            const float re = v[2 * j], im = v[2 * j + 1];
+            if (head < p.nq + p.nkv) {
+                const float c = p.cos_t[(int64_t)pos * p.half + i];
+                const float sn = p.sin_t[(int64_t)pos * p.half + i];
+                const float o0 = re * c - im * sn, o1 = re * sn + im * c;
+                float* dst = head < p.nq ? p.q_out + (int64_t)head * D
+                                         : p.kc + ((int64_t)(head - p.nq) * p.max_seq + pos) * D;
+                dst[i] = o0;
+                dst[i + p.half] = o1;
+            } else {
+                float* dst = p.vc + ((int64_t)(head - p.nq - p.nkv) * p.max_seq + pos) * D;
+                dst[i] = re;
+                dst[i + p.half] = im;
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------ attention ---
+// Causal GQA decode attention, split over key positions: block (c, h) scores
+// positions [64c, 64c+64) for q head h (4 lanes per key row, 32 dims each),
+// keeps (max, sum, p.V) partials, and the last block of head h to finish --
+// counted with a device-scope atomic after a release fence -- merges the
+// partials in chunk order (so the result does not depend on which block is
+// last) and re-arms the counter for the next layer.
+constexpr int ATT_CHUNK = 64;
+
+__global__ __launch_bounds__(256) void dec_attn_split_kernel(
+    const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
+    const int32_t* __restrict__ state, float* __restrict__ out, float* __restrict__ part_o,
+    float* __restrict__ part_ml, int* __restrict__ counters, int nq, int nkv, int max_seq,
+    float scale) {
+    constexpr int D = 128;
+    __shared__ float sc[ATT_CHUNK];
+    __shared__ float po[256];
+    __shared__ float red[2];
+    __shared__ int last;
+    const int pos = state[0];
+    if (pos >= max_seq) return;
+    const int L = pos + 1;
+    const int nchunks = (L + ATT_CHUNK - 1) / ATT_CHUNK;
+    const int c = blockIdx.x, h = blockIdx.y;
+    if (c >= nchunks) return;
+    const int kvh = h / (nq / nkv);
+    const int t0 = c * ATT_CHUNK;
+    const int n = min(ATT_CHUNK, L - t0);
+    const float* kb = kc + ((int64_t)kvh * max_seq + t0) * D;
+    const float* vb = vc + ((int64_t)kvh * max_seq + t0) * D;
+    const int tid = threadIdx.x;
+
+    // scores: thread (t = tid/4, part = tid%4) covers dims [32*part, 32*part+32)
+    {
+        const int t = tid >> 2, part = tid & 3;
+        float dot = 0.f;
+        if (t < n) {
+            const float* qh = q + (int64_t)h * D + part * 32;
+            const float* kr = kb + (int64_t)t * D + part * 32;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 a = *(const float4*)(qh + 4 * i);
+                const float4 b = *(const float4*)(kr + 4 * i);
+                dot += a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+            }
+        }
+        dot += __shfl_xor(dot, 1, 64);
+        dot += __shfl_xor(dot, 2, 64);
+        if (part == 0 && t < ATT_CHUNK) sc[t] = t < n ? dot * scale : -INFINITY;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        float m = wave_max(sc[tid]);
+        const float e = tid < n ? expf(sc[tid] - m) : 0.f;
+        sc[tid] = e;
+        const float l = wave_sum(e);
+        if (tid == 0) { red[0] = m; red[1] = l; }
+    }
+    __syncthreads();
+    // o[d] = sum_t p[t] v[t][d]: threads split into two t-halves of 32.
+    {
+        const int d = tid & (D - 1), hf = tid >> 7;
+        float o = 0.f;
+        const int tb = hf * 32, te = min(n, tb + 32);
+        for (int t = tb; t < te; t++) o += sc[t] * vb[(int64_t)t * D + d];
+        po[tid] = o;
+    }
+    __syncthreads();
+    if (nchunks == 1) {
+        if (tid < D) out[(int64_t)h * D + tid] = (po[tid] + po[tid + D]) / red[1];
+        return;
+    }
+    const int maxc = (max_seq + ATT_CHUNK - 1) / ATT_CHUNK;
+    if (tid < D) part_o[((int64_t)h * maxc + c) * D + tid] = po[tid] + po[tid + D];
+    if (tid == 0) {
+        part_ml[((int64_t)h * maxc + c) * 2] = red[0];
+        part_ml[((int64_t)h * maxc + c) * 2 + 1] = red[1];
+    }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) last = atomicAdd(&counters[h], 1) == nchunks - 1;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    if (tid < D) {
+        float M = -INFINITY;
+        for (int i = 0; i < nchunks; i++)
+            M = fmaxf(M, __builtin_nontemporal_load(&part_ml[((int64_t)h * maxc + i) * 2]));
+        float num = 0.f, den = 0.f;
+        for (int i = 0; i < nchunks; i++) {
+            const float f = expf(__builtin_nontemporal_load(&part_ml[((int64_t)h * maxc + i) * 2]) - M);
+            num += f * __builtin_nontemporal_load(&part_o[((int64_t)h * maxc + i) * D + tid]);
+            den += f * __builtin_nontemporal_load(&part_ml[((int64_t)h * maxc + i) * 2 + 1]);
+        }
+        out[(int64_t)h * D + tid] = num / den;
+    }
+    if (tid == 0) atomicExch(&counters[h], 0);
+}
+
+// Argmax over the lm_head blocks' keys (reference tie rule: first maximum,
+// tensor_ops.c:649-662), then ids[pos+1] = argmax unless pos+1 is a prompt
+// position, and pos += 1.
+__global__ __launch_bounds__(1024) void dec_finish_kernel(int32_t* state,
+                                                          const unsigned long long* part_keys,
+                                                          int nparts, int32_t* ids, int max_seq) {
+    __shared__ unsigned long long wb[16];
+    unsigned long long best = 0ull;
+    for (int i = threadIdx.x; i < nparts; i += blockDim.x) best = part_keys[i] > best ? part_keys[i] : best;
     for (int o = 32; o >= 1; o >>= 1) {
         const unsigned long long other = __shfl_xor(best, o, 64);
         best = other > best ? other : best;
     }
-    __shared__ unsigned long long wb[4];
     if ((threadIdx.x & 63) == 0) wb[threadIdx.x >> 6] = best;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int i = 1; i < 4; i++) best = wb[i] > best ? wb[i] : best;
-        best = wb[0] > best ? wb[0] : best;
-        atomicMax(key, best);
-    }
-}
-
-// ids[pos+1] = argmax unless pos+1 is still a prompt position; pos += 1.
-__global__ void dec_finish_kernel(int32_t* state, const unsigned long long* key, int32_t* ids,
-                                  int max_seq) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    if (threadIdx.x != 0) return;
+    for (int i = 0; i < (int)(blockDim.x >> 6); i++) best = wb[i] > best ? wb[i] : best;
     const int pos = state[0];
     if (pos >= max_seq) return;
-    const int id = (int)(0xffffffffu - (uint32_t)(*key & 0xffffffffull));
+    const int id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffull));
     if (pos + 1 >= state[1]) ids[pos + 1] = id;
     state[2] = id;
     state[0] = pos + 1;
@@ -221,55 +343,71 @@ struct Qwen3Dec {
     hipStream_t st = nullptr;
     bool own_stream = false;
     void* block = nullptr;
-    float *x, *xn, *qkv, *q, *attn, *gu, *act, *logits, *kc, *vc, *cos_t, *sin_t;
-    int32_t *state, *ids;
-    unsigned long long* key;
+    float *x, *q, *attn, *act, *logits, *kc, *vc, *cos_t, *sin_t, *part_o, *part_ml;
+    int32_t *state, *ids, *counters;
+    unsigned long long* part_keys;
+    int lm_blocks = 0, max_chunks = 0;
     int host_pos = 0;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
 };
 
+template <int EPI, int R>
+static int launch_dec_gemv(const DecGemv& p, int rows_per_block, hipStream_t st) {
+    dec_gemv_kernel<EPI, R><<<ceil_div(p.N, rows_per_block), 256, 0, st>>>(p);
+    PIO_LAUNCHED();
+    return PIO_OK;
+}
+
+// One decode step: 1 + 5 per layer + 2 launches.
 static int enqueue_step(Qwen3Dec* d) {
     const pio_qwen3_config& c = d->c;
     const int H = c.hidden, D = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads, I = c.intermediate;
     const int nqkv = (nq + 2 * nkv) * D;
     hipStream_t st = d->st;
-    dec_embed_kernel<<<1, 256, 0, st>>>(d->embed, d->ids, d->state, d->x, H, c.vocab, c.max_seq,
-                                        d->key);
+    dec_embed_kernel<<<1, 256, 0, st>>>(d->embed, d->ids, d->state, d->x, H, c.vocab, c.max_seq);
     PIO_LAUNCHED();
     const float scale = 1.0f / sqrtf((float)D);
+    DecGemv base{};
+    base.eps = c.rms_eps;
+    base.cos_t = d->cos_t;
+    base.sin_t = d->sin_t;
+    base.state = d->state;
+    base.nq = nq;
+    base.nkv = nkv;
+    base.max_seq = c.max_seq;
     for (int l = 0; l < c.n_layers; l++) {
         const pio_qwen3_layer& L = d->layers[l];
         float* kc = d->kc + (int64_t)l * nkv * c.max_seq * D;
         float* vc = d->vc + (int64_t)l * nkv * c.max_seq * D;
-        dec_rmsnorm_kernel<<<1, 1024, 0, st>>>(d->x, L.in_norm, d->xn, H, c.rms_eps);
+        // qkv: rmsnorm(x) -> W8 + bias -> RoPE -> q, k/v cache
+        DecGemv g = base;
+        g.x = d->x; g.norm_w = L.in_norm; g.W = L.w_qkv; g.s_w = L.s_qkv; g.bias = L.b_qkv;
+        g.N = nqkv; g.K = H; g.half = D / 2; g.q_out = d->q; g.kc = kc; g.vc = vc;
+        PIO_TRY((launch_dec_gemv<EPI_ROPE, 2>(g, 8, st)));
+        dec_attn_split_kernel<<<dim3(d->max_chunks, nq), 256, 0, st>>>(
+            d->q, kc, vc, d->state, d->attn, d->part_o, d->part_ml, d->counters, nq, nkv,
+            c.max_seq, scale);
         PIO_LAUNCHED();
-        PIO_TRY(gemv_w8_res(d->xn, PIO_F32, L.w_qkv, L.s_qkv, L.b_qkv, nullptr, d->qkv, PIO_F32, 1,
-                            nqkv, H, st));
-        dec_rope_cache_kernel<<<4, 256, 0, st>>>(d->qkv, d->cos_t, d->sin_t, d->state, d->q, kc, vc,
-                                                 nq, nkv, D, c.max_seq);
-        PIO_LAUNCHED();
-        dec_attn_kernel<<<nq, 256, 0, st>>>(d->q, kc, vc, d->state, d->attn, nq, nkv, D, c.max_seq,
-                                            scale);
-        PIO_LAUNCHED();
-        PIO_TRY(gemv_w8_res(d->attn, PIO_F32, L.w_o, L.s_o, nullptr, d->x, d->x, PIO_F32, 1, H,
-                            nq * D, st));
-        dec_rmsnorm_kernel<<<1, 1024, 0, st>>>(d->x, L.post_norm, d->xn, H, c.rms_eps);
-        PIO_LAUNCHED();
-        PIO_TRY(gemv_w8_res(d->xn, PIO_F32, L.w_gu, L.s_gu, nullptr, nullptr, d->gu, PIO_F32, 1,
-                            2 * I, H, st));
-        dec_swiglu_kernel<<<ceil_div(I, 256), 256, 0, st>>>(d->gu, d->act, I);
-        PIO_LAUNCHED();
-        PIO_TRY(gemv_w8_res(d->act, PIO_F32, L.w_down, L.s_down, nullptr, d->x, d->x, PIO_F32, 1,
-                            H, I, st));
+        // o_proj: x += W8(attn)
+        g = base;
+        g.x = d->attn; g.W = L.w_o; g.s_w = L.s_o; g.N = H; g.K = nq * D; g.y = d->x;
+        PIO_TRY((launch_dec_gemv<EPI_RESID, 2>(g, 8, st)));
+        // gate_up: rmsnorm(x) -> W8 -> silu(g)*u
+        g = base;
+        g.x = d->x; g.norm_w = L.post_norm; g.W = L.w_gu; g.s_w = L.s_gu; g.N = 2 * I; g.K = H;
+        g.half = I; g.y = d->act;
+        PIO_TRY((launch_dec_gemv<EPI_SWIGLU, 2>(g, 8, st)));
+        // down: x += W8(act)
+        g = base;
+        g.x = d->act; g.W = L.w_down; g.s_w = L.s_down; g.N = H; g.K = I; g.y = d->x;
+        PIO_TRY((launch_dec_gemv<EPI_RESID, 2>(g, 8, st)));
     }
-    dec_rmsnorm_kernel<<<1, 1024, 0, st>>>(d->x, d->final_norm, d->xn, H, c.rms_eps);
-    PIO_LAUNCHED();
-    PIO_TRY(gemv_w8_res(d->xn, PIO_F32, d->lm_head, d->s_lm, nullptr, nullptr, d->logits, PIO_F32,
-                        1, c.vocab, H, st));
-    dec_argmax_kernel<<<256, 256, 0, st>>>(d->logits, c.vocab, d->key);
-    PIO_LAUNCHED();
-    dec_finish_kernel<<<1, 64, 0, st>>>(d->state, d->key, d->ids, c.max_seq);
+    DecGemv g = base;
+    g.x = d->x; g.norm_w = d->final_norm; g.W = d->lm_head; g.s_w = d->s_lm; g.N = c.vocab;
+    g.K = H; g.y = d->logits; g.part_keys = d->part_keys;
+    PIO_TRY((launch_dec_gemv<EPI_LOGITS, 4>(g, 16, st)));
+    dec_finish_kernel<<<1, 1024, 0, st>>>(d->state, d->part_keys, d->lm_blocks, d->ids, c.max_seq);
     PIO_LAUNCHED();
     return PIO_OK;
 }
@@ -298,11 +436,14 @@ PIO_EXPORT void* pio_qwen3_create(const pio_qwen3_config* cfg, const float* embe
         return nullptr;
     }
     const pio_qwen3_config& c = *cfg;
+    // The attention kernel is specialized for head_dim 128 (the Qwen3 family's);
+    // every GEMV K (hidden, heads*head_dim, intermediate) must be a multiple of 16.
     if (c.n_layers < 1 || c.hidden < 16 || c.hidden % 16 || c.n_heads < 1 || c.n_kv_heads < 1 ||
-        c.n_heads % c.n_kv_heads || c.head_dim < 2 || c.head_dim % 2 || c.head_dim > 256 ||
-        c.intermediate % 16 || c.intermediate < 16 || c.vocab < 1 || c.max_seq < 1 ||
-        c.max_seq > DEC_MAX_SEQ || (c.n_heads * c.head_dim) % 16) {
-        set_error(PIO_ERR_INVALID, "pio_qwen3_create: unsupported config");
+        c.n_heads % c.n_kv_heads || c.head_dim != 128 || c.intermediate % 16 ||
+        c.intermediate < 16 || c.vocab < 1 || c.max_seq < 1 || c.max_seq > DEC_MAX_SEQ) {
+        set_error(PIO_ERR_INVALID, "pio_qwen3_create: unsupported config (head_dim must be 128; "
+                                   "hidden and intermediate multiples of 16; max_seq <= %d)",
+                  DEC_MAX_SEQ);
         return nullptr;
     }
     for (int l = 0; l < c.n_layers; l++) {
@@ -330,18 +471,27 @@ PIO_EXPORT void* pio_qwen3_create(const pio_qwen3_config* cfg, const float* embe
         }
         d->own_stream = true;
     }
-    const int H = c.hidden, D = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads;
-    const size_t nqkv = (size_t)(nq + 2 * nkv) * D;
+    const int D = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads;
     const size_t kv = (size_t)c.n_layers * nkv * c.max_seq * D;
     const size_t half = D / 2;
+    d->lm_blocks = ceil_div(c.vocab, 16);
+    d->max_chunks = ceil_div(c.max_seq, ATT_CHUNK);
     size_t sizes[] = {
-        al256(H * 4), al256(H * 4), al256(nqkv * 4), al256((size_t)nq * D * 4),
-        al256((size_t)nq * D * 4), al256((size_t)2 * c.intermediate * 4),
-        al256((size_t)c.intermediate * 4), al256((size_t)c.vocab * 4), al256(kv * 4),
-        al256(kv * 4), al256(c.max_seq * half * 4), al256(c.max_seq * half * 4), al256(16 * 4),
-        al256((size_t)(c.max_seq + 1) * 4), al256(8)};
+        al256((size_t)c.hidden * 4),                      // x
+        al256((size_t)nq * D * 4),                        // q
+        al256((size_t)nq * D * 4),                        // attn
+        al256((size_t)c.intermediate * 4),                // act
+        al256((size_t)c.vocab * 4),                       // logits
+        al256(kv * 4), al256(kv * 4),                     // k, v cache
+        al256(c.max_seq * half * 4), al256(c.max_seq * half * 4),   // cos, sin
+        al256((size_t)nq * d->max_chunks * D * 4),        // attention partial o
+        al256((size_t)nq * d->max_chunks * 2 * 4),        // attention partial (max, sum)
+        al256(16 * 4),                                    // state
+        al256((size_t)(c.max_seq + 1) * 4),               // ids
+        al256((size_t)nq * 4),                            // attention counters
+        al256((size_t)d->lm_blocks * 8)};                 // argmax partial keys
     size_t total = 0;
-    for (size_t s : sizes) total += s;
+    for (size_t sz : sizes) total += sz;
     if (device_alloc(&d->block, total) != PIO_OK) {
         destroy(d);
         return nullptr;
@@ -350,20 +500,20 @@ PIO_EXPORT void* pio_qwen3_create(const pio_qwen3_config* cfg, const float* embe
     size_t o = 0;
     auto take = [&](int i) { char* r = p + o; o += sizes[i]; return r; };
     d->x = (float*)take(0);
-    d->xn = (float*)take(1);
-    d->qkv = (float*)take(2);
-    d->q = (float*)take(3);
-    d->attn = (float*)take(4);
-    d->gu = (float*)take(5);
-    d->act = (float*)take(6);
-    d->logits = (float*)take(7);
-    d->kc = (float*)take(8);
-    d->vc = (float*)take(9);
-    d->cos_t = (float*)take(10);
-    d->sin_t = (float*)take(11);
-    d->state = (int32_t*)take(12);
-    d->ids = (int32_t*)take(13);
-    d->key = (unsigned long long*)take(14);
+    d->q = (float*)take(1);
+    d->attn = (float*)take(2);
+    d->act = (float*)take(3);
+    d->logits = (float*)take(4);
+    d->kc = (float*)take(5);
+    d->vc = (float*)take(6);
+    d->cos_t = (float*)take(7);
+    d->sin_t = (float*)take(8);
+    d->part_o = (float*)take(9);
+    d->part_ml = (float*)take(10);
+    d->state = (int32_t*)take(11);
+    d->ids = (int32_t*)take(12);
+    d->counters = (int32_t*)take(13);
+    d->part_keys = (unsigned long long*)take(14);
     // RoPE table: angle(pos, j) = pos * theta^(-2j/D), computed in double.
     std::vector<float> ct((size_t)c.max_seq * half), stt((size_t)c.max_seq * half);
     for (int pos = 0; pos < c.max_seq; pos++)
@@ -376,6 +526,9 @@ PIO_EXPORT void* pio_qwen3_create(const pio_qwen3_config* cfg, const float* embe
     hipError_t e = hipMemcpyAsync(d->cos_t, ct.data(), ct.size() * 4, hipMemcpyHostToDevice, d->st);
     if (e == hipSuccess)
         e = hipMemcpyAsync(d->sin_t, stt.data(), stt.size() * 4, hipMemcpyHostToDevice, d->st);
+    std::vector<int32_t> zeros((size_t)nq + 16, 0);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(d->counters, zeros.data(), (size_t)nq * 4, hipMemcpyHostToDevice, d->st);
     if (e == hipSuccess) e = hipStreamSynchronize(d->st);
     if (e != hipSuccess) {
         set_error(PIO_ERR_HIP, "pio_qwen3_create: table upload failed: %s", hipGetErrorString(e));
@@ -402,6 +555,10 @@ PIO_EXPORT int pio_qwen3_reset(void* h, const int32_t* ids, int prompt_len) {
     st[1] = prompt_len;
     PIO_HIP(hipMemcpyAsync(d->ids, ids, (size_t)prompt_len * 4, hipMemcpyHostToDevice, d->st));
     PIO_HIP(hipMemcpyAsync(d->state, st.data(), 16 * 4, hipMemcpyHostToDevice, d->st));
+    // Re-arm the attention merge counters (only an interrupted step leaves them set).
+    std::vector<int32_t> zeros((size_t)d->c.n_heads, 0);
+    PIO_HIP(hipMemcpyAsync(d->counters, zeros.data(), zeros.size() * 4, hipMemcpyHostToDevice,
+                           d->st));
     PIO_HIP(hipStreamSynchronize(d->st));
     d->host_pos = 0;
     return PIO_OK;

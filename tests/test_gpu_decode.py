@@ -1,13 +1,18 @@
 """GPU parity of the native int8 decoder against the numpy restatement
-(oracle/qwen3_ref.py). Logits are compared teacher-forced (same token history
-on both sides) at rel 1e-3 (fp32 path, floor 1e-2 * rms); greedy tokens must
-match wherever the oracle's top-2 logit gap exceeds the tolerance band."""
+(oracle/qwen3_ref.py), teacher-forced (same token history on both sides).
+
+Bar for logits (fp32 path): the GPU's max error against the float64 oracle,
+relative to the logits' rms, must be <= max(1e-4, 4x the error of an
+independent fp32 implementation -- numpy's -- on the same inputs). Per-linear
+outputs are held to rel 1e-3 by the kernel tests; through 2..28 layers of
+attention and residual adds fp32 rounding compounds, which this bar measures
+against a known-good fp32 path instead of a fixed number. Greedy tokens must
+match wherever the oracle's top-2 logit gap is clear."""
 import sys
 
 import numpy as np
 import pytest
 
-from conftest import assert_rel
 from oracle import qwen3_ref
 
 pytestmark = pytest.mark.gpu
@@ -21,8 +26,8 @@ def _say(m):
 def _cfgs(small: bool):
     from mod_amd.qwen3 import Qwen3Config
     if small:
-        kw = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, intermediate=512,
-                  vocab=1000, max_seq=64)
+        kw = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=128, intermediate=512,
+                  vocab=1000, max_seq=192)
     else:
         kw = dict(max_seq=384)
     return Qwen3Config(**kw), qwen3_ref.Qwen3Config(**kw)
@@ -37,20 +42,34 @@ def _check_argmax(got_logits, ref_logits, rtol):
             assert int(np.argmax(g)) == int(np.argmax(r)), f"argmax differs at position {i}"
 
 
+def _check_logits(got, ids, rcfg, w, what):
+    r64 = qwen3_ref.Qwen3Ref(rcfg, w, np.float64)
+    r32 = qwen3_ref.Qwen3Ref(rcfg, w, np.float32)
+    worst = 0.0
+    for i, t in enumerate(ids[:len(got)]):
+        e64 = r64.step(int(t))
+        e32 = r32.step(int(t)).astype(np.float64)
+        rms = float(np.sqrt(np.mean(e64 * e64)))
+        err_gpu = float(np.abs(got[i] - e64).max()) / rms
+        err_np32 = float(np.abs(e32 - e64).max()) / rms
+        worst = max(worst, err_gpu)
+        assert err_gpu <= max(1e-4, 4 * err_np32), (what, i, err_gpu, err_np32)
+        _check_argmax(got[i:i + 1], e64[None], 1e-3)
+    _say(f"{what}: worst logit err {worst:.2e} x rms")
+
+
 def test_decoder_small_teacher_forced(torch_dev):
     from mod_amd.qwen3 import Qwen3Int8Decoder, random_weights
     cfg, rcfg = _cfgs(True)
     w = random_weights(cfg, seed=0)
     dec = Qwen3Int8Decoder(cfg, w)
     rng = np.random.default_rng(1)
-    ids = rng.integers(0, cfg.vocab, size=20).astype(np.int32)
+    # 150 positions: the attention splits keys into 64-position chunks, so this
+    # covers 1-, 2- and 3-chunk merges.
+    ids = rng.integers(0, cfg.vocab, size=150).astype(np.int32)
     _say("decoder small: teacher forced")
     got = dec.teacher_forced_logits(ids, use_graph=False)
-    ref = qwen3_ref.Qwen3Ref(rcfg, w, np.float64)
-    exp = np.stack([ref.step(int(t)) for t in ids[:-1]])
-    for i in range(len(exp)):
-        assert_rel(got[i], exp[i], 1e-3, f"logits pos {i}")
-    _check_argmax(got, exp, 1e-3)
+    _check_logits(got, ids, rcfg, w, "small teacher-forced")
 
 
 def test_decoder_small_greedy_graph_equals_eager(torch_dev):
@@ -68,11 +87,7 @@ def test_decoder_small_greedy_graph_equals_eager(torch_dev):
     ref_ids, ref_logits = qwen3_ref.greedy(rcfg, w, list(prompt), 24)
     # Teacher-forced on the GPU's own tokens: every clear-margin step agrees.
     got = dec.teacher_forced_logits(eager, use_graph=True)
-    ref = qwen3_ref.Qwen3Ref(rcfg, w, np.float64)
-    exp = np.stack([ref.step(int(t)) for t in eager[:-1]])
-    for i in range(len(exp)):
-        assert_rel(got[i], exp[i], 1e-3, f"graph logits pos {i}")
-    _check_argmax(got[7:], exp[7:], 1e-3)
+    _check_logits(got, eager, rcfg, w, "small greedy (graph)")
     match = np.mean(np.array(ref_ids) == eager)
     assert match >= 0.9, f"greedy token match {match:.2f}"
 
@@ -90,7 +105,7 @@ def test_decoder_rejects_overflow(torch_dev):
 
 
 def test_decoder_c2_shape_teacher_forced(torch_dev):
-    """Full Qwen3-0.6B shape (28 layers, vocab 151936), 6 positions, fp32 oracle."""
+    """Full Qwen3-0.6B shape (28 layers, vocab 151936), 6 teacher-forced positions."""
     from mod_amd.qwen3 import Qwen3Int8Decoder, random_weights
     cfg, rcfg = _cfgs(False)
     _say("decoder C2: building weights")
@@ -99,8 +114,4 @@ def test_decoder_c2_shape_teacher_forced(torch_dev):
     ids = np.random.default_rng(8).integers(0, cfg.vocab, size=7).astype(np.int32)
     _say("decoder C2: teacher forced")
     got = dec.teacher_forced_logits(ids, use_graph=True)
-    ref = qwen3_ref.Qwen3Ref(rcfg, w, np.float32)
-    exp = np.stack([ref.step(int(t)) for t in ids[:-1]])
-    for i in range(len(exp)):
-        assert_rel(got[i], exp[i], 1e-3, f"C2 logits pos {i}")
-    _check_argmax(got, exp, 1e-3)
+    _check_logits(got, ids, rcfg, w, "C2 teacher-forced")

@@ -18,6 +18,7 @@
 #include "pio_common.hpp"
 
 #include <math.h>
+#include <algorithm>
 #include <vector>
 
 namespace pio {
@@ -89,223 +90,291 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
     return ((unsigned long long)b << 32) | (unsigned long long)(0xffffffffu - (uint32_t)i);
 }
 
-template <int EPI, int R>
+// KC = number of 1024-wide K chunks a lane covers (K <= KC * 1024). The first
+// row group's weight loads are issued before the x prologue so their HBM
+// latency overlaps it; x (times the norm weight) is staged once per block in
+// LDS; waves that own several row groups prefetch the next group's weights
+// before reducing the current one.
+template <int EPI, int R, int KC>
 __global__ __launch_bounds__(256) void dec_gemv_kernel(DecGemv p) {
     constexpr bool PAIRED = (EPI == EPI_ROPE || EPI == EPI_SWIGLU);
-    const int lane = threadIdx.x & 63;
-    const int g = blockIdx.x * 4 + (threadIdx.x >> 6);
+    __shared__ __attribute__((aligned(16))) float xs[KC * 1024];
+    __shared__ float red[4];
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int K = p.K, N = p.N;
+    const int waves = gridDim.x * 4;
+    const int groups = (N + R - 1) / R;
 
+    auto rows_of = [&](int g, int (&row)[R], bool (&ok)[R]) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            int n;
+            if (PAIRED) {
+                const int pi = g * (R / 2) + r / 2;
+                n = (pi / p.half) * 2 * p.half + (pi % p.half) + (r & 1) * p.half;
+            } else {
+                n = g * R + r;
+            }
+            ok[r] = n < N;
+            row[r] = ok[r] ? n : N - 1;
+        }
+    };
+    auto load_w = [&](const int (&row)[R], v4i_t (&w)[KC][R]) {
+#pragma unroll
+        for (int c = 0; c < KC; c++) {
+            const int k = c * 1024 + lane * 16;
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                w[c][r] = k < K ? __builtin_nontemporal_load((const v4i_t*)(p.W + (int64_t)row[r] * K + k))
+                                : v4i_t{0, 0, 0, 0};
+        }
+    };
+
+    int g = blockIdx.x * 4 + wid;
     int row[R];
     bool ok[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        int n;
-        if (PAIRED) {
-            const int pi = g * (R / 2) + r / 2;
-            n = (pi / p.half) * 2 * p.half + (pi % p.half) + (r & 1) * p.half;
-        } else {
-            n = g * R + r;
-        }
-        ok[r] = n < N;
-        row[r] = ok[r] ? n : N - 1;
-    }
+    v4i_t w[KC][R];
+    rows_of(g < groups ? g : 0, row, ok);
+    if (g < groups) load_w(row, w);
 
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = 0.f;
+    // Block prologue: xs = x * norm_w (or x), and the RMSNorm scale.
     float ss = 0.f;
-    for (int k = lane * 16; k < K; k += 1024) {
-        v4i_t w[R];
-#pragma unroll
-        for (int r = 0; r < R; r++)
-            w[r] = __builtin_nontemporal_load((const v4i_t*)(p.W + (int64_t)row[r] * K + k));
-        float xv[16];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float4 a = *(const float4*)(p.x + k + 4 * i);
-            xv[4 * i] = a.x; xv[4 * i + 1] = a.y; xv[4 * i + 2] = a.z; xv[4 * i + 3] = a.w;
-        }
+    for (int k = threadIdx.x * 4; k < K; k += 1024) {
+        float4 a = *(const float4*)(p.x + k);
         if (p.norm_w) {
+            ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+            const float4 gw = *(const float4*)(p.norm_w + k);
+            a.x *= gw.x; a.y *= gw.y; a.z *= gw.z; a.w *= gw.w;
+        }
+        *(float4*)&xs[k] = a;
+    }
+    float nscale = 1.f;
+    if (p.norm_w) {
+        ss = wave_sum(ss);
+        if (lane == 0) red[wid] = ss;
+    }
+    __syncthreads();
+    if (p.norm_w) nscale = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + p.eps);
+
+    unsigned long long best = 0ull;
+    while (g < groups) {
+        const int gn = g + waves;
+        int rown[R];
+        bool okn[R];
+        v4i_t wn[KC][R];
+        if (gn < groups) {
+            rows_of(gn, rown, okn);
+            load_w(rown, wn);
+        }
+        float acc[R];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float4 gw = *(const float4*)(p.norm_w + k + 4 * i);
-                ss += xv[4 * i] * xv[4 * i] + xv[4 * i + 1] * xv[4 * i + 1] +
-                      xv[4 * i + 2] * xv[4 * i + 2] + xv[4 * i + 3] * xv[4 * i + 3];
-                xv[4 * i] *= gw.x; xv[4 * i + 1] *= gw.y; xv[4 * i + 2] *= gw.z; xv[4 * i + 3] *= gw.w;
+        for (int r = 0; r < R; r++) acc[r] = 0.f;
+#pragma unroll
+        for (int c = 0; c < KC; c++) {
+            const int k = c * 1024 + lane * 16;
+            if (k < K) {
+                float xv[16];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float4 a = *(const float4*)&xs[k + 4 * i];
+                    xv[4 * i] = a.x; xv[4 * i + 1] = a.y; xv[4 * i + 2] = a.z; xv[4 * i + 3] = a.w;
+                }
+#pragma unroll
+                for (int r = 0; r < R; r++) acc[r] = dot16i8(xv, w[c][r], acc[r]);
             }
         }
 #pragma unroll
-        for (int r = 0; r < R; r++) acc[r] = dot16i8(xv, w[r], acc[r]);
-    }
+        for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
+        float v[R];
 #pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
-    float nscale = 1.f;
-    if (p.norm_w) nscale = 1.0f / sqrtf(wave_sum(ss) / (float)K + p.eps);
+        for (int r = 0; r < R; r++) {
+            v[r] = acc[r] * p.s_w[row[r]] * nscale;
+            if (p.bias) v[r] += p.bias[row[r]];
+        }
 
-    float v[R];
+        if (EPI == EPI_PLAIN || EPI == EPI_RESID || EPI == EPI_LOGITS) {
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        v[r] = acc[r] * p.s_w[row[r]] * nscale;
-        if (p.bias) v[r] += p.bias[row[r]];
-    }
-
-    if (EPI == EPI_PLAIN || EPI == EPI_RESID || EPI == EPI_LOGITS) {
+            for (int r = 0; r < R; r++)
+                if (lane == r && ok[r]) {
+                    if (EPI == EPI_RESID) p.y[row[r]] += v[r];
+                    else p.y[row[r]] = v[r];
+                }
+        }
+        if (EPI == EPI_LOGITS) {
 #pragma unroll
-        for (int r = 0; r < R; r++)
-            if (lane == r && ok[r]) {
-                if (EPI == EPI_RESID) p.y[row[r]] += v[r];
-                else p.y[row[r]] = v[r];
+            for (int r = 0; r < R; r++)
+                if (ok[r]) {
+                    const unsigned long long kk = argmax_key(v[r], row[r]);
+                    best = kk > best ? kk : best;
+                }
+        }
+        if (EPI == EPI_SWIGLU) {
+#pragma unroll
+            for (int j = 0; j < R / 2; j++)
+                if (lane == j && ok[2 * j]) {
+                    const float gg = v[2 * j], u = v[2 * j + 1];
+                    p.y[row[2 * j]] = gg * (1.0f / (1.0f + expf(-gg))) * u;
+                }
+        }
+        if (EPI == EPI_ROPE) {
+            const int pos = p.state[0];
+            const int D = 2 * p.half;
+#pragma unroll
+            for (int j = 0; j < R / 2; j++) {
+                if (lane != j || !ok[2 * j] || pos >= p.max_seq) continue;
+                const int n0 = row[2 * j];
+                const int head = n0 / D, i = n0 % D;
+                const float re = v[2 * j], im = v[2 * j + 1];
+                if (head < p.nq + p.nkv) {
+                    const float c = p.cos_t[(int64_t)pos * p.half + i];
+                    const float sn = p.sin_t[(int64_t)pos * p.half + i];
+                    const float o0 = re * c - im * sn, o1 = re * sn + im * c;
+                    float* dst = head < p.nq
+                                     ? p.q_out + (int64_t)head * D
+                                     : p.kc + ((int64_t)(head - p.nq) * p.max_seq + pos) * D;
+                    dst[i] = o0;
+                    dst[i + p.half] = o1;
+                } else {
+                    float* dst = p.vc + ((int64_t)(head - p.nq - p.nkv) * p.max_seq + pos) * D;
+                    dst[i] = re;
+                    dst[i + p.half] = im;
+                }
             }
+        }
+        if (gn >= groups) break;
+#pragma unroll
+        for (int r = 0; r < R; r++) { row[r] = rown[r]; ok[r] = okn[r]; }
+#pragma unroll
+        for (int c = 0; c < KC; c++)
+#pragma unroll
+            for (int r = 0; r < R; r++) w[c][r] = wn[c][r];
+        g = gn;
     }
     if (EPI == EPI_LOGITS) {
-        unsigned long long best = 0ull;
-#pragma unroll
-        for (int r = 0; r < R; r++)
-            if (ok[r]) {
-                const unsigned long long kk = argmax_key(v[r], row[r]);
-                best = kk > best ? kk : best;
-            }
         __shared__ unsigned long long wbest[4];
-        if (lane == 0) wbest[threadIdx.x >> 6] = best;
+        if (lane == 0) wbest[wid] = best;
         __syncthreads();
         if (threadIdx.x == 0) {
             for (int i = 1; i < 4; i++) best = wbest[i] > best ? wbest[i] : best;
             p.part_keys[blockIdx.x] = best;
         }
     }
-    if (EPI == EPI_SWIGLU) {
-#pragma unroll
-        for (int j = 0; j < R / 2; j++)
-            if (lane == j && ok[2 * j]) {
-                const float gg = v[2 * j], u = v[2 * j + 1];
-                p.y[row[2 * j]] = gg * (1.0f / (1.0f + expf(-gg))) * u;
-            }
-    }
-    if (EPI == EPI_ROPE) {
-        const int pos = p.state[0];
-        if (pos >= p.max_seq) return;
-        const int D = 2 * p.half;
-#pragma unroll
-        for (int j = 0; j < R / 2; j++) {
-            if (lane != j || !ok[2 * j]) continue;
-            const int n0 = row[2 * j];
-            const int head = n0 / D, i = n0 % D;
-            const float re = v[2 * j], im = v[2 * j + 1];
-            if (head < p.nq + p.nkv) {
-                const float c = p.cos_t[(int64_t)pos * p.half + i];
-                const float sn = p.sin_t[(int64_t)pos * p.half + i];
-                const float o0 = re * c - im * sn, o1 = re * sn + im * c;
-                float* dst = head < p.nq ? p.q_out + (int64_t)head * D
-                                         : p.kc + ((int64_t)(head - p.nq) * p.max_seq + pos) * D;
-                dst[i] = o0;
-                dst[i + p.half] = o1;
-            } else {
-                float* dst = p.vc + ((int64_t)(head - p.nq - p.nkv) * p.max_seq + pos) * D;
-                dst[i] = re;
-                dst[i + p.half] = im;
-            }
-        }
-    }
 }
 
 // ------------------------------------------------------------ attention ---
-// Causal GQA decode attention, split over key positions: block (c, h) scores
-// positions [64c, 64c+64) for q head h (4 lanes per key row, 32 dims each),
-// keeps (max, sum, p.V) partials, and the last block of head h to finish --
-// counted with a device-scope atomic after a release fence -- merges the
-// partials in chunk order (so the result does not depend on which block is
-// last) and re-arms the counter for the next layer.
-constexpr int ATT_CHUNK = 64;
+// Causal GQA decode attention. One 1024-thread block per KV head serves its
+// G = nq/nkv query heads over all L = pos+1 cached positions, so every K/V row
+// is read once per step and no block depends on another:
+//   scores  8 threads per key row (16 dims each), G dot products per row;
+//   softmax per query head over the block (max, exp, sum);
+//   values  32 dim-groups (float4) x 32 position-groups, LDS reduction.
+constexpr int ATT_THREADS = 1024, ATT_MAX_G = 4;
 
-__global__ __launch_bounds__(256) void dec_attn_split_kernel(
+__global__ __launch_bounds__(ATT_THREADS) void dec_attn_kernel(
     const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
-    const int32_t* __restrict__ state, float* __restrict__ out, float* __restrict__ part_o,
-    float* __restrict__ part_ml, int* __restrict__ counters, int nq, int nkv, int max_seq,
+    const int32_t* __restrict__ state, float* __restrict__ out, int nq, int nkv, int max_seq,
     float scale) {
     constexpr int D = 128;
-    __shared__ float sc[ATT_CHUNK];
-    __shared__ float po[256];
-    __shared__ float red[2];
-    __shared__ int last;
+    extern __shared__ __attribute__((aligned(16))) float att_lds[];
+    const int G = nq / nkv;
+    float* sc = att_lds;                              // [G][max_seq]
+    float* po = att_lds + G * max_seq;                // [32][G][D]
+    __shared__ float red[ATT_MAX_G][2][16];
     const int pos = state[0];
     if (pos >= max_seq) return;
     const int L = pos + 1;
-    const int nchunks = (L + ATT_CHUNK - 1) / ATT_CHUNK;
-    const int c = blockIdx.x, h = blockIdx.y;
-    if (c >= nchunks) return;
-    const int kvh = h / (nq / nkv);
-    const int t0 = c * ATT_CHUNK;
-    const int n = min(ATT_CHUNK, L - t0);
-    const float* kb = kc + ((int64_t)kvh * max_seq + t0) * D;
-    const float* vb = vc + ((int64_t)kvh * max_seq + t0) * D;
-    const int tid = threadIdx.x;
+    const int kvh = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const float* kb = kc + (int64_t)kvh * max_seq * D;
+    const float* vb = vc + (int64_t)kvh * max_seq * D;
+    const float* qg = q + (int64_t)kvh * G * D;
 
-    // scores: thread (t = tid/4, part = tid%4) covers dims [32*part, 32*part+32)
+    // scores
     {
-        const int t = tid >> 2, part = tid & 3;
-        float dot = 0.f;
-        if (t < n) {
-            const float* qh = q + (int64_t)h * D + part * 32;
-            const float* kr = kb + (int64_t)t * D + part * 32;
+        const int part = tid & 7, sub = tid >> 3;      // 128 rows per pass
+        float qv[ATT_MAX_G][16];
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float4 a = *(const float4*)(qh + 4 * i);
-                const float4 b = *(const float4*)(kr + 4 * i);
-                dot += a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+        for (int h = 0; h < ATT_MAX_G; h++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                if (h >= G) continue;
+                const float4 a = *(const float4*)(qg + h * D + part * 16 + 4 * i);
+                qv[h][4 * i] = a.x; qv[h][4 * i + 1] = a.y; qv[h][4 * i + 2] = a.z; qv[h][4 * i + 3] = a.w;
+            }
+        for (int t = sub; t < ((L + 127) / 128) * 128; t += 128) {
+            float kv[16];
+            if (t < L) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float4 a = *(const float4*)(kb + (int64_t)t * D + part * 16 + 4 * i);
+                    kv[4 * i] = a.x; kv[4 * i + 1] = a.y; kv[4 * i + 2] = a.z; kv[4 * i + 3] = a.w;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; i++) kv[i] = 0.f;
+            }
+#pragma unroll
+            for (int h = 0; h < ATT_MAX_G; h++) {
+                if (h >= G) continue;
+                float d = 0.f;
+#pragma unroll
+                for (int i = 0; i < 16; i++) d += qv[h][i] * kv[i];
+                d += __shfl_xor(d, 1, 64);
+                d += __shfl_xor(d, 2, 64);
+                d += __shfl_xor(d, 4, 64);
+                if (part == 0 && t < L) sc[h * max_seq + t] = d * scale;
             }
         }
-        dot += __shfl_xor(dot, 1, 64);
-        dot += __shfl_xor(dot, 2, 64);
-        if (part == 0 && t < ATT_CHUNK) sc[t] = t < n ? dot * scale : -INFINITY;
     }
     __syncthreads();
-    if (tid < 64) {
-        float m = wave_max(sc[tid]);
-        const float e = tid < n ? expf(sc[tid] - m) : 0.f;
-        sc[tid] = e;
-        const float l = wave_sum(e);
-        if (tid == 0) { red[0] = m; red[1] = l; }
+    // softmax per head: block max, then exp and block sum
+    for (int h = 0; h < G; h++) {
+        float m = -INFINITY;
+        for (int t = tid; t < L; t += ATT_THREADS) m = fmaxf(m, sc[h * max_seq + t]);
+        m = wave_max(m);
+        if (lane == 0) red[h][0][wid] = m;
     }
     __syncthreads();
-    // o[d] = sum_t p[t] v[t][d]: threads split into two t-halves of 32.
-    {
-        const int d = tid & (D - 1), hf = tid >> 7;
-        float o = 0.f;
-        const int tb = hf * 32, te = min(n, tb + 32);
-        for (int t = tb; t < te; t++) o += sc[t] * vb[(int64_t)t * D + d];
-        po[tid] = o;
-    }
-    __syncthreads();
-    if (nchunks == 1) {
-        if (tid < D) out[(int64_t)h * D + tid] = (po[tid] + po[tid + D]) / red[1];
-        return;
-    }
-    const int maxc = (max_seq + ATT_CHUNK - 1) / ATT_CHUNK;
-    if (tid < D) part_o[((int64_t)h * maxc + c) * D + tid] = po[tid] + po[tid + D];
-    if (tid == 0) {
-        part_ml[((int64_t)h * maxc + c) * 2] = red[0];
-        part_ml[((int64_t)h * maxc + c) * 2 + 1] = red[1];
-    }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) last = atomicAdd(&counters[h], 1) == nchunks - 1;
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    if (tid < D) {
-        float M = -INFINITY;
-        for (int i = 0; i < nchunks; i++)
-            M = fmaxf(M, __builtin_nontemporal_load(&part_ml[((int64_t)h * maxc + i) * 2]));
-        float num = 0.f, den = 0.f;
-        for (int i = 0; i < nchunks; i++) {
-            const float f = expf(__builtin_nontemporal_load(&part_ml[((int64_t)h * maxc + i) * 2]) - M);
-            num += f * __builtin_nontemporal_load(&part_o[((int64_t)h * maxc + i) * D + tid]);
-            den += f * __builtin_nontemporal_load(&part_ml[((int64_t)h * maxc + i) * 2 + 1]);
+    for (int h = 0; h < G; h++) {
+        float m = red[h][0][0];
+        for (int i = 1; i < 16; i++) m = fmaxf(m, red[h][0][i]);
+        float l = 0.f;
+        for (int t = tid; t < L; t += ATT_THREADS) {
+            const float e = expf(sc[h * max_seq + t] - m);
+            sc[h * max_seq + t] = e;
+            l += e;
         }
-        out[(int64_t)h * D + tid] = num / den;
+        l = wave_sum(l);
+        if (lane == 0) red[h][1][wid] = l;
     }
-    if (tid == 0) atomicExch(&counters[h], 0);
+    __syncthreads();
+    // values
+    {
+        const int dg = tid & 31, pg = tid >> 5;
+        float4 o[ATT_MAX_G];
+#pragma unroll
+        for (int h = 0; h < ATT_MAX_G; h++) o[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int t = pg; t < L; t += 32) {
+            const float4 vv = *(const float4*)(vb + (int64_t)t * D + 4 * dg);
+#pragma unroll
+            for (int h = 0; h < ATT_MAX_G; h++) {
+                if (h >= G) continue;
+                const float pt = sc[h * max_seq + t];
+                o[h].x += pt * vv.x; o[h].y += pt * vv.y; o[h].z += pt * vv.z; o[h].w += pt * vv.w;
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < ATT_MAX_G; h++)
+            if (h < G) *(float4*)&po[(pg * G + h) * D + 4 * dg] = o[h];
+    }
+    __syncthreads();
+    if (tid < G * D) {
+        const int h = tid / D, d = tid % D;
+        float l = 0.f;
+        for (int i = 0; i < 16; i++) l += red[h][1][i];
+        float o = 0.f;
+        for (int i = 0; i < 32; i++) o += po[(i * G + h) * D + d];
+        out[(int64_t)(kvh * G + h) * D + d] = o / l;
+    }
 }
 
 // Argmax over the lm_head blocks' keys (reference tie rule: first maximum,
@@ -343,18 +412,29 @@ struct Qwen3Dec {
     hipStream_t st = nullptr;
     bool own_stream = false;
     void* block = nullptr;
-    float *x, *q, *attn, *act, *logits, *kc, *vc, *cos_t, *sin_t, *part_o, *part_ml;
-    int32_t *state, *ids, *counters;
+    float *x, *q, *attn, *act, *logits, *kc, *vc, *cos_t, *sin_t;
+    int32_t *state, *ids;
     unsigned long long* part_keys;
-    int lm_blocks = 0, max_chunks = 0;
+    int lm_blocks = 0;
+    size_t att_lds = 0;
     int host_pos = 0;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
 };
 
+// Per-layer GEMVs get one row group per wave (grid covers N); lm_head gets a
+// fixed grid of LM_BLOCKS blocks whose waves stride over the row groups.
+constexpr int LM_BLOCKS = 1024;
+
 template <int EPI, int R>
-static int launch_dec_gemv(const DecGemv& p, int rows_per_block, hipStream_t st) {
-    dec_gemv_kernel<EPI, R><<<ceil_div(p.N, rows_per_block), 256, 0, st>>>(p);
+static int launch_dec_gemv(const DecGemv& p, int blocks, hipStream_t st) {
+    switch ((p.K + 1023) / 1024) {
+    case 1: dec_gemv_kernel<EPI, R, 1><<<blocks, 256, 0, st>>>(p); break;
+    case 2: dec_gemv_kernel<EPI, R, 2><<<blocks, 256, 0, st>>>(p); break;
+    case 3: dec_gemv_kernel<EPI, R, 3><<<blocks, 256, 0, st>>>(p); break;
+    case 4: dec_gemv_kernel<EPI, R, 4><<<blocks, 256, 0, st>>>(p); break;
+    default: return set_error(PIO_ERR_UNSUPPORTED, "decoder GEMV: K=%d > 4096", p.K);
+    }
     PIO_LAUNCHED();
     return PIO_OK;
 }
@@ -384,29 +464,28 @@ static int enqueue_step(Qwen3Dec* d) {
         DecGemv g = base;
         g.x = d->x; g.norm_w = L.in_norm; g.W = L.w_qkv; g.s_w = L.s_qkv; g.bias = L.b_qkv;
         g.N = nqkv; g.K = H; g.half = D / 2; g.q_out = d->q; g.kc = kc; g.vc = vc;
-        PIO_TRY((launch_dec_gemv<EPI_ROPE, 2>(g, 8, st)));
-        dec_attn_split_kernel<<<dim3(d->max_chunks, nq), 256, 0, st>>>(
-            d->q, kc, vc, d->state, d->attn, d->part_o, d->part_ml, d->counters, nq, nkv,
-            c.max_seq, scale);
+        PIO_TRY((launch_dec_gemv<EPI_ROPE, 2>(g, ceil_div(g.N, 8), st)));
+        dec_attn_kernel<<<nkv, ATT_THREADS, d->att_lds, st>>>(d->q, kc, vc, d->state, d->attn, nq,
+                                                              nkv, c.max_seq, scale);
         PIO_LAUNCHED();
         // o_proj: x += W8(attn)
         g = base;
         g.x = d->attn; g.W = L.w_o; g.s_w = L.s_o; g.N = H; g.K = nq * D; g.y = d->x;
-        PIO_TRY((launch_dec_gemv<EPI_RESID, 2>(g, 8, st)));
+        PIO_TRY((launch_dec_gemv<EPI_RESID, 2>(g, ceil_div(g.N, 8), st)));
         // gate_up: rmsnorm(x) -> W8 -> silu(g)*u
         g = base;
         g.x = d->x; g.norm_w = L.post_norm; g.W = L.w_gu; g.s_w = L.s_gu; g.N = 2 * I; g.K = H;
         g.half = I; g.y = d->act;
-        PIO_TRY((launch_dec_gemv<EPI_SWIGLU, 2>(g, 8, st)));
+        PIO_TRY((launch_dec_gemv<EPI_SWIGLU, 2>(g, ceil_div(g.N, 8), st)));
         // down: x += W8(act)
         g = base;
         g.x = d->act; g.W = L.w_down; g.s_w = L.s_down; g.N = H; g.K = I; g.y = d->x;
-        PIO_TRY((launch_dec_gemv<EPI_RESID, 2>(g, 8, st)));
+        PIO_TRY((launch_dec_gemv<EPI_RESID, 2>(g, ceil_div(g.N, 8), st)));
     }
     DecGemv g = base;
     g.x = d->x; g.norm_w = d->final_norm; g.W = d->lm_head; g.s_w = d->s_lm; g.N = c.vocab;
     g.K = H; g.y = d->logits; g.part_keys = d->part_keys;
-    PIO_TRY((launch_dec_gemv<EPI_LOGITS, 4>(g, 16, st)));
+    PIO_TRY((launch_dec_gemv<EPI_LOGITS, 4>(g, d->lm_blocks, st)));
     dec_finish_kernel<<<1, 1024, 0, st>>>(d->state, d->part_keys, d->lm_blocks, d->ids, c.max_seq);
     PIO_LAUNCHED();
     return PIO_OK;
@@ -474,8 +553,16 @@ PIO_EXPORT void* pio_qwen3_create(const pio_qwen3_config* cfg, const float* embe
     const int D = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads;
     const size_t kv = (size_t)c.n_layers * nkv * c.max_seq * D;
     const size_t half = D / 2;
-    d->lm_blocks = ceil_div(c.vocab, 16);
-    d->max_chunks = ceil_div(c.max_seq, ATT_CHUNK);
+    d->lm_blocks = std::min(LM_BLOCKS, ceil_div(c.vocab, 16));
+    // attention LDS: scores [G][max_seq] + value partials [32][G][128], <= 64 KB
+    d->att_lds = (size_t)(nq / nkv) * (c.max_seq + 32 * D) * 4;
+    if (nq / nkv > ATT_MAX_G || d->att_lds > 65536) {
+        set_error(PIO_ERR_UNSUPPORTED, "pio_qwen3_create: %d query heads per KV head and max_seq "
+                  "%d need %zu B of attention LDS (limits: %d heads, 65536 B)", nq / nkv,
+                  c.max_seq, d->att_lds, ATT_MAX_G);
+        destroy(d);
+        return nullptr;
+    }
     size_t sizes[] = {
         al256((size_t)c.hidden * 4),                      // x
         al256((size_t)nq * D * 4),                        // q
@@ -484,11 +571,8 @@ PIO_EXPORT void* pio_qwen3_create(const pio_qwen3_config* cfg, const float* embe
         al256((size_t)c.vocab * 4),                       // logits
         al256(kv * 4), al256(kv * 4),                     // k, v cache
         al256(c.max_seq * half * 4), al256(c.max_seq * half * 4),   // cos, sin
-        al256((size_t)nq * d->max_chunks * D * 4),        // attention partial o
-        al256((size_t)nq * d->max_chunks * 2 * 4),        // attention partial (max, sum)
         al256(16 * 4),                                    // state
         al256((size_t)(c.max_seq + 1) * 4),               // ids
-        al256((size_t)nq * 4),                            // attention counters
         al256((size_t)d->lm_blocks * 8)};                 // argmax partial keys
     size_t total = 0;
     for (size_t sz : sizes) total += sz;
@@ -508,12 +592,9 @@ PIO_EXPORT void* pio_qwen3_create(const pio_qwen3_config* cfg, const float* embe
     d->vc = (float*)take(6);
     d->cos_t = (float*)take(7);
     d->sin_t = (float*)take(8);
-    d->part_o = (float*)take(9);
-    d->part_ml = (float*)take(10);
-    d->state = (int32_t*)take(11);
-    d->ids = (int32_t*)take(12);
-    d->counters = (int32_t*)take(13);
-    d->part_keys = (unsigned long long*)take(14);
+    d->state = (int32_t*)take(9);
+    d->ids = (int32_t*)take(10);
+    d->part_keys = (unsigned long long*)take(11);
     // RoPE table: angle(pos, j) = pos * theta^(-2j/D), computed in double.
     std::vector<float> ct((size_t)c.max_seq * half), stt((size_t)c.max_seq * half);
     for (int pos = 0; pos < c.max_seq; pos++)
@@ -526,9 +607,6 @@ PIO_EXPORT void* pio_qwen3_create(const pio_qwen3_config* cfg, const float* embe
     hipError_t e = hipMemcpyAsync(d->cos_t, ct.data(), ct.size() * 4, hipMemcpyHostToDevice, d->st);
     if (e == hipSuccess)
         e = hipMemcpyAsync(d->sin_t, stt.data(), stt.size() * 4, hipMemcpyHostToDevice, d->st);
-    std::vector<int32_t> zeros((size_t)nq + 16, 0);
-    if (e == hipSuccess)
-        e = hipMemcpyAsync(d->counters, zeros.data(), (size_t)nq * 4, hipMemcpyHostToDevice, d->st);
     if (e == hipSuccess) e = hipStreamSynchronize(d->st);
     if (e != hipSuccess) {
         set_error(PIO_ERR_HIP, "pio_qwen3_create: table upload failed: %s", hipGetErrorString(e));
@@ -555,10 +633,6 @@ PIO_EXPORT int pio_qwen3_reset(void* h, const int32_t* ids, int prompt_len) {
     st[1] = prompt_len;
     PIO_HIP(hipMemcpyAsync(d->ids, ids, (size_t)prompt_len * 4, hipMemcpyHostToDevice, d->st));
     PIO_HIP(hipMemcpyAsync(d->state, st.data(), 16 * 4, hipMemcpyHostToDevice, d->st));
-    // Re-arm the attention merge counters (only an interrupted step leaves them set).
-    std::vector<int32_t> zeros((size_t)d->c.n_heads, 0);
-    PIO_HIP(hipMemcpyAsync(d->counters, zeros.data(), zeros.size() * 4, hipMemcpyHostToDevice,
-                           d->st));
     PIO_HIP(hipStreamSynchronize(d->st));
     d->host_pos = 0;
     return PIO_OK;

@@ -68,6 +68,10 @@ struct DecGemv {
     float* vc;
     int nq, nkv, max_seq;
     unsigned long long* part_keys;
+    // o_proj prologue: merge the attention splits into x (x must be nullptr)
+    const float* att_o;    // [S][nq*D] unnormalized sum_t p v per split
+    const float* att_ml;   // [S][nq][2] (max, sum) per split
+    int att_splits;
 };
 
 typedef int v4i_t __attribute__((ext_vector_type(4)));
@@ -137,10 +141,30 @@ __global__ __launch_bounds__(256) void dec_gemv_kernel(DecGemv p) {
     rows_of(g < groups ? g : 0, row, ok);
     if (g < groups) load_w(row, w);
 
-    // Block prologue: xs = x * norm_w (or x), and the RMSNorm scale.
+    // Block prologue: xs = x * norm_w (or x, or the merged attention output),
+    // and the RMSNorm scale.
     float ss = 0.f;
     for (int k = threadIdx.x * 4; k < K; k += 1024) {
-        float4 a = *(const float4*)(p.x + k);
+        float4 a;
+        if (p.att_o) {
+            // softmax-merge of the splits for q head k/128, in split order
+            const int h = k >> 7, S = p.att_splits, nh = K >> 7;
+            float M = -INFINITY;
+            for (int i = 0; i < S; i++) M = fmaxf(M, p.att_ml[(i * nh + h) * 2]);
+            float den = 0.f;
+            a = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int i = 0; i < S; i++) {
+                const float m = p.att_ml[(i * nh + h) * 2];
+                const float f = m == -INFINITY ? 0.f : expf(m - M);
+                den += f * p.att_ml[(i * nh + h) * 2 + 1];
+                const float4 o = *(const float4*)(p.att_o + (int64_t)i * K + k);
+                a.x += f * o.x; a.y += f * o.y; a.z += f * o.z; a.w += f * o.w;
+            }
+            const float inv = 1.0f / den;
+            a.x *= inv; a.y *= inv; a.z *= inv; a.w *= inv;
+        } else {
+            a = *(const float4*)(p.x + k);
+        }
         if (p.norm_w) {
             ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
             const float4 gw = *(const float4*)(p.norm_w + k);
@@ -262,35 +286,48 @@ __global__ __launch_bounds__(256) void dec_gemv_kernel(DecGemv p) {
 }
 
 // ------------------------------------------------------------ attention ---
-// Causal GQA decode attention. One 1024-thread block per KV head serves its
-// G = nq/nkv query heads over all L = pos+1 cached positions, so every K/V row
-// is read once per step and no block depends on another:
-//   scores  8 threads per key row (16 dims each), G dot products per row;
-//   softmax per query head over the block (max, exp, sum);
-//   values  32 dim-groups (float4) x 32 position-groups, LDS reduction.
-constexpr int ATT_THREADS = 1024, ATT_MAX_G = 4;
+// Causal GQA decode attention, split ATT_SPLITS ways over the L = pos+1 cached
+// positions: block (s, kv head) takes positions [s*c, s*c + c), c = ceil(L/S),
+// for the G = nq/nkv query heads sharing that KV head (each K/V row is read
+// once per step), and writes unnormalized partials (sum_t p v, max, sum).
+// The o_proj GEMV that consumes them merges the splits in split order in its
+// block prologue, so no block waits on another and no cache flush is needed.
+//   scores  8 threads per key row (16 dims each), 32 rows per pass;
+//   values  32 dim-groups (float4) x 8 position-groups, LDS reduction.
+constexpr int ATT_SPLITS = 8, ATT_MAX_G = 4;
 
-__global__ __launch_bounds__(ATT_THREADS) void dec_attn_kernel(
+__global__ __launch_bounds__(256) void dec_attn_kernel(
     const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
-    const int32_t* __restrict__ state, float* __restrict__ out, int nq, int nkv, int max_seq,
-    float scale) {
+    const int32_t* __restrict__ state, float* __restrict__ att_o, float* __restrict__ att_ml,
+    int nq, int nkv, int max_seq, float scale) {
     constexpr int D = 128;
     extern __shared__ __attribute__((aligned(16))) float att_lds[];
     const int G = nq / nkv;
-    float* sc = att_lds;                              // [G][max_seq]
-    float* po = att_lds + G * max_seq;                // [32][G][D]
-    __shared__ float red[ATT_MAX_G][2][16];
+    const int cmax = (max_seq + ATT_SPLITS - 1) / ATT_SPLITS;
+    float* sc = att_lds;                              // [G][cmax]
+    float* po = att_lds + G * cmax;                   // [8][G][D]
+    __shared__ float red[ATT_MAX_G][2][4];
     const int pos = state[0];
     if (pos >= max_seq) return;
     const int L = pos + 1;
-    const int kvh = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const float* kb = kc + (int64_t)kvh * max_seq * D;
-    const float* vb = vc + (int64_t)kvh * max_seq * D;
+    const int s = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int c = (L + ATT_SPLITS - 1) / ATT_SPLITS;
+    const int t0 = s * c, n = min(c, L - t0);
+    if (n <= 0) {
+        // empty split: contributes exp(-inf) = 0 to the merge
+        if (tid < G * D) att_o[(int64_t)s * nq * D + (int64_t)kvh * G * D + tid] = 0.f;
+        if (tid < G) {
+            att_ml[((int64_t)s * nq + kvh * G + tid) * 2] = -INFINITY;
+            att_ml[((int64_t)s * nq + kvh * G + tid) * 2 + 1] = 0.f;
+        }
+        return;
+    }
+    const float* kb = kc + ((int64_t)kvh * max_seq + t0) * D;
+    const float* vb = vc + ((int64_t)kvh * max_seq + t0) * D;
     const float* qg = q + (int64_t)kvh * G * D;
 
-    // scores
     {
-        const int part = tid & 7, sub = tid >> 3;      // 128 rows per pass
+        const int part = tid & 7, sub = tid >> 3;
         float qv[ATT_MAX_G][16];
 #pragma unroll
         for (int h = 0; h < ATT_MAX_G; h++)
@@ -300,66 +337,77 @@ __global__ __launch_bounds__(ATT_THREADS) void dec_attn_kernel(
                 const float4 a = *(const float4*)(qg + h * D + part * 16 + 4 * i);
                 qv[h][4 * i] = a.x; qv[h][4 * i + 1] = a.y; qv[h][4 * i + 2] = a.z; qv[h][4 * i + 3] = a.w;
             }
-        for (int t = sub; t < ((L + 127) / 128) * 128; t += 128) {
-            float kv[16];
-            if (t < L) {
+        for (int tb = 0; tb < n; tb += 64) {
+            float kv[2][16];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int t = tb + sub + 32 * u;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const float4 a = *(const float4*)(kb + (int64_t)t * D + part * 16 + 4 * i);
-                    kv[4 * i] = a.x; kv[4 * i + 1] = a.y; kv[4 * i + 2] = a.z; kv[4 * i + 3] = a.w;
+                    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (t < n) a = *(const float4*)(kb + (int64_t)t * D + part * 16 + 4 * i);
+                    kv[u][4 * i] = a.x; kv[u][4 * i + 1] = a.y; kv[u][4 * i + 2] = a.z; kv[u][4 * i + 3] = a.w;
                 }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 16; i++) kv[i] = 0.f;
             }
 #pragma unroll
-            for (int h = 0; h < ATT_MAX_G; h++) {
-                if (h >= G) continue;
-                float d = 0.f;
+            for (int u = 0; u < 2; u++) {
+                const int t = tb + sub + 32 * u;
 #pragma unroll
-                for (int i = 0; i < 16; i++) d += qv[h][i] * kv[i];
-                d += __shfl_xor(d, 1, 64);
-                d += __shfl_xor(d, 2, 64);
-                d += __shfl_xor(d, 4, 64);
-                if (part == 0 && t < L) sc[h * max_seq + t] = d * scale;
+                for (int h = 0; h < ATT_MAX_G; h++) {
+                    if (h >= G) continue;
+                    float d = 0.f;
+#pragma unroll
+                    for (int i = 0; i < 16; i++) d += qv[h][i] * kv[u][i];
+                    d += __shfl_xor(d, 1, 64);
+                    d += __shfl_xor(d, 2, 64);
+                    d += __shfl_xor(d, 4, 64);
+                    if (part == 0 && t < n) sc[h * cmax + t] = d * scale;
+                }
             }
         }
     }
     __syncthreads();
-    // softmax per head: block max, then exp and block sum
     for (int h = 0; h < G; h++) {
         float m = -INFINITY;
-        for (int t = tid; t < L; t += ATT_THREADS) m = fmaxf(m, sc[h * max_seq + t]);
+        for (int t = tid; t < n; t += 256) m = fmaxf(m, sc[h * cmax + t]);
         m = wave_max(m);
         if (lane == 0) red[h][0][wid] = m;
     }
     __syncthreads();
     for (int h = 0; h < G; h++) {
-        float m = red[h][0][0];
-        for (int i = 1; i < 16; i++) m = fmaxf(m, red[h][0][i]);
+        const float m = fmaxf(fmaxf(red[h][0][0], red[h][0][1]), fmaxf(red[h][0][2], red[h][0][3]));
         float l = 0.f;
-        for (int t = tid; t < L; t += ATT_THREADS) {
-            const float e = expf(sc[h * max_seq + t] - m);
-            sc[h * max_seq + t] = e;
+        for (int t = tid; t < n; t += 256) {
+            const float e = expf(sc[h * cmax + t] - m);
+            sc[h * cmax + t] = e;
             l += e;
         }
         l = wave_sum(l);
         if (lane == 0) red[h][1][wid] = l;
     }
     __syncthreads();
-    // values
     {
         const int dg = tid & 31, pg = tid >> 5;
         float4 o[ATT_MAX_G];
 #pragma unroll
         for (int h = 0; h < ATT_MAX_G; h++) o[h] = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int t = pg; t < L; t += 32) {
-            const float4 vv = *(const float4*)(vb + (int64_t)t * D + 4 * dg);
+        for (int tb = pg; tb < n; tb += 32) {
+            float4 vv[4];
 #pragma unroll
-            for (int h = 0; h < ATT_MAX_G; h++) {
-                if (h >= G) continue;
-                const float pt = sc[h * max_seq + t];
-                o[h].x += pt * vv.x; o[h].y += pt * vv.y; o[h].z += pt * vv.z; o[h].w += pt * vv.w;
+            for (int u = 0; u < 4; u++) {
+                const int t = tb + 8 * u;
+                vv[u] = t < n ? *(const float4*)(vb + (int64_t)t * D + 4 * dg) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int t = tb + 8 * u;
+                if (t >= n) continue;
+#pragma unroll
+                for (int h = 0; h < ATT_MAX_G; h++) {
+                    if (h >= G) continue;
+                    const float pt = sc[h * cmax + t];
+                    o[h].x += pt * vv[u].x; o[h].y += pt * vv[u].y; o[h].z += pt * vv[u].z; o[h].w += pt * vv[u].w;
+                }
             }
         }
 #pragma unroll
@@ -369,11 +417,16 @@ __global__ __launch_bounds__(ATT_THREADS) void dec_attn_kernel(
     __syncthreads();
     if (tid < G * D) {
         const int h = tid / D, d = tid % D;
-        float l = 0.f;
-        for (int i = 0; i < 16; i++) l += red[h][1][i];
         float o = 0.f;
-        for (int i = 0; i < 32; i++) o += po[(i * G + h) * D + d];
-        out[(int64_t)(kvh * G + h) * D + d] = o / l;
+#pragma unroll
+        for (int i = 0; i < 8; i++) o += po[(i * G + h) * D + d];
+        att_o[(int64_t)s * nq * D + (int64_t)(kvh * G + h) * D + d] = o;
+    }
+    if (tid < G) {
+        att_ml[((int64_t)s * nq + kvh * G + tid) * 2] =
+            fmaxf(fmaxf(red[tid][0][0], red[tid][0][1]), fmaxf(red[tid][0][2], red[tid][0][3]));
+        att_ml[((int64_t)s * nq + kvh * G + tid) * 2 + 1] =
+            red[tid][1][0] + red[tid][1][1] + red[tid][1][2] + red[tid][1][3];
     }
 }
 
@@ -412,7 +465,7 @@ struct Qwen3Dec {
     hipStream_t st = nullptr;
     bool own_stream = false;
     void* block = nullptr;
-    float *x, *q, *attn, *act, *logits, *kc, *vc, *cos_t, *sin_t;
+    float *x, *q, *att_o, *att_ml, *act, *logits, *kc, *vc, *cos_t, *sin_t;
     int32_t *state, *ids;
     unsigned long long* part_keys;
     int lm_blocks = 0;
@@ -422,9 +475,8 @@ struct Qwen3Dec {
     hipGraphExec_t exec = nullptr;
 };
 
-// Per-layer GEMVs get one row group per wave (grid covers N); lm_head gets a
-// fixed grid of LM_BLOCKS blocks whose waves stride over the row groups.
-constexpr int LM_BLOCKS = 1024;
+// Every launch gives each wave one row group (grid covers N); the kernel also
+// supports fewer blocks, whose waves then stride over the row groups.
 
 template <int EPI, int R>
 static int launch_dec_gemv(const DecGemv& p, int blocks, hipStream_t st) {
@@ -465,13 +517,14 @@ static int enqueue_step(Qwen3Dec* d) {
         g.x = d->x; g.norm_w = L.in_norm; g.W = L.w_qkv; g.s_w = L.s_qkv; g.bias = L.b_qkv;
         g.N = nqkv; g.K = H; g.half = D / 2; g.q_out = d->q; g.kc = kc; g.vc = vc;
         PIO_TRY((launch_dec_gemv<EPI_ROPE, 2>(g, ceil_div(g.N, 8), st)));
-        dec_attn_kernel<<<nkv, ATT_THREADS, d->att_lds, st>>>(d->q, kc, vc, d->state, d->attn, nq,
-                                                              nkv, c.max_seq, scale);
+        dec_attn_kernel<<<dim3(ATT_SPLITS, nkv), 256, d->att_lds, st>>>(
+            d->q, kc, vc, d->state, d->att_o, d->att_ml, nq, nkv, c.max_seq, scale);
         PIO_LAUNCHED();
         // o_proj: x += W8(attn)
         g = base;
-        g.x = d->attn; g.W = L.w_o; g.s_w = L.s_o; g.N = H; g.K = nq * D; g.y = d->x;
-        PIO_TRY((launch_dec_gemv<EPI_RESID, 2>(g, ceil_div(g.N, 8), st)));
+        g.att_o = d->att_o; g.att_ml = d->att_ml; g.att_splits = ATT_SPLITS;
+        g.W = L.w_o; g.s_w = L.s_o; g.N = H; g.K = nq * D; g.y = d->x;
+        PIO_TRY((launch_dec_gemv<EPI_RESID, 1>(g, ceil_div(g.N, 4), st)));
         // gate_up: rmsnorm(x) -> W8 -> silu(g)*u
         g = base;
         g.x = d->x; g.norm_w = L.post_norm; g.W = L.w_gu; g.s_w = L.s_gu; g.N = 2 * I; g.K = H;
@@ -480,7 +533,7 @@ static int enqueue_step(Qwen3Dec* d) {
         // down: x += W8(act)
         g = base;
         g.x = d->act; g.W = L.w_down; g.s_w = L.s_down; g.N = H; g.K = I; g.y = d->x;
-        PIO_TRY((launch_dec_gemv<EPI_RESID, 2>(g, ceil_div(g.N, 8), st)));
+        PIO_TRY((launch_dec_gemv<EPI_RESID, 1>(g, ceil_div(g.N, 4), st)));
     }
     DecGemv g = base;
     g.x = d->x; g.norm_w = d->final_norm; g.W = d->lm_head; g.s_w = d->s_lm; g.N = c.vocab;
@@ -553,9 +606,9 @@ PIO_EXPORT void* pio_qwen3_create(const pio_qwen3_config* cfg, const float* embe
     const int D = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads;
     const size_t kv = (size_t)c.n_layers * nkv * c.max_seq * D;
     const size_t half = D / 2;
-    d->lm_blocks = std::min(LM_BLOCKS, ceil_div(c.vocab, 16));
-    // attention LDS: scores [G][max_seq] + value partials [32][G][128], <= 64 KB
-    d->att_lds = (size_t)(nq / nkv) * (c.max_seq + 32 * D) * 4;
+    d->lm_blocks = ceil_div(c.vocab, 16);
+    // attention LDS: scores [G][ceil(max_seq/S)] + value partials [8][G][128], <= 64 KB
+    d->att_lds = (size_t)(nq / nkv) * (ceil_div(c.max_seq, ATT_SPLITS) + 8 * D) * 4;
     if (nq / nkv > ATT_MAX_G || d->att_lds > 65536) {
         set_error(PIO_ERR_UNSUPPORTED, "pio_qwen3_create: %d query heads per KV head and max_seq "
                   "%d need %zu B of attention LDS (limits: %d heads, 65536 B)", nq / nkv,
@@ -566,7 +619,8 @@ PIO_EXPORT void* pio_qwen3_create(const pio_qwen3_config* cfg, const float* embe
     size_t sizes[] = {
         al256((size_t)c.hidden * 4),                      // x
         al256((size_t)nq * D * 4),                        // q
-        al256((size_t)nq * D * 4),                        // attn
+        al256((size_t)ATT_SPLITS * nq * D * 4),           // attention partial o
+        al256((size_t)ATT_SPLITS * nq * 2 * 4),           // attention partial (max, sum)
         al256((size_t)c.intermediate * 4),                // act
         al256((size_t)c.vocab * 4),                       // logits
         al256(kv * 4), al256(kv * 4),                     // k, v cache
@@ -585,16 +639,17 @@ PIO_EXPORT void* pio_qwen3_create(const pio_qwen3_config* cfg, const float* embe
     auto take = [&](int i) { char* r = p + o; o += sizes[i]; return r; };
     d->x = (float*)take(0);
     d->q = (float*)take(1);
-    d->attn = (float*)take(2);
-    d->act = (float*)take(3);
-    d->logits = (float*)take(4);
-    d->kc = (float*)take(5);
-    d->vc = (float*)take(6);
-    d->cos_t = (float*)take(7);
-    d->sin_t = (float*)take(8);
-    d->state = (int32_t*)take(9);
-    d->ids = (int32_t*)take(10);
-    d->part_keys = (unsigned long long*)take(11);
+    d->att_o = (float*)take(2);
+    d->att_ml = (float*)take(3);
+    d->act = (float*)take(4);
+    d->logits = (float*)take(5);
+    d->kc = (float*)take(6);
+    d->vc = (float*)take(7);
+    d->cos_t = (float*)take(8);
+    d->sin_t = (float*)take(9);
+    d->state = (int32_t*)take(10);
+    d->ids = (int32_t*)take(11);
+    d->part_keys = (unsigned long long*)take(12);
     // RoPE table: angle(pos, j) = pos * theta^(-2j/D), computed in double.
     std::vector<float> ct((size_t)c.max_seq * half), stt((size_t)c.max_seq * half);
     for (int pos = 0; pos < c.max_seq; pos++)

@@ -24,6 +24,7 @@
 namespace pio {
 
 constexpr int DEC_MAX_SEQ = 8192;
+constexpr int ATT_SPLITS = 8;   // attention splits over key positions
 
 // x = embed[ids[pos]] (an out-of-range id reads row 0, as tensor_embed,
 // tensor_ops.c:663-671).
@@ -71,7 +72,6 @@ struct DecGemv {
     // o_proj prologue: merge the attention splits into x (x must be nullptr)
     const float* att_o;    // [S][nq*D] unnormalized sum_t p v per split
     const float* att_ml;   // [S][nq][2] (max, sum) per split
-    int att_splits;
 };
 
 typedef int v4i_t __attribute__((ext_vector_type(4)));
@@ -147,18 +147,27 @@ __global__ __launch_bounds__(256) void dec_gemv_kernel(DecGemv p) {
     for (int k = threadIdx.x * 4; k < K; k += 1024) {
         float4 a;
         if (p.att_o) {
-            // softmax-merge of the splits for q head k/128, in split order
-            const int h = k >> 7, S = p.att_splits, nh = K >> 7;
-            float M = -INFINITY;
-            for (int i = 0; i < S; i++) M = fmaxf(M, p.att_ml[(i * nh + h) * 2]);
+            // softmax-merge of the splits for q head k/128, in split order; all
+            // split loads are issued before any is used.
+            const int h = k >> 7, nh = K >> 7;
+            float m[ATT_SPLITS], l[ATT_SPLITS];
+            float4 o[ATT_SPLITS];
+#pragma unroll
+            for (int i = 0; i < ATT_SPLITS; i++) {
+                m[i] = p.att_ml[(i * nh + h) * 2];
+                l[i] = p.att_ml[(i * nh + h) * 2 + 1];
+                o[i] = *(const float4*)(p.att_o + (int64_t)i * K + k);
+            }
+            float M = m[0];
+#pragma unroll
+            for (int i = 1; i < ATT_SPLITS; i++) M = fmaxf(M, m[i]);
             float den = 0.f;
             a = make_float4(0.f, 0.f, 0.f, 0.f);
-            for (int i = 0; i < S; i++) {
-                const float m = p.att_ml[(i * nh + h) * 2];
-                const float f = m == -INFINITY ? 0.f : expf(m - M);
-                den += f * p.att_ml[(i * nh + h) * 2 + 1];
-                const float4 o = *(const float4*)(p.att_o + (int64_t)i * K + k);
-                a.x += f * o.x; a.y += f * o.y; a.z += f * o.z; a.w += f * o.w;
+#pragma unroll
+            for (int i = 0; i < ATT_SPLITS; i++) {
+                const float f = m[i] == -INFINITY ? 0.f : expf(m[i] - M);
+                den += f * l[i];
+                a.x += f * o[i].x; a.y += f * o[i].y; a.z += f * o[i].z; a.w += f * o[i].w;
             }
             const float inv = 1.0f / den;
             a.x *= inv; a.y *= inv; a.z *= inv; a.w *= inv;
@@ -294,7 +303,7 @@ __global__ __launch_bounds__(256) void dec_gemv_kernel(DecGemv p) {
 // block prologue, so no block waits on another and no cache flush is needed.
 //   scores  8 threads per key row (16 dims each), 32 rows per pass;
 //   values  32 dim-groups (float4) x 8 position-groups, LDS reduction.
-constexpr int ATT_SPLITS = 8, ATT_MAX_G = 4;
+constexpr int ATT_MAX_G = 4;
 
 __global__ __launch_bounds__(256) void dec_attn_kernel(
     const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
@@ -522,7 +531,7 @@ static int enqueue_step(Qwen3Dec* d) {
         PIO_LAUNCHED();
         // o_proj: x += W8(attn)
         g = base;
-        g.att_o = d->att_o; g.att_ml = d->att_ml; g.att_splits = ATT_SPLITS;
+        g.att_o = d->att_o; g.att_ml = d->att_ml;
         g.W = L.w_o; g.s_w = L.s_o; g.N = H; g.K = nq * D; g.y = d->x;
         PIO_TRY((launch_dec_gemv<EPI_RESID, 1>(g, ceil_div(g.N, 4), st)));
         // gate_up: rmsnorm(x) -> W8 -> silu(g)*u

@@ -18,6 +18,8 @@
 // lane l holds D[4*(l/16) + v][l % 16], v = 0..3.
 #include "gemm_core.hpp"
 
+#include <stdlib.h>
+
 namespace pio {
 
 enum { OUT_F32 = 0, OUT_F16 = 1, OUT_I32 = 2, OUT_F32_RAW = 3 };
@@ -85,6 +87,162 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_kernel(GemmParams p) {
     }
 }
 
+// ----------------------------------------------------------------- v2 ---
+// Dense W8A8 on the 32x32x32 engine. Block b is mapped XCD-aware: the
+// dispatcher places block b on XCD b % 8, so tile t = (b % 8) * T/8 + b / 8
+// gives each XCD a contiguous run of T/8 row-major tiles whose A and B rows
+// stay in that XCD's L2 (identity map when T % 8 != 0).
+// STAGES == 0: register-staged v2 engine (any K % 16 == 0); otherwise the
+// direct-to-LDS v3 engine with that many stages (K % 128 == 0).
+template <int WMT, int WNT, int OUT, int STAGES>
+__global__ __launch_bounds__(256, 1) void gemm_v2_kernel(GemmParams p, int tiles_n) {
+    using T = TileV2<WMT, WNT>;
+    extern __shared__ __attribute__((aligned(16))) int8_t lds_v2[];
+    const int tiles = gridDim.x;
+    const int b = blockIdx.x;
+    const int t = (tiles % 8 == 0) ? (b % 8) * (tiles / 8) + b / 8 : b;
+    const int m0 = (t / tiles_n) * T::BM, n0 = (t % tiles_n) * T::BN, z = blockIdx.z;
+    constexpr bool SCALED = (OUT == OUT_F32 || OUT == OUT_F16);
+    // Interior tiles (the common case) take a branch-free epilogue: with no
+    // per-element bounds checks the stores issue back to back, while a
+    // bounds-checked store sequence makes the compiler wait for every earlier
+    // store (gfx9 counts stores in vmcnt). Epilogue operands are loaded before
+    // the main loop so their latency hides behind it.
+    const bool full = (m0 + T::BM <= p.M) && (n0 + T::BN <= p.N);
+    float sa[WMT][16], sw[WNT], bn[WNT];
+    if (SCALED) {
+#pragma unroll
+        for (int i = 0; i < WMT; i++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) sa[i][e] = p.s_a[min(m0 + v2_row<WMT>(i, e), p.M - 1)];
+#pragma unroll
+        for (int j = 0; j < WNT; j++) {
+            const int n = min(n0 + v2_col<WNT>(j), p.N - 1);
+            sw[j] = p.s_w[n];
+            bn[j] = p.bias ? p.bias[n] : 0.f;
+        }
+    }
+    v16i acc[WMT][WNT];
+    if (STAGES == 0)
+        mma_tile_v2<WMT, WNT>(p.A + z * p.a_batch + (int64_t)m0 * p.lda, p.lda, p.M - m0,
+                              p.B + z * p.b_batch + (int64_t)n0 * p.ldb, p.ldb, p.N - n0, p.K,
+                              lds_v2, acc);
+    else
+        mma_tile_v3<WMT, WNT, (STAGES > 0 ? STAGES : 2)>(
+            p.A + z * p.a_batch + (int64_t)m0 * p.lda, p.lda, p.M - m0,
+            p.B + z * p.b_batch + (int64_t)n0 * p.ldb, p.ldb, p.N - n0, p.K, lds_v2, acc);
+    char* C = (char*)p.C + z * p.c_batch * (OUT == OUT_F16 ? 2 : 4);
+    auto store = [&](int i, int j, int e, int m, int n) {
+        const int64_t off = (int64_t)m * p.ldc + n;
+        const int a = acc[i][j][e];
+        if (OUT == OUT_I32) {
+            ((int32_t*)C)[off] = a;
+        } else if (OUT == OUT_F32_RAW) {
+            ((float*)C)[off] = (float)a;
+        } else {
+            float val = (float)a * sa[i][e] * sw[j];
+            if (p.bias) val += bn[j];
+            if (OUT == OUT_F32) ((float*)C)[off] = val;
+            else ((_Float16*)C)[off] = (_Float16)val;
+        }
+    };
+    if (full) {
+#pragma unroll
+        for (int j = 0; j < WNT; j++)
+#pragma unroll
+            for (int i = 0; i < WMT; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++)
+                    store(i, j, e, m0 + v2_row<WMT>(i, e), n0 + v2_col<WNT>(j));
+    } else {
+#pragma unroll
+        for (int j = 0; j < WNT; j++) {
+            const int n = n0 + v2_col<WNT>(j);
+            if (n >= p.N) continue;
+#pragma unroll
+            for (int i = 0; i < WMT; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int m = m0 + v2_row<WMT>(i, e);
+                    if (m < p.M) store(i, j, e, m, n);
+                }
+        }
+    }
+}
+
+// Raises a kernel's dynamic-LDS limit once (tiles above 64 KB of LDS).
+template <typename F>
+static int allow_lds(F* kernel, size_t bytes) {
+    static bool done = false;   // one flag per kernel instantiation
+    if (!done && bytes > 65536) {
+        PIO_HIP(hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)bytes));
+        done = true;
+    }
+    return PIO_OK;
+}
+
+// LDS stages of the v3 engine per tile shape: as many as fit in 144 KB.
+template <int WMT, int WNT>
+constexpr int v3_stages() {
+    return (144 * 1024) / ((64 * WMT + 64 * WNT) * 128) >= 4 ? 4 : 3;
+}
+
+template <int WMT, int WNT, int OUT, int STAGES>
+static int launch_v2_out(const GemmParams& p, dim3 grid, int tn, hipStream_t st) {
+    constexpr size_t lds = STAGES == 0 ? (size_t)TileV2<WMT, WNT>::LDS_BYTES
+                                       : (size_t)TileV3<WMT, WNT, (STAGES ? STAGES : 2)>::LDS_BYTES;
+    PIO_TRY(allow_lds(gemm_v2_kernel<WMT, WNT, OUT, STAGES>, lds));
+    gemm_v2_kernel<WMT, WNT, OUT, STAGES><<<grid, 256, lds, st>>>(p, tn);
+    PIO_LAUNCHED();
+    return PIO_OK;
+}
+
+template <int WMT, int WNT, int STAGES>
+static int launch_v2_s(const GemmParams& p, int out_mode, dim3 grid, int tn, hipStream_t st) {
+    switch (out_mode) {
+    case OUT_F32: return launch_v2_out<WMT, WNT, OUT_F32, STAGES>(p, grid, tn, st);
+    case OUT_F16: return launch_v2_out<WMT, WNT, OUT_F16, STAGES>(p, grid, tn, st);
+    case OUT_I32: return launch_v2_out<WMT, WNT, OUT_I32, STAGES>(p, grid, tn, st);
+    case OUT_F32_RAW: return launch_v2_out<WMT, WNT, OUT_F32_RAW, STAGES>(p, grid, tn, st);
+    default: return set_error(PIO_ERR_INVALID, "gemm: bad output mode");
+    }
+}
+
+template <int WMT, int WNT>
+static int launch_v2(const GemmParams& p, int out_mode, int batch, hipStream_t st) {
+    using T = TileV2<WMT, WNT>;
+    const int tn = ceil_div(p.N, T::BN), tm = ceil_div(p.M, T::BM);
+    dim3 grid(tm * tn, 1, batch);
+    const bool direct = (p.K % 128 == 0) && aligned16(p.A) && aligned16(p.B) &&
+                        p.lda % 16 == 0 && p.ldb % 16 == 0 && !getenv("PIO_GEMM_NO_DIRECT");
+    if (direct) return launch_v2_s<WMT, WNT, v3_stages<WMT, WNT>()>(p, out_mode, grid, tn, st);
+    return launch_v2_s<WMT, WNT, 0>(p, out_mode, grid, tn, st);
+}
+
+// Picks the block tile whose tile count best fills whole waves of 256 CUs
+// (ties go to the larger tile), among BM = 128 and BN in {64, 128, 192, 256}.
+static int launch_dense(const GemmParams& p, int out_mode, int batch, hipStream_t st) {
+    static const int cfg[][2] = {{2, 4}, {2, 3}, {2, 2}, {2, 1}};
+    int best = 0;
+    double best_eff = -1.0;
+    // PIO_GEMM_TILE=<0..3> pins the tile shape (tuning experiments only).
+    static const char* force = getenv("PIO_GEMM_TILE");
+    if (force) best_eff = 2.0, best = atoi(force) & 3;
+    for (int i = 0; i < 4; i++) {
+        const int64_t tiles = (int64_t)ceil_div(p.M, 64 * cfg[i][0]) * ceil_div(p.N, 64 * cfg[i][1]) * batch;
+        const int64_t rounds = (tiles + 255) / 256;
+        const double eff = (double)tiles / (double)(rounds * 256);
+        if (eff > best_eff + 1e-9) { best_eff = eff; best = i; }
+    }
+    switch (best) {
+    case 0: return launch_v2<2, 4>(p, out_mode, batch, st);
+    case 1: return launch_v2<2, 3>(p, out_mode, batch, st);
+    case 2: return launch_v2<2, 2>(p, out_mode, batch, st);
+    default: return launch_v2<2, 1>(p, out_mode, batch, st);
+    }
+}
+
 int launch_gemm(const GemmParams& p, int out_mode, int batch, hipStream_t st) {
     dim3 grid(ceil_div(p.N, TN), ceil_div(p.M, TM), batch), block(256);
     switch (out_mode) {
@@ -117,7 +275,7 @@ int gemm_w8a8(const int8_t* q, const float* s_a, const int8_t* w, const float* s
     p.s_a = s_a; p.s_w = s_w; p.bias = bias;
     p.C = y; p.ldc = N;
     p.M = M; p.N = N; p.K = K;
-    return launch_gemm(p, mode, 1, st);
+    return launch_dense(p, mode, 1, st);
 }
 
 // [K,N] -> [N,K] int8 transpose through a 64x64 LDS tile (per batch z).
@@ -213,8 +371,7 @@ static int matmul_int8_impl(const int8_t* a, const int8_t* b, void* c, int out_i
     p.B = bt; p.ldb = Kp; p.b_batch = (int64_t)N * Kp;
     p.C = c; p.ldc = N; p.c_batch = (int64_t)M * N;
     p.M = M; p.N = N; p.K = Kp;
-    int rc = launch_gemm(p, out_i32 ? OUT_I32 : OUT_F32_RAW, batch, st);
-    return rc;
+    return launch_dense(p, out_i32 ? OUT_I32 : OUT_F32_RAW, batch, st);
 }
 
 PIO_EXPORT int pio_matmul_int8(const int8_t* a, const int8_t* b, void* c, int out_i32, int batch,

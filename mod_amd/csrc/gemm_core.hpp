@@ -119,3 +119,252 @@ __device__ __forceinline__ int acc_col(int j) {
 }
 
 }  // namespace pio
+
+namespace pio {
+
+// ---------------------------------------------------------------------------
+// Dense tile engine v2: v_mfma_i32_32x32x32_i8, K step 128 bytes.
+//
+// Block = 256 threads = 2x2 waves; a wave owns WMT x WNT MFMA tiles of 32x32,
+// so the block tile is BM = 64*WMT by BN = 64*WNT. LDS rows are 128 bytes (one
+// K step) with no padding; 16-byte chunk c of row r is stored at slot
+// c ^ ((r >> 1) & 7), which puts the 16 lanes of every ds_read_b128 phase (16
+// consecutive rows, same chunk) on 16 distinct 4-bank groups.
+//
+// MFMA 32x32x32 operand layout: lane l supplies A row (l % 32) and B column
+// (l % 32), 16 K bytes starting at 16 * (l / 32) of a 32-byte K slice (A and B
+// identically, so the unit's internal K order cannot matter). Accumulator:
+// lane l holds D[8*(i/4) + 4*(l/32) + (i%4)][l % 32], i = 0..15.
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
+
+template <int WMT, int WNT>
+struct TileV2 {
+    static constexpr int BM = 64 * WMT, BN = 64 * WNT, BK = 128;
+    static constexpr int A_CHUNKS = BM * 8 / 256;   // 16-byte chunks per thread per K step
+    static constexpr int B_CHUNKS = BN * 8 / 256;
+    static constexpr int STAGE = (BM + BN) * BK;     // bytes per LDS stage
+    static constexpr int LDS_BYTES = 2 * STAGE;
+};
+
+// Computes the block tile's int32 accumulators. A rows [0, m_rem) and B rows
+// [0, n_rem) are valid (others read as zero); K % 16 == 0.
+template <int WMT, int WNT>
+__device__ __forceinline__ void mma_tile_v2(const int8_t* __restrict__ A, int64_t lda, int m_rem,
+                                            const int8_t* __restrict__ B, int64_t ldb, int n_rem,
+                                            int K, int8_t* lds, v16i (&acc)[WMT][WNT]) {
+    using T = TileV2<WMT, WNT>;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // Global chunk assignment: chunk idx -> (row idx/8, col idx%8).
+    const int8_t* ga[T::A_CHUNKS];
+    const int8_t* gb[T::B_CHUNKS];
+    int la[T::A_CHUNKS], lb[T::B_CHUNKS], ca[T::A_CHUNKS], cb[T::B_CHUNKS];
+    bool va[T::A_CHUNKS], vb[T::B_CHUNKS];
+#pragma unroll
+    for (int j = 0; j < T::A_CHUNKS; j++) {
+        const int idx = tid + 256 * j, r = idx >> 3, c = idx & 7;
+        va[j] = r < m_rem;
+        ga[j] = A + (int64_t)(va[j] ? r : 0) * lda + c * 16;
+        ca[j] = c * 16;
+        la[j] = swz(r, c);
+    }
+#pragma unroll
+    for (int j = 0; j < T::B_CHUNKS; j++) {
+        const int idx = tid + 256 * j, r = idx >> 3, c = idx & 7;
+        vb[j] = r < n_rem;
+        gb[j] = B + (int64_t)(vb[j] ? r : 0) * ldb + c * 16;
+        cb[j] = c * 16;
+        lb[j] = T::BM * 128 + swz(r, c);
+    }
+    v4i ra[T::A_CHUNKS], rb[T::B_CHUNKS];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int j = 0; j < T::A_CHUNKS; j++)
+            ra[j] = (va[j] && k0 + ca[j] < K) ? *(const v4i*)(ga[j] + k0) : v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < T::B_CHUNKS; j++)
+            rb[j] = (vb[j] && k0 + cb[j] < K) ? *(const v4i*)(gb[j] + k0) : v4i{0, 0, 0, 0};
+    };
+    auto sstore = [&](int buf) {
+        int8_t* base = lds + buf * T::STAGE;
+#pragma unroll
+        for (int j = 0; j < T::A_CHUNKS; j++) *(v4i*)(base + la[j]) = ra[j];
+#pragma unroll
+        for (int j = 0; j < T::B_CHUNKS; j++) *(v4i*)(base + lb[j]) = rb[j];
+    };
+
+#pragma unroll
+    for (int i = 0; i < WMT; i++)
+#pragma unroll
+        for (int j = 0; j < WNT; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0;
+
+    const int nk = (K + T::BK - 1) / T::BK;
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    const int fr = lane & 31, fh = lane >> 5;
+    for (int kt = 0; kt < nk; kt++) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) gload((kt + 1) * T::BK);
+        const int8_t* base = lds + cur * T::STAGE;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const int c = 2 * ks + fh;
+            v4i a[WMT], b[WNT];
+#pragma unroll
+            for (int i = 0; i < WMT; i++) {
+                const int r = wm * 32 * WMT + i * 32 + fr;
+                a[i] = *(const v4i*)(base + swz(r, c));
+            }
+#pragma unroll
+            for (int j = 0; j < WNT; j++) {
+                const int r = wn * 32 * WNT + j * 32 + fr;
+                b[j] = *(const v4i*)(base + T::BM * 128 + swz(r, c));
+            }
+#pragma unroll
+            for (int i = 0; i < WMT; i++)
+#pragma unroll
+                for (int j = 0; j < WNT; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) sstore(cur ^ 1);
+        __syncthreads();
+    }
+}
+
+// Tile-relative row / column of accumulator element e of MFMA tile (i, j).
+template <int WMT>
+__device__ __forceinline__ int v2_row(int i, int e) {
+    const int lane = threadIdx.x & 63, wm = (threadIdx.x >> 6) >> 1;
+    return wm * 32 * WMT + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+}
+template <int WNT>
+__device__ __forceinline__ int v2_col(int j) {
+    const int lane = threadIdx.x & 63, wn = (threadIdx.x >> 6) & 1;
+    return wn * 32 * WNT + j * 32 + (lane & 31);
+}
+
+}  // namespace pio
+
+namespace pio {
+
+// ---------------------------------------------------------------------------
+// Dense tile engine v3: same MFMA tiling and LDS swizzle as v2, but operands
+// go straight from global memory into an S-stage LDS ring with
+// global_load_lds_dwordx4 (no register staging), S-1 K steps in flight.
+//
+// One wave instruction moves a 1 KB block = 8 rows x 128 B: lane l lands at
+// LDS byte 16*l of the block, i.e. row l/8, slot l%8, so it fetches global
+// chunk (l%8) ^ ((row >> 1) & 7) -- the v2 swizzle applied on the read side of
+// the copy. Requires K % 128 == 0 (a K tail cannot be zero-filled on this
+// path). Rows past m_rem / n_rem re-read the last valid row; they only feed
+// output rows / columns the caller discards. With `a_rows`, tile row r of A is
+// global row a_rows[r] (MoE token gather).
+template <int WMT, int WNT, int S>
+struct TileV3 {
+    static constexpr int BM = 64 * WMT, BN = 64 * WNT, BK = 128, STAGES = S;
+    static constexpr int A_BLK = BM / 8, B_BLK = BN / 8;          // 1 KB blocks per stage
+    static constexpr int A_PER_WAVE = A_BLK / 4, B_PER_WAVE = B_BLK / 4;
+    static constexpr int LOADS = A_PER_WAVE + B_PER_WAVE;         // per wave per stage
+    static constexpr int STAGE = (BM + BN) * BK;
+    static constexpr int LDS_BYTES = S * STAGE;
+};
+
+// Waits until at most N vector-memory loads of this wave are outstanding and
+// all its LDS operations are done, then joins the workgroup barrier. Unlike
+// __syncthreads() (whose workgroup fence waits for *every* outstanding load,
+// vmcnt(0)), this keeps the later stages' global->LDS loads in flight. The
+// empty asm statements stop the compiler from moving memory accesses across.
+template <int N>
+__device__ __forceinline__ void stage_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int WMT, int WNT, int S>
+__device__ __forceinline__ void mma_tile_v3(const int8_t* __restrict__ A, int64_t lda, int m_rem,
+                                            const int8_t* __restrict__ B, int64_t ldb, int n_rem,
+                                            int K, int8_t* lds, v16i (&acc)[WMT][WNT],
+                                            const int32_t* __restrict__ a_rows = nullptr) {
+    using T = TileV3<WMT, WNT, S>;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // Per-lane global source of each of this wave's block loads.
+    const int8_t* ga[T::A_PER_WAVE];
+    const int8_t* gb[T::B_PER_WAVE];
+#pragma unroll
+    for (int j = 0; j < T::A_PER_WAVE; j++) {
+        const int q = j * 4 + wave, r = q * 8 + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
+        const int rr = min(r, m_rem - 1);   // A row r of the tile: A[a_rows[r]] when gathering
+        ga[j] = A + (int64_t)(a_rows ? a_rows[rr] : rr) * lda + c * 16;
+    }
+#pragma unroll
+    for (int j = 0; j < T::B_PER_WAVE; j++) {
+        const int q = j * 4 + wave, r = q * 8 + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
+        gb[j] = B + (int64_t)min(r, n_rem - 1) * ldb + c * 16;
+    }
+    typedef __attribute__((address_space(3))) void lds_t;
+    auto issue = [&](int kstep) {
+        int8_t* base = lds + (kstep % S) * T::STAGE;
+        const int k0 = kstep * T::BK;
+#pragma unroll
+        for (int j = 0; j < T::A_PER_WAVE; j++)
+            __builtin_amdgcn_global_load_lds((const void*)(ga[j] + k0),
+                                             (lds_t*)(base + (j * 4 + wave) * 1024), 16, 0, 0);
+#pragma unroll
+        for (int j = 0; j < T::B_PER_WAVE; j++)
+            __builtin_amdgcn_global_load_lds((const void*)(gb[j] + k0),
+                                             (lds_t*)(base + T::BM * 128 + (j * 4 + wave) * 1024),
+                                             16, 0, 0);
+    };
+
+#pragma unroll
+    for (int i = 0; i < WMT; i++)
+#pragma unroll
+        for (int j = 0; j < WNT; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0;
+
+    const int nk = K / T::BK;
+#pragma unroll
+    for (int s = 0; s < S - 1; s++)
+        if (s < nk) issue(s);
+    const int fr = lane & 31, fh = lane >> 5;
+    for (int kt = 0; kt < nk; kt++) {
+        // Stages issued so far: min(nk, kt + S - 1); wait for stage kt.
+        const int ahead = min(nk, kt + S - 1) - kt - 1;
+        if (S >= 4 && ahead >= 2) stage_barrier<(S >= 4 ? 2 : 0) * T::LOADS>();
+        else if (ahead >= 1) stage_barrier<T::LOADS>();
+        else stage_barrier<0>();
+        if (kt + S - 1 < nk) issue(kt + S - 1);
+        const int8_t* base = lds + (kt % S) * T::STAGE;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const int c = 2 * ks + fh;
+            v4i a[WMT], b[WNT];
+#pragma unroll
+            for (int i = 0; i < WMT; i++)
+                a[i] = *(const v4i*)(base + swz(wm * 32 * WMT + i * 32 + fr, c));
+#pragma unroll
+            for (int j = 0; j < WNT; j++)
+                b[j] = *(const v4i*)(base + T::BM * 128 + swz(wn * 32 * WNT + j * 32 + fr, c));
+#pragma unroll
+            for (int i = 0; i < WMT; i++)
+#pragma unroll
+                for (int j = 0; j < WNT; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+    }
+}
+
+}  // namespace pio

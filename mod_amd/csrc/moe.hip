@@ -86,10 +86,20 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
 }
 
 // ------------------------------------------------------------------ group ---
-// Single block. bitmap[t][e/32] marks (t, e) pairs; thread e counts column e,
-// an exclusive scan gives expert offsets, then thread e lays out its rows in
-// token order. Limits: T * ceil(E/32) <= GROUP_LDS_WORDS (56 KB of LDS).
-constexpr int GROUP_LDS_WORDS = 14336;
+// Single block of 1024 threads, no serial dependency chains:
+//  1. top-k ids staged in LDS; bitmap[t][e/32] marks the (t, e) pairs;
+//  2. work item (e, slice) -- slices of 64 tokens -- packs column e of its
+//     slice into a 64-bit mask (64 independent LDS reads) and counts it;
+//  3. one wave scans the counts (slices in order, then experts in order) with
+//     shuffles, giving each item its first row;
+//  4. each set bit j of an item's mask goes to row start + popcount(bits < j),
+//     its top-k slot found in one 16-byte read of the token's id row.
+// The layout equals a serial walk over (expert, token). Limits:
+// T * ceil(E/32) <= GROUP_LDS_WORDS, T * top_k <= GROUP_MAX_PAIRS,
+// E * ceil(T/64) <= GROUP_MAX_ITEMS, top_k <= 8.
+constexpr int GROUP_LDS_WORDS = 8192;     // token x expert bitmap (32 KB)
+constexpr int GROUP_MAX_PAIRS = 8192;     // staged topk ids (16 KB)
+constexpr int GROUP_MAX_ITEMS = 4096;     // (expert, 64-token slice) items
 
 __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t* __restrict__ topk_id,
                                                          int T, int E, int top_k,
@@ -97,43 +107,71 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t* __restri
                                                          int32_t* __restrict__ row_token,
                                                          int32_t* __restrict__ pos_of_pair) {
     __shared__ uint32_t bm[GROUP_LDS_WORDS];
-    __shared__ int32_t cnt[ROUTE_MAX_E + 1];
+    __shared__ __attribute__((aligned(16))) int16_t ids[GROUP_MAX_PAIRS];
+    __shared__ unsigned long long masks[GROUP_MAX_ITEMS];
+    __shared__ int32_t start[GROUP_MAX_ITEMS];
     const int words = (E + 31) / 32;
+    const int nsl = (T + 63) / 64;
+    const int items = E * nsl;   // item = e * nsl + slice
     for (int i = threadIdx.x; i < T * words; i += blockDim.x) bm[i] = 0;
+    for (int i = threadIdx.x; i < T * 8; i += blockDim.x) {
+        const int t = i >> 3, kk = i & 7;
+        ids[i] = kk < top_k ? (int16_t)topk_id[t * top_k + kk] : (int16_t)-1;
+    }
     __syncthreads();
     for (int i = threadIdx.x; i < T * top_k; i += blockDim.x) {
-        const int t = i / top_k, e = topk_id[i];
+        const int t = i / top_k, e = ids[t * 8 + i % top_k];
         atomicOr(&bm[t * words + (e >> 5)], 1u << (e & 31));
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
-        int c = 0;
-        for (int t = 0; t < T; t++) c += (bm[t * words + (e >> 5)] >> (e & 31)) & 1;
-        cnt[e] = c;
+    for (int it = threadIdx.x; it < items; it += blockDim.x) {
+        const int e = it / nsl, sl = it % nsl, t0 = sl * 64;
+        const uint32_t* col = bm + (e >> 5);
+        const int sh = e & 31;
+        unsigned long long m = 0ull;
+#pragma unroll 16
+        for (int j = 0; j < 64; j++)
+            if (t0 + j < T) m |= (unsigned long long)((col[(t0 + j) * words] >> sh) & 1u) << j;
+        masks[it] = m;
+        start[it] = __popcll(m);
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int run = 0;
-        for (int e = 0; e < E; e++) {
-            const int c = cnt[e];
-            cnt[e] = run;
-            offsets[e] = run;
-            run += c;
-        }
-        cnt[E] = run;
-        offsets[E] = run;
-    }
-    __syncthreads();
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
-        int pos = cnt[e];
-        for (int t = 0; t < T; t++) {
-            if ((bm[t * words + (e >> 5)] >> (e & 31)) & 1) {
-                int kk = 0;
-                while (kk < top_k && topk_id[t * top_k + kk] != e) kk++;
-                row_token[pos] = t;
-                pos_of_pair[t * top_k + kk] = pos;
-                pos++;
+    if (threadIdx.x < 64) {
+        // exclusive scan of start[] in item order (= expert-major, slices in order)
+        int carry = 0;
+        const int lane = threadIdx.x;
+        for (int b = 0; b < items; b += 64) {
+            const int i = b + lane;
+            const int v = i < items ? start[i] : 0;
+            int x = v;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int y = __shfl_up(x, o, 64);
+                if (lane >= o) x += y;
             }
+            if (i < items) start[i] = carry + x - v;
+            carry += __shfl(x, 63, 64);
+        }
+        for (int e = lane; e <= E; e += 64) offsets[e] = e < E ? start[e * nsl] : carry;
+    }
+    __syncthreads();
+    for (int it = threadIdx.x; it < items; it += blockDim.x) {
+        const int e = it / nsl, sl = it % nsl, t0 = sl * 64;
+        unsigned long long m = masks[it];
+        int pos = start[it];
+        while (m) {
+            const int j = __ffsll((long long)m) - 1;
+            m &= m - 1;
+            const int t = t0 + j;
+            const int4 row = *(const int4*)&ids[t * 8];
+            const int16_t* r16 = (const int16_t*)&row;
+            int kk = 0;
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+                if (r16[q] == e) kk = q;
+            row_token[pos] = t;
+            pos_of_pair[t * top_k + kk] = pos;
+            pos++;
         }
     }
 }
@@ -150,45 +188,59 @@ struct GroupedParams {
     int N, K;
 };
 
+// Block (n-tile, expert) on the pipelined direct-to-LDS engine: 64 x 128 tiles
+// (2x2 waves of 32x64), 3 LDS stages (72 KB, two blocks per CU), A rows
+// gathered through the expert's token list. The block walks its expert's row
+// tiles, so each weight tile is streamed from HBM once per 64 tokens.
+constexpr int MOE_WMT = 1, MOE_WNT = 2, MOE_STAGES = 3;
+using MoeTile = TileV3<MOE_WMT, MOE_WNT, MOE_STAGES>;
+
 __global__ __launch_bounds__(256, 2) void moe_grouped_gemm_kernel(GroupedParams p) {
-    __shared__ __attribute__((aligned(16))) int8_t lds[TILE_LDS_BYTES];
-    const int e = blockIdx.y, n0 = blockIdx.x * TN;
+    extern __shared__ __attribute__((aligned(16))) int8_t lds_moe[];
+    const int e = blockIdx.y, n0 = blockIdx.x * MoeTile::BN;
     const int beg = p.offsets[e], cnt = p.offsets[e + 1] - beg;
-    const int8_t* W = p.W + (int64_t)e * p.N * p.K;
+    const int8_t* W = p.W + ((int64_t)e * p.N + n0) * p.K;
     const float* sw = p.s_w + (int64_t)e * p.N;
-    for (int m0 = 0; m0 < cnt; m0 += TM) {
-        TileSrc s;
-        if (p.a_rows) {
-            s.A = p.A;
-            s.a_rows = p.a_rows + beg + m0;
-        } else {
-            s.A = p.A + (int64_t)(beg + m0) * p.K;
-            s.a_rows = nullptr;
+    for (int m0 = 0; m0 < cnt; m0 += MoeTile::BM) {
+        // Epilogue scales: thread r < BM fetches row r's activation scale (through
+        // the token gather), thread BM + c fetches column c's weight scale,
+        // before the main loop so the latency overlaps it. After the loop they
+        // go through LDS, so the bounds-checked stores below consume only
+        // LDS/VALU results and issue without waiting on one another.
+        const int tid = threadIdx.x;
+        float my_scale = 0.f;
+        if (tid < MoeTile::BM) {
+            const int pos = beg + min(m0 + tid, cnt - 1);
+            my_scale = p.s_a[p.a_rows ? p.a_rows[pos] : pos];
+        } else if (tid < MoeTile::BM + MoeTile::BN) {
+            my_scale = sw[min(n0 + tid - MoeTile::BM, p.N - 1)];
         }
-        s.lda = p.K;
-        s.m_rem = cnt - m0;
-        s.B = W + (int64_t)n0 * p.K;
-        s.ldb = p.K;
-        s.n_rem = p.N - n0;
-        s.K = p.K;
-        v4i acc[4][4];
-        mma_tile_128(s, lds, acc);
+        v16i acc[MOE_WMT][MOE_WNT];
+        if (p.a_rows)
+            mma_tile_v3<MOE_WMT, MOE_WNT, MOE_STAGES>(p.A, p.K, cnt - m0, W, p.K, p.N - n0, p.K,
+                                                      lds_moe, acc, p.a_rows + beg + m0);
+        else
+            mma_tile_v3<MOE_WMT, MOE_WNT, MOE_STAGES>(p.A + (int64_t)(beg + m0) * p.K, p.K,
+                                                      cnt - m0, W, p.K, p.N - n0, p.K, lds_moe,
+                                                      acc);
+        float* scl = (float*)lds_moe;   // the ring is free once every wave is past this barrier
+        __syncthreads();
+        if (tid < MoeTile::BM + MoeTile::BN) scl[tid] = my_scale;
+        __syncthreads();
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int n = n0 + acc_col(j);
-            if (n >= p.N) continue;
-            const float swn = sw[n];
+        for (int j = 0; j < MOE_WNT; j++) {
+            const int c = v2_col<MOE_WNT>(j), n = n0 + c;
+            const float swn = scl[MoeTile::BM + c];
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int i = 0; i < MOE_WMT; i++)
 #pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const int r = m0 + acc_row(i, v);
-                    if (r >= cnt) continue;
-                    const int pos = beg + r;
-                    const float sa = p.s_a[p.a_rows ? p.a_rows[pos] : pos];
-                    p.C[(int64_t)pos * p.N + n] = (float)acc[i][j][v] * sa * swn;
+                for (int v = 0; v < 16; v++) {
+                    const int rl = v2_row<MOE_WMT>(i, v), r = m0 + rl;
+                    const float val = (float)acc[i][j][v] * scl[rl] * swn;
+                    if (r < cnt && n < p.N) p.C[(int64_t)(beg + r) * p.N + n] = val;
                 }
         }
+        __syncthreads();   // the next row tile reuses the LDS ring
     }
 }
 
@@ -290,13 +342,21 @@ int moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* w_gu
              hipStream_t st) {
     PIO_REQUIRE(x && logits && w_gu && s_gu && w_down && s_down && out, "moe: null pointer");
     PIO_REQUIRE(T >= 0 && H > 0 && I > 0, "moe: bad shape");
-    PIO_REQUIRE(H % 16 == 0 && I % 16 == 0, "moe: H=%d and I=%d must be multiples of 16", H, I);
+    PIO_REQUIRE(H % 128 == 0 && I % 128 == 0, "moe: H=%d and I=%d must be multiples of 128", H, I);
     PIO_REQUIRE(out_dtype == PIO_F32 || out_dtype == PIO_F16, "moe: out must be fp32 or fp16");
-    PIO_REQUIRE((int64_t)T * ((E + 31) / 32) <= GROUP_LDS_WORDS,
-                "moe: T*ceil(E/32) = %lld exceeds the grouping limit %d",
-                (long long)T * ((E + 31) / 32), GROUP_LDS_WORDS);
+    PIO_REQUIRE((int64_t)T * ((E + 31) / 32) <= GROUP_LDS_WORDS && (int64_t)T * 8 <= GROUP_MAX_PAIRS &&
+                    (int64_t)E * ((T + 63) / 64) <= GROUP_MAX_ITEMS && top_k <= 8,
+                "moe: T=%d tokens, E=%d experts, top_k=%d exceed the grouping limits "
+                "(T*ceil(E/32) <= %d, T*8 <= %d, E*ceil(T/64) <= %d, top_k <= 8)", T, E, top_k,
+                GROUP_LDS_WORDS, GROUP_MAX_PAIRS, GROUP_MAX_ITEMS);
     PIO_REQUIRE(aligned16(w_gu) && aligned16(w_down), "moe: weights must be 16-byte aligned");
     if (T == 0) return PIO_OK;
+    static bool lds_ok = false;
+    if (!lds_ok) {
+        PIO_HIP(hipFuncSetAttribute((const void*)moe_grouped_gemm_kernel,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, MoeTile::LDS_BYTES));
+        lds_ok = true;
+    }
     Scratch own;
     if (!ws) {
         PIO_TRY(own.get(moe_layout(nullptr, T, H, I, E, top_k).total));
@@ -315,7 +375,7 @@ int moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* w_gu
     g.A = w.qx; g.a_rows = w.row_token; g.s_a = w.sx;
     g.W = w_gu; g.s_w = s_gu; g.offsets = w.offsets; g.C = w.gu;
     g.N = 2 * I; g.K = H;
-    moe_grouped_gemm_kernel<<<dim3(ceil_div(2 * I, TN), E), 256, 0, st>>>(g);
+    moe_grouped_gemm_kernel<<<dim3(ceil_div(2 * I, MoeTile::BN), E), 256, MoeTile::LDS_BYTES, st>>>(g);
     PIO_LAUNCHED();
 
     moe_swiglu_quant_kernel<<<ceil_div(P, 4), 256, 0, st>>>(w.gu, w.qh, w.sh, P, I);
@@ -325,7 +385,7 @@ int moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* w_gu
     d.A = w.qh; d.a_rows = nullptr; d.s_a = w.sh;
     d.W = w_down; d.s_w = s_down; d.offsets = w.offsets; d.C = w.d;
     d.N = H; d.K = I;
-    moe_grouped_gemm_kernel<<<dim3(ceil_div(H, TN), E), 256, 0, st>>>(d);
+    moe_grouped_gemm_kernel<<<dim3(ceil_div(H, MoeTile::BN), E), 256, MoeTile::LDS_BYTES, st>>>(d);
     PIO_LAUNCHED();
 
     dim3 cg(ceil_div(H, 256), T);

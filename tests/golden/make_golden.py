@@ -70,10 +70,10 @@ def main():
     v, i = oracle.ref_topk(p, 2)
     np.savez_compressed(OUT / "route_tiny.npz", logits=logits, probs=p, topv=v, topi=i)
 
-    # 5. MoE tiny (8 experts, top-2, 16 tokens, H=32, I=16): oracle output,
+    # 5. MoE tiny (8 experts, top-2, 16 tokens, H=128, I=128): oracle output,
     #    fixed so later oracle edits are caught.
     rng = np.random.default_rng(4)
-    T, H, I, E, K = 16, 32, 16, 8, 2
+    T, H, I, E, K = 16, 128, 128, 8, 2
     xm = rng.standard_normal((T, H), dtype=np.float32)
     lg = rng.standard_normal((T, E), dtype=np.float32)
     wgu = rng.integers(-127, 127, size=(E, 2 * I, H), dtype=np.int8)

@@ -94,7 +94,7 @@ def test_quantizer_and_moe_reject_bad_args():
     assert ops.lib.pio_moe_route(16, 16, 16, 4, 2000, 8, 0, FAKE_STREAM) == ops.ERR_INVALID
     assert ops.lib.pio_moe_w8a8(16, ops.F32, 16, 16, 16, 16, 16, 16, ops.F32, 8, 30, 16, 8, 2, 0,
                                 None, FAKE_STREAM) == ops.ERR_INVALID
-    assert "multiples of 16" in ops.last_error()
+    assert "multiples of 128" in ops.last_error()
 
 
 def test_tensor_layer_rejects_host_tensors_and_nulls():

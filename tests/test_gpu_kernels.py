@@ -239,7 +239,7 @@ def test_moe_route_matches_oracle(env):
     assert list(host(i)[0]) == list(range(8))
 
 
-@pytest.mark.parametrize("T,H,I,E,k,xdt", [(16, 32, 16, 8, 2, np.float32),
+@pytest.mark.parametrize("T,H,I,E,k,xdt", [(16, 128, 128, 8, 2, np.float32),
                                            (64, 256, 128, 16, 4, np.float16),
                                            (512, 2048, 768, 128, 8, np.float16)])
 def test_moe_layer_matches_oracle(env, T, H, I, E, k, xdt):

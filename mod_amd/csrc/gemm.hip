@@ -1,21 +1,11 @@
 // W8A8 int8 GEMM on gfx950 MFMA (dense prefill linears and tensor_matmul_int8).
 //   acc[m,n] = sum_k A[m,k] * B[n,k]          int32, exact (|acc| < 2^31 for K < 133144)
 //   C[m,n]   = cvt(float(acc) * s_a[m] * s_w[n] (+ bias[n]))   or raw acc / float(acc)
-// A int8 [M,K] (quantized activations, optionally row-gathered through an index
-// list for MoE groups), B int8 [N,K] (weights, K contiguous), both "K-major", so
-// one v_mfma_i32_16x16x64_i8 consumes 16 contiguous bytes per lane from each.
-//
-// Block tile 128x128, K step 64, 256 threads = 4 waves in a 2x2 grid, each wave
-// owning a 64x64 sub-tile = 4x4 MFMA tiles (64 int32 accumulators per lane).
-// Operand tiles are staged through LDS (row stride padded 64 -> 80 B so the 16
-// lanes of one ds_read_b128 phase hit distinct banks), double buffered, with the
-// next K step's global loads issued before the current step's MFMAs.
-//
-// MFMA operand layout used (16x16xK): lane l supplies A row (l % 16) and B
-// column (l % 16), K bytes [16*(l/16), 16*(l/16)+16) of the 64-wide K step.
-// A and B use the same per-lane K assignment, so whatever internal K order the
-// instruction uses, every A[m,k] meets B[n,k] exactly once. Result layout:
-// lane l holds D[4*(l/16) + v][l % 16], v = 0..3.
+// A int8 [M,K] (quantized activations), B int8 [N,K] (weights, K contiguous),
+// both "K-major", so one v_mfma_i32_32x32x32_i8 consumes 16 contiguous bytes per
+// lane from each. The tile engines live in gemm_core.hpp; this file holds the
+// dense kernel (XCD-aware tile order, scale epilogue), the tile-shape choice and
+// the tensor_matmul_int8 adapter (B given as [K,N] is transposed once).
 #include "gemm_core.hpp"
 
 #include <stdlib.h>
@@ -36,56 +26,6 @@ struct GemmParams {
     int64_t ldc, c_batch;
     int M, N, K;
 };
-
-// Dense tiles: blockIdx.x = N tile, blockIdx.y = M tile, blockIdx.z = batch.
-template <int OUT>
-__global__ __launch_bounds__(256, 2) void gemm_i8_kernel(GemmParams p) {
-    __shared__ __attribute__((aligned(16))) int8_t lds[TILE_LDS_BYTES];
-    const int m0 = blockIdx.y * TM, n0 = blockIdx.x * TN, z = blockIdx.z;
-    TileSrc s;
-    s.A = p.A + z * p.a_batch + (int64_t)m0 * p.lda;
-    s.a_rows = nullptr;
-    s.lda = p.lda;
-    s.m_rem = p.M - m0;
-    s.B = p.B + z * p.b_batch + (int64_t)n0 * p.ldb;
-    s.ldb = p.ldb;
-    s.n_rem = p.N - n0;
-    s.K = p.K;
-    v4i acc[4][4];
-    mma_tile_128(s, lds, acc);
-
-    char* C = (char*)p.C;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int n = n0 + acc_col(j);
-        if (n >= p.N) continue;
-        float sw = 0.f, bn = 0.f;
-        if (OUT == OUT_F32 || OUT == OUT_F16) {
-            sw = p.s_w[n];
-            if (p.bias) bn = p.bias[n];
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-#pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int m = m0 + acc_row(i, v);
-                if (m >= p.M) continue;
-                const int64_t off = z * p.c_batch + (int64_t)m * p.ldc + n;
-                const int a = acc[i][j][v];
-                if (OUT == OUT_I32) {
-                    ((int32_t*)C)[off] = a;
-                } else if (OUT == OUT_F32_RAW) {
-                    ((float*)C)[off] = (float)a;
-                } else {
-                    float val = (float)a * p.s_a[m] * sw;
-                    if (p.bias) val += bn;
-                    if (OUT == OUT_F32) ((float*)C)[off] = val;
-                    else ((_Float16*)C)[off] = (_Float16)val;
-                }
-            }
-        }
-    }
-}
 
 // ----------------------------------------------------------------- v2 ---
 // Dense W8A8 on the 32x32x32 engine. Block b is mapped XCD-aware: the
@@ -241,19 +181,6 @@ static int launch_dense(const GemmParams& p, int out_mode, int batch, hipStream_
     case 2: return launch_v2<2, 2>(p, out_mode, batch, st);
     default: return launch_v2<2, 1>(p, out_mode, batch, st);
     }
-}
-
-int launch_gemm(const GemmParams& p, int out_mode, int batch, hipStream_t st) {
-    dim3 grid(ceil_div(p.N, TN), ceil_div(p.M, TM), batch), block(256);
-    switch (out_mode) {
-    case OUT_F32: gemm_i8_kernel<OUT_F32><<<grid, block, 0, st>>>(p); break;
-    case OUT_F16: gemm_i8_kernel<OUT_F16><<<grid, block, 0, st>>>(p); break;
-    case OUT_I32: gemm_i8_kernel<OUT_I32><<<grid, block, 0, st>>>(p); break;
-    case OUT_F32_RAW: gemm_i8_kernel<OUT_F32_RAW><<<grid, block, 0, st>>>(p); break;
-    default: return set_error(PIO_ERR_INVALID, "gemm: bad output mode");
-    }
-    PIO_LAUNCHED();
-    return PIO_OK;
 }
 
 int gemm_w8a8(const int8_t* q, const float* s_a, const int8_t* w, const float* s_w,

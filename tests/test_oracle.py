@@ -342,3 +342,84 @@ def test_moe_identical_experts_invariant():
     y = oracle.moe_w8a8(x, lg, rep(wgu1), rep(sgu1), rep(wd1), rep(sd1), k, renorm=True)
     single = oracle.moe_w8a8(x, np.zeros((T, 1), np.float32), wgu1, sgu1, wd1, sd1, 1, renorm=True)
     np.testing.assert_allclose(y, single, rtol=1e-5, atol=1e-5 * np.abs(single).max())
+
+
+# ------------------------------------------------------------ decoder oracle
+def _qwen2_logits_and_oracle(monkey_rope=None):
+    """Teacher-forced logits of transformers' Qwen2ForCausalLM (float64) and of
+    oracle/qwen3_ref.py stepping through the same 20 ids, same weights."""
+    torch = pytest.importorskip("torch")
+    tf = pytest.importorskip("transformers")
+    import oracle.qwen3_ref as q3
+    from mod_amd.qwen3 import random_weights
+
+    cfg = q3.Qwen3Config(n_layers=2, hidden=128, n_heads=4, n_kv_heads=2, head_dim=64,
+                         intermediate=256, vocab=300, max_seq=32)
+    w = random_weights(cfg, seed=3)
+    w["final_norm"] = (1.0 + 0.1 * np.random.default_rng(4).standard_normal(cfg.hidden)).astype(np.float32)
+    hf_cfg = tf.Qwen2Config(vocab_size=cfg.vocab, hidden_size=cfg.hidden,
+                            intermediate_size=cfg.intermediate, num_hidden_layers=cfg.n_layers,
+                            num_attention_heads=cfg.n_heads, num_key_value_heads=cfg.n_kv_heads,
+                            head_dim=cfg.head_dim, rms_norm_eps=cfg.rms_eps,
+                            rope_theta=cfg.rope_theta, max_position_embeddings=cfg.max_seq,
+                            tie_word_embeddings=False, attn_implementation="eager")
+    model = tf.Qwen2ForCausalLM(hf_cfg).to(torch.float64).eval()
+    deq = lambda W, s: torch.from_numpy(W.astype(np.float64) * s.astype(np.float64)[:, None])  # noqa: E731
+    t64 = lambda a: torch.from_numpy(np.asarray(a, np.float64))  # noqa: E731
+    nq, D, I = cfg.n_heads * cfg.head_dim, cfg.head_dim, cfg.intermediate
+    nk = cfg.n_kv_heads * D
+    with torch.no_grad():
+        model.model.embed_tokens.weight.copy_(t64(w["embed"]))
+        model.model.norm.weight.copy_(t64(w["final_norm"]))
+        model.lm_head.weight.copy_(deq(w["lm_head"], w["s_lm_head"]))
+        for L, blk in zip(w["layers"], model.model.layers):
+            Wqkv = deq(L["w_qkv"], L["s_qkv"])
+            a = blk.self_attn
+            a.q_proj.weight.copy_(Wqkv[:nq]); a.q_proj.bias.copy_(t64(L["b_qkv"][:nq]))
+            a.k_proj.weight.copy_(Wqkv[nq:nq + nk]); a.k_proj.bias.copy_(t64(L["b_qkv"][nq:nq + nk]))
+            a.v_proj.weight.copy_(Wqkv[nq + nk:]); a.v_proj.bias.copy_(t64(L["b_qkv"][nq + nk:]))
+            a.o_proj.weight.copy_(deq(L["w_o"], L["s_o"]))
+            Wgu = deq(L["w_gu"], L["s_gu"])
+            blk.mlp.gate_proj.weight.copy_(Wgu[:I])
+            blk.mlp.up_proj.weight.copy_(Wgu[I:])
+            blk.mlp.down_proj.weight.copy_(deq(L["w_down"], L["s_down"]))
+            blk.input_layernorm.weight.copy_(t64(L["in_norm"]))
+            blk.post_attention_layernorm.weight.copy_(t64(L["post_norm"]))
+        ids = np.random.default_rng(5).integers(0, cfg.vocab, 20)
+        hf = model(torch.from_numpy(ids)[None]).logits[0].numpy()
+    ref = q3.Qwen3Ref(cfg, w, np.float64)
+    ours = np.stack([ref.step(int(t)) for t in ids])
+    return ours, hf
+
+
+def test_decoder_oracle_vs_transformers_qwen2():
+    """oracle/qwen3_ref.py against an independent implementation: transformers'
+    Qwen2 block has the reference architecture's structure (q/k/v projections
+    with bias, no q/k norm, rotate-half RoPE, GQA, pre-norm, SwiGLU;
+    ip/models/qwen3_0_6b/architecture.py:21-221). Loaded with the same
+    dequantized int8 weights and run in float64, its teacher-forced logits
+    must equal the oracle's step-by-step logits. transformers rounds its
+    RMSNorm and RoPE tables through float32 (observed gap 1.1e-5 of the logit
+    rms; with a float64 RMSNorm it falls below 1e-5), hence the 5e-5 bar."""
+    ours, hf = _qwen2_logits_and_oracle()
+    err = np.abs(ours - hf).max() / np.sqrt(np.mean(hf * hf))
+    assert err < 5e-5, err
+
+
+def test_decoder_oracle_pin_resolves_a_rope_slip(monkeypatch):
+    """The comparison above resolves plausible mistakes: the oracle with RoPE
+    pairs taken interleaved (2i, 2i+1) instead of rotate-half (i, i+D/2)
+    misses transformers by orders of magnitude more than the bar."""
+    import oracle.qwen3_ref as q3
+
+    def rope_interleaved(v, c, s):
+        r, im = v[..., 0::2], v[..., 1::2]
+        out = np.empty_like(v)
+        out[..., 0::2] = r * c - im * s
+        out[..., 1::2] = r * s + im * c
+        return out
+
+    monkeypatch.setattr(q3, "_rope", rope_interleaved)
+    ours, hf = _qwen2_logits_and_oracle()
+    err = np.abs(ours - hf).max() / np.sqrt(np.mean(hf * hf))
+    assert err > 1e-2, err

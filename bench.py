@@ -7,12 +7,16 @@ SwiGLU 3072, vocab 151936, int8 lm_head), batch 1, 128-token random prompt then
 256 generated tokens. A "step" is one generated token. Random-init int8 weights
 (no checkpoint is available offline) and random prompt ids; every input is
 resident in HBM before the timed region; the timed region is exactly `--steps`
-decode steps (captured-graph replays) bracketed by device synchronization.
+decode steps bracketed by device synchronization. The steps run in the
+persistent decode kernel (one cooperative launch for all timed steps) when the
+config supports it; the captured-graph step path is timed the same way and
+reported next to it.
 
 Also in the same line:
-  roofline      the dominant kernel (the per-layer W8 GEMV, 112 launches per
-                token) replayed alone from a graph and timed with HIP events on
-                its stream: algorithmic bytes per launch / average launch time.
+  roofline      the dominant kernel: the persistent decode kernel (algorithmic
+                bytes of all timed tokens / its launch time, HIP events on the
+                decoder's stream); on the graph path, the per-layer W8 GEMV
+                replayed alone from a graph.
   cpu_baseline  the reference CPU path (oracle/_ref/libtensor_ops_ref.so, built
                 from the reference's own tensor_ops.c): its fp32 tensor_linear on
                 per-channel-dequantized weights over every linear of one decode
@@ -88,41 +92,50 @@ def bench_decode(torch, args):
     st = torch.cuda.Stream()
     dec = Qwen3Int8Decoder(cfg, w, stream=st.cuda_stream)
     prompt = np.random.default_rng(1).integers(0, cfg.vocab, size=P).astype(np.int32)
+    modes = ["persistent", "graph"] if dec.persistent_supported() else ["graph"]
 
-    # Warmup: capture the step graph and run W decode steps (untimed).
-    dec.reset(prompt)
-    dec.run(P - 1 + min(args.warmup, cfg.max_seq - P + 1), use_graph=True)
-    torch.cuda.synchronize()
-
-    # Timed: the exact config-2 run. Prefill (P-1 prompt steps) is timed apart.
-    dec.reset(prompt)
-    e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-    torch.cuda.synchronize()
-    e[0].record(st)
-    dec.run(P - 1, use_graph=True)
-    e[1].record(st)
-    dec.run(args.steps, use_graph=True)
-    e[2].record(st)
-    e[2].synchronize()
-    torch.cuda.synchronize()
-    prefill_s = e[0].elapsed_time(e[1]) * 1e-3
-    decode_s = e[1].elapsed_time(e[2]) * 1e-3
-    ids = dec.read(P + args.steps)
-    assert np.array_equal(ids[:P], prompt)
+    def timed_run(mode):
+        # Warmup: builds the mode's resources (graph / weight stream), untimed.
+        dec.reset(prompt)
+        dec.run(P - 1 + min(args.warmup, cfg.max_seq - P + 1), mode=mode)
+        torch.cuda.synchronize()
+        # Timed: the exact config-2 run. Prefill (P-1 prompt steps) is timed apart.
+        dec.reset(prompt)
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        torch.cuda.synchronize()
+        e[0].record(st)
+        dec.run(P - 1, mode=mode)
+        e[1].record(st)
+        dec.run(args.steps, mode=mode)
+        e[2].record(st)
+        e[2].synchronize()
+        torch.cuda.synchronize()
+        ids = dec.read(P + args.steps)
+        assert np.array_equal(ids[:P], prompt)
+        return e[0].elapsed_time(e[1]) * 1e-3, e[1].elapsed_time(e[2]) * 1e-3, ids
 
     wb = cfg.weight_bytes()
     mean_ctx = P + (args.steps - 1) / 2.0
     bytes_tok = wb["int8"] + wb["scales"] + wb["bias_norms"] + cfg.kv_bytes_per_pos() * mean_ctx
-    res = {
-        "tok_s": args.steps / decode_s,
-        "ms_per_token": decode_s / args.steps * 1e3,
-        "prefill_ms": prefill_s * 1e3,
-        "prefill_tok_s": (P - 1) / prefill_s,
-        "bytes_per_token": bytes_tok,
-        "hbm_frac": bytes_tok * args.steps / decode_s / (HBM_PEAK_GBS * 1e9),
-        "ceiling_tok_s": HBM_PEAK_GBS * 1e9 / bytes_tok,
-        "generated_head": ids[P:P + 8].tolist(),
-    }
+    res = {}
+    for mode in modes:
+        prefill_s, decode_s, ids = timed_run(mode)
+        res[mode] = {
+            "tok_s": args.steps / decode_s,
+            "ms_per_token": decode_s / args.steps * 1e3,
+            "prefill_ms": prefill_s * 1e3,
+            "prefill_tok_s": (P - 1) / prefill_s,
+            "bytes_per_token": bytes_tok,
+            "hbm_frac": bytes_tok * args.steps / decode_s / (HBM_PEAK_GBS * 1e9),
+            "ceiling_tok_s": HBM_PEAK_GBS * 1e9 / bytes_tok,
+            "generated_head": ids[P:P + 8].tolist(),
+        }
+        log(f"[decode:{mode}] {res[mode]['tok_s']:.1f} tok/s ({res[mode]['ms_per_token']:.3f} ms/token), "
+            f"prefill {res[mode]['prefill_ms']:.1f} ms")
+    if len(modes) == 2:
+        same = res["persistent"]["generated_head"] == res["graph"]["generated_head"]
+        res["persistent"]["same_tokens_as_graph"] = same
+    res["mode"] = modes[0]
     return cfg, w, dec, st, res
 
 
@@ -344,9 +357,8 @@ def main():
     log(f"[bench] {ops.version()}  lib={ops.LIB_FILE}")
     timer = Timer(torch)
 
-    cfg, w, dec, st, dres = bench_decode(torch, args)
-    log(f"[decode] {dres['tok_s']:.1f} tok/s ({dres['ms_per_token']:.3f} ms/token), "
-        f"prefill {dres['prefill_ms']:.1f} ms")
+    cfg, w, dec, st, dall = bench_decode(torch, args)
+    dres = dall[dall["mode"]]
     g = bench_decode_gemv(torch, timer, cfg, dec)
     log(f"[gemv] layer GEMV {g['layer_gemv_us_per_launch']:.2f} us/launch "
         f"{g['layer_gemv_GBs']:.0f} GB/s; lm_head {g['lm_head_us']:.1f} us {g['lm_head_GBs']:.0f} GB/s")
@@ -363,7 +375,33 @@ def main():
         if cpu:
             log(f"[cpu] {cpu['value']:.3f} tok/s ({cpu['ms_per_token']:.1f} ms/token)")
 
-    achieved = g["layer_gemv_GBs"]
+    if dall["mode"] == "persistent":
+        # Dominant kernel = the persistent decode kernel itself: one launch runs
+        # all timed tokens, so bytes per launch = bytes per token x steps.
+        roof = {
+            "bound": "hbm",
+            "kernel": "decode_loop_kernel (persistent decode: every timed token in one launch)",
+            "achieved": round(dres["bytes_per_token"] * dres["tok_s"] / 1e9, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dres["hbm_frac"], 4),
+            "traffic": None,
+            "bytes_per_launch": round(dres["bytes_per_token"] * args.steps),
+            "us_per_launch": round(dres["ms_per_token"] * args.steps * 1e3, 1),
+        }
+    else:
+        achieved = g["layer_gemv_GBs"]
+        roof = {
+            "bound": "hbm",
+            "kernel": "gemv_w8_kernel (per-layer decode GEMVs: qkv, o, gate_up, down)",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": round(g["layer_gemv_bytes_per_launch"]),
+            "us_per_launch": round(g["layer_gemv_us_per_launch"], 3),
+        }
     line = {
         "metric": METRIC,
         "value": round(dres["tok_s"], 2),
@@ -377,6 +415,7 @@ def main():
         "vs_baseline": None,
         "dtype": "int8 weights, fp32 activations/accumulate",
         "data": "synthetic: random-init int8 weights (seed 0), random 128-token prompt",
+        "decode_mode": dall["mode"],
         "config": {
             "workload": "BASELINE config 2: Qwen3-0.6B-shaped int8 greedy decode, batch 1, "
                         "128-token prompt + 256 generated tokens (steps = generated tokens)",
@@ -385,20 +424,11 @@ def main():
             "head_dim": cfg.head_dim, "intermediate": cfg.intermediate, "vocab": cfg.vocab,
             "parallelism": "single GPU",
         },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "gemv_w8_kernel (per-layer decode GEMVs: qkv, o, gate_up, down)",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "bytes_per_launch": round(g["layer_gemv_bytes_per_launch"]),
-            "us_per_launch": round(g["layer_gemv_us_per_launch"], 3),
-        },
+        "roofline": roof,
         "cpu_baseline": cpu and {k: (round(v, 4) if isinstance(v, float) else v)
                                  for k, v in cpu.items()},
-        "decode": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in dres.items()},
+        "decode": {m: ({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+                       if isinstance(r, dict) else r) for m, r in dall.items()},
         "decode_gemv": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in g.items()},
         "kernels": kern,
     }

@@ -274,10 +274,25 @@ void* pio_qwen3_create(const pio_qwen3_config* cfg, const float* embed, const fl
 void pio_qwen3_destroy(void* dec);
 /* Loads `ids` (host, prompt_len tokens) and rewinds to position 0. */
 int pio_qwen3_reset(void* dec, const int32_t* ids, int prompt_len);
-/* Enqueues n decode steps; use_graph != 0 replays one captured step graph. */
-int pio_qwen3_run(void* dec, int n_steps, int use_graph);
+/* Enqueues n decode steps. mode PIO_DECODE_EAGER launches the step kernels,
+ * PIO_DECODE_GRAPH replays one captured step graph per token, and
+ * PIO_DECODE_PERSISTENT runs all n steps in one cooperative kernel (one
+ * workgroup per CU; weights stream through LDS while each phase waits for its
+ * input). The modes share the KV cache and position, so they can alternate.
+ * Persistent mode builds a per-workgroup copy of the weights on first use
+ * (the size of the int8 weights) and needs the config checked by
+ * pio_qwen3_persistent_supported. */
+#define PIO_DECODE_EAGER 0
+#define PIO_DECODE_GRAPH 1
+#define PIO_DECODE_PERSISTENT 2
+int pio_qwen3_run(void* dec, int n_steps, int mode);
+/* 1 if the persistent mode supports this decoder's config on the current
+ * device, else 0 (the reason is in tensor_last_error). No counterpart in the
+ * reference. */
+int pio_qwen3_persistent_supported(void* dec);
 /* Waits for the stream, then copies out ids[0..n) and, if logits != NULL, the
- * last step's logits [vocab]. */
+ * last step's logits [vocab]. Reports an error if a persistent run since the
+ * last read gave up on a wait (its results are then invalid). */
 int pio_qwen3_read(void* dec, int32_t* ids, int n, float* logits);
 /* Device pointer of the last step's logits ([vocab] fp32). */
 const float* pio_qwen3_logits(void* dec);

@@ -15,7 +15,7 @@
 // mask), GQA without materializing repeated heads (architecture.py:57-66),
 // residual adds kept (architecture.py:129-132 drops one on CPU), RoPE on the
 // key heads' own count (tensor_ops.c:390 indexes k with q's head count).
-#include "pio_common.hpp"
+#include "decode.hpp"
 
 #include <math.h>
 #include <algorithm>
@@ -23,8 +23,6 @@
 
 namespace pio {
 
-constexpr int DEC_MAX_SEQ = 8192;
-constexpr int ATT_SPLITS = 8;   // attention splits over key positions
 
 // x = embed[ids[pos]] (an out-of-range id reads row 0, as tensor_embed,
 // tensor_ops.c:663-671).
@@ -464,26 +462,6 @@ __global__ __launch_bounds__(1024) void dec_finish_kernel(int32_t* state,
     state[0] = pos + 1;
 }
 
-struct Qwen3Dec {
-    pio_qwen3_config c{};
-    const float* embed = nullptr;
-    const float* final_norm = nullptr;
-    const int8_t* lm_head = nullptr;
-    const float* s_lm = nullptr;
-    std::vector<pio_qwen3_layer> layers;
-    hipStream_t st = nullptr;
-    bool own_stream = false;
-    void* block = nullptr;
-    float *x, *q, *att_o, *att_ml, *act, *logits, *kc, *vc, *cos_t, *sin_t;
-    int32_t *state, *ids;
-    unsigned long long* part_keys;
-    int lm_blocks = 0;
-    size_t att_lds = 0;
-    int host_pos = 0;
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
-};
-
 // Every launch gives each wave one row group (grid covers N); the kernel also
 // supports fewer blocks, whose waves then stride over the row groups.
 
@@ -557,6 +535,7 @@ static size_t al256(size_t b) { return (b + 255) / 256 * 256; }
 
 static void destroy(Qwen3Dec* d) {
     if (!d) return;
+    loop_destroy(d);
     if (d->exec) (void)hipGraphExecDestroy(d->exec);
     if (d->graph) (void)hipGraphDestroy(d->graph);
     if (d->block) device_free(d->block);
@@ -699,15 +678,24 @@ PIO_EXPORT int pio_qwen3_reset(void* h, const int32_t* ids, int prompt_len) {
     PIO_HIP(hipMemcpyAsync(d->state, st.data(), 16 * 4, hipMemcpyHostToDevice, d->st));
     PIO_HIP(hipStreamSynchronize(d->st));
     d->host_pos = 0;
+    d->prompt_len = prompt_len;
     return PIO_OK;
 }
 
-PIO_EXPORT int pio_qwen3_run(void* h, int n_steps, int use_graph) {
+PIO_EXPORT int pio_qwen3_run(void* h, int n_steps, int mode) {
     Qwen3Dec* d = (Qwen3Dec*)h;
     PIO_REQUIRE(d, "pio_qwen3_run: null handle");
     PIO_REQUIRE(n_steps >= 0 && d->host_pos + n_steps <= d->c.max_seq,
                 "pio_qwen3_run: %d more steps exceed max_seq %d (at %d)", n_steps, d->c.max_seq,
                 d->host_pos);
+    PIO_REQUIRE(mode >= PIO_DECODE_EAGER && mode <= PIO_DECODE_PERSISTENT,
+                "pio_qwen3_run: unknown mode %d", mode);
+    if (mode == PIO_DECODE_PERSISTENT) {
+        PIO_TRY(loop_run(d, n_steps));
+        d->host_pos += n_steps;
+        return PIO_OK;
+    }
+    const bool use_graph = mode == PIO_DECODE_GRAPH;
     if (use_graph && !d->exec && n_steps > 0) {
         PIO_HIP(hipStreamBeginCapture(d->st, hipStreamCaptureModeRelaxed));
         int rc = enqueue_step(d);
@@ -729,6 +717,12 @@ PIO_EXPORT int pio_qwen3_run(void* h, int n_steps, int use_graph) {
     return PIO_OK;
 }
 
+PIO_EXPORT int pio_qwen3_persistent_supported(void* h) {
+    Qwen3Dec* d = (Qwen3Dec*)h;
+    PIO_REQUIRE(d, "pio_qwen3_persistent_supported: null handle");
+    return loop_check(d) == PIO_OK ? 1 : 0;
+}
+
 PIO_EXPORT int pio_qwen3_read(void* h, int32_t* ids, int n, float* logits) {
     Qwen3Dec* d = (Qwen3Dec*)h;
     PIO_REQUIRE(d, "pio_qwen3_read: null handle");
@@ -741,7 +735,7 @@ PIO_EXPORT int pio_qwen3_read(void* h, int32_t* ids, int n, float* logits) {
         PIO_HIP(hipMemcpyAsync(logits, d->logits, (size_t)d->c.vocab * 4, hipMemcpyDeviceToHost,
                                d->st));
     PIO_HIP(hipStreamSynchronize(d->st));
-    return PIO_OK;
+    return loop_status(d);
 }
 
 PIO_EXPORT const float* pio_qwen3_logits(void* h) { return h ? ((Qwen3Dec*)h)->logits : nullptr; }

@@ -1,0 +1,46 @@
+// Decoder state shared by the step kernels (decode.hip) and the persistent
+// decode loop (decode_loop.hip).
+#pragma once
+
+#include "pio_common.hpp"
+
+#include <vector>
+
+namespace pio {
+
+constexpr int DEC_MAX_SEQ = 8192;
+constexpr int ATT_SPLITS = 8;   // attention splits over key positions
+
+struct LoopState;               // decode_loop.hip
+
+struct Qwen3Dec {
+    pio_qwen3_config c{};
+    const float* embed = nullptr;
+    const float* final_norm = nullptr;
+    const int8_t* lm_head = nullptr;
+    const float* s_lm = nullptr;
+    std::vector<pio_qwen3_layer> layers;
+    hipStream_t st = nullptr;
+    bool own_stream = false;
+    void* block = nullptr;
+    float *x, *q, *att_o, *att_ml, *act, *logits, *kc, *vc, *cos_t, *sin_t;
+    int32_t *state, *ids;
+    unsigned long long* part_keys;
+    int lm_blocks = 0;
+    size_t att_lds = 0;
+    int host_pos = 0;
+    int prompt_len = 0;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    LoopState* loop = nullptr;   // persistent-loop resources, built on first use
+};
+
+// Persistent decode loop (decode_loop.hip): one cooperative launch runs
+// n_steps tokens. loop_check() says whether the config fits its kernel.
+int loop_check(const Qwen3Dec* d);
+int loop_run(Qwen3Dec* d, int n_steps);
+// Error words of the last persistent run; call after the stream has drained.
+int loop_status(Qwen3Dec* d);
+void loop_destroy(Qwen3Dec* d);
+
+}  // namespace pio

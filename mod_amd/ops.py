@@ -99,6 +99,7 @@ SIGNATURES: dict[str, tuple] = {
     "pio_qwen3_destroy": (None, [_vp]),
     "pio_qwen3_reset": (_i, [_vp, _vp, _i]),
     "pio_qwen3_run": (_i, [_vp, _i, _i]),
+    "pio_qwen3_persistent_supported": (_i, [_vp]),
     "pio_qwen3_read": (_i, [_vp, _vp, _i, _vp]),
     "pio_qwen3_logits": (_vp, [_vp]),
     "pio_version": (ctypes.c_char_p, []),

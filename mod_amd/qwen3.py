@@ -1,9 +1,14 @@
 """Host side of the int8 Qwen3-style decoder (BASELINE config 2 shape).
 
 ``Qwen3Int8Decoder`` uploads int8 weights (numpy) into library-owned HBM
-tensors and drives the native decoder (pio_qwen3_* in libtensor_ops_rocm.so):
-one device-driven decode step, captured once as a HIP graph and replayed per
-token. Replaces Qwen3ForCausalLM.generate (ip/models/qwen3_0_6b/architecture.py:
+tensors and drives the native decoder (pio_qwen3_* in libtensor_ops_rocm.so).
+Three ways to run steps, sharing one KV cache and position:
+  "eager"       the step's kernels launched one by one,
+  "graph"       one device-driven step captured once as a HIP graph and
+                replayed per token,
+  "persistent"  every step of the call in one cooperative kernel (Qwen3-0.6B
+                layer shape only; see ``persistent_supported``).
+Replaces Qwen3ForCausalLM.generate (ip/models/qwen3_0_6b/architecture.py:
 183-221), whose loop makes ~30 ctypes calls and allocations per layer per token.
 """
 from __future__ import annotations
@@ -95,6 +100,17 @@ def random_weights(cfg: Qwen3Config, seed: int = 0, qkv_bias: bool = True) -> di
             "s_lm_head": (s_lm * 10).astype(np.float32), "layers": layers}
 
 
+MODES = {"eager": 0, "graph": 1, "persistent": 2}
+
+
+def _mode(use_graph, mode) -> int:
+    if mode is None:
+        mode = "graph" if use_graph else "eager"
+    if mode not in MODES:
+        raise ValueError(f"unknown decode mode {mode!r}; one of {sorted(MODES)}")
+    return MODES[mode]
+
+
 class Qwen3Int8Decoder:
     """Native greedy decoder over library-owned device weights."""
 
@@ -139,8 +155,12 @@ class Qwen3Int8Decoder:
         check(lib.pio_qwen3_reset(self._h, ids.ctypes.data, ids.size), "pio_qwen3_reset")
         self.prompt_len = int(ids.size)
 
-    def run(self, n_steps: int, use_graph: bool = True) -> None:
-        check(lib.pio_qwen3_run(self._h, n_steps, int(use_graph)), "pio_qwen3_run")
+    def persistent_supported(self) -> bool:
+        """Whether the "persistent" mode runs this config on this device."""
+        return bool(lib.pio_qwen3_persistent_supported(self._h))
+
+    def run(self, n_steps: int, use_graph: bool = True, mode: Optional[str] = None) -> None:
+        check(lib.pio_qwen3_run(self._h, n_steps, _mode(use_graph, mode)), "pio_qwen3_run")
 
     def read(self, n: int, with_logits: bool = False):
         ids = np.zeros(n, np.int32)
@@ -150,19 +170,21 @@ class Qwen3Int8Decoder:
               "pio_qwen3_read")
         return (ids, logits) if with_logits else ids
 
-    def generate(self, prompt, n_new: int, use_graph: bool = True) -> np.ndarray:
+    def generate(self, prompt, n_new: int, use_graph: bool = True,
+                 mode: Optional[str] = None) -> np.ndarray:
         """Greedy decode: prompt (P ids) -> P + n_new ids. The prompt is consumed
         one position per step (P-1 steps), then n_new steps generate."""
         self.reset(prompt)
         P = len(prompt)
-        self.run(P - 1 + n_new, use_graph)
+        self.run(P - 1 + n_new, use_graph, mode)
         return self.read(P + n_new)
 
-    def teacher_forced_logits(self, ids, use_graph: bool = False) -> np.ndarray:
+    def teacher_forced_logits(self, ids, use_graph: bool = False,
+                              mode: Optional[str] = None) -> np.ndarray:
         """Logits after each position of a fixed id sequence ([len-1, vocab])."""
         self.reset(ids)
         out = []
         for _ in range(len(ids) - 1):
-            self.run(1, use_graph)
+            self.run(1, use_graph, mode)
             out.append(self.read(0, with_logits=True)[1].copy())
         return np.stack(out)

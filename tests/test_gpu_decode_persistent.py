@@ -1,0 +1,148 @@
+"""GPU parity of the persistent decode loop (pio_qwen3_run with
+PIO_DECODE_PERSISTENT): all steps of a call run in one cooperative kernel that
+hands data between workgroups through tagged words instead of kernel launches.
+
+Same bar as the step-kernel decoder (test_gpu_decode.py): teacher-forced logits
+against the float64 oracle within max(1e-4, 4x numpy-fp32's own error) of the
+logit rms, argmax agreement wherever the oracle's top-2 gap is clear. On top:
+the persistent kernel must agree with the graph path to fp32 rounding, and a
+sequence decoded in one launch must equal the same sequence decoded over
+several launches bit for bit (same arithmetic, positions/tags carried over)."""
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import qwen3_ref
+from tests.test_gpu_decode import _check_logits
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(m):
+    print(m, flush=True)
+    sys.stdout.flush()
+
+
+def _cfgs(**over):
+    """Qwen3-0.6B layer shape (the persistent kernel's), fewer layers / vocab."""
+    from mod_amd.qwen3 import Qwen3Config
+    kw = dict(n_layers=2, hidden=1024, n_heads=16, n_kv_heads=8, head_dim=128, intermediate=3072,
+              vocab=1000, max_seq=192)
+    kw.update(over)
+    return Qwen3Config(**kw), qwen3_ref.Qwen3Config(**kw)
+
+
+def _decoder(cfg, seed):
+    from mod_amd.qwen3 import Qwen3Int8Decoder, random_weights
+    w = random_weights(cfg, seed=seed)
+    dec = Qwen3Int8Decoder(cfg, w)
+    if not dec.persistent_supported():
+        from mod_amd import ops
+        pytest.fail(f"persistent mode unsupported: {ops.last_error()}")
+    return dec, w
+
+
+def test_persistent_teacher_forced_small(torch_dev):
+    cfg, rcfg = _cfgs()
+    dec, w = _decoder(cfg, seed=11)
+    ids = np.random.default_rng(12).integers(0, cfg.vocab, size=72).astype(np.int32)
+    _say("persistent small: teacher forced, one launch per position")
+    got = dec.teacher_forced_logits(ids, mode="persistent")
+    _check_logits(got, ids, rcfg, w, "persistent small teacher-forced")
+    _say("persistent small: graph path on the same ids")
+    ref = dec.teacher_forced_logits(ids, mode="graph")
+    rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
+    diff = float(np.abs(got - ref).max()) / rms
+    _say(f"persistent vs graph: max diff {diff:.2e} x rms")
+    assert diff <= 1e-4, diff
+
+
+def test_persistent_one_launch_equals_many(torch_dev):
+    cfg, rcfg = _cfgs()
+    dec, w = _decoder(cfg, seed=21)
+    prompt = np.random.default_rng(22).integers(0, cfg.vocab, size=9).astype(np.int32)
+    n_new = 40
+    _say("persistent: one launch")
+    one = dec.generate(prompt, n_new, mode="persistent")
+    _say("persistent: four launches")
+    dec.reset(prompt)
+    for n in (5, 3, 25, len(prompt) - 1 + n_new - 33):
+        dec.run(n, mode="persistent")
+    many = dec.read(len(prompt) + n_new)
+    assert np.array_equal(one[:len(prompt)], prompt)
+    assert np.array_equal(one, many), (one, many)
+    # mixed: prompt through the graph path, generation persistent (shared cache)
+    _say("graph prompt + persistent generation")
+    dec.reset(prompt)
+    dec.run(len(prompt) - 1, mode="graph")
+    dec.run(n_new, mode="persistent")
+    mixed = dec.read(len(prompt) + n_new)
+    got = dec.teacher_forced_logits(one, mode="persistent")
+    _check_logits(got[:16], one, rcfg, w, "persistent greedy (own tokens)")
+    ref_ids, _ = qwen3_ref.greedy(rcfg, w, list(prompt), n_new)
+    match = np.mean(np.array(ref_ids) == one)
+    _say(f"greedy token match vs oracle {match:.2f}; mixed-mode match {np.mean(mixed == one):.2f}")
+    assert match >= 0.9, match
+    assert np.mean(mixed == one) >= 0.9
+
+
+def test_persistent_long_context(torch_dev):
+    """Contexts past 384 positions read part of each split's keys straight from
+    the cache instead of the prefetched registers."""
+    cfg, rcfg = _cfgs(max_seq=640)
+    dec, w = _decoder(cfg, seed=31)
+    ids = np.random.default_rng(32).integers(0, cfg.vocab, size=600).astype(np.int32)
+    dec.reset(ids)
+    tail = 4
+    _say("persistent long context: prompt")
+    dec.run(len(ids) - 1 - tail, mode="persistent")
+    got = []
+    for _ in range(tail):
+        dec.run(1, mode="persistent")
+        got.append(dec.read(0, with_logits=True)[1].copy())
+    _say("persistent long context: oracle")
+    r64 = qwen3_ref.Qwen3Ref(rcfg, w, np.float64)
+    r32 = qwen3_ref.Qwen3Ref(rcfg, w, np.float32)
+    for i, t in enumerate(ids[:-1]):
+        e64 = r64.step(int(t))
+        e32 = r32.step(int(t)).astype(np.float64)
+        k = i - (len(ids) - 1 - tail)
+        if k < 0:
+            continue
+        rms = float(np.sqrt(np.mean(e64 * e64)))
+        err = float(np.abs(got[k] - e64).max()) / rms
+        err32 = float(np.abs(e32 - e64).max()) / rms
+        _say(f"position {i}: err {err:.2e} (numpy fp32 {err32:.2e})")
+        assert err <= max(1e-4, 4 * err32), (i, err, err32)
+
+
+def test_persistent_c2_shape(torch_dev):
+    """Full Qwen3-0.6B shape (28 layers, vocab 151936)."""
+    cfg, rcfg = _cfgs(n_layers=28, vocab=151936, max_seq=384)
+    _say("persistent C2: building weights")
+    dec, w = _decoder(cfg, seed=41)
+    ids = np.random.default_rng(42).integers(0, cfg.vocab, size=7).astype(np.int32)
+    _say("persistent C2: teacher forced")
+    got = dec.teacher_forced_logits(ids, mode="persistent")
+    _check_logits(got, ids, rcfg, w, "persistent C2 teacher-forced")
+    _say("persistent C2: greedy persistent vs graph")
+    prompt = ids[:5]
+    a = dec.generate(prompt, 48, mode="persistent")
+    b = dec.generate(prompt, 48, mode="graph")
+    match = float(np.mean(a == b))
+    _say(f"persistent vs graph greedy token match {match:.2f}")
+    assert match >= 0.9
+
+
+def test_persistent_rejects_other_shapes(torch_dev):
+    from mod_amd.ops import RocmError
+    from mod_amd.qwen3 import Qwen3Config, Qwen3Int8Decoder, random_weights
+    cfg = Qwen3Config(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=128,
+                      intermediate=512, vocab=1000, max_seq=64)
+    dec = Qwen3Int8Decoder(cfg, random_weights(cfg, seed=5))
+    assert not dec.persistent_supported()
+    dec.reset(np.arange(4, dtype=np.int32))
+    with pytest.raises(RocmError):
+        dec.run(2, mode="persistent")
+    dec.run(2, mode="graph")   # the step path still serves it

@@ -129,6 +129,9 @@ __device__ __forceinline__ void dev_store(float* p, float v) {
 __device__ __forceinline__ int lds_ld(const int* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
+// Same word in every lane: read it as a scalar so that loop exits on it are
+// scalar branches (no exec-mask bookkeeping around every wait).
+__device__ __forceinline__ int lds_ld_u(const int* p) { return __builtin_amdgcn_readfirstlane(lds_ld(p)); }
 __device__ __forceinline__ void lds_st(int* p, int v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
@@ -228,6 +231,19 @@ __device__ __forceinline__ float sum_stride8(float x) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// 16 int8 weights times 16 fp32 x with signed byte conversions (one
+// v_cvt_f32_i32 with a sign-extending byte select each), 4 independent chains.
+__device__ __forceinline__ void lp_dot16s(const float* x, lp_v4i w, float (&acc)[4]) {
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        const int u = w[d];
+        acc[0] = fmaf(x[4 * d + 0], (float)(int8_t)(u), acc[0]);
+        acc[1] = fmaf(x[4 * d + 1], (float)(int8_t)(u >> 8), acc[1]);
+        acc[2] = fmaf(x[4 * d + 2], (float)(int8_t)(u >> 16), acc[2]);
+        acc[3] = fmaf(x[4 * d + 3], (float)(int8_t)(u >> 24), acc[3]);
+    }
+}
+
 // 16 int8 weights (one 16-byte lane slice of a line) times 16 fp32 x, into 4
 // independent accumulator chains (byte position within each dword): with one
 // compute wave per SIMD there is no other wave to hide a dependent chain's
@@ -304,7 +320,7 @@ __device__ void lp_fail(const LoopParams& p, int where) {
 // calls or long paths sit inside the wait loops.
 __device__ __forceinline__ bool keep_waiting(const LoopParams& p, Cx& c, uint32_t it, uint32_t limit,
                                              int where) {
-    if (lds_ld(c.abort)) return false;
+    if (lds_ld_u(c.abort)) return false;
     if ((it & 63) != 63) return true;
     if (__hip_atomic_load(&p.err[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) || it > limit) {
         if (it > limit) c.fail_where = where;
@@ -354,7 +370,7 @@ __device__ __forceinline__ bool csync(const LoopParams& p, Cx& c, int where) {
     cbar();
     if (c.lane == 0) __hip_atomic_fetch_add(c.csync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     const int target = LP_CW * c.nsync;
-    for (uint32_t it = 0; lds_ld(c.csync) < target; it++) {
+    for (uint32_t it = 0; lds_ld_u(c.csync) < target; it++) {
         if (!keep_waiting(p, c, it, LP_LDS_LIMIT, where)) return false;
         __builtin_amdgcn_s_sleep(1);
     }
@@ -368,7 +384,7 @@ __device__ __forceinline__ bool wait_upto(const LoopParams& p, Cx& c, int last, 
     for (uint32_t it = 0;; it++) {
         bool ok = true;
 #pragma unroll
-        for (int r = 0; r < LP_SW; r++) ok &= last < r || lds_ld(&c.ready[r]) >= ((last - r) >> 2) + 1;
+        for (int r = 0; r < LP_SW; r++) ok &= last < r || lds_ld_u(&c.ready[r]) >= ((last - r) >> 2) + 1;
         if (ok) break;
         if (!keep_waiting(p, c, it, LP_LDS_LIMIT, where)) return false;
         __builtin_amdgcn_s_sleep(1);
@@ -459,16 +475,13 @@ __device__ __forceinline__ bool phase_dots(const LoopParams& p, Cx& c, int line0
 #pragma unroll
             for (int ch = 0; ch < C; ch++)
                 wv[m][r][ch] = ring_line(c, line0 + (c.w + LP_CW * m) * lpu + r * C + ch);
-    float xoff = 0.f;
-#pragma unroll
-    for (int ch = 0; ch < C; ch++) xoff += lp_xoff(xr[ch]);
 #pragma unroll
     for (int m = 0; m < MU; m++) {
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            float s[4] = {xoff, 0.f, 0.f, 0.f};
+            float s[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ch = 0; ch < C; ch++) lp_dot16(xr[ch], wv[m][r][ch], s);
+            for (int ch = 0; ch < C; ch++) lp_dot16s(xr[ch], wv[m][r][ch], s);
             acc[m][r] = (s[0] + s[1]) + (s[2] + s[3]);
         }
     }

@@ -25,23 +25,34 @@ struct GemmParams {
     void* C;
     int64_t ldc, c_batch;
     int M, N, K;
+    int xr, xc;   // XCD rectangles: tile rows split xr ways, tile columns xc ways (xr*xc == 8), or 0
 };
 
 // ----------------------------------------------------------------- v2 ---
 // Dense W8A8 on the 32x32x32 engine. Block b is mapped XCD-aware: the
-// dispatcher places block b on XCD b % 8, so tile t = (b % 8) * T/8 + b / 8
-// gives each XCD a contiguous run of T/8 row-major tiles whose A and B rows
-// stay in that XCD's L2 (identity map when T % 8 != 0).
+// dispatcher places block b on XCD b % 8, so each XCD is given one rectangle
+// of the tile grid (tile rows split xr ways, columns xc ways, chosen on the
+// host to minimize the A + B panel bytes one XCD's L2 has to hold); inside it,
+// the XCD's blocks walk the rectangle row by row. Identity map when the grid
+// does not split into 8 rectangles.
 // STAGES == 0: register-staged v2 engine (any K % 16 == 0); otherwise the
 // direct-to-LDS v3 engine with that many stages (K % 128 == 0).
 template <int WMT, int WNT, int OUT, int STAGES>
 __global__ __launch_bounds__(256, 1) void gemm_v2_kernel(GemmParams p, int tiles_n) {
     using T = TileV2<WMT, WNT>;
     extern __shared__ __attribute__((aligned(16))) int8_t lds_v2[];
-    const int tiles = gridDim.x;
     const int b = blockIdx.x;
-    const int t = (tiles % 8 == 0) ? (b % 8) * (tiles / 8) + b / 8 : b;
-    const int m0 = (t / tiles_n) * T::BM, n0 = (t % tiles_n) * T::BN, z = blockIdx.z;
+    int tr, tc;
+    if (p.xr) {
+        const int x = b % 8, k = b / 8;
+        const int R = ((int)gridDim.x / tiles_n) / p.xr, Cc = tiles_n / p.xc;
+        tr = (x / p.xc) * R + k / Cc;
+        tc = (x % p.xc) * Cc + k % Cc;
+    } else {
+        tr = b / tiles_n;
+        tc = b % tiles_n;
+    }
+    const int m0 = tr * T::BM, n0 = tc * T::BN, z = blockIdx.z;
     constexpr bool SCALED = (OUT == OUT_F32 || OUT == OUT_F16);
     // Interior tiles (the common case) take a branch-free epilogue: with no
     // per-element bounds checks the stores issue back to back, while a
@@ -72,8 +83,12 @@ __global__ __launch_bounds__(256, 1) void gemm_v2_kernel(GemmParams p, int tiles
             p.A + z * p.a_batch + (int64_t)m0 * p.lda, p.lda, p.M - m0,
             p.B + z * p.b_batch + (int64_t)n0 * p.ldb, p.ldb, p.N - n0, p.K, lds_v2, acc);
     char* C = (char*)p.C + z * p.c_batch * (OUT == OUT_F16 ? 2 : 4);
-    auto store = [&](int i, int j, int e, int m, int n) {
-        const int64_t off = (int64_t)m * p.ldc + n;
+    const bool has_bias = SCALED && p.bias;
+    // off = m * ldc + n in 32 bits when the whole output fits (it does at every
+    // shape this path serves; the 64-bit form stays for the rest)
+    const bool small = (int64_t)p.M * p.ldc < (int64_t)INT32_MAX;
+    auto store = [&](int i, int j, int e, int m, int n, bool bias) {
+        const int64_t off = small ? (int64_t)(m * (int)p.ldc + n) : (int64_t)m * p.ldc + n;
         const int a = acc[i][j][e];
         if (OUT == OUT_I32) {
             ((int32_t*)C)[off] = a;
@@ -81,19 +96,27 @@ __global__ __launch_bounds__(256, 1) void gemm_v2_kernel(GemmParams p, int tiles
             ((float*)C)[off] = (float)a;
         } else {
             float val = (float)a * sa[i][e] * sw[j];
-            if (p.bias) val += bn[j];
+            if (bias) val += bn[j];
+            // val is rounded to f32 before the f16 store, as the reference
+            // computes it: without the operand barrier fmul+fptrunc becomes
+            // one v_fma_mix that rounds once, straight to f16
+            if (OUT == OUT_F16) asm volatile("" : "+v"(val));
             if (OUT == OUT_F32) ((float*)C)[off] = val;
             else ((_Float16*)C)[off] = (_Float16)val;
         }
     };
     if (full) {
+        auto all = [&](bool bias) {
 #pragma unroll
-        for (int j = 0; j < WNT; j++)
+            for (int j = 0; j < WNT; j++)
 #pragma unroll
-            for (int i = 0; i < WMT; i++)
+                for (int i = 0; i < WMT; i++)
 #pragma unroll
-                for (int e = 0; e < 16; e++)
-                    store(i, j, e, m0 + v2_row<WMT>(i, e), n0 + v2_col<WNT>(j));
+                    for (int e = 0; e < 16; e++)
+                        store(i, j, e, m0 + v2_row<WMT>(i, e), n0 + v2_col<WNT>(j), bias);
+        };
+        if (has_bias) all(true);
+        else all(false);
     } else {
 #pragma unroll
         for (int j = 0; j < WNT; j++) {
@@ -104,7 +127,7 @@ __global__ __launch_bounds__(256, 1) void gemm_v2_kernel(GemmParams p, int tiles
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
                     const int m = m0 + v2_row<WMT>(i, e);
-                    if (m < p.M) store(i, j, e, m, n);
+                    if (m < p.M) store(i, j, e, m, n, has_bias);
                 }
         }
     }
@@ -149,11 +172,26 @@ static int launch_v2_s(const GemmParams& p, int out_mode, dim3 grid, int tn, hip
     }
 }
 
+// XCD rectangle split of a tm x tn tile grid: the (xr, xc), xr * xc = 8,
+// with the fewest A + B rows per rectangle; (0, 0) if none divides the grid.
+static void xcd_split(int tm, int tn, int BM, int BN, int& xr, int& xc) {
+    xr = xc = 0;
+    int64_t best = -1;
+    for (int r = 1; r <= 8; r *= 2) {
+        const int c = 8 / r;
+        if (tm % r || tn % c) continue;
+        const int64_t rows = (int64_t)(tm / r) * BM + (int64_t)(tn / c) * BN;
+        if (best < 0 || rows < best) { best = rows; xr = r; xc = c; }
+    }
+}
+
 template <int WMT, int WNT>
-static int launch_v2(const GemmParams& p, int out_mode, int batch, hipStream_t st) {
+static int launch_v2(const GemmParams& p0, int out_mode, int batch, hipStream_t st) {
     using T = TileV2<WMT, WNT>;
-    const int tn = ceil_div(p.N, T::BN), tm = ceil_div(p.M, T::BM);
+    const int tn = ceil_div(p0.N, T::BN), tm = ceil_div(p0.M, T::BM);
     dim3 grid(tm * tn, 1, batch);
+    GemmParams p = p0;
+    xcd_split(tm, tn, T::BM, T::BN, p.xr, p.xc);
     const bool direct = (p.K % 128 == 0) && aligned16(p.A) && aligned16(p.B) &&
                         p.lda % 16 == 0 && p.ldb % 16 == 0 && !getenv("PIO_GEMM_NO_DIRECT");
     if (direct) return launch_v2_s<WMT, WNT, v3_stages<WMT, WNT>()>(p, out_mode, grid, tn, st);

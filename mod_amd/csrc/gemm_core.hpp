@@ -198,18 +198,22 @@ __device__ __forceinline__ void mma_tile_v3(const int8_t* __restrict__ A, int64_
         gb[j] = B + (int64_t)min(r, n_rem - 1) * ldb + c * 16;
     }
     typedef __attribute__((address_space(3))) void lds_t;
-    auto issue = [&](int kstep) {
+    // Issues this wave's loads number [from, to) of K step `kstep` (its A
+    // blocks first, then its B blocks).
+    auto issue = [&](int kstep, int from, int to) {
         int8_t* base = lds + (kstep % S) * T::STAGE;
         const int k0 = kstep * T::BK;
 #pragma unroll
         for (int j = 0; j < T::A_PER_WAVE; j++)
-            __builtin_amdgcn_global_load_lds((const void*)(ga[j] + k0),
-                                             (lds_t*)(base + (j * 4 + wave) * 1024), 16, 0, 0);
+            if (j >= from && j < to)
+                __builtin_amdgcn_global_load_lds((const void*)(ga[j] + k0),
+                                                 (lds_t*)(base + (j * 4 + wave) * 1024), 16, 0, 0);
 #pragma unroll
         for (int j = 0; j < T::B_PER_WAVE; j++)
-            __builtin_amdgcn_global_load_lds((const void*)(gb[j] + k0),
-                                             (lds_t*)(base + T::BM * 128 + (j * 4 + wave) * 1024),
-                                             16, 0, 0);
+            if (T::A_PER_WAVE + j >= from && T::A_PER_WAVE + j < to)
+                __builtin_amdgcn_global_load_lds((const void*)(gb[j] + k0),
+                                                 (lds_t*)(base + T::BM * 128 + (j * 4 + wave) * 1024),
+                                                 16, 0, 0);
     };
 
 #pragma unroll
@@ -222,31 +226,39 @@ __device__ __forceinline__ void mma_tile_v3(const int8_t* __restrict__ A, int64_
     const int nk = K / T::BK;
 #pragma unroll
     for (int s = 0; s < S - 1; s++)
-        if (s < nk) issue(s);
+        if (s < nk) issue(s, 0, T::A_PER_WAVE + T::B_PER_WAVE);
     const int fr = lane & 31, fh = lane >> 5;
+    // Fragments of k sub-step ks of the current stage; double-buffered so the
+    // next sub-step's LDS reads are in flight while this one's MFMAs run.
+    auto frag = [&](const int8_t* base, int ks, v4i (&a)[WMT], v4i (&b)[WNT]) {
+        const int c = 2 * ks + fh;
+#pragma unroll
+        for (int i = 0; i < WMT; i++) a[i] = *(const v4i*)(base + swz(wm * 32 * WMT + i * 32 + fr, c));
+#pragma unroll
+        for (int j = 0; j < WNT; j++)
+            b[j] = *(const v4i*)(base + T::BM * 128 + swz(wn * 32 * WNT + j * 32 + fr, c));
+    };
     for (int kt = 0; kt < nk; kt++) {
         // Stages issued so far: min(nk, kt + S - 1); wait for stage kt.
         const int ahead = min(nk, kt + S - 1) - kt - 1;
         if (S >= 4 && ahead >= 2) stage_barrier<(S >= 4 ? 2 : 0) * T::LOADS>();
         else if (ahead >= 1) stage_barrier<T::LOADS>();
         else stage_barrier<0>();
-        if (kt + S - 1 < nk) issue(kt + S - 1);
+        const bool more = kt + S - 1 < nk;
         const int8_t* base = lds + (kt % S) * T::STAGE;
+        v4i fa[2][WMT], fb[2][WNT];
+        frag(base, 0, fa[0], fb[0]);
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
-            const int c = 2 * ks + fh;
-            v4i a[WMT], b[WNT];
-#pragma unroll
-            for (int i = 0; i < WMT; i++)
-                a[i] = *(const v4i*)(base + swz(wm * 32 * WMT + i * 32 + fr, c));
-#pragma unroll
-            for (int j = 0; j < WNT; j++)
-                b[j] = *(const v4i*)(base + T::BM * 128 + swz(wn * 32 * WNT + j * 32 + fr, c));
+            if (ks < 3) frag(base, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
+            // a quarter of the next stage's global->LDS copies per sub-step
+            if (more) issue(kt + S - 1, ks * T::LOADS / 4, (ks + 1) * T::LOADS / 4);
 #pragma unroll
             for (int i = 0; i < WMT; i++)
 #pragma unroll
                 for (int j = 0; j < WNT; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[ks & 1][i], fb[ks & 1][j],
+                                                                      acc[i][j], 0, 0, 0);
         }
     }
 }

@@ -155,42 +155,10 @@ __device__ __forceinline__ void wait_vm() {
     cbar();
 }
 
-// ---- cross-lane ops on the VALU (DPP, permlane swaps, readlane). The LDS
-// queue (where __shfl's ds_swizzle / ds_bpermute go) is busy with the stream
-// waves' copies, so every reduction here avoids it.
-template <int CTRL>
-__device__ __forceinline__ float dpp(float x) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float rlane(float x, int i) {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), i));
-}
-enum : int {
-    DPP_XOR1 = 0xB1,       // quad_perm [1,0,3,2]
-    DPP_XOR2 = 0x4E,       // quad_perm [2,3,0,1]
-    DPP_ROR8 = 0x128,      // row_ror:8 (lane i <- lane i^8 within a 16-lane row)
-    DPP_MIRROR = 0x140,    // row_mirror (i <- 15-i)
-    DPP_HMIRROR = 0x141,   // row_half_mirror (i <- 7-i within 8)
-};
-// Sum over each group of 8 consecutive lanes, in every lane of the group.
-__device__ __forceinline__ float sum8(float x) {
-    x += dpp<DPP_XOR1>(x);
-    x += dpp<DPP_XOR2>(x);
-    return x + dpp<DPP_HMIRROR>(x);
-}
-// Sum over all 64 lanes (same value, bit for bit, in every lane).
-__device__ __forceinline__ float wsum(float x) {
-    x = sum8(x);
-    x += dpp<DPP_MIRROR>(x);
-    return (rlane(x, 0) + rlane(x, 16)) + (rlane(x, 32) + rlane(x, 48));
-}
-__device__ __forceinline__ float wmax(float x) {
-    x = fmaxf(x, dpp<DPP_XOR1>(x));
-    x = fmaxf(x, dpp<DPP_XOR2>(x));
-    x = fmaxf(x, dpp<DPP_HMIRROR>(x));
-    x = fmaxf(x, dpp<DPP_MIRROR>(x));
-    return fmaxf(fmaxf(rlane(x, 0), rlane(x, 16)), fmaxf(rlane(x, 32), rlane(x, 48)));
-}
+// ---- cross-lane ops on the VALU (DPP, permlane swaps, readlane; dpp, rlane,
+// sum8, wsum and wmax come from pio_common.hpp). The LDS queue (where __shfl's
+// ds_swizzle / ds_bpermute go) is busy with the stream waves' copies, so every
+// reduction here avoids it.
 // Four wave sums at once (each returned uniform): halves, then quarters are
 // folded together with lane swaps so that lane rows 0..3 hold a, b, c, d, and a
 // single 16-lane DPP reduction finishes all four.

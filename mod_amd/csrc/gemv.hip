@@ -2,16 +2,16 @@
 //   y[m,n] = s_w[n] * sum_k x[m,k] * float(W[n,k]) (+ bias[n])
 // W int8 [N,K] row-major, x fp32|fp16 [M,K], y fp32|fp16 [M,N].
 //
-// The op is HBM-bound: every weight byte is used M times (M <= 8 per launch).
-// Mapping: a wavefront owns R consecutive output rows; lane l covers the 16
-// bytes k = c*1024 + 16*l of each row in K-chunk c, so one 64-lane load
-// instruction (global_load_dwordx4) fetches 1 KiB contiguous of one row and the
-// R rows give R independent 16 B loads in flight per lane. The matching 16 x
-// values are loaded once per chunk and reused across the R rows. Bytes are
-// converted with v_cvt_f32_i32_sdwa (sign-extended byte select, 1 VALU op) and
-// accumulated with fp32 FMA; the per-channel scale is applied once per output
-// after the cross-lane reduction. Requires K % 16 == 0 and 16 B aligned rows.
+// The op is HBM-bound: every weight byte is used M times (M <= 4 per launch).
+// The stream kernel (gemv_w8_stream_kernel) keeps x in LDS and streams the
+// weights with persistent waves; the direct kernel (gemv_w8_direct_kernel)
+// takes the shapes whose x does not fit the LDS. Both convert each weight byte to fp32 once (v_cvt_f32_i32_sdwa,
+// sign-extended byte select), accumulate in fp32 FMA, and apply the
+// per-channel scale once per output after the cross-lane reduction. Requires
+// K % 16 == 0 and 16 B aligned x and W rows.
 #include "pio_common.hpp"
+
+#include <algorithm>
 
 namespace pio {
 
@@ -50,14 +50,17 @@ __device__ __forceinline__ float dot16(const float (&x)[16], v4i w, float acc) {
     return acc;
 }
 
-// R rows per wave, MT x-rows per launch, 4 waves per block.
+// Direct kernel: a wave owns R consecutive output rows; lane l covers the 16
+// bytes k = c*1024 + 16*l of each row in K-chunk c (one 64-lane 16 B load
+// fetches 1 KiB contiguous of a row), with the matching 16 x values loaded
+// from global memory once per chunk and reused across the R rows. MT x-rows
+// per launch, 4 waves per block.
 template <int R, int MT, typename XT, typename YT>
-__global__ __launch_bounds__(256) void gemv_w8_kernel(const XT* __restrict__ x,
-                                                      const int8_t* __restrict__ W,
-                                                      const float* __restrict__ s_w,
-                                                      const float* __restrict__ bias,
-                                                      const float* residual,
-                                                      YT* y, int N, int K, int ldy) {
+__global__ __launch_bounds__(256) void gemv_w8_direct_kernel(const XT* __restrict__ x,
+                                                             const int8_t* __restrict__ W,
+                                                             const float* __restrict__ s_w,
+                                                             const float* __restrict__ bias,
+                                                             YT* y, int N, int K, int ldy) {
     const int lane = threadIdx.x & 63;
     const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
     if (n0 >= N) return;
@@ -98,48 +101,270 @@ __global__ __launch_bounds__(256) void gemv_w8_kernel(const XT* __restrict__ x,
             if (lane == m * R + r && n0 + r < N) {
                 float v = acc[m][r] * s_w[n0 + r];
                 if (bias) v += bias[n0 + r];
-                // residual may alias y (in-place x += W x'): same lane reads then writes.
-                if (residual) v += residual[(int64_t)m * ldy + n0 + r];
                 y[(int64_t)m * ldy + n0 + r] = from_f32<YT>(v);
             }
         }
 }
 
+// ---------------------------------------------------------------- v2 ---
+// Persistent weight stream. A block of GEMV_WAVES waves stages x once in LDS;
+// each wave then walks its row groups (R rows each; group g goes to wave
+// g % n_waves, so the waves in flight read neighbouring rows) and, per step,
+// issues the 16 B loads of U 1 KiB chunks of each of its R rows -- every load
+// unconditional, addresses clamped into the weight, so the compiler counts
+// them and waits for each in order as the math consumes it -- then converts and
+// accumulates them. Overlap of memory and math comes from the 16 resident
+// waves per CU (4 per SIMD) rather than from software pipelining: plain
+// 16 B loads into VGPRs stream from HBM faster here than LDS-DMA copies, and a
+// loop-carried register double buffer makes the compiler wait for all loads.
+// x in LDS is fp32 and lane-transposed: K-chunk c of x row m sits at
+// xs[(m*nch + c)*1024], and within it the 4 floats a lane needs for its j-th
+// 16 B read sit at j*256 + lane*4, so each of a lane's four ds_read_b128 per
+// chunk reads 64 lanes' contiguous 16 B (no bank conflicts). Each weight byte
+// is converted to fp32 once and used for the MT x rows.
+constexpr int GEMV_WAVES = 16;                // waves per block = resident waves per CU
+constexpr int GEMV_XLDS = 64 * 1024;          // x bytes the LDS stage takes
+
+template <typename XT>
+__device__ __forceinline__ void load_x4(const XT* p, float (&v)[4]);
+template <>
+__device__ __forceinline__ void load_x4<float>(const float* p, float (&v)[4]) {
+    const float4 a = *(const float4*)p;
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+}
+template <>
+__device__ __forceinline__ void load_x4<_Float16>(const _Float16* p, float (&v)[4]) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 h = *(const h4*)p;
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] = (float)h[j];
+}
+
 template <int R, int MT, typename XT, typename YT>
-static void launch_gemv(const XT* x, const int8_t* w, const float* s_w, const float* bias,
-                        const float* res, YT* y, int N, int K, hipStream_t st) {
-    dim3 grid(ceil_div(N, 4 * R)), block(256);
-    gemv_w8_kernel<R, MT, XT, YT><<<grid, block, 0, st>>>(x, w, s_w, bias, res, y, N, K, N);
+__global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_w8_stream_kernel(const XT* __restrict__ x,
+                                                                      const int8_t* __restrict__ W,
+                                                                      const float* __restrict__ s_w,
+                                                                      const float* __restrict__ bias,
+                                                                      YT* y, int N, int K, int ldy) {
+    constexpr int U = 4 / R;   // 1 KiB chunks per row per step: 4 loads per lane
+    extern __shared__ __attribute__((aligned(16))) float xs[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int nch = (K + 1023) >> 10;
+    const int nst = (nch + U - 1) / U;
+    const int ngroups = (N + R - 1) / R;
+    // waves numbered block-fastest, so a grid with fewer row groups than waves
+    // still spreads them over every block (CU)
+    const int wave_id = (tid >> 6) * gridDim.x + blockIdx.x, n_waves = gridDim.x * GEMV_WAVES;
+
+    // loads of U chunks of the R rows of group g at step st (addresses clamped
+    // into the weight: every load is issued)
+    auto load = [&](int g, int st, v4i (&w)[U][R]) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int k = min(min(st * U + u, nch - 1) * 1024 + lane * 16, K - 16);
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                w[u][r] = __builtin_nontemporal_load((const v4i*)(W + (int64_t)min(g * R + r, N - 1) * K + k));
+        }
+    };
+    float acc[MT][R];
+    auto math = [&](int st, const v4i (&w)[U][R]) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int c = st * U + u;
+            if (c >= nch) continue;   // wave-uniform: a clamped duplicate chunk
+            float xv[MT][16];
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+                const float* src = xs + (m * nch + c) * 1024 + lane * 4;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float4 q = *(const float4*)(src + j * 256);
+                    xv[m][4 * j + 0] = q.x; xv[m][4 * j + 1] = q.y;
+                    xv[m][4 * j + 2] = q.z; xv[m][4 * j + 3] = q.w;
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                float wf[16];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int v = w[u][r][e];
+                    wf[4 * e + 0] = (float)(int8_t)v;
+                    wf[4 * e + 1] = (float)(int8_t)(v >> 8);
+                    wf[4 * e + 2] = (float)(int8_t)(v >> 16);
+                    wf[4 * e + 3] = (float)(v >> 24);
+                }
+#pragma unroll
+                for (int m = 0; m < MT; m++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) acc[m][r] = fmaf(xv[m][e], wf[e], acc[m][r]);
+            }
+        }
+    };
+    // lane m*R + r writes output (m, g*R + r)
+    auto finish = [&](int g) {
+        const int n0 = g * R;
+        float mine = 0.f;
+#pragma unroll
+        for (int m = 0; m < MT; m++)
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const float t = wsum(acc[m][r]);
+                if (lane == m * R + r) mine = t;
+                acc[m][r] = 0.f;
+            }
+        const int em = lane / R, er = lane % R;
+        if (lane < MT * R && n0 + er < N) {
+            float v = mine * s_w[n0 + er];
+            if (bias) v += bias[n0 + er];
+            y[(int64_t)em * ldy + n0 + er] = from_f32<YT>(v);
+        }
+    };
+
+    // the first step's weights are requested before x is staged, so the two
+    // latencies overlap
+    v4i w0[U][R];
+    load(min(wave_id, ngroups - 1), 0, w0);
+    for (int q = tid; q < MT * nch * 256; q += 64 * GEMV_WAVES) {
+        const int m = q / (nch * 256), k = (q - m * nch * 256) * 4;
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        if (k < K) load_x4<XT>(x + (int64_t)m * K + k, v);
+        float* d = xs + (m * nch + (k >> 10)) * 1024 + ((k & 15) >> 2) * 256 + ((k & 1023) >> 4) * 4;
+        *(float4*)d = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    __syncthreads();
+    if (wave_id >= ngroups) return;
+
+#pragma unroll
+    for (int m = 0; m < MT; m++)
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[m][r] = 0.f;
+    math(0, w0);
+    for (int st = 1; st < nst; st++) {
+        v4i w[U][R];
+        load(wave_id, st, w);
+        math(st, w);
+    }
+    finish(wave_id);
+    for (int g = wave_id + n_waves; g < ngroups; g += n_waves) {
+        for (int st = 0; st < nst; st++) {
+            v4i w[U][R];
+            load(g, st, w);
+            math(st, w);
+        }
+        finish(g);
+    }
+}
+
+static int device_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    return cus;
+}
+
+// Fraction of wave-rounds doing work when ceil(N/R) row groups are dealt to
+// the resident waves round-robin.
+static double stream_balance(int N, int R) {
+    const int64_t waves = (int64_t)device_cus() * GEMV_WAVES;
+    const int64_t groups = ceil_div(N, R);
+    const int64_t rounds = (groups + waves - 1) / waves;
+    return (double)groups / (double)(rounds * waves);
+}
+
+// Rows per group for the stream kernel: among R = 4, 2, 1 (U = 4/R chunks
+// per step), those whose U divides the row's chunk count first (no duplicate
+// chunk loads), then the best-balanced round-robin, ties to more rows (each x
+// value read from LDS then serves more weight rows). 0: x does not fit the LDS.
+static int stream_pick(int MT, int N, int K) {
+    const int nch = (K + 1023) / 1024;
+    if ((size_t)MT * nch * 4096 > (size_t)GEMV_XLDS) return 0;
+    double best = -1;
+    int pick = 0;
+    for (int R : {4, 2, 1}) {
+        if (R * MT > 8) continue;   // 4 rows x 4 x-rows: more registers than 16 waves per CU leave
+        const int U = 4 / R;
+        double e = stream_balance(N, R) - (nch % U ? 1.0 : 0.0);
+        if (e > best + 1e-9) { best = e; pick = R; }
+    }
+    return pick;
+}
+
+template <int R, int MT, typename XT, typename YT>
+static int launch_stream_r(const XT* x, const int8_t* w, const float* s_w, const float* bias, YT* y,
+                           int N, int K, hipStream_t st) {
+    const size_t lds = (size_t)MT * ((K + 1023) / 1024) * 4096;
+    const int blocks = (int)std::min<int64_t>(ceil_div(N, R), device_cus());
+    gemv_w8_stream_kernel<R, MT, XT, YT><<<blocks, 64 * GEMV_WAVES, lds, st>>>(x, w, s_w, bias, y, N, K, N);
+    return PIO_OK;
+}
+
+template <int MT, typename XT, typename YT>
+static int launch_stream(const XT* x, const int8_t* w, const float* s_w, const float* bias, YT* y,
+                         int N, int K, int R, hipStream_t st) {
+    if constexpr (MT * 4 <= 8) {
+        if (R == 4) return launch_stream_r<4, MT>(x, w, s_w, bias, y, N, K, st);
+    }
+    if (R == 2) return launch_stream_r<2, MT>(x, w, s_w, bias, y, N, K, st);
+    return launch_stream_r<1, MT>(x, w, s_w, bias, y, N, K, st);
+}
+
+template <int R, int MT, typename XT, typename YT>
+static void launch_direct(const XT* x, const int8_t* w, const float* s_w, const float* bias, YT* y,
+                          int N, int K, hipStream_t st) {
+    gemv_w8_direct_kernel<R, MT, XT, YT><<<ceil_div(N, 4 * R), 256, 0, st>>>(x, w, s_w, bias, y, N, K, N);
 }
 
 template <int R, typename XT, typename YT>
-static void launch_rows(const XT* x, const int8_t* w, const float* s_w, const float* bias,
-                        const float* res, YT* y, int M, int N, int K, hipStream_t st) {
-    // x rows are processed in launches of up to 8; each launch re-streams W.
+static void launch_direct_rows(const XT* x, const int8_t* w, const float* s_w, const float* bias,
+                               YT* y, int M, int N, int K, hipStream_t st) {
+    // x rows in launches of up to 8; each launch re-streams W
     for (int m0 = 0; m0 < M;) {
         const int left = M - m0;
         const XT* xm = x + (int64_t)m0 * K;
         YT* ym = y + (int64_t)m0 * N;
-        const float* rm = res ? res + (int64_t)m0 * N : nullptr;
-        if (left >= 8) { launch_gemv<R, 8>(xm, w, s_w, bias, rm, ym, N, K, st); m0 += 8; }
-        else if (left >= 4) { launch_gemv<R, 4>(xm, w, s_w, bias, rm, ym, N, K, st); m0 += 4; }
-        else if (left >= 2) { launch_gemv<R, 2>(xm, w, s_w, bias, rm, ym, N, K, st); m0 += 2; }
-        else { launch_gemv<R, 1>(xm, w, s_w, bias, rm, ym, N, K, st); m0 += 1; }
+        if (left >= 8) { launch_direct<R, 8>(xm, w, s_w, bias, ym, N, K, st); m0 += 8; }
+        else if (left >= 4) { launch_direct<R, 4>(xm, w, s_w, bias, ym, N, K, st); m0 += 4; }
+        else if (left >= 2) { launch_direct<R, 2>(xm, w, s_w, bias, ym, N, K, st); m0 += 2; }
+        else { launch_direct<R, 1>(xm, w, s_w, bias, ym, N, K, st); m0 += 1; }
     }
 }
 
 template <typename XT, typename YT>
-static void dispatch_r(const XT* x, const int8_t* w, const float* s_w, const float* bias,
-                       const float* res, YT* y, int M, int N, int K, hipStream_t st) {
-    // Few rows -> fewer rows per wave so the grid still spreads over 256 CUs.
-    if (N >= 32768) launch_rows<4>(x, w, s_w, bias, res, y, M, N, K, st);
-    else launch_rows<2>(x, w, s_w, bias, res, y, M, N, K, st);
+static int dispatch(const XT* x, const int8_t* w, const float* s_w, const float* bias, YT* y,
+                    int M, int N, int K, hipStream_t st) {
+    if (stream_pick(1, N, K)) {
+        // x rows in launches of up to 4 (as many as the LDS takes); each launch re-streams W
+        for (int m0 = 0; m0 < M;) {
+            const int left = M - m0;
+            const XT* xm = x + (int64_t)m0 * K;
+            YT* ym = y + (int64_t)m0 * N;
+            int rc, R;
+            if (left >= 4 && (R = stream_pick(4, N, K))) {
+                rc = launch_stream<4>(xm, w, s_w, bias, ym, N, K, R, st); m0 += 4;
+            } else if (left >= 2 && (R = stream_pick(2, N, K))) {
+                rc = launch_stream<2>(xm, w, s_w, bias, ym, N, K, R, st); m0 += 2;
+            } else {
+                R = stream_pick(1, N, K);
+                rc = launch_stream<1>(xm, w, s_w, bias, ym, N, K, R, st); m0 += 1;
+            }
+            if (rc != PIO_OK) return rc;
+        }
+        return PIO_OK;
+    }
+    // few rows -> fewer rows per wave so the grid still spreads over the CUs
+    if (N >= 32768) launch_direct_rows<4>(x, w, s_w, bias, y, M, N, K, st);
+    else launch_direct_rows<2>(x, w, s_w, bias, y, M, N, K, st);
+    return PIO_OK;
 }
 
-// GEMV with an optional fp32 residual added in the epilogue (y may alias it;
-// y must then be fp32).
-int gemv_w8_res(const void* x, int x_dtype, const int8_t* w, const float* s_w, const float* bias,
-                const float* res, void* y, int y_dtype, int M, int N, int K, hipStream_t st) {
+int gemv_w8(const void* x, int x_dtype, const int8_t* w, const float* s_w, const float* bias,
+            void* y, int y_dtype, int M, int N, int K, hipStream_t st) {
     PIO_REQUIRE(x && w && s_w && y, "gemv_w8: null pointer");
     PIO_REQUIRE(M >= 0 && N >= 0 && K >= 0, "gemv_w8: negative shape");
     PIO_REQUIRE(K % 16 == 0, "gemv_w8: K=%d must be a multiple of 16", K);
@@ -147,20 +372,17 @@ int gemv_w8_res(const void* x, int x_dtype, const int8_t* w, const float* s_w, c
     PIO_REQUIRE(x_dtype == PIO_F32 || x_dtype == PIO_F16, "gemv_w8: x must be fp32 or fp16");
     PIO_REQUIRE(y_dtype == PIO_F32 || y_dtype == PIO_F16, "gemv_w8: y must be fp32 or fp16");
     if (M == 0 || N == 0) return PIO_OK;
+    int rc;
     if (x_dtype == PIO_F32) {
-        if (y_dtype == PIO_F32) dispatch_r((const float*)x, w, s_w, bias, res, (float*)y, M, N, K, st);
-        else dispatch_r((const float*)x, w, s_w, bias, res, (_Float16*)y, M, N, K, st);
+        if (y_dtype == PIO_F32) rc = dispatch((const float*)x, w, s_w, bias, (float*)y, M, N, K, st);
+        else rc = dispatch((const float*)x, w, s_w, bias, (_Float16*)y, M, N, K, st);
     } else {
-        if (y_dtype == PIO_F32) dispatch_r((const _Float16*)x, w, s_w, bias, res, (float*)y, M, N, K, st);
-        else dispatch_r((const _Float16*)x, w, s_w, bias, res, (_Float16*)y, M, N, K, st);
+        if (y_dtype == PIO_F32) rc = dispatch((const _Float16*)x, w, s_w, bias, (float*)y, M, N, K, st);
+        else rc = dispatch((const _Float16*)x, w, s_w, bias, (_Float16*)y, M, N, K, st);
     }
+    if (rc != PIO_OK) return rc;
     PIO_LAUNCHED();
     return PIO_OK;
-}
-
-int gemv_w8(const void* x, int x_dtype, const int8_t* w, const float* s_w, const float* bias,
-            void* y, int y_dtype, int M, int N, int K, hipStream_t st) {
-    return gemv_w8_res(x, x_dtype, w, s_w, bias, nullptr, y, y_dtype, M, N, K, st);
 }
 
 }  // namespace pio

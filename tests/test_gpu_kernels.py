@@ -91,6 +91,49 @@ def test_gemv_shapes(env, M, N, K, xdt, ydt, bias):
                1e-2 if (ydt == np.float16 or xdt == np.float16) else 1e-3, "gemv")
 
 
+@pytest.mark.parametrize("M,N,K,xdt", [
+    (1, 151936, 1024, np.float16),   # lm_head-sized N: many row groups per wave
+    (5, 20000, 4096, np.float16),    # 4 + 1 x rows
+    (1, 50001, 3072, np.float32),    # 4-row groups, ragged last group
+])
+def test_gemv_many_row_groups(env, M, N, K, xdt):
+    """Large N: every persistent wave walks many row groups; every output must
+    be written exactly once with the oracle's value (y starts as NaN)."""
+    torch, ops, d = env
+    _say(f"gemv many groups M={M} N={N} K={K}")
+    x, W, s = _inputs(N + K, M, N, K, xdt)
+    y = torch.full((M, N), float("nan"), dtype=torch.float32, device=d)
+    ops.gemv_w8(dev(torch, x, d), dev(torch, W, d), dev(torch, s, d), None, y, M, N, K)
+    sync(torch)
+    got = host(y)
+    assert np.isfinite(got).all(), "an output row was never written"
+    assert_rel(got, oracle.gemv_w8(x, W, s), 1e-2 if xdt == np.float16 else 1e-3, "gemv many groups")
+
+
+def test_gemv_repeated_launches_identical(env):
+    """Back-to-back launches, interleaved with another shape, give
+    bit-identical outputs (each output's sum has one fixed order)."""
+    torch, ops, d = env
+    M, N, K = 1, 40000, 2048
+    x, W, s = _inputs(11, M, N, K)
+    xd, wd, sd = dev(torch, x, d), dev(torch, W, d), dev(torch, s, d)
+    x2, W2, s2 = _inputs(12, 2, 3000, 1024)
+    outs = []
+    for i in range(70):
+        y = torch.empty((M, N), dtype=torch.float32, device=d)
+        ops.gemv_w8(xd, wd, sd, None, y, M, N, K)
+        if i % 7 == 0:
+            y2 = torch.empty((2, 3000), dtype=torch.float32, device=d)
+            ops.gemv_w8(dev(torch, x2, d), dev(torch, W2, d), dev(torch, s2, d), None, y2, 2, 3000, 1024)
+        if i % 10 == 0:
+            outs.append(y)
+    sync(torch)
+    first = host(outs[0])
+    for o in outs[1:]:
+        assert np.array_equal(host(o).view(np.uint32), first.view(np.uint32))
+    assert_rel(first, oracle.gemv_w8(x, W, s), 1e-3, "gemv repeated")
+
+
 def test_gemv_extreme_weights(env):
     torch, ops, d = env
     M, N, K = 1, 64, 2048

@@ -35,9 +35,10 @@ struct GemmParams {
 // host to minimize the A + B panel bytes one XCD's L2 has to hold); inside it,
 // the XCD's blocks walk the rectangle row by row. Identity map when the grid
 // does not split into 8 rectangles.
-// STAGES == 0: register-staged v2 engine (any K % 16 == 0); otherwise the
-// direct-to-LDS v3 engine with that many stages (K % 128 == 0).
-template <int WMT, int WNT, int OUT, int STAGES>
+// ENG 2: register-staged v2 engine (any K % 16 == 0); 3: direct-to-LDS v3
+// engine with S stages (K % 128 == 0); 4: direct-to-LDS v4 engine, square
+// tiles, half-step ring (K % 128 == 0).
+template <int WMT, int WNT, int OUT, int ENG, int S>
 __global__ __launch_bounds__(256, 1) void gemm_v2_kernel(GemmParams p, int tiles_n) {
     using T = TileV2<WMT, WNT>;
     extern __shared__ __attribute__((aligned(16))) int8_t lds_v2[];
@@ -58,10 +59,13 @@ __global__ __launch_bounds__(256, 1) void gemm_v2_kernel(GemmParams p, int tiles
     // per-element bounds checks the stores issue back to back, while a
     // bounds-checked store sequence makes the compiler wait for every earlier
     // store (gfx9 counts stores in vmcnt). Epilogue operands are loaded before
-    // the main loop so their latency hides behind it.
+    // the main loop so their latency hides behind it -- except for the
+    // 256 x 256 tile, whose 256 accumulator registers per lane leave no room:
+    // it loads them after the loop.
+    constexpr bool LATE = WMT * WNT >= 16;
     const bool full = (m0 + T::BM <= p.M) && (n0 + T::BN <= p.N);
     float sa[WMT][16], sw[WNT], bn[WNT];
-    if (SCALED) {
+    auto load_scales = [&]() {
 #pragma unroll
         for (int i = 0; i < WMT; i++)
 #pragma unroll
@@ -72,16 +76,15 @@ __global__ __launch_bounds__(256, 1) void gemm_v2_kernel(GemmParams p, int tiles
             sw[j] = p.s_w[n];
             bn[j] = p.bias ? p.bias[n] : 0.f;
         }
-    }
+    };
+    if (SCALED && !LATE) load_scales();
     v16i acc[WMT][WNT];
-    if (STAGES == 0)
-        mma_tile_v2<WMT, WNT>(p.A + z * p.a_batch + (int64_t)m0 * p.lda, p.lda, p.M - m0,
-                              p.B + z * p.b_batch + (int64_t)n0 * p.ldb, p.ldb, p.N - n0, p.K,
-                              lds_v2, acc);
-    else
-        mma_tile_v3<WMT, WNT, (STAGES > 0 ? STAGES : 2)>(
-            p.A + z * p.a_batch + (int64_t)m0 * p.lda, p.lda, p.M - m0,
-            p.B + z * p.b_batch + (int64_t)n0 * p.ldb, p.ldb, p.N - n0, p.K, lds_v2, acc);
+    const int8_t* A = p.A + z * p.a_batch + (int64_t)m0 * p.lda;
+    const int8_t* B = p.B + z * p.b_batch + (int64_t)n0 * p.ldb;
+    if constexpr (ENG == 2) mma_tile_v2<WMT, WNT>(A, p.lda, p.M - m0, B, p.ldb, p.N - n0, p.K, lds_v2, acc);
+    else if constexpr (ENG == 3) mma_tile_v3<WMT, WNT, S>(A, p.lda, p.M - m0, B, p.ldb, p.N - n0, p.K, lds_v2, acc);
+    else mma_tile_v4<WMT>(A, p.lda, p.M - m0, B, p.ldb, p.N - n0, p.K, lds_v2, acc);
+    if (SCALED && LATE) load_scales();
     char* C = (char*)p.C + z * p.c_batch * (OUT == OUT_F16 ? 2 : 4);
     const bool has_bias = SCALED && p.bias;
     // off = m * ldc + n in 32 bits when the whole output fits (it does at every
@@ -95,11 +98,16 @@ __global__ __launch_bounds__(256, 1) void gemm_v2_kernel(GemmParams p, int tiles
         } else if (OUT == OUT_F32_RAW) {
             ((float*)C)[off] = (float)a;
         } else {
+            // each product and the bias add round to f32 separately, and val
+            // is rounded to f32 before the f16 store, as the reference
+            // computes them: the empty operand barriers stop the compiler from
+            // fusing the product and the add into one FMA, or the product and
+            // the f16 conversion into one v_fma_mix (each rounds once)
             float val = (float)a * sa[i][e] * sw[j];
-            if (bias) val += bn[j];
-            // val is rounded to f32 before the f16 store, as the reference
-            // computes it: without the operand barrier fmul+fptrunc becomes
-            // one v_fma_mix that rounds once, straight to f16
+            if (bias) {
+                asm volatile("" : "+v"(val));
+                val += bn[j];
+            }
             if (OUT == OUT_F16) asm volatile("" : "+v"(val));
             if (OUT == OUT_F32) ((float*)C)[off] = val;
             else ((_Float16*)C)[off] = (_Float16)val;
@@ -151,23 +159,29 @@ constexpr int v3_stages() {
     return (144 * 1024) / ((64 * WMT + 64 * WNT) * 128) >= 4 ? 4 : 3;
 }
 
-template <int WMT, int WNT, int OUT, int STAGES>
+template <int WMT, int WNT, int ENG, int S>
+constexpr size_t engine_lds() {
+    return ENG == 2 ? (size_t)TileV2<WMT, WNT>::LDS_BYTES
+         : ENG == 3 ? (size_t)TileV3<WMT, WNT, S>::LDS_BYTES
+                    : (size_t)TileV4<WMT>::LDS_BYTES;
+}
+
+template <int WMT, int WNT, int OUT, int ENG, int S>
 static int launch_v2_out(const GemmParams& p, dim3 grid, int tn, hipStream_t st) {
-    constexpr size_t lds = STAGES == 0 ? (size_t)TileV2<WMT, WNT>::LDS_BYTES
-                                       : (size_t)TileV3<WMT, WNT, (STAGES ? STAGES : 2)>::LDS_BYTES;
-    PIO_TRY(allow_lds(gemm_v2_kernel<WMT, WNT, OUT, STAGES>, lds));
-    gemm_v2_kernel<WMT, WNT, OUT, STAGES><<<grid, 256, lds, st>>>(p, tn);
+    constexpr size_t lds = engine_lds<WMT, WNT, ENG, S>();
+    PIO_TRY(allow_lds(gemm_v2_kernel<WMT, WNT, OUT, ENG, S>, lds));
+    gemm_v2_kernel<WMT, WNT, OUT, ENG, S><<<grid, 256, lds, st>>>(p, tn);
     PIO_LAUNCHED();
     return PIO_OK;
 }
 
-template <int WMT, int WNT, int STAGES>
+template <int WMT, int WNT, int ENG, int S>
 static int launch_v2_s(const GemmParams& p, int out_mode, dim3 grid, int tn, hipStream_t st) {
     switch (out_mode) {
-    case OUT_F32: return launch_v2_out<WMT, WNT, OUT_F32, STAGES>(p, grid, tn, st);
-    case OUT_F16: return launch_v2_out<WMT, WNT, OUT_F16, STAGES>(p, grid, tn, st);
-    case OUT_I32: return launch_v2_out<WMT, WNT, OUT_I32, STAGES>(p, grid, tn, st);
-    case OUT_F32_RAW: return launch_v2_out<WMT, WNT, OUT_F32_RAW, STAGES>(p, grid, tn, st);
+    case OUT_F32: return launch_v2_out<WMT, WNT, OUT_F32, ENG, S>(p, grid, tn, st);
+    case OUT_F16: return launch_v2_out<WMT, WNT, OUT_F16, ENG, S>(p, grid, tn, st);
+    case OUT_I32: return launch_v2_out<WMT, WNT, OUT_I32, ENG, S>(p, grid, tn, st);
+    case OUT_F32_RAW: return launch_v2_out<WMT, WNT, OUT_F32_RAW, ENG, S>(p, grid, tn, st);
     default: return set_error(PIO_ERR_INVALID, "gemm: bad output mode");
     }
 }
@@ -185,6 +199,11 @@ static void xcd_split(int tm, int tn, int BM, int BN, int& xr, int& xc) {
     }
 }
 
+// Direct-to-LDS engines need 16-byte aligned rows and K a multiple of the step.
+static bool direct_ok(const GemmParams& p, int kstep) {
+    return aligned16(p.A) && aligned16(p.B) && p.lda % 16 == 0 && p.ldb % 16 == 0 && p.K % kstep == 0;
+}
+
 template <int WMT, int WNT>
 static int launch_v2(const GemmParams& p0, int out_mode, int batch, hipStream_t st) {
     using T = TileV2<WMT, WNT>;
@@ -192,25 +211,31 @@ static int launch_v2(const GemmParams& p0, int out_mode, int batch, hipStream_t 
     dim3 grid(tm * tn, 1, batch);
     GemmParams p = p0;
     xcd_split(tm, tn, T::BM, T::BN, p.xr, p.xc);
-    const bool direct = (p.K % 128 == 0) && aligned16(p.A) && aligned16(p.B) &&
-                        p.lda % 16 == 0 && p.ldb % 16 == 0 && !getenv("PIO_GEMM_NO_DIRECT");
-    if (direct) return launch_v2_s<WMT, WNT, v3_stages<WMT, WNT>()>(p, out_mode, grid, tn, st);
-    return launch_v2_s<WMT, WNT, 0>(p, out_mode, grid, tn, st);
+    if constexpr (WMT * WNT >= 16) {
+        // 256 x 256: the half-step-ring engine (the caller checked its conditions)
+        return launch_v2_s<WMT, WNT, 4, 0>(p, out_mode, grid, tn, st);
+    } else {
+        if (direct_ok(p, 128)) return launch_v2_s<WMT, WNT, 3, v3_stages<WMT, WNT>()>(p, out_mode, grid, tn, st);
+        return launch_v2_s<WMT, WNT, 2, 0>(p, out_mode, grid, tn, st);
+    }
 }
 
-// Picks the block tile whose tile count best fills whole waves of 256 CUs
-// (ties go to the larger tile), among BM = 128 and BN in {64, 128, 192, 256}.
+// Picks the block tile: 256 x 256 when it fills every CU (its LDS and operand
+// traffic per MFMA is the lowest), else among BM = 128 and BN in {64, 128,
+// 192, 256} the one whose tile count best fills whole waves of the CUs (ties
+// go to the larger tile).
 static int launch_dense(const GemmParams& p, int out_mode, int batch, hipStream_t st) {
+    const int64_t cus = 256;
+    const int64_t big = (int64_t)ceil_div(p.M, 256) * ceil_div(p.N, 256) * batch;
+    if (direct_ok(p, 128) && big >= cus && (double)big / (double)(((big + cus - 1) / cus) * cus) >= 0.9)
+        return launch_v2<4, 4>(p, out_mode, batch, st);
     static const int cfg[][2] = {{2, 4}, {2, 3}, {2, 2}, {2, 1}};
     int best = 0;
     double best_eff = -1.0;
-    // PIO_GEMM_TILE=<0..3> pins the tile shape (tuning experiments only).
-    static const char* force = getenv("PIO_GEMM_TILE");
-    if (force) best_eff = 2.0, best = atoi(force) & 3;
     for (int i = 0; i < 4; i++) {
         const int64_t tiles = (int64_t)ceil_div(p.M, 64 * cfg[i][0]) * ceil_div(p.N, 64 * cfg[i][1]) * batch;
-        const int64_t rounds = (tiles + 255) / 256;
-        const double eff = (double)tiles / (double)(rounds * 256);
+        const int64_t rounds = (tiles + cus - 1) / cus;
+        const double eff = (double)tiles / (double)(rounds * cus);
         if (eff > best_eff + 1e-9) { best_eff = eff; best = i; }
     }
     switch (best) {

@@ -263,4 +263,130 @@ __device__ __forceinline__ void mma_tile_v3(const int8_t* __restrict__ A, int64_
     }
 }
 
+// ---------------------------------------------------------------------------
+// Dense tile engine v4, for the big square block tile (256 x 256: each wave
+// 128 x 128 = 4 x 4 MFMA tiles, so one ds_read_b128 fragment feeds 4 MFMAs).
+// A K step is 128 bytes, as in v3: a copy instruction moves 8 rows x 128 B,
+// whole cache lines (copies of 16 rows x 64 B -- half lines -- fill the LDS at
+// little more than half the rate). A full step of both operands is 64 KB, so
+// the LDS holds the A slice and the B slice of a step as separate 32 KB
+// halves in a ring of 5 (160 KB): half h = 2*step + (0: A, 1: B) sits in slot
+// h % 5. While step kt is multiplied, the halves of steps kt+1 (B) and kt+2
+// (A) are being copied -- the only slots not holding step kt or kt+1's A.
+// Slot layout as v3: 16-byte chunk c of row r at c ^ ((r >> 1) & 7).
+template <int WT>
+struct TileV4 {
+    static constexpr int BM = 64 * WT, BN = 64 * WT, BK = 128, SLOTS = 5;
+    static constexpr int BLK = BM / 8;                 // 1 KiB copies per half
+    static constexpr int PER_WAVE = BLK / 4;            // per wave per half
+    static constexpr int HALF = BM * BK;                // bytes per half
+    static constexpr int LDS_BYTES = SLOTS * HALF;
+    static_assert(BLK % 4 == 0, "tile rows per wave");
+};
+
+template <int WT>
+__device__ __forceinline__ void mma_tile_v4(const int8_t* __restrict__ A, int64_t lda, int m_rem,
+                                            const int8_t* __restrict__ B, int64_t ldb, int n_rem,
+                                            int K, int8_t* lds, v16i (&acc)[WT][WT]) {
+    using T = TileV4<WT>;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    const int8_t* ga[T::PER_WAVE];
+    const int8_t* gb[T::PER_WAVE];
+#pragma unroll
+    for (int j = 0; j < T::PER_WAVE; j++) {
+        const int q = j * 4 + wave, r = q * 8 + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
+        ga[j] = A + (int64_t)min(r, m_rem - 1) * lda + c * 16;
+        gb[j] = B + (int64_t)min(r, n_rem - 1) * ldb + c * 16;
+    }
+    typedef __attribute__((address_space(3))) void lds_t;
+    const int nk = K / T::BK, nh = 2 * nk;
+    // copy j of this wave's share of half h (A slice of step h/2 if h is even,
+    // else B). Issued for every h, also past the end (the last step again, into
+    // a slot nothing reads any more), so no copy sits behind a branch and the
+    // wait counts stay constant.
+    auto copy = [&](int h, int j) {
+        int8_t* base = lds + (h % T::SLOTS) * T::HALF;
+        const int k0 = min(h >> 1, nk - 1) * T::BK;
+        __builtin_amdgcn_global_load_lds((const void*)(((h & 1) ? gb[j] : ga[j]) + k0),
+                                         (lds_t*)(base + (j * 4 + wave) * 1024), 16, 0, 0);
+    };
+
+#pragma unroll
+    for (int i = 0; i < WT; i++)
+#pragma unroll
+        for (int j = 0; j < WT; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0;
+
+    if (nk <= 0) return;
+#pragma unroll
+    for (int h = 0; h < 3; h++)
+#pragma unroll
+        for (int j = 0; j < T::PER_WAVE; j++) copy(h, j);
+    const int fr = lane & 31, fh = lane >> 5;
+    // fragment q of sub-step ks: q < WT an A fragment, else a B fragment
+    auto frag1 = [&](const int8_t* a_base, const int8_t* b_base, int ks, int q, v4i (&a)[WT], v4i (&b)[WT]) {
+        const int c = 2 * ks + fh;
+        if (q < WT) a[q] = *(const v4i*)(a_base + swz(wm * 32 * WT + q * 32 + fr, c));
+        else b[q - WT] = *(const v4i*)(b_base + swz(wn * 32 * WT + (q - WT) * 32 + fr, c));
+    };
+    // One sub-step: its WT*WT MFMAs, with the next sub-step's 2*WT fragment
+    // reads and (h >= 0) the PER_WAVE copies of half h placed one at a time
+    // between MFMA pairs, in this order exactly (scheduling barriers): a burst
+    // of copies stalls the wave, and with one wave per SIMD that idles the
+    // MFMA unit.
+    static_assert(2 * WT == T::PER_WAVE && WT * WT == 4 * WT, "one MFMA pair, read and copy per slot");
+    auto substep = [&](const v4i (&a)[WT], const v4i (&b)[WT], const int8_t* na, const int8_t* nb, int nks,
+                       v4i (&a2)[WT], v4i (&b2)[WT], int h) {
+#pragma unroll
+        for (int q = 0; q < 2 * WT; q++) {
+            const int i = q >> 1, j0 = (q & 1) * 2;
+            acc[i][j0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j0], acc[i][j0], 0, 0, 0);
+            acc[i][j0 + 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j0 + 1], acc[i][j0 + 1], 0, 0, 0);
+            // the reads go two per slot from the second slot on: they land long
+            // before the next sub-step needs them, and the previous sub-step's
+            // MFMAs (whose operand registers they overwrite) are long issued
+            if (q >= 1 && q <= WT) {
+                frag1(na, nb, nks, 2 * (q - 1), a2, b2);
+                frag1(na, nb, nks, 2 * (q - 1) + 1, a2, b2);
+            }
+            if (h >= 0) copy(h, q);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // keep this sub-step's operands live to its end, so the register
+        // allocator cannot give a next-sub-step read a register that an MFMA
+        // issued just before still reads
+#pragma unroll
+        for (int i = 0; i < WT; i++) asm volatile("" ::"v"(a[i]), "v"(b[i]));
+    };
+    // One barrier per step, before its last sub-step: by then every wave has
+    // read all of step kt's fragments (sub-step 3's were read during sub-step
+    // 2), so step kt's slots may be refilled from the next step on, and step
+    // kt+1's halves are waited for here and its first fragments read while
+    // sub-step 3's MFMAs run.
+    // Halves issued: 0..2 before the loop, 2kt+3 during sub-step 0 of step kt
+    // and 2kt+4 during its sub-step 1; step j's halves are complete once only
+    // the newest half (2j+4) may still be in flight.
+    v4i fa[2][WT], fb[2][WT];
+    stage_barrier<T::PER_WAVE>();
+#pragma unroll
+    for (int q = 0; q < 2 * WT; q++) frag1(lds, lds + T::HALF, 0, q, fa[0], fb[0]);
+    for (int kt = 0; kt < nk; kt++) {
+        const int8_t* a_base = lds + ((2 * kt) % T::SLOTS) * T::HALF;
+        const int8_t* b_base = lds + ((2 * kt + 1) % T::SLOTS) * T::HALF;
+        // B of kt+1 and A of kt+2 go into the slots of step kt-1, which every
+        // wave finished reading before step kt-1's barrier
+        substep(fa[0], fb[0], a_base, b_base, 1, fa[1], fb[1], 2 * kt + 3);
+        substep(fa[1], fb[1], a_base, b_base, 2, fa[0], fb[0], 2 * kt + 4);
+        substep(fa[0], fb[0], a_base, b_base, 3, fa[1], fb[1], -1);
+        stage_barrier<T::PER_WAVE>();
+        substep(fa[1], fb[1], lds + ((2 * kt + 2) % T::SLOTS) * T::HALF,
+                lds + ((2 * kt + 3) % T::SLOTS) * T::HALF, 0, fa[0], fb[0], -1);
+    }
+    // the copies issued past the end must land before the wave moves on
+    stage_barrier<0>();
+}
+
 }  // namespace pio

@@ -123,7 +123,7 @@ __global__ __launch_bounds__(256) void gemv_w8_direct_kernel(const XT* __restric
 // chunk reads 64 lanes' contiguous 16 B (no bank conflicts). Each weight byte
 // is converted to fp32 once and used for the MT x rows.
 constexpr int GEMV_WAVES = 16;                // waves per block = resident waves per CU
-constexpr int GEMV_XLDS = 64 * 1024;          // x bytes the LDS stage takes
+constexpr int GEMV_XLDS = 160 * 1024;         // x bytes the LDS stage takes (one block per CU)
 
 template <typename XT>
 __device__ __forceinline__ void load_x4(const XT* p, float (&v)[4]);
@@ -299,6 +299,12 @@ template <int R, int MT, typename XT, typename YT>
 static int launch_stream_r(const XT* x, const int8_t* w, const float* s_w, const float* bias, YT* y,
                            int N, int K, hipStream_t st) {
     const size_t lds = (size_t)MT * ((K + 1023) / 1024) * 4096;
+    static bool attr = false;   // one flag per instantiation
+    if (!attr) {
+        PIO_HIP(hipFuncSetAttribute((const void*)gemv_w8_stream_kernel<R, MT, XT, YT>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, GEMV_XLDS));
+        attr = true;
+    }
     const int blocks = (int)std::min<int64_t>(ceil_div(N, R), device_cus());
     gemv_w8_stream_kernel<R, MT, XT, YT><<<blocks, 64 * GEMV_WAVES, lds, st>>>(x, w, s_w, bias, y, N, K, N);
     return PIO_OK;

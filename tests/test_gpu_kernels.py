@@ -195,6 +195,45 @@ def test_gemm_int32_bitexact(env, M, N, K):
     assert np.array_equal(host(c), oracle.matmul_nt_i32(q, W))
 
 
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 128), (4096, 4096, 256), (4096, 4096, 640),
+                                   (4000, 4000, 640), (2048, 8192, 512)])
+def test_gemm_big_tile_int32_bitexact(env, M, N, K):
+    """Grids of >= 256 tiles of 256 x 256 take the 256 x 256 engine (half-step
+    LDS ring): one and two K steps, a ring in steady state, ragged tile edges.
+    Three launches each, every one bit-exact (a timing-dependent fault in the
+    copy/read pipeline would show as a mismatch in some launch)."""
+    torch, ops, d = env
+    _say(f"gemm big tile M={M} N={N} K={K}")
+    rng = np.random.default_rng(M + N + K + 1)
+    q = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    W = rng.integers(-127, 127, size=(N, K), dtype=np.int8)
+    ref = oracle.matmul_nt_i32(q, W)
+    qd, wd = dev(torch, q, d), dev(torch, W, d)
+    for _ in range(3):
+        c = torch.full((M, N), -1, dtype=torch.int32, device=d)
+        ops.gemm_w8a8(qd, None, wd, None, None, c, M, N, K)
+        sync(torch)
+        assert np.array_equal(host(c), ref)
+
+
+def test_gemm_big_tile_fp16_scaled(env):
+    """The 256 x 256 engine's scaled fp16 epilogue, byte-equal to the oracle."""
+    torch, ops, d = env
+    M, N, K = 4096, 4096, 512
+    rng = np.random.default_rng(77)
+    q = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    W = rng.integers(-127, 127, size=(N, K), dtype=np.int8)
+    sa = rng.uniform(0.001, 0.05, size=M).astype(np.float32)
+    sw = rng.uniform(0.001, 0.02, size=N).astype(np.float32)
+    b = rng.standard_normal(N, dtype=np.float32)
+    y = torch.empty((M, N), dtype=torch.float16, device=d)
+    ops.gemm_w8a8(dev(torch, q, d), dev(torch, sa, d), dev(torch, W, d), dev(torch, sw, d), dev(torch, b, d),
+                  y, M, N, K)
+    sync(torch)
+    yr = oracle.w8a8(q, sa, W, sw, b, out="f16")
+    assert np.array_equal(host(y).view(np.uint16), yr.view(np.uint16))
+
+
 @pytest.mark.parametrize("K,N", [(1024, 3072), (3072, 1024), (1024, 2048)])
 def test_gemm_c3_fp16_pipeline(env, K, N):
     """C3: x fp16 -> per-token quant -> W8A8 GEMM -> fp16, vs the oracle."""

@@ -16,7 +16,13 @@ Also in the same line:
   roofline      the dominant kernel: the persistent decode kernel (algorithmic
                 bytes of all timed tokens / its launch time, HIP events on the
                 decoder's stream); on the graph path, the per-layer W8 GEMV
-                replayed alone from a graph.
+                replayed alone from a graph. `traffic` is the HBM bytes of that
+                launch measured with rocprofv3 counters (FETCH_SIZE and
+                WRITE_SIZE passes over this same command, each scaled by what
+                the counter reads for a plain 1 GiB device copy, see
+                --calibrate-copy), read from the profile summary
+                profiles/decode_loop_kernel_traffic.txt when its step count
+                matches; null otherwise.
   cpu_baseline  the reference CPU path (oracle/_ref/libtensor_ops_ref.so, built
                 from the reference's own tensor_ops.c): its fp32 tensor_linear on
                 per-channel-dequantized weights over every linear of one decode
@@ -93,6 +99,8 @@ def bench_decode(torch, args):
     dec = Qwen3Int8Decoder(cfg, w, stream=st.cuda_stream)
     prompt = np.random.default_rng(1).integers(0, cfg.vocab, size=P).astype(np.int32)
     modes = ["persistent", "graph"] if dec.persistent_supported() else ["graph"]
+    if args.decode_only:
+        modes = modes[:1]
 
     def timed_run(mode):
         # Warmup: builds the mode's resources (graph / weight stream), untimed.
@@ -336,6 +344,24 @@ def cpu_baseline(cfg, w, budget_s=20.0):
     }
 
 
+# ----------------------------------------------------------------- traffic
+TRAFFIC_PROFILE = ROOT / "profiles" / "decode_loop_kernel_traffic.txt"
+
+
+def measured_traffic(steps):
+    """HBM bytes of one persistent-decode launch of `steps` tokens, from the
+    committed counter summary (its `traffic_bytes_per_launch` and `steps`
+    lines), or None when there is none for this step count."""
+    try:
+        kv = dict(l.split("=", 1) for l in TRAFFIC_PROFILE.read_text().splitlines()
+                  if "=" in l and not l.startswith("#"))
+        if int(kv["steps"]) == steps:
+            return int(float(kv["traffic_bytes_per_launch"]))
+    except (OSError, KeyError, ValueError):
+        pass
+    return None
+
+
 # -------------------------------------------------------------------- main
 def main():
     ap = argparse.ArgumentParser()
@@ -344,6 +370,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--no-kernels", action="store_true", help="skip the C1/C3/C4/C5 kernel suite")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="time only the decode (its fastest supported mode; no graph-replayed "
+                         "GEMVs, kernel suite or CPU baseline) -- the command the counter passes "
+                         "of the traffic measurement profile")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 1 GiB device-to-device copy (three times), for scaling "
+                         "the FETCH_SIZE / WRITE_SIZE counters of the traffic measurement")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: the int8 path has no multi-GPU component in this "
@@ -353,15 +386,28 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 2
+    if args.calibrate_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": 1 << 30, "copies": 3}))
+        return 0
     from mod_amd import ops
     log(f"[bench] {ops.version()}  lib={ops.LIB_FILE}")
     timer = Timer(torch)
 
     cfg, w, dec, st, dall = bench_decode(torch, args)
     dres = dall[dall["mode"]]
-    g = bench_decode_gemv(torch, timer, cfg, dec)
-    log(f"[gemv] layer GEMV {g['layer_gemv_us_per_launch']:.2f} us/launch "
-        f"{g['layer_gemv_GBs']:.0f} GB/s; lm_head {g['lm_head_us']:.1f} us {g['lm_head_GBs']:.0f} GB/s")
+    if args.decode_only:
+        args.no_kernels = args.no_cpu = True
+        g = None
+    else:
+        g = bench_decode_gemv(torch, timer, cfg, dec)
+        log(f"[gemv] layer GEMV {g['layer_gemv_us_per_launch']:.2f} us/launch "
+            f"{g['layer_gemv_GBs']:.0f} GB/s; lm_head {g['lm_head_us']:.1f} us {g['lm_head_GBs']:.0f} GB/s")
     kern = {}
     if not args.no_kernels:
         kern = bench_kernels(torch, timer)
@@ -375,17 +421,18 @@ def main():
         if cpu:
             log(f"[cpu] {cpu['value']:.3f} tok/s ({cpu['ms_per_token']:.1f} ms/token)")
 
-    if dall["mode"] == "persistent":
+    if dall["mode"] == "persistent" or g is None:
         # Dominant kernel = the persistent decode kernel itself: one launch runs
         # all timed tokens, so bytes per launch = bytes per token x steps.
         roof = {
             "bound": "hbm",
-            "kernel": "decode_loop_kernel (persistent decode: every timed token in one launch)",
+            "kernel": ("decode_loop_kernel (persistent decode: every timed token in one launch)"
+                       if dall["mode"] == "persistent" else "decode step graph (all timed tokens)"),
             "achieved": round(dres["bytes_per_token"] * dres["tok_s"] / 1e9, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dres["hbm_frac"], 4),
-            "traffic": None,
+            "traffic": measured_traffic(args.steps) if dall["mode"] == "persistent" else None,
             "bytes_per_launch": round(dres["bytes_per_token"] * args.steps),
             "us_per_launch": round(dres["ms_per_token"] * args.steps * 1e3, 1),
         }
@@ -393,7 +440,7 @@ def main():
         achieved = g["layer_gemv_GBs"]
         roof = {
             "bound": "hbm",
-            "kernel": "gemv_w8_kernel (per-layer decode GEMVs: qkv, o, gate_up, down)",
+            "kernel": "gemv_w8_stream_kernel (per-layer decode GEMVs: qkv, o, gate_up, down)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -429,13 +476,21 @@ def main():
                                  for k, v in cpu.items()},
         "decode": {m: ({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
                        if isinstance(r, dict) else r) for m, r in dall.items()},
-        "decode_gemv": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in g.items()},
+        "decode_gemv": g and {k: (round(v, 3) if isinstance(v, float) else v) for k, v in g.items()},
         "kernels": kern,
     }
     print(json.dumps(line), flush=True)
-    dec.close()
+    if not args.decode_only:
+        # (a decode-only run leaves the decoder to process exit: under a counter
+        # profiler, tearing it down first has crashed the profiler's own exit)
+        dec.close()
     return 0
 
 
 if __name__ == "__main__":
-    sys.exit(main())
+    # A clean run returns normally instead of raising SystemExit: under
+    # rocprofv3 the SystemExit teardown path has crashed the profiler before
+    # it wrote its results.
+    rc = main()
+    if rc:
+        sys.exit(rc)

@@ -188,3 +188,36 @@ class Qwen3Int8Decoder:
             self.run(1, use_graph, mode)
             out.append(self.read(0, with_logits=True)[1].copy())
         return np.stack(out)
+
+
+def _main(argv=None) -> int:
+    """Runs the config-2 decode workload once and exits: random-init weights
+    (seed 0), a random 128-token prompt (seed 1), then `--steps` generated
+    tokens in the fastest supported mode -- the same launches as bench.py's
+    timed decode (a warmup run, the prompt steps, the generated steps), as a
+    plain driver for profilers (rocprofv3 counter passes)."""
+    import argparse
+    ap = argparse.ArgumentParser(prog="python -m mod_amd.qwen3")
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--mode", choices=sorted(MODES), default=None)
+    args = ap.parse_args(argv)
+    P = 128
+    cfg = Qwen3Config(max_seq=max(384, P + args.steps))
+    dec = Qwen3Int8Decoder(cfg, random_weights(cfg, seed=0))
+    mode = args.mode or ("persistent" if dec.persistent_supported() else "graph")
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab, size=P).astype(np.int32)
+    dec.reset(prompt)
+    dec.run(P - 1 + min(args.warmup, cfg.max_seq - P + 1), mode=mode)
+    dec.reset(prompt)
+    dec.run(P - 1, mode=mode)
+    dec.run(args.steps, mode=mode)
+    ids = dec.read(P + args.steps)
+    print(f"decoded {args.steps} tokens ({mode}); first generated ids {ids[P:P + 4].tolist()}", flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    # returns normally (no SystemExit): a counter profiler's exit hook then
+    # writes its results (with sys.exit it has crashed before writing them)
+    _main()

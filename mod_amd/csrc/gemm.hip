@@ -37,7 +37,8 @@ struct GemmParams {
 // does not split into 8 rectangles.
 // ENG 2: register-staged v2 engine (any K % 16 == 0); 3: direct-to-LDS v3
 // engine with S stages (K % 128 == 0); 4: direct-to-LDS v4 engine, square
-// tiles, half-step ring (K % 128 == 0).
+// tiles, half-step ring (K % 128 == 0); 5: direct-to-LDS v5 engine, S-stage
+// ring on the v4 schedule (K % 128 == 0).
 template <int WMT, int WNT, int OUT, int ENG, int S>
 __global__ __launch_bounds__(256, 1) void gemm_v2_kernel(GemmParams p, int tiles_n) {
     using T = TileV2<WMT, WNT>;
@@ -83,6 +84,7 @@ __global__ __launch_bounds__(256, 1) void gemm_v2_kernel(GemmParams p, int tiles
     const int8_t* B = p.B + z * p.b_batch + (int64_t)n0 * p.ldb;
     if constexpr (ENG == 2) mma_tile_v2<WMT, WNT>(A, p.lda, p.M - m0, B, p.ldb, p.N - n0, p.K, lds_v2, acc);
     else if constexpr (ENG == 3) mma_tile_v3<WMT, WNT, S>(A, p.lda, p.M - m0, B, p.ldb, p.N - n0, p.K, lds_v2, acc);
+    else if constexpr (ENG == 5) mma_tile_v5<WMT, WNT, S>(A, p.lda, p.M - m0, B, p.ldb, p.N - n0, p.K, lds_v2, acc);
     else mma_tile_v4<WMT>(A, p.lda, p.M - m0, B, p.ldb, p.N - n0, p.K, lds_v2, acc);
     if (SCALED && LATE) load_scales();
     char* C = (char*)p.C + z * p.c_batch * (OUT == OUT_F16 ? 2 : 4);
@@ -153,17 +155,12 @@ static int allow_lds(F* kernel, size_t bytes) {
     return PIO_OK;
 }
 
-// LDS stages of the v3 engine per tile shape: as many as fit in 144 KB.
-template <int WMT, int WNT>
-constexpr int v3_stages() {
-    return (144 * 1024) / ((64 * WMT + 64 * WNT) * 128) >= 4 ? 4 : 3;
-}
-
 template <int WMT, int WNT, int ENG, int S>
 constexpr size_t engine_lds() {
-    return ENG == 2 ? (size_t)TileV2<WMT, WNT>::LDS_BYTES
-         : ENG == 3 ? (size_t)TileV3<WMT, WNT, S>::LDS_BYTES
-                    : (size_t)TileV4<WMT>::LDS_BYTES;
+    if constexpr (ENG == 2) return TileV2<WMT, WNT>::LDS_BYTES;
+    else if constexpr (ENG == 3) return TileV3<WMT, WNT, S>::LDS_BYTES;
+    else if constexpr (ENG == 5) return TileV5<WMT, WNT, S>::LDS_BYTES;
+    else return TileV4<WMT>::LDS_BYTES;
 }
 
 template <int WMT, int WNT, int OUT, int ENG, int S>
@@ -215,7 +212,7 @@ static int launch_v2(const GemmParams& p0, int out_mode, int batch, hipStream_t 
         // 256 x 256: the half-step-ring engine (the caller checked its conditions)
         return launch_v2_s<WMT, WNT, 4, 0>(p, out_mode, grid, tn, st);
     } else {
-        if (direct_ok(p, 128)) return launch_v2_s<WMT, WNT, 3, v3_stages<WMT, WNT>()>(p, out_mode, grid, tn, st);
+        if (direct_ok(p, 128)) return launch_v2_s<WMT, WNT, 5, v5_stages<WMT, WNT>()>(p, out_mode, grid, tn, st);
         return launch_v2_s<WMT, WNT, 2, 0>(p, out_mode, grid, tn, st);
     }
 }

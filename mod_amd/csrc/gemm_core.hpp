@@ -174,6 +174,20 @@ __device__ __forceinline__ void stage_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// stage_barrier<n * L>() for a wave-uniform n in [0, MAXN].
+template <int L, int MAXN>
+__device__ __forceinline__ void stage_barrier_steps(int n) {
+    if constexpr (MAXN > 0) {
+        if (n >= MAXN) {
+            stage_barrier<MAXN * L>();
+            return;
+        }
+        stage_barrier_steps<L, MAXN - 1>(n);
+    } else {
+        stage_barrier<0>();
+    }
+}
+
 template <int WMT, int WNT, int S>
 __device__ __forceinline__ void mma_tile_v3(const int8_t* __restrict__ A, int64_t lda, int m_rem,
                                             const int8_t* __restrict__ B, int64_t ldb, int n_rem,
@@ -387,6 +401,164 @@ __device__ __forceinline__ void mma_tile_v4(const int8_t* __restrict__ A, int64_
     }
     // the copies issued past the end must land before the wave moves on
     stage_barrier<0>();
+}
+
+// ---------------------------------------------------------------------------
+// Dense tile engine v5: the v3 tiling (2 x 2 waves of WMT x WNT MFMA tiles, an
+// S-stage LDS ring of whole K steps, filled by 8-row x 128 B copies) run on
+// the v4 schedule:
+//   - one barrier per K step, before its last sub-step: by then every wave has
+//     read all of step kt's fragments, and step kt+1's stage is waited for, so
+//     its first fragments are read while the last sub-step's MFMAs run;
+//   - the copies of step kt+S-1 (into the slot of step kt-1, which every wave
+//     finished reading before step kt-1's barrier) are spread over sub-steps
+//     0-2 of step kt, and the next sub-step's fragment reads over the first
+//     half of each sub-step, one at a time between the MFMAs (scheduling
+//     barriers pin the order: a burst of copies stalls the only wave on the
+//     SIMD);
+//   - the loop runs in two parts: while step kt+S-1 exists every sub-step's
+//     copies are issued unconditionally and the wait count is a constant; the
+//     last S-1 steps copy nothing (a short K would otherwise spend a third of
+//     its copy bandwidth on steps past the end) and wait for whatever is left.
+// Fragments rotate through four register sets (sub-step ks uses set ks) and
+// each sub-step keeps its own and the previous sub-step's operands alive to
+// its end, so a fragment read never lands in a register an MFMA issued within
+// the last sub-step still reads.
+template <int WMT, int WNT, int S>
+struct TileV5 {
+    static constexpr int BM = 64 * WMT, BN = 64 * WNT, BK = 128, STAGES = S;
+    static constexpr int A_PW = BM / 32, B_PW = BN / 32;   // 1 KiB copies per wave per step
+    static constexpr int LOADS = A_PW + B_PW;
+    static constexpr int STAGE = (BM + BN) * BK;
+    static constexpr int LDS_BYTES = S * STAGE;
+    static_assert(S >= 3 && (S - 2) * LOADS < 64, "ring depth / vmcnt range");
+};
+
+// Stages of the v5 ring for a tile shape: as many as fit in 160 KB, at most 6.
+template <int WMT, int WNT>
+constexpr int v5_stages() {
+    return (160 * 1024) / ((64 * WMT + 64 * WNT) * 128) >= 6 ? 6 : (160 * 1024) / ((64 * WMT + 64 * WNT) * 128);
+}
+
+template <int WMT, int WNT, int S>
+__device__ __forceinline__ void mma_tile_v5(const int8_t* __restrict__ A, int64_t lda, int m_rem,
+                                            const int8_t* __restrict__ B, int64_t ldb, int n_rem,
+                                            int K, int8_t* lds, v16i (&acc)[WMT][WNT],
+                                            const int32_t* __restrict__ a_rows = nullptr) {
+    using T = TileV5<WMT, WNT, S>;
+    constexpr int P = WMT * WNT, F = WMT + WNT, L = T::LOADS;
+    constexpr int RS = (P + 1) / 2;   // slots that carry the fragment reads
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // copy j of this wave's share of a step: j < A_PW an A block, else a B
+    // block; block q = (j % per-operand) * 4 + wave holds tile rows 8q..8q+7
+    const int8_t* src[L];
+    int dst[L];
+#pragma unroll
+    for (int j = 0; j < L; j++) {
+        const bool is_a = j < T::A_PW;
+        const int q = (is_a ? j : j - T::A_PW) * 4 + wave;
+        const int r = q * 8 + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
+        if (is_a) {
+            const int rr = min(r, m_rem - 1);   // A row r of the tile: A[a_rows[r]] when gathering
+            src[j] = A + (int64_t)(a_rows ? a_rows[rr] : rr) * lda + c * 16;
+            dst[j] = q * 1024;
+        } else {
+            src[j] = B + (int64_t)min(r, n_rem - 1) * ldb + c * 16;
+            dst[j] = T::BM * 128 + q * 1024;
+        }
+    }
+    typedef __attribute__((address_space(3))) void lds_t;
+    const int nk = K / T::BK;
+    auto copy = [&](int step, int j) {
+        int8_t* base = lds + (step % S) * T::STAGE;
+        __builtin_amdgcn_global_load_lds((const void*)(src[j] + step * T::BK), (lds_t*)(base + dst[j]), 16, 0,
+                                         0);
+    };
+
+#pragma unroll
+    for (int i = 0; i < WMT; i++)
+#pragma unroll
+        for (int j = 0; j < WNT; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0;
+    if (nk <= 0) return;
+
+#pragma unroll
+    for (int s = 0; s < S - 1; s++)
+        if (s < nk) {
+#pragma unroll
+            for (int j = 0; j < L; j++) copy(s, j);
+        }
+
+    const int fr = lane & 31, fh = lane >> 5;
+    // fragment f of sub-step ks: f < WMT an A fragment, else a B fragment
+    auto frag1 = [&](const int8_t* base, int ks, int f, v4i (&a)[WMT], v4i (&b)[WNT]) {
+        const int c = 2 * ks + fh;
+        if (f < WMT) a[f] = *(const v4i*)(base + swz(wm * 32 * WMT + f * 32 + fr, c));
+        else b[f - WMT] = *(const v4i*)(base + T::BM * 128 + swz(wn * 32 * WNT + (f - WMT) * 32 + fr, c));
+    };
+    // One sub-step: MFMA q (A fragment q / WNT, B fragment q % WNT) in slot q;
+    // the next sub-step's read f goes in slot f * RS / F; with part >= 0, the
+    // step's copies [part*L/3, (part+1)*L/3) of step `cstep` are spread over
+    // the slots.
+    auto substep = [&](const v4i (&a)[WMT], const v4i (&b)[WNT], const v4i (&pa)[WMT],
+                       const v4i (&pb)[WNT], const int8_t* nbase, int nks, v4i (&na)[WMT],
+                       v4i (&nb)[WNT], int cstep, int part) {
+#pragma unroll
+        for (int q = 0; q < P; q++) {
+            const int i = q / WNT, j = q % WNT;
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);   // the MFMA first: reads issued before it would join its wait
+#pragma unroll
+            for (int f = 0; f < F; f++)
+                if (f * RS / F == q) frag1(nbase, nks, f, na, nb);
+            if (part >= 0) {
+                const int c0 = part * L / 3, c1 = (part + 1) * L / 3;
+#pragma unroll
+                for (int c = 0; c < L; c++)
+                    if (c >= c0 && c < c1 && (c - c0) * P / (c1 - c0) == q) copy(cstep, c);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int i = 0; i < WMT; i++) asm volatile("" ::"v"(a[i]), "v"(pa[i]));
+#pragma unroll
+        for (int j = 0; j < WNT; j++) asm volatile("" ::"v"(b[j]), "v"(pb[j]));
+    };
+
+    v4i fa[4][WMT], fb[4][WNT];
+#pragma unroll
+    for (int i = 0; i < WMT; i++) fa[3][i] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < WNT; j++) fb[3][j] = v4i{0, 0, 0, 0};
+    // Steps copied: 0..min(S-1, nk)-1 before the loop, kt+S-1 during step kt
+    // of the main part. Step kt+1 is complete once at most the steps copied
+    // after it are in flight.
+    stage_barrier_steps<L, S - 2>(min(S - 2, nk - 1));
+#pragma unroll
+    for (int f = 0; f < F; f++) frag1(lds, 0, f, fa[0], fb[0]);
+    int kt = 0;
+    for (; kt + S - 1 < nk; kt++) {
+        const int8_t* cur = lds + (kt % S) * T::STAGE;
+        const int8_t* nxt = lds + ((kt + 1) % S) * T::STAGE;
+        const int cs = kt + S - 1;
+        substep(fa[0], fb[0], fa[3], fb[3], cur, 1, fa[1], fb[1], cs, 0);
+        substep(fa[1], fb[1], fa[0], fb[0], cur, 2, fa[2], fb[2], cs, 1);
+        substep(fa[2], fb[2], fa[1], fb[1], cur, 3, fa[3], fb[3], cs, 2);
+        stage_barrier<(S - 2) * L>();
+        substep(fa[3], fb[3], fa[2], fb[2], nxt, 0, fa[0], fb[0], -1, -1);
+    }
+    for (; kt < nk; kt++) {
+        const int8_t* cur = lds + (kt % S) * T::STAGE;
+        const int8_t* nxt = lds + ((kt + 1) % S) * T::STAGE;
+        substep(fa[0], fb[0], fa[3], fb[3], cur, 1, fa[1], fb[1], -1, -1);
+        substep(fa[1], fb[1], fa[0], fb[0], cur, 2, fa[2], fb[2], -1, -1);
+        substep(fa[2], fb[2], fa[1], fb[1], cur, 3, fa[3], fb[3], -1, -1);
+        stage_barrier_steps<L, S - 2>(max(0, nk - 2 - kt));
+        substep(fa[3], fb[3], fa[2], fb[2], nxt, 0, fa[0], fb[0], -1, -1);
+    }
 }
 
 }  // namespace pio

@@ -5,10 +5,11 @@
 // The op is HBM-bound: every weight byte is used M times (M <= 4 per launch).
 // The stream kernel (gemv_w8_stream_kernel) keeps x in LDS and streams the
 // weights with persistent waves; the direct kernel (gemv_w8_direct_kernel)
-// takes the shapes whose x does not fit the LDS. Both convert each weight byte to fp32 once (v_cvt_f32_i32_sdwa,
-// sign-extended byte select), accumulate in fp32 FMA, and apply the
-// per-channel scale once per output after the cross-lane reduction. Requires
-// K % 16 == 0 and 16 B aligned x and W rows.
+// takes small weights and the shapes whose x does not fit the LDS. Both
+// convert each weight byte to fp32 once (v_cvt_f32_i32_sdwa, sign-extended
+// byte select), accumulate in fp32 FMA, and apply the per-channel scale once
+// per output after the cross-lane reduction. Requires K % 16 == 0 and 16 B
+// aligned x and W rows.
 #include "pio_common.hpp"
 
 #include <algorithm>
@@ -341,10 +342,16 @@ static void launch_direct_rows(const XT* x, const int8_t* w, const float* s_w, c
     }
 }
 
+// Below this weight size a launch is bounded by its start-up (one HBM round
+// trip), not by streaming: the direct kernel's one-wave-per-row-group grid
+// reaches its first weight bytes sooner than the stream kernel, which first
+// stages x through LDS in 1024-thread blocks (3 MB: 3.05 vs 3.9 us).
+constexpr size_t GEMV_STREAM_MIN_BYTES = 16u << 20;
+
 template <typename XT, typename YT>
 static int dispatch(const XT* x, const int8_t* w, const float* s_w, const float* bias, YT* y,
                     int M, int N, int K, hipStream_t st) {
-    if (stream_pick(1, N, K)) {
+    if ((size_t)N * K >= GEMV_STREAM_MIN_BYTES && stream_pick(1, N, K)) {
         // x rows in launches of up to 4 (as many as the LDS takes); each launch re-streams W
         for (int m0 = 0; m0 < M;) {
             const int left = M - m0;

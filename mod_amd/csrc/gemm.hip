@@ -28,6 +28,22 @@ struct GemmParams {
     int xr, xc;   // XCD rectangles: tile rows split xr ways, tile columns xc ways (xr*xc == 8), or 0
 };
 
+// Scaled output value of one int32 accumulator. Each product and the bias add
+// round to f32 separately, and the value is rounded to f32 before an f16
+// store, as the reference computes them: the empty operand barriers stop the
+// compiler from fusing the product and the add into one FMA, or the product
+// and the f16 conversion into one v_fma_mix (each rounds once).
+template <int OUT>
+__device__ __forceinline__ float scaled_value(int a, float sa, float sw, float bn, bool bias) {
+    float val = (float)a * sa * sw;
+    if (bias) {
+        asm volatile("" : "+v"(val));
+        val += bn;
+    }
+    if (OUT == OUT_F16) asm volatile("" : "+v"(val));
+    return val;
+}
+
 // ----------------------------------------------------------------- v2 ---
 // Dense W8A8 on the 32x32x32 engine. Block b is mapped XCD-aware: the
 // dispatcher places block b on XCD b % 8, so each XCD is given one rectangle
@@ -100,17 +116,7 @@ __global__ __launch_bounds__(256, 1) void gemm_v2_kernel(GemmParams p, int tiles
         } else if (OUT == OUT_F32_RAW) {
             ((float*)C)[off] = (float)a;
         } else {
-            // each product and the bias add round to f32 separately, and val
-            // is rounded to f32 before the f16 store, as the reference
-            // computes them: the empty operand barriers stop the compiler from
-            // fusing the product and the add into one FMA, or the product and
-            // the f16 conversion into one v_fma_mix (each rounds once)
-            float val = (float)a * sa[i][e] * sw[j];
-            if (bias) {
-                asm volatile("" : "+v"(val));
-                val += bn[j];
-            }
-            if (OUT == OUT_F16) asm volatile("" : "+v"(val));
+            const float val = scaled_value<OUT>(a, sa[i][e], sw[j], bn[j], bias);
             if (OUT == OUT_F32) ((float*)C)[off] = val;
             else ((_Float16*)C)[off] = (_Float16)val;
         }
@@ -243,6 +249,141 @@ static int launch_dense(const GemmParams& p, int out_mode, int batch, hipStream_
     }
 }
 
+// ---------------------------------------------------------- split-K ---
+// Skinny products (few tile rows: decode batches, MoE-free small-M linears)
+// leave most CUs idle with one tile per output block. The split-K path runs
+// `splits` K slices of every output tile as the batch dimension of the dense
+// kernel (slice z reads A and B from column z*Kc, same row pitch) into int32
+// partials ws[z][M][N], then splitk_reduce_kernel sums the slices in slice
+// order and applies the epilogue. Integer sums are exact, so the result is
+// bit-identical to the one-pass kernel's for every output type.
+template <int OUT>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const int32_t* __restrict__ ws, int splits,
+                                                            int M, int N, const float* __restrict__ s_a,
+                                                            const float* __restrict__ s_w,
+                                                            const float* __restrict__ bias, void* C) {
+    const int64_t MN = (int64_t)M * N;
+    const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i0 >= MN) return;
+    int acc[4] = {0, 0, 0, 0};
+    const bool vec = (N % 4) == 0;   // then the four elements share a row and 16 B alignment
+    for (int z = 0; z < splits; z++) {
+        const int32_t* src = ws + z * MN + i0;
+        if (vec) {
+            const int4 v = *(const int4*)src;
+            acc[0] += v.x; acc[1] += v.y; acc[2] += v.z; acc[3] += v.w;
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (i0 + u < MN) acc[u] += src[u];
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int64_t i = i0 + u;
+        if (i >= MN) break;
+        const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
+        if (OUT == OUT_I32) {
+            ((int32_t*)C)[i] = acc[u];
+        } else {
+            const float val = scaled_value<OUT>(acc[u], s_a[m], s_w[n], bias ? bias[n] : 0.f, bias != nullptr);
+            if (OUT == OUT_F32) ((float*)C)[i] = val;
+            else ((_Float16*)C)[i] = (_Float16)val;
+        }
+    }
+}
+
+// Split-K plan: block tile (WMT x WNT waves of 32 x 32) and slice count.
+struct SplitPlan {
+    int wmt = 0, wnt = 0, splits = 1;
+};
+
+// Cost model for skinny products (M <= 256): a tile's time is its copy
+// traffic per CU (BM + BN rows of Kc bytes through the LDS) plus a fixed
+// start-up per round (the first copies' latency before the ring is full,
+// ~1.5 us, counted as the 96 KB a CU copies meanwhile), times the rounds of
+// units over the CUs, plus the split path's int32 partials (written and read
+// back, spread over the CUs). The one-pass launch is costed with the tile
+// launch_dense would choose; a split plan is taken when it is at least 10%
+// cheaper. Slices are multiples of 128 bytes (the direct-to-LDS step) and at
+// least 512 (4 steps, so the copy ring overlaps). 64-row tiles when M <= 64
+// (a 128-row tile copies duplicated A rows).
+static SplitPlan plan_split(const GemmParams& p, int cus) {
+    SplitPlan best;
+    if (!direct_ok(p, 128) || p.M > 256) return best;
+    constexpr double RAMP = 96.0 * 1024;
+    auto rounds = [&](int64_t units) { return (double)((units + cus - 1) / cus); };
+    double base = 0, best_eff = -1.0;
+    {
+        static const int cfg[] = {4, 3, 2, 1};
+        for (int wnt : cfg) {
+            const int64_t tiles = (int64_t)ceil_div(p.M, 128) * ceil_div(p.N, 64 * wnt);
+            const double eff = (double)tiles / (rounds(tiles) * cus);
+            if (eff > best_eff + 1e-9) {
+                best_eff = eff;
+                base = rounds(tiles) * ((128.0 + 64.0 * wnt) * p.K + RAMP);
+            }
+        }
+    }
+    double best_cost = 0.9 * base;
+    const int wmt = p.M <= 64 ? 1 : 2;
+    for (int wnt : {4, 2, 1}) {
+        const int64_t tiles = (int64_t)ceil_div(p.M, 64 * wmt) * ceil_div(p.N, 64 * wnt);
+        for (int sp : {2, 3, 4, 6, 8}) {
+            if (p.K % (sp * 128) || p.K / sp < 512) continue;
+            const double cost = rounds(tiles * sp) * ((64.0 * (wmt + wnt)) * (p.K / sp) + RAMP) +
+                                (double)sp * p.M * p.N * 8.0 / cus;
+            if (cost < best_cost) {
+                best_cost = cost;
+                best.wmt = wmt; best.wnt = wnt; best.splits = sp;
+            }
+        }
+    }
+    return best;
+}
+
+template <int WMT, int WNT>
+static int launch_split_tiles(const GemmParams& p, int splits, hipStream_t st) {
+    using T = TileV5<WMT, WNT, v5_stages<WMT, WNT>()>;
+    const int tn = ceil_div(p.N, T::BN), tm = ceil_div(p.M, T::BM);
+    return launch_v2_out<WMT, WNT, OUT_I32, 5, v5_stages<WMT, WNT>()>(p, dim3(tm * tn, 1, splits), tn, st);
+}
+
+static int launch_splitk(const GemmParams& p0, int out_mode, const SplitPlan& sp, hipStream_t st) {
+    Scratch ws;
+    PIO_TRY(ws.get((size_t)sp.splits * p0.M * p0.N * sizeof(int32_t)));
+    GemmParams p = p0;
+    p.a_batch = p.b_batch = p0.K / sp.splits;   // slice z starts at column z*Kc
+    p.K = p0.K / sp.splits;
+    p.C = ws.ptr;
+    p.ldc = p0.N;
+    p.c_batch = (int64_t)p0.M * p0.N;
+    p.s_a = p.s_w = p.bias = nullptr;
+    p.xr = p.xc = 0;
+    int rc;
+    if (sp.wmt == 1) {
+        rc = sp.wnt == 4 ? launch_split_tiles<1, 4>(p, sp.splits, st)
+           : sp.wnt == 2 ? launch_split_tiles<1, 2>(p, sp.splits, st)
+                         : launch_split_tiles<1, 1>(p, sp.splits, st);
+    } else {
+        rc = sp.wnt == 4 ? launch_split_tiles<2, 4>(p, sp.splits, st)
+           : sp.wnt == 2 ? launch_split_tiles<2, 2>(p, sp.splits, st)
+                         : launch_split_tiles<2, 1>(p, sp.splits, st);
+    }
+    if (rc != PIO_OK) return rc;
+    const int64_t MN = (int64_t)p0.M * p0.N;
+    const int blocks = (int)ceil_div(MN, (int64_t)1024);
+    const int32_t* w = (const int32_t*)ws.ptr;
+    switch (out_mode) {
+    case OUT_I32: splitk_reduce_kernel<OUT_I32><<<blocks, 256, 0, st>>>(w, sp.splits, p0.M, p0.N, nullptr, nullptr, nullptr, p0.C); break;
+    case OUT_F32: splitk_reduce_kernel<OUT_F32><<<blocks, 256, 0, st>>>(w, sp.splits, p0.M, p0.N, p0.s_a, p0.s_w, p0.bias, p0.C); break;
+    case OUT_F16: splitk_reduce_kernel<OUT_F16><<<blocks, 256, 0, st>>>(w, sp.splits, p0.M, p0.N, p0.s_a, p0.s_w, p0.bias, p0.C); break;
+    default: return set_error(PIO_ERR_INVALID, "gemm: bad output mode");
+    }
+    PIO_LAUNCHED();
+    return PIO_OK;
+}
+
 int gemm_w8a8(const int8_t* q, const float* s_a, const int8_t* w, const float* s_w,
               const float* bias, void* y, int y_dtype, int M, int N, int K, hipStream_t st) {
     PIO_REQUIRE(q && w && y, "gemm_w8a8: null pointer");
@@ -262,6 +403,8 @@ int gemm_w8a8(const int8_t* q, const float* s_a, const int8_t* w, const float* s
     p.s_a = s_a; p.s_w = s_w; p.bias = bias;
     p.C = y; p.ldc = N;
     p.M = M; p.N = N; p.K = K;
+    const SplitPlan sp = plan_split(p, 256);
+    if (sp.splits > 1) return launch_splitk(p, mode, sp, st);
     return launch_dense(p, mode, 1, st);
 }
 

@@ -234,6 +234,39 @@ def test_gemm_big_tile_fp16_scaled(env):
     assert np.array_equal(host(y).view(np.uint16), yr.view(np.uint16))
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 12288, 4096), (16, 12288, 4096), (64, 12288, 4096),
+                                   (64, 4096, 12288), (100, 1000, 2048), (33, 1536, 2048),
+                                   (256, 3072, 1024), (7, 130, 1536)])
+def test_gemm_split_k(env, M, N, K):
+    """Skinny M takes the split-K path (K slices as a batch into int32
+    partials, summed in slice order): int32 bit-exact, and the scaled fp16 /
+    fp32 outputs (with bias) byte-equal to the oracle, on two calls in a row
+    (the partial workspace is reused)."""
+    torch, ops, d = env
+    _say(f"split-K M={M} N={N} K={K}")
+    rng = np.random.default_rng(M * 7 + N + K)
+    q = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    W = rng.integers(-127, 127, size=(N, K), dtype=np.int8)
+    sa = rng.uniform(0.001, 0.05, size=M).astype(np.float32)
+    sw = rng.uniform(0.001, 0.02, size=N).astype(np.float32)
+    b = rng.standard_normal(N, dtype=np.float32)
+    qd, Wd, sad, swd, bd = (dev(torch, a, d) for a in (q, W, sa, sw, b))
+    acc_ref = oracle.matmul_nt_i32(q, W)
+    for rep in range(2):
+        acc = torch.full((M, N), 7, dtype=torch.int32, device=d)
+        y16 = torch.full((M, N), float("nan"), dtype=torch.float16, device=d)
+        y32 = torch.full((M, N), float("nan"), dtype=torch.float32, device=d)
+        ops.gemm_w8a8(qd, None, Wd, None, None, acc, M, N, K)
+        ops.gemm_w8a8(qd, sad, Wd, swd, bd, y16, M, N, K)
+        ops.gemm_w8a8(qd, sad, Wd, swd, None, y32, M, N, K)
+        sync(torch)
+        assert np.array_equal(host(acc), acc_ref), f"int32 call {rep}"
+        yr16 = oracle.w8a8(q, sa, W, sw, b, out="f16")
+        assert np.array_equal(host(y16).view(np.uint16), yr16.view(np.uint16)), f"f16 call {rep}"
+        yr32 = oracle.w8a8(q, sa, W, sw, None, out="f32")
+        assert np.array_equal(host(y32).view(np.uint32), yr32.view(np.uint32)), f"f32 call {rep}"
+
+
 @pytest.mark.parametrize("K,N", [(1024, 3072), (3072, 1024), (1024, 2048)])
 def test_gemm_c3_fp16_pipeline(env, K, N):
     """C3: x fp16 -> per-token quant -> W8A8 GEMM -> fp16, vs the oracle."""

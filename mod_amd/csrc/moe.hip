@@ -26,6 +26,20 @@ namespace pio {
 int quantize_per_token(const void* x, int x_dtype, int8_t* q, float* s, int M, int K,
                        hipStream_t st);
 
+// Minimum over the 64 lanes (in every lane), on DPP lane moves and readlane.
+template <int CTRL>
+__device__ __forceinline__ int dppi(int x) {
+    return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ int wmin_i(int x) {
+    x = min(x, dppi<DPP_XOR1>(x));
+    x = min(x, dppi<DPP_XOR2>(x));
+    x = min(x, dppi<DPP_HMIRROR>(x));
+    x = min(x, dppi<DPP_MIRROR>(x));
+    return min(min(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
+               min(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
+}
+
 // ------------------------------------------------------------------ route ---
 // One wave per token, 4 tokens per block; the token's E probabilities live in LDS.
 constexpr int ROUTE_MAX_E = 1024;
@@ -58,7 +72,10 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
     for (int e = lane; e < E; e += 64) p[e] *= inv;
 
     // k rounds of (max value, then min index) selection; chosen entries are
-    // retired by setting them to -inf (probabilities are >= 0).
+    // retired by setting them to -inf (probabilities are >= 0). Each lane's
+    // best (strict '>' over ascending e: its lowest index among equals), then
+    // the wave max and the lowest index holding it, both as DPP reductions
+    // (no LDS-queue shuffles in the dependent chain).
     float wsum = 0.f;
     float myw = 0.f;
     int myid = 0;
@@ -69,15 +86,11 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
             const float v = p[e];
             if (v > bv) { bv = v; bi = e; }
         }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-        }
-        if (lane == kk) { myw = bv; myid = bi; }
-        wsum += bv;
-        if (lane == (bi & 63)) p[bi] = -INFINITY;
+        const float m = wmax(bv);
+        const int mi = wmin_i(bv == m ? bi : 0x7fffffff);
+        if (lane == kk) { myw = m; myid = mi; }
+        wsum += m;
+        if (lane == (mi & 63)) p[mi] = -INFINITY;
     }
     if (lane < top_k) {
         topk_w[(int64_t)t * top_k + lane] = renorm ? myw / wsum : myw;
@@ -86,18 +99,19 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
 }
 
 // ------------------------------------------------------------------ group ---
-// Single block of 1024 threads, no serial dependency chains:
-//  1. top-k ids staged in LDS; bitmap[t][e/32] marks the (t, e) pairs;
-//  2. work item (e, slice) -- slices of 64 tokens -- packs column e of its
-//     slice into a 64-bit mask (64 independent LDS reads) and counts it;
-//  3. one wave scans the counts (slices in order, then experts in order) with
-//     shuffles, giving each item its first row;
-//  4. each set bit j of an item's mask goes to row start + popcount(bits < j),
-//     its top-k slot found in one 16-byte read of the token's id row.
+// Single block of 1024 threads (16 waves); wave w takes the 64-token slices
+// sl = w, w + 16, ... with lane j on token sl*64 + j:
+//  1. top-k ids staged in LDS (8 per token);
+//  2. each lane builds its token's expert bitmap one 32-expert word at a time
+//     in registers, and one wave ballot per expert gives that expert's 64-bit
+//     token mask of the slice (item (e, slice)) and its count;
+//  3. the counts are scanned in item order (experts in order, slices in order
+//     within an expert), all waves on contiguous chunks, then the chunk totals;
+//  4. each lane places its token's k pairs: row = item start + the number of
+//     the item's tokens below it (popcount of the mask under the lane).
 // The layout equals a serial walk over (expert, token). Limits:
-// T * ceil(E/32) <= GROUP_LDS_WORDS, T * top_k <= GROUP_MAX_PAIRS,
-// E * ceil(T/64) <= GROUP_MAX_ITEMS, top_k <= 8.
-constexpr int GROUP_LDS_WORDS = 8192;     // token x expert bitmap (32 KB)
+// T * top_k <= GROUP_MAX_PAIRS (T <= 1024 at top_k 8), E * ceil(T/64) <=
+// GROUP_MAX_ITEMS, top_k <= 8.
 constexpr int GROUP_MAX_PAIRS = 8192;     // staged topk ids (16 KB)
 constexpr int GROUP_MAX_ITEMS = 4096;     // (expert, 64-token slice) items
 
@@ -106,72 +120,83 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t* __restri
                                                          int32_t* __restrict__ offsets,
                                                          int32_t* __restrict__ row_token,
                                                          int32_t* __restrict__ pos_of_pair) {
-    __shared__ uint32_t bm[GROUP_LDS_WORDS];
     __shared__ __attribute__((aligned(16))) int16_t ids[GROUP_MAX_PAIRS];
     __shared__ unsigned long long masks[GROUP_MAX_ITEMS];
     __shared__ int32_t start[GROUP_MAX_ITEMS];
-    const int words = (E + 31) / 32;
+    __shared__ int32_t chunk[1024 / 64 + 1];
     const int nsl = (T + 63) / 64;
     const int items = E * nsl;   // item = e * nsl + slice
-    for (int i = threadIdx.x; i < T * words; i += blockDim.x) bm[i] = 0;
+    const int nw = blockDim.x >> 6, wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
     for (int i = threadIdx.x; i < T * 8; i += blockDim.x) {
         const int t = i >> 3, kk = i & 7;
         ids[i] = kk < top_k ? (int16_t)topk_id[t * top_k + kk] : (int16_t)-1;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < T * top_k; i += blockDim.x) {
-        const int t = i / top_k, e = ids[t * 8 + i % top_k];
-        atomicOr(&bm[t * words + (e >> 5)], 1u << (e & 31));
+    const unsigned long long below = (1ull << lane) - 1ull;   // lanes under this one
+    for (int sl = wv; sl < nsl; sl += nw) {
+        const int t = sl * 64 + lane;
+        int my[8];
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) my[kk] = t < T ? ids[t * 8 + kk] : -1;
+        for (int e0 = 0; e0 < E; e0 += 32) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++)
+                if (my[kk] >= e0 && my[kk] < e0 + 32) word |= 1u << (my[kk] - e0);
+            const int ne = min(32, E - e0);
+            unsigned long long mine = 0ull;   // lane b keeps expert e0 + b's mask
+            for (int b = 0; b < ne; b++) {
+                const unsigned long long m = __ballot((word >> b) & 1u);
+                if (lane == b) mine = m;
+            }
+            if (lane < ne) {
+                masks[(e0 + lane) * nsl + sl] = mine;
+                start[(e0 + lane) * nsl + sl] = __popcll(mine);
+            }
+        }
     }
     __syncthreads();
-    for (int it = threadIdx.x; it < items; it += blockDim.x) {
-        const int e = it / nsl, sl = it % nsl, t0 = sl * 64;
-        const uint32_t* col = bm + (e >> 5);
-        const int sh = e & 31;
-        unsigned long long m = 0ull;
-#pragma unroll 16
-        for (int j = 0; j < 64; j++)
-            if (t0 + j < T) m |= (unsigned long long)((col[(t0 + j) * words] >> sh) & 1u) << j;
-        masks[it] = m;
-        start[it] = __popcll(m);
-    }
-    __syncthreads();
-    if (threadIdx.x < 64) {
-        // exclusive scan of start[] in item order (= expert-major, slices in order)
+    // exclusive scan of start[] in item order: every wave scans a contiguous
+    // chunk, then the chunk totals are scanned and added
+    {
+        const int per = (items + nw - 1) / nw, b0 = wv * per, b1 = min(items, b0 + per);
         int carry = 0;
-        const int lane = threadIdx.x;
-        for (int b = 0; b < items; b += 64) {
+        for (int b = b0; b < b1; b += 64) {
             const int i = b + lane;
-            const int v = i < items ? start[i] : 0;
+            const int v = i < b1 ? start[i] : 0;
             int x = v;
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
                 const int y = __shfl_up(x, o, 64);
                 if (lane >= o) x += y;
             }
-            if (i < items) start[i] = carry + x - v;
+            if (i < b1) start[i] = carry + x - v;
             carry += __shfl(x, 63, 64);
         }
-        for (int e = lane; e <= E; e += 64) offsets[e] = e < E ? start[e * nsl] : carry;
+        if (lane == 0) chunk[wv] = carry;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int a = 0;
+            for (int w = 0; w < nw; w++) {
+                const int c = chunk[w];
+                chunk[w] = a;
+                a += c;
+            }
+            chunk[nw] = a;
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < items; i += blockDim.x) start[i] += chunk[i / per];
+        __syncthreads();
+        for (int e = threadIdx.x; e <= E; e += blockDim.x) offsets[e] = e < E ? start[e * nsl] : chunk[nw];
     }
-    __syncthreads();
-    for (int it = threadIdx.x; it < items; it += blockDim.x) {
-        const int e = it / nsl, sl = it % nsl, t0 = sl * 64;
-        unsigned long long m = masks[it];
-        int pos = start[it];
-        while (m) {
-            const int j = __ffsll((long long)m) - 1;
-            m &= m - 1;
-            const int t = t0 + j;
-            const int4 row = *(const int4*)&ids[t * 8];
-            const int16_t* r16 = (const int16_t*)&row;
-            int kk = 0;
-#pragma unroll
-            for (int q = 0; q < 8; q++)
-                if (r16[q] == e) kk = q;
+    for (int sl = wv; sl < nsl; sl += nw) {
+        const int t = sl * 64 + lane;
+        if (t >= T) continue;
+        for (int kk = 0; kk < top_k; kk++) {
+            const int e = ids[t * 8 + kk], it = e * nsl + sl;
+            const int pos = start[it] + __popcll(masks[it] & below);
             row_token[pos] = t;
             pos_of_pair[t * top_k + kk] = pos;
-            pos++;
         }
     }
 }
@@ -249,6 +274,56 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return g * (1.0f / (1.0f + expf(-g))) * u;
 }
 
+// One pass: a lane keeps its h values in registers (4 consecutive columns per
+// float4 group, SWIGLU_NV groups at most: I <= 64 * 4 * SWIGLU_NV), so g and u
+// are read once and silu evaluated once per element.
+constexpr int SWIGLU_NV = 8;
+
+__global__ __launch_bounds__(256) void moe_swiglu_quant_reg_kernel(const float* __restrict__ gu,
+                                                                   int8_t* __restrict__ q,
+                                                                   float* __restrict__ s, int rows,
+                                                                   int I) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const float4* g4 = (const float4*)(gu + (int64_t)r * 2 * I);
+    const float4* u4 = (const float4*)(gu + (int64_t)r * 2 * I + I);
+    const int nv = I / 4;
+    float h[SWIGLU_NV][4];
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < SWIGLU_NV; j++) {
+        const int c = lane + 64 * j;
+        if (c < nv) {
+            const float4 g = g4[c], u = u4[c];
+            h[j][0] = silu_mul(g.x, u.x);
+            h[j][1] = silu_mul(g.y, u.y);
+            h[j][2] = silu_mul(g.z, u.z);
+            h[j][3] = silu_mul(g.w, u.w);
+#pragma unroll
+            for (int e = 0; e < 4; e++) amax = fmaxf(amax, fabsf(h[j][e]));
+        }
+    }
+    amax = wave_max(amax);
+    const float sc = amax == 0.f ? 1.f : amax / 127.0f;
+    if (lane == 0) s[r] = sc;
+    uint32_t* qr = (uint32_t*)(q + (int64_t)r * I);
+#pragma unroll
+    for (int j = 0; j < SWIGLU_NV; j++) {
+        const int c = lane + 64 * j;
+        if (c < nv) {
+            uint32_t packed = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float v = __builtin_rintf(h[j][e] / sc);
+                v = fminf(fmaxf(v, -127.f), 127.f);
+                packed |= (uint32_t)(uint8_t)(int8_t)(int)v << (8 * e);
+            }
+            qr[c] = packed;
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void moe_swiglu_quant_kernel(const float* __restrict__ gu,
                                                                int8_t* __restrict__ q,
                                                                float* __restrict__ s, int rows,
@@ -270,6 +345,7 @@ __global__ __launch_bounds__(256) void moe_swiglu_quant_kernel(const float* __re
 }
 
 // ---------------------------------------------------------------- combine ---
+// Four consecutive columns per thread (H % 4 == 0), summed in k order.
 template <typename OT>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ d,
                                                           const float* __restrict__ topk_w,
@@ -277,14 +353,20 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
                                                           OT* __restrict__ out, int T, int H,
                                                           int top_k) {
     const int t = blockIdx.y;
-    for (int n = blockIdx.x * 256 + threadIdx.x; n < H; n += gridDim.x * 256) {
-        float acc = 0.f;
-        for (int kk = 0; kk < top_k; kk++) {
-            const int pr = t * top_k + kk;
-            acc += topk_w[pr] * d[(int64_t)pos_of_pair[pr] * H + n];
-        }
-        out[(int64_t)t * H + n] = from_f32<OT>(acc);
+    const int n = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (n >= H) return;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int kk = 0; kk < top_k; kk++) {
+        const int pr = t * top_k + kk;
+        const float wk = topk_w[pr];
+        const float4 v = *(const float4*)(d + (int64_t)pos_of_pair[pr] * H + n);
+        acc[0] += wk * v.x;
+        acc[1] += wk * v.y;
+        acc[2] += wk * v.z;
+        acc[3] += wk * v.w;
     }
+#pragma unroll
+    for (int e = 0; e < 4; e++) out[(int64_t)t * H + n + e] = from_f32<OT>(acc[e]);
 }
 
 // --------------------------------------------------------------- workspace ---
@@ -344,11 +426,11 @@ int moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* w_gu
     PIO_REQUIRE(T >= 0 && H > 0 && I > 0, "moe: bad shape");
     PIO_REQUIRE(H % 128 == 0 && I % 128 == 0, "moe: H=%d and I=%d must be multiples of 128", H, I);
     PIO_REQUIRE(out_dtype == PIO_F32 || out_dtype == PIO_F16, "moe: out must be fp32 or fp16");
-    PIO_REQUIRE((int64_t)T * ((E + 31) / 32) <= GROUP_LDS_WORDS && (int64_t)T * 8 <= GROUP_MAX_PAIRS &&
-                    (int64_t)E * ((T + 63) / 64) <= GROUP_MAX_ITEMS && top_k <= 8,
+    PIO_REQUIRE((int64_t)T * 8 <= GROUP_MAX_PAIRS && (int64_t)E * ((T + 63) / 64) <= GROUP_MAX_ITEMS &&
+                    top_k <= 8 && E <= 32767,
                 "moe: T=%d tokens, E=%d experts, top_k=%d exceed the grouping limits "
-                "(T*ceil(E/32) <= %d, T*8 <= %d, E*ceil(T/64) <= %d, top_k <= 8)", T, E, top_k,
-                GROUP_LDS_WORDS, GROUP_MAX_PAIRS, GROUP_MAX_ITEMS);
+                "(T*8 <= %d, E*ceil(T/64) <= %d, top_k <= 8)", T, E, top_k, GROUP_MAX_PAIRS,
+                GROUP_MAX_ITEMS);
     PIO_REQUIRE(aligned16(w_gu) && aligned16(w_down), "moe: weights must be 16-byte aligned");
     if (T == 0) return PIO_OK;
     static bool lds_ok = false;
@@ -378,7 +460,10 @@ int moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* w_gu
     moe_grouped_gemm_kernel<<<dim3(ceil_div(2 * I, MoeTile::BN), E), 256, MoeTile::LDS_BYTES, st>>>(g);
     PIO_LAUNCHED();
 
-    moe_swiglu_quant_kernel<<<ceil_div(P, 4), 256, 0, st>>>(w.gu, w.qh, w.sh, P, I);
+    if (I <= 64 * 4 * SWIGLU_NV)
+        moe_swiglu_quant_reg_kernel<<<ceil_div(P, 4), 256, 0, st>>>(w.gu, w.qh, w.sh, P, I);
+    else
+        moe_swiglu_quant_kernel<<<ceil_div(P, 4), 256, 0, st>>>(w.gu, w.qh, w.sh, P, I);
     PIO_LAUNCHED();
 
     GroupedParams d{};
@@ -388,7 +473,7 @@ int moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* w_gu
     moe_grouped_gemm_kernel<<<dim3(ceil_div(H, MoeTile::BN), E), 256, MoeTile::LDS_BYTES, st>>>(d);
     PIO_LAUNCHED();
 
-    dim3 cg(ceil_div(H, 256), T);
+    dim3 cg(ceil_div(H, 1024), T);
     if (out_dtype == PIO_F32)
         moe_combine_kernel<float><<<cg, 256, 0, st>>>(w.d, w.topk_w, w.pos_of_pair, (float*)out, T, H, top_k);
     else

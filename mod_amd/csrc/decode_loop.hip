@@ -123,6 +123,15 @@ __device__ __forceinline__ void ll_store(u64* p, float v, uint32_t tag) {
     __hip_atomic_store(p, ((u64)tag << 32) | (u64)__float_as_uint(v), __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
 }
+// Loads through the global address space (not flat): a flat load also counts
+// in lgkmcnt, so every later LDS wait of the wave (stage, rendezvous, ring
+// checks) would wait for it too. Pointers read from the parameter block are
+// generic to the compiler, hence the casts.
+template <typename T>
+__device__ __forceinline__ T gld(const T* p) {
+    return *(const __attribute__((address_space(1))) T*)p;
+}
+
 __device__ __forceinline__ void dev_store(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -475,14 +484,14 @@ __device__ __forceinline__ Pre pre_qkv(const LoopParams& p, const Cx& c, int l, 
     const int ub = c.w + LP_CW * (c.lane >> 1);
     if (ub < nu) {
         const int u = u0 + ub, row = (u >> 6) * 128 + (u & 63) + (c.lane & 1) * 64;
-        q.a = Lw.s_qkv[row];
-        q.b = Lw.b_qkv ? Lw.b_qkv[row] : 0.f;
+        q.a = gld(Lw.s_qkv + row);
+        q.b = Lw.b_qkv ? gld(Lw.b_qkv + row) : 0.f;
     }
     const int ubc = c.w + LP_CW * c.lane;
     if (ubc < nu) {
         const int i = (u0 + ubc) & 63;
-        q.cs = p.cos_t[(int64_t)pos * 64 + i];
-        q.sn = p.sin_t[(int64_t)pos * 64 + i];
+        q.cs = gld(p.cos_t + (int64_t)pos * 64 + i);
+        q.sn = gld(p.sin_t + (int64_t)pos * 64 + i);
     }
     return q;
 }
@@ -536,7 +545,7 @@ __device__ __forceinline__ Pre pre_resid(const LoopParams& p, const Cx& c, const
     Pre q;
     const int ub = c.w + LP_CW * c.lane;
     if (ub < nu) {
-        q.a = s_w[u0 + ub];
+        q.a = gld(s_w + u0 + ub);
         if (rin) q.r = ll_load(rin + u0 + ub);
     }
     return q;
@@ -560,7 +569,7 @@ __device__ bool phase_resid(const LoopParams& p, Cx& c, int line0, const u64* ri
             res = __int_as_float(__builtin_amdgcn_readlane((int)(uint32_t)pre.r, m));
             if (rt != rtag && !ll_poll1(p, c, rin + n, rtag, res, where + 1)) return false;
         } else {
-            res = emb[n];
+            res = gld(emb + n);
         }
         const float v = res + acc[m][0] * rlane(pre.a, m);
         if (c.lane == 0) ll_store(out + n, v, tag);
@@ -573,7 +582,7 @@ __device__ __forceinline__ Pre pre_gu(const LoopParams& p, const Cx& c, int l) {
     const int u0 = c.ui0, nu = c.nui;
     Pre q;
     const int ub = c.w + LP_CW * (c.lane >> 1);
-    if (ub < nu) q.a = p.layers[l].s_gu[u0 + ub + (c.lane & 1) * p.I];
+    if (ub < nu) q.a = gld(p.layers[l].s_gu + u0 + ub + (c.lane & 1) * p.I);
     return q;
 }
 
@@ -734,6 +743,15 @@ __device__ __forceinline__ void load_row16(const float* src, float (&d)[16]) {
         d[4 * i] = a.x; d[4 * i + 1] = a.y; d[4 * i + 2] = a.z; d[4 * i + 3] = a.w;
     }
 }
+// The same from global memory (the KV cache), through the global address space.
+typedef float lp_f4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void load_row16g(const float* src, float (&d)[16]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const lp_f4 a = gld((const lp_f4*)(src + 4 * i));
+        d[4 * i] = a[0]; d[4 * i + 1] = a[1]; d[4 * i + 2] = a[2]; d[4 * i + 3] = a[3];
+    }
+}
 
 // Partial attention of split s over this workgroup's positions. Lane layout:
 // 8 lanes per position (16 dims each), 8 positions per pass, both query heads
@@ -759,8 +777,8 @@ __device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t q
     for (int ps = 0; ps < LP_NPF; ps++) {
         const int tp = r.tw0 + ps * 8 + j;
         if (tp < r.tw1 && tp != pos) {
-            load_row16(kb + (int64_t)tp * 128 + part * 16, kp[ps]);
-            load_row16(vb + (int64_t)tp * 128 + part * 16, vp[ps]);
+            load_row16g(kb + (int64_t)tp * 128 + part * 16, kp[ps]);
+            load_row16g(vb + (int64_t)tp * 128 + part * 16, vp[ps]);
         } else {
 #pragma unroll
             for (int i = 0; i < 16; i++) { kp[ps][i] = 0.f; vp[ps][i] = 0.f; }
@@ -835,8 +853,8 @@ __device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t q
         const bool valid = tp < r.tw1 && tp != pos;
         float kk[16], vv[16];
         if (valid) {
-            load_row16(kb + (int64_t)tp * 128 + part * 16, kk);
-            load_row16(vb + (int64_t)tp * 128 + part * 16, vv);
+            load_row16g(kb + (int64_t)tp * 128 + part * 16, kk);
+            load_row16g(vb + (int64_t)tp * 128 + part * 16, vv);
         } else {
 #pragma unroll
             for (int i = 0; i < 16; i++) { kk[i] = 0.f; vv[i] = 0.f; }
@@ -1024,10 +1042,10 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
                 const Pre pq = pre_qkv(p, c, l, pos);
                 float v[NX], g[NX], xr[LP_CMAX][16], nscale;
 #pragma unroll
-                for (int i = 0; i < NX; i++) g[i] = Lw.in_norm[c.w * (H / 4) + c.lane + 64 * i];
+                for (int i = 0; i < NX; i++) g[i] = gld(Lw.in_norm + c.w * (H / 4) + c.lane + 64 * i);
                 if (l == 0) {
 #pragma unroll
-                    for (int i = 0; i < NX; i++) v[i] = emb[c.w * (H / 4) + c.lane + 64 * i];
+                    for (int i = 0; i < NX; i++) v[i] = gld(emb + c.w * (H / 4) + c.lane + 64 * i);
                 } else if (!ll_poll<NX>(p, c, p.xa + c.w * (H / 4), NX, tag_of(p, t, l - 1, PH_DN), v, 1)) {
                     return;
                 }
@@ -1061,7 +1079,7 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
                 constexpr int NX = CH * 4;
                 float v[NX], g[NX], xr[LP_CMAX][16], nscale;
 #pragma unroll
-                for (int i = 0; i < NX; i++) g[i] = Lw.post_norm[c.w * (H / 4) + c.lane + 64 * i];
+                for (int i = 0; i < NX; i++) g[i] = gld(Lw.post_norm + c.w * (H / 4) + c.lane + 64 * i);
                 cbar();   // the preloads must not move above the previous phase
                 const Pre pg = pre_gu(p, c, l);
                 if (!ll_poll<NX>(p, c, p.xb + c.w * (H / 4), NX, tag_of(p, t, l, PH_O), v, 5)) return;
@@ -1089,7 +1107,7 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
             constexpr int NX = CH * 4;
             float v[NX], g[NX], xr[LP_CMAX][16], nscale;
 #pragma unroll
-            for (int i = 0; i < NX; i++) g[i] = p.final_norm[c.w * (H / 4) + c.lane + 64 * i];
+            for (int i = 0; i < NX; i++) g[i] = gld(p.final_norm + c.w * (H / 4) + c.lane + 64 * i);
             if (!ll_poll<NX>(p, c, p.xa + c.w * (H / 4), NX, tag_of(p, t, p.L - 1, PH_DN), v, 9)) return;
             if (!stage_x<NX, CH>(p, c, buf, H, v, g, true, xr, nscale, 11)) return;
             const uint32_t tl = tag_of(p, t, p.L, 0);

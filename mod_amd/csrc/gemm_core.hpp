@@ -434,6 +434,141 @@ struct TileV5 {
     static_assert(S >= 3 && (S - 2) * LOADS < 64, "ring depth / vmcnt range");
 };
 
+// ---------------------------------------------------------------------------
+// Tile engine v6, for products that stream their weights from HBM (MoE
+// experts): global_load_lds copies of 8 rows x 128 B reach ~4.4 TB/s from
+// HBM, while plain 16-byte loads of the same rows into registers, written to
+// LDS by the wave, reach ~6.1 TB/s with 8+ waves per CU. Block = 8 waves
+// (2 x 4): wave (wm = w & 1, wn = w >> 1) owns WMT x WNT 32x32 MFMA tiles, so
+// the block tile is BM = 64*WMT by BN = 128*WNT. Every wave loads L = (BM +
+// BN) / 64 rows-of-8 blocks (1 KiB each) per K step, D steps ahead, into
+// register sets; at step kt it multiplies LDS stage kt % 2, then writes step
+// kt+1's set into the other stage (layout and swizzle as v3/v5) and refills
+// the set with step kt+D+1. D steps are unrolled per loop iteration, so each
+// register set has a static name; the compiler's vmcnt tracking waits for the
+// set being written and keeps the later steps' loads in flight.
+template <int WMT, int WNT, int D>
+struct TileV6 {
+    static constexpr int BM = 64 * WMT, BN = 128 * WNT, BK = 128;
+    static constexpr int L = (BM + BN) / 64;   // 1 KiB copies per wave per step (8 waves)
+    static constexpr int STAGE = (BM + BN) * BK;
+    static constexpr int LDS_BYTES = 2 * STAGE;
+    static_assert(D >= 2, "prefetch depth");
+};
+
+// LDS writes complete, then the workgroup barrier (no wait on vector memory).
+__device__ __forceinline__ void v6_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Tile-relative row / column of accumulator element e of MFMA tile (i, j) in
+// the v6 wave layout.
+template <int WMT>
+__device__ __forceinline__ int v6_row(int i, int e) {
+    const int lane = threadIdx.x & 63, wm = (threadIdx.x >> 6) & 1;
+    return wm * 32 * WMT + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+}
+template <int WNT>
+__device__ __forceinline__ int v6_col(int j) {
+    const int lane = threadIdx.x & 63, wn = (threadIdx.x >> 6) >> 1;
+    return wn * 32 * WNT + j * 32 + (lane & 31);
+}
+
+// Computes the block tile's int32 accumulators for K = 128 * NK exactly. A
+// rows past m_rem and B rows past n_rem re-read the last valid row (their
+// outputs are discarded by the caller); with a_rows, tile row r of A is
+// A[a_rows[r]]. B (the weights) is read with nontemporal loads. The K loop is
+// unrolled completely: with no loop-carried load results (a loop head makes
+// the compiler wait for every load in flight) its vmcnt tracking waits
+// exactly for the set being written and keeps the later steps' loads in
+// flight.
+template <int WMT, int WNT, int D, int NK>
+__device__ __forceinline__ void mma_tile_v6(const int8_t* __restrict__ A, int64_t lda, int m_rem,
+                                            const int8_t* __restrict__ B, int64_t ldb, int n_rem,
+                                            int8_t* lds, v16i (&acc)[WMT][WNT],
+                                            const int32_t* __restrict__ a_rows = nullptr) {
+    using T = TileV6<WMT, WNT, D>;
+    constexpr int L = T::L, ABLK = T::BM / 8;
+    static_assert(ABLK == 8 * WMT, "copies j < WMT are A blocks, the rest B blocks");
+    static_assert(NK >= 1, "K steps");
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int8_t* src[L];
+    int dst[L];
+#pragma unroll
+    for (int j = 0; j < L; j++) {
+        const int q = j * 8 + wave;   // block of 8 rows: A blocks first, then B blocks
+        if (j < WMT) {
+            const int r = q * 8 + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
+            const int rr = min(r, m_rem - 1);
+            src[j] = A + (int64_t)(a_rows ? a_rows[rr] : rr) * lda + c * 16;
+        } else {
+            const int r = (q - ABLK) * 8 + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
+            src[j] = B + (int64_t)min(r, n_rem - 1) * ldb + c * 16;
+        }
+        dst[j] = q * 1024 + lane * 16;
+    }
+    auto issue = [&](int step, v4i (&set)[L]) {
+#pragma unroll
+        for (int j = 0; j < L; j++) {
+            const int8_t* g = src[j] + step * T::BK;
+            set[j] = j < WMT ? *(const v4i*)g : __builtin_nontemporal_load((const v4i*)g);
+        }
+        __builtin_amdgcn_sched_barrier(0);   // keep the loads where they are issued
+    };
+    auto put = [&](int stage, const v4i (&set)[L]) {
+        int8_t* base = lds + stage * T::STAGE;
+#pragma unroll
+        for (int j = 0; j < L; j++) *(v4i*)(base + dst[j]) = set[j];
+    };
+    const int fr = lane & 31, fh = lane >> 5;
+    auto mma = [&](int stage) {
+        const int8_t* base = lds + stage * T::STAGE;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const int c = 2 * ks + fh;
+            v4i a[WMT], b[WNT];
+#pragma unroll
+            for (int i = 0; i < WMT; i++) a[i] = *(const v4i*)(base + swz(wm * 32 * WMT + i * 32 + fr, c));
+#pragma unroll
+            for (int j = 0; j < WNT; j++)
+                b[j] = *(const v4i*)(base + T::BM * 128 + swz(wn * 32 * WNT + j * 32 + fr, c));
+#pragma unroll
+            for (int i = 0; i < WMT; i++)
+#pragma unroll
+                for (int j = 0; j < WNT; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+#pragma unroll
+    for (int i = 0; i < WMT; i++)
+#pragma unroll
+        for (int j = 0; j < WNT; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0;
+
+    v4i rs[D][L];
+#pragma unroll
+    for (int s = 0; s < D; s++)
+        if (s < NK) issue(s, rs[s]);
+    put(0, rs[0]);
+    if (D < NK) issue(D, rs[0]);
+    v6_barrier();
+#pragma unroll
+    for (int kt = 0; kt < NK; kt++) {
+        mma(kt & 1);
+        if (kt + 1 < NK) {
+            put((kt + 1) & 1, rs[(kt + 1) % D]);
+            if (kt + D + 1 < NK) issue(kt + D + 1, rs[(kt + 1) % D]);
+        }
+        v6_barrier();
+    }
+}
+
 // Stages of the v5 ring for a tile shape: as many as fit in 160 KB, at most 6.
 template <int WMT, int WNT>
 constexpr int v5_stages() {

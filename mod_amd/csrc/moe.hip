@@ -213,14 +213,17 @@ struct GroupedParams {
     int N, K;
 };
 
-// Block (n-tile, expert) on the pipelined direct-to-LDS engine: 64 x 128 tiles
-// (2x2 waves of 32x64), 3 LDS stages (72 KB, two blocks per CU), A rows
-// gathered through the expert's token list. The block walks its expert's row
-// tiles, so each weight tile is streamed from HBM once per 64 tokens.
-constexpr int MOE_WMT = 1, MOE_WNT = 2, MOE_STAGES = 3;
-using MoeTile = TileV3<MOE_WMT, MOE_WNT, MOE_STAGES>;
+// Block (n-tile, expert) on the register-staged v6 engine (the expert layer
+// streams its weights from HBM once): 64 x 128 tiles, 8 waves, 4 K steps of
+// loads in flight per wave, 48 KB of LDS (two blocks per CU), A rows gathered
+// through the expert's token list. The block walks its expert's row tiles, so
+// each weight tile is streamed from HBM once per 64 tokens.
+constexpr int MOE_WMT = 1, MOE_WNT = 1, MOE_D = 4;
+using MoeTile = TileV6<MOE_WMT, MOE_WNT, MOE_D>;
+constexpr int MOE_THREADS = 512;
 
-__global__ __launch_bounds__(256, 2) void moe_grouped_gemm_kernel(GroupedParams p) {
+template <int NK>
+__global__ __launch_bounds__(MOE_THREADS, 2) void moe_grouped_gemm_kernel(GroupedParams p) {
     extern __shared__ __attribute__((aligned(16))) int8_t lds_moe[];
     const int e = blockIdx.y, n0 = blockIdx.x * MoeTile::BN;
     const int beg = p.offsets[e], cnt = p.offsets[e + 1] - beg;
@@ -242,30 +245,39 @@ __global__ __launch_bounds__(256, 2) void moe_grouped_gemm_kernel(GroupedParams 
         }
         v16i acc[MOE_WMT][MOE_WNT];
         if (p.a_rows)
-            mma_tile_v3<MOE_WMT, MOE_WNT, MOE_STAGES>(p.A, p.K, cnt - m0, W, p.K, p.N - n0, p.K,
-                                                      lds_moe, acc, p.a_rows + beg + m0);
+            mma_tile_v6<MOE_WMT, MOE_WNT, MOE_D, NK>(p.A, p.K, cnt - m0, W, p.K, p.N - n0, lds_moe, acc,
+                                                     p.a_rows + beg + m0);
         else
-            mma_tile_v3<MOE_WMT, MOE_WNT, MOE_STAGES>(p.A + (int64_t)(beg + m0) * p.K, p.K,
-                                                      cnt - m0, W, p.K, p.N - n0, p.K, lds_moe,
-                                                      acc);
-        float* scl = (float*)lds_moe;   // the ring is free once every wave is past this barrier
+            mma_tile_v6<MOE_WMT, MOE_WNT, MOE_D, NK>(p.A + (int64_t)(beg + m0) * p.K, p.K, cnt - m0, W, p.K,
+                                                     p.N - n0, lds_moe, acc);
+        float* scl = (float*)lds_moe;   // the stages are free once every wave is past this barrier
         __syncthreads();
         if (tid < MoeTile::BM + MoeTile::BN) scl[tid] = my_scale;
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < MOE_WNT; j++) {
-            const int c = v2_col<MOE_WNT>(j), n = n0 + c;
+            const int c = v6_col<MOE_WNT>(j), n = n0 + c;
             const float swn = scl[MoeTile::BM + c];
 #pragma unroll
             for (int i = 0; i < MOE_WMT; i++)
 #pragma unroll
                 for (int v = 0; v < 16; v++) {
-                    const int rl = v2_row<MOE_WMT>(i, v), r = m0 + rl;
+                    const int rl = v6_row<MOE_WMT>(i, v), r = m0 + rl;
                     const float val = (float)acc[i][j][v] * scl[rl] * swn;
                     if (r < cnt && n < p.N) p.C[(int64_t)(beg + r) * p.N + n] = val;
                 }
         }
-        __syncthreads();   // the next row tile reuses the LDS ring
+        __syncthreads();   // the next row tile reuses the LDS stages
+    }
+}
+
+// Launches the instance for K = 128 * nk (1 <= nk <= MOE_MAX_NK).
+constexpr int MOE_MAX_NK = 32;
+template <int NK>
+static void launch_grouped(const GroupedParams& g, dim3 grid, int nk, hipStream_t st) {
+    if constexpr (NK <= MOE_MAX_NK) {
+        if (nk == NK) moe_grouped_gemm_kernel<NK><<<grid, MOE_THREADS, MoeTile::LDS_BYTES, st>>>(g);
+        else launch_grouped<NK + 1>(g, grid, nk, st);
     }
 }
 
@@ -425,6 +437,8 @@ int moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* w_gu
     PIO_REQUIRE(x && logits && w_gu && s_gu && w_down && s_down && out, "moe: null pointer");
     PIO_REQUIRE(T >= 0 && H > 0 && I > 0, "moe: bad shape");
     PIO_REQUIRE(H % 128 == 0 && I % 128 == 0, "moe: H=%d and I=%d must be multiples of 128", H, I);
+    PIO_REQUIRE(H <= 128 * MOE_MAX_NK && I <= 128 * MOE_MAX_NK, "moe: H=%d and I=%d must be <= %d", H,
+                I, 128 * MOE_MAX_NK);
     PIO_REQUIRE(out_dtype == PIO_F32 || out_dtype == PIO_F16, "moe: out must be fp32 or fp16");
     PIO_REQUIRE((int64_t)T * 8 <= GROUP_MAX_PAIRS && (int64_t)E * ((T + 63) / 64) <= GROUP_MAX_ITEMS &&
                     top_k <= 8 && E <= 32767,
@@ -433,12 +447,6 @@ int moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* w_gu
                 GROUP_MAX_ITEMS);
     PIO_REQUIRE(aligned16(w_gu) && aligned16(w_down), "moe: weights must be 16-byte aligned");
     if (T == 0) return PIO_OK;
-    static bool lds_ok = false;
-    if (!lds_ok) {
-        PIO_HIP(hipFuncSetAttribute((const void*)moe_grouped_gemm_kernel,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, MoeTile::LDS_BYTES));
-        lds_ok = true;
-    }
     Scratch own;
     if (!ws) {
         PIO_TRY(own.get(moe_layout(nullptr, T, H, I, E, top_k).total));
@@ -457,7 +465,7 @@ int moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* w_gu
     g.A = w.qx; g.a_rows = w.row_token; g.s_a = w.sx;
     g.W = w_gu; g.s_w = s_gu; g.offsets = w.offsets; g.C = w.gu;
     g.N = 2 * I; g.K = H;
-    moe_grouped_gemm_kernel<<<dim3(ceil_div(2 * I, MoeTile::BN), E), 256, MoeTile::LDS_BYTES, st>>>(g);
+    launch_grouped<1>(g, dim3(ceil_div(2 * I, MoeTile::BN), E), H / 128, st);
     PIO_LAUNCHED();
 
     if (I <= 64 * 4 * SWIGLU_NV)
@@ -470,7 +478,7 @@ int moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* w_gu
     d.A = w.qh; d.a_rows = nullptr; d.s_a = w.sh;
     d.W = w_down; d.s_w = s_down; d.offsets = w.offsets; d.C = w.d;
     d.N = H; d.K = I;
-    moe_grouped_gemm_kernel<<<dim3(ceil_div(H, MoeTile::BN), E), 256, MoeTile::LDS_BYTES, st>>>(d);
+    launch_grouped<1>(d, dim3(ceil_div(H, MoeTile::BN), E), I / 128, st);
     PIO_LAUNCHED();
 
     dim3 cg(ceil_div(H, 1024), T);

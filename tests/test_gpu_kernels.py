@@ -151,7 +151,9 @@ def test_gemv_extreme_weights(env):
 # --------------------------------------------------------------- quantizer
 @pytest.mark.parametrize("M,K,xdt", [(2048, 1024, np.float16), (2048, 3072, np.float16),
                                      (17, 1000, np.float32), (5, 13, np.float32),
-                                     (512, 2048, np.float16), (3, 12288, np.float32)])
+                                     (512, 2048, np.float16), (3, 12288, np.float32),
+                                     (1, 12288, np.float16), (64, 4096, np.float16),
+                                     (1030, 8200, np.float32), (1500, 520, np.float16)])
 def test_quant_bitexact(env, M, K, xdt):
     torch, ops, d = env
     _say(f"quant M={M} K={K}")

@@ -51,10 +51,9 @@ __device__ __forceinline__ float scaled_value(int a, float sa, float sw, float b
 // host to minimize the A + B panel bytes one XCD's L2 has to hold); inside it,
 // the XCD's blocks walk the rectangle row by row. Identity map when the grid
 // does not split into 8 rectangles.
-// ENG 2: register-staged v2 engine (any K % 16 == 0); 3: direct-to-LDS v3
-// engine with S stages (K % 128 == 0); 4: direct-to-LDS v4 engine, square
-// tiles, half-step ring (K % 128 == 0); 5: direct-to-LDS v5 engine, S-stage
-// ring on the v4 schedule (K % 128 == 0).
+// ENG 2: register-staged v2 engine (any K % 16 == 0); 4: direct-to-LDS v4
+// engine, square tiles, half-step ring (K % 128 == 0); 5: direct-to-LDS v5
+// engine, S-stage ring on the v4 schedule (K % 128 == 0).
 template <int WMT, int WNT, int OUT, int ENG, int S>
 __global__ __launch_bounds__(256, 1) void gemm_v2_kernel(GemmParams p, int tiles_n) {
     using T = TileV2<WMT, WNT>;
@@ -99,7 +98,6 @@ __global__ __launch_bounds__(256, 1) void gemm_v2_kernel(GemmParams p, int tiles
     const int8_t* A = p.A + z * p.a_batch + (int64_t)m0 * p.lda;
     const int8_t* B = p.B + z * p.b_batch + (int64_t)n0 * p.ldb;
     if constexpr (ENG == 2) mma_tile_v2<WMT, WNT>(A, p.lda, p.M - m0, B, p.ldb, p.N - n0, p.K, lds_v2, acc);
-    else if constexpr (ENG == 3) mma_tile_v3<WMT, WNT, S>(A, p.lda, p.M - m0, B, p.ldb, p.N - n0, p.K, lds_v2, acc);
     else if constexpr (ENG == 5) mma_tile_v5<WMT, WNT, S>(A, p.lda, p.M - m0, B, p.ldb, p.N - n0, p.K, lds_v2, acc);
     else mma_tile_v4<WMT>(A, p.lda, p.M - m0, B, p.ldb, p.N - n0, p.K, lds_v2, acc);
     if (SCALED && LATE) load_scales();
@@ -164,7 +162,6 @@ static int allow_lds(F* kernel, size_t bytes) {
 template <int WMT, int WNT, int ENG, int S>
 constexpr size_t engine_lds() {
     if constexpr (ENG == 2) return TileV2<WMT, WNT>::LDS_BYTES;
-    else if constexpr (ENG == 3) return TileV3<WMT, WNT, S>::LDS_BYTES;
     else if constexpr (ENG == 5) return TileV5<WMT, WNT, S>::LDS_BYTES;
     else return TileV4<WMT>::LDS_BYTES;
 }

@@ -138,26 +138,13 @@ __device__ __forceinline__ int v2_col(int j) {
 namespace pio {
 
 // ---------------------------------------------------------------------------
-// Dense tile engine v3: same MFMA tiling and LDS swizzle as v2, but operands
-// go straight from global memory into an S-stage LDS ring with
-// global_load_lds_dwordx4 (no register staging), S-1 K steps in flight.
-//
-// One wave instruction moves a 1 KB block = 8 rows x 128 B: lane l lands at
-// LDS byte 16*l of the block, i.e. row l/8, slot l%8, so it fetches global
-// chunk (l%8) ^ ((row >> 1) & 7) -- the v2 swizzle applied on the read side of
-// the copy. Requires K % 128 == 0 (a K tail cannot be zero-filled on this
-// path). Rows past m_rem / n_rem re-read the last valid row; they only feed
-// output rows / columns the caller discards. With `a_rows`, tile row r of A is
-// global row a_rows[r] (MoE token gather).
-template <int WMT, int WNT, int S>
-struct TileV3 {
-    static constexpr int BM = 64 * WMT, BN = 64 * WNT, BK = 128, STAGES = S;
-    static constexpr int A_BLK = BM / 8, B_BLK = BN / 8;          // 1 KB blocks per stage
-    static constexpr int A_PER_WAVE = A_BLK / 4, B_PER_WAVE = B_BLK / 4;
-    static constexpr int LOADS = A_PER_WAVE + B_PER_WAVE;         // per wave per stage
-    static constexpr int STAGE = (BM + BN) * BK;
-    static constexpr int LDS_BYTES = S * STAGE;
-};
+// Direct-to-LDS copies (engines v4 and v5): global_load_lds_dwordx4 moves a
+// 1 KB block = 8 rows x 128 B per wave instruction, whole cache lines: lane l
+// lands at LDS byte 16*l of the block, i.e. row l/8, slot l%8, so it fetches
+// global chunk (l%8) ^ ((row >> 1) & 7) -- the v2 swizzle applied on the read
+// side of the copy. Requires K % 128 == 0 (a K tail cannot be zero-filled on
+// this path). Rows past m_rem / n_rem re-read the last valid row; they only
+// feed output rows / columns the caller discards.
 
 // Waits until at most N vector-memory loads of this wave are outstanding and
 // all its LDS operations are done, then joins the workgroup barrier. Unlike
@@ -188,106 +175,17 @@ __device__ __forceinline__ void stage_barrier_steps(int n) {
     }
 }
 
-template <int WMT, int WNT, int S>
-__device__ __forceinline__ void mma_tile_v3(const int8_t* __restrict__ A, int64_t lda, int m_rem,
-                                            const int8_t* __restrict__ B, int64_t ldb, int n_rem,
-                                            int K, int8_t* lds, v16i (&acc)[WMT][WNT],
-                                            const int32_t* __restrict__ a_rows = nullptr) {
-    using T = TileV3<WMT, WNT, S>;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-
-    // Per-lane global source of each of this wave's block loads.
-    const int8_t* ga[T::A_PER_WAVE];
-    const int8_t* gb[T::B_PER_WAVE];
-#pragma unroll
-    for (int j = 0; j < T::A_PER_WAVE; j++) {
-        const int q = j * 4 + wave, r = q * 8 + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
-        const int rr = min(r, m_rem - 1);   // A row r of the tile: A[a_rows[r]] when gathering
-        ga[j] = A + (int64_t)(a_rows ? a_rows[rr] : rr) * lda + c * 16;
-    }
-#pragma unroll
-    for (int j = 0; j < T::B_PER_WAVE; j++) {
-        const int q = j * 4 + wave, r = q * 8 + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
-        gb[j] = B + (int64_t)min(r, n_rem - 1) * ldb + c * 16;
-    }
-    typedef __attribute__((address_space(3))) void lds_t;
-    // Issues this wave's loads number [from, to) of K step `kstep` (its A
-    // blocks first, then its B blocks).
-    auto issue = [&](int kstep, int from, int to) {
-        int8_t* base = lds + (kstep % S) * T::STAGE;
-        const int k0 = kstep * T::BK;
-#pragma unroll
-        for (int j = 0; j < T::A_PER_WAVE; j++)
-            if (j >= from && j < to)
-                __builtin_amdgcn_global_load_lds((const void*)(ga[j] + k0),
-                                                 (lds_t*)(base + (j * 4 + wave) * 1024), 16, 0, 0);
-#pragma unroll
-        for (int j = 0; j < T::B_PER_WAVE; j++)
-            if (T::A_PER_WAVE + j >= from && T::A_PER_WAVE + j < to)
-                __builtin_amdgcn_global_load_lds((const void*)(gb[j] + k0),
-                                                 (lds_t*)(base + T::BM * 128 + (j * 4 + wave) * 1024),
-                                                 16, 0, 0);
-    };
-
-#pragma unroll
-    for (int i = 0; i < WMT; i++)
-#pragma unroll
-        for (int j = 0; j < WNT; j++)
-#pragma unroll
-            for (int e = 0; e < 16; e++) acc[i][j][e] = 0;
-
-    const int nk = K / T::BK;
-#pragma unroll
-    for (int s = 0; s < S - 1; s++)
-        if (s < nk) issue(s, 0, T::A_PER_WAVE + T::B_PER_WAVE);
-    const int fr = lane & 31, fh = lane >> 5;
-    // Fragments of k sub-step ks of the current stage; double-buffered so the
-    // next sub-step's LDS reads are in flight while this one's MFMAs run.
-    auto frag = [&](const int8_t* base, int ks, v4i (&a)[WMT], v4i (&b)[WNT]) {
-        const int c = 2 * ks + fh;
-#pragma unroll
-        for (int i = 0; i < WMT; i++) a[i] = *(const v4i*)(base + swz(wm * 32 * WMT + i * 32 + fr, c));
-#pragma unroll
-        for (int j = 0; j < WNT; j++)
-            b[j] = *(const v4i*)(base + T::BM * 128 + swz(wn * 32 * WNT + j * 32 + fr, c));
-    };
-    for (int kt = 0; kt < nk; kt++) {
-        // Stages issued so far: min(nk, kt + S - 1); wait for stage kt.
-        const int ahead = min(nk, kt + S - 1) - kt - 1;
-        if (S >= 4 && ahead >= 2) stage_barrier<(S >= 4 ? 2 : 0) * T::LOADS>();
-        else if (ahead >= 1) stage_barrier<T::LOADS>();
-        else stage_barrier<0>();
-        const bool more = kt + S - 1 < nk;
-        const int8_t* base = lds + (kt % S) * T::STAGE;
-        v4i fa[2][WMT], fb[2][WNT];
-        frag(base, 0, fa[0], fb[0]);
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            if (ks < 3) frag(base, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
-            // a quarter of the next stage's global->LDS copies per sub-step
-            if (more) issue(kt + S - 1, ks * T::LOADS / 4, (ks + 1) * T::LOADS / 4);
-#pragma unroll
-            for (int i = 0; i < WMT; i++)
-#pragma unroll
-                for (int j = 0; j < WNT; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[ks & 1][i], fb[ks & 1][j],
-                                                                      acc[i][j], 0, 0, 0);
-        }
-    }
-}
-
 // ---------------------------------------------------------------------------
 // Dense tile engine v4, for the big square block tile (256 x 256: each wave
 // 128 x 128 = 4 x 4 MFMA tiles, so one ds_read_b128 fragment feeds 4 MFMAs).
-// A K step is 128 bytes, as in v3: a copy instruction moves 8 rows x 128 B,
-// whole cache lines (copies of 16 rows x 64 B -- half lines -- fill the LDS at
-// little more than half the rate). A full step of both operands is 64 KB, so
+// A K step is 128 bytes: a copy instruction moves 8 rows x 128 B, whole cache
+// lines (copies of 16 rows x 64 B -- half lines -- fill the LDS at little
+// more than half the rate). A full step of both operands is 64 KB, so
 // the LDS holds the A slice and the B slice of a step as separate 32 KB
 // halves in a ring of 5 (160 KB): half h = 2*step + (0: A, 1: B) sits in slot
 // h % 5. While step kt is multiplied, the halves of steps kt+1 (B) and kt+2
 // (A) are being copied -- the only slots not holding step kt or kt+1's A.
-// Slot layout as v3: 16-byte chunk c of row r at c ^ ((r >> 1) & 7).
+// Slot layout: 16-byte chunk c of row r at c ^ ((r >> 1) & 7).
 template <int WT>
 struct TileV4 {
     static constexpr int BM = 64 * WT, BN = 64 * WT, BK = 128, SLOTS = 5;
@@ -404,9 +302,9 @@ __device__ __forceinline__ void mma_tile_v4(const int8_t* __restrict__ A, int64_
 }
 
 // ---------------------------------------------------------------------------
-// Dense tile engine v5: the v3 tiling (2 x 2 waves of WMT x WNT MFMA tiles, an
-// S-stage LDS ring of whole K steps, filled by 8-row x 128 B copies) run on
-// the v4 schedule:
+// Dense tile engine v5: 2 x 2 waves of WMT x WNT MFMA tiles (the v2 tiling),
+// an S-stage LDS ring of whole K steps filled by 8-row x 128 B direct copies,
+// run on the v4 schedule:
 //   - one barrier per K step, before its last sub-step: by then every wave has
 //     read all of step kt's fragments, and step kt+1's stage is waited for, so
 //     its first fragments are read while the last sub-step's MFMAs run;
@@ -443,7 +341,7 @@ struct TileV5 {
 // the block tile is BM = 64*WMT by BN = 128*WNT. Every wave loads L = (BM +
 // BN) / 64 rows-of-8 blocks (1 KiB each) per K step, D steps ahead, into
 // register sets; at step kt it multiplies LDS stage kt % 2, then writes step
-// kt+1's set into the other stage (layout and swizzle as v3/v5) and refills
+// kt+1's set into the other stage (layout and swizzle as v4/v5) and refills
 // the set with step kt+D+1. D steps are unrolled per loop iteration, so each
 // register set has a static name; the compiler's vmcnt tracking waits for the
 // set being written and keeps the later steps' loads in flight.

@@ -344,6 +344,138 @@ def cpu_baseline(cfg, w, budget_s=20.0):
     }
 
 
+# ----------------------------------------------------------- checkpoint load
+def _ckpt_tensors(cfg, w, fp: bool):
+    """Config-2 decoder weights under Hugging Face names (fused qkv / gate_up,
+    the reference layout): int8 + _scale pairs, or (fp) bf16 bits of the
+    dequantized weights. Embedding stored bf16, norms and biases fp32."""
+    import numpy as np
+
+    def bf16(a):
+        return (np.ascontiguousarray(a, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+    t, dts = {}, {}
+
+    def lin(name, q, s):
+        if fp:
+            t[name] = bf16(q.astype(np.float32) * s[:, None])
+            dts[name] = "BF16"
+        else:
+            t[name], t[name + "_scale"] = q, s
+
+    for i, L in enumerate(w["layers"]):
+        p = f"model.layers.{i}."
+        t[p + "input_layernorm.weight"] = L["in_norm"]
+        t[p + "post_attention_layernorm.weight"] = L["post_norm"]
+        lin(p + "self_attn.qkv_proj.weight", L["w_qkv"], L["s_qkv"])
+        t[p + "self_attn.qkv_proj.bias"] = L["b_qkv"]
+        lin(p + "self_attn.o_proj.weight", L["w_o"], L["s_o"])
+        lin(p + "mlp.gate_up_proj.weight", L["w_gu"], L["s_gu"])
+        lin(p + "mlp.down_proj.weight", L["w_down"], L["s_down"])
+    t["model.embed_tokens.weight"] = bf16(w["embed"])
+    dts["model.embed_tokens.weight"] = "BF16"
+    t["model.norm.weight"] = w["final_norm"]
+    lin("lm_head.weight", w["lm_head"], w["s_lm_head"])
+    return t, dts
+
+
+def bench_weights(torch):
+    """Checkpoint -> HBM for the config-2 decoder, from the page cache (files
+    just written): the int8 format loaded as stored, a BF16 checkpoint
+    quantized on the GPU while loading, and the offline BF16 -> int8
+    conversion; beside them a plain pinned host-to-device copy of the int8
+    file's bytes, and the reference's loader (load_tensor_data into host fp32)
+    over the BF16 file."""
+    import shutil
+    import tempfile
+    import numpy as np
+    from mod_amd import weights as W
+    from mod_amd.qwen3 import Qwen3Config, random_weights, weights_from_checkpoint
+
+    cfg = Qwen3Config()
+    w = random_weights(cfg, seed=0)
+    tmp = Path(tempfile.mkdtemp(prefix="pio_ckpt_", dir=os.environ.get("TMPDIR", "/tmp")))
+    res = {}
+    try:
+        paths = {}
+        for kind in ("int8", "bf16"):
+            t, dts = _ckpt_tensors(cfg, w, fp=kind == "bf16")
+            paths[kind] = tmp / f"{kind}.safetensors"
+            t0 = time.perf_counter()
+            W.save_safetensors(paths[kind], t, dtypes=dts)
+            log(f"[weights] wrote {kind} checkpoint {paths[kind].stat().st_size / 1e6:.0f} MB "
+                f"in {time.perf_counter() - t0:.1f}s")
+            del t
+        for kind in ("int8", "bf16"):
+            times = []
+            for _ in range(2):
+                t0 = time.perf_counter()
+                dw = weights_from_checkpoint(paths[kind], cfg)
+                torch.cuda.synchronize()
+                times.append(time.perf_counter() - t0)
+                del dw
+            nb = paths[kind].stat().st_size
+            res[kind] = {"bytes": nb, "s": times[-1], "GBs": nb / times[-1] / 1e9,
+                         "first_s": times[0]}
+            log(f"[weights] {kind} checkpoint -> HBM: {times[-1]:.3f}s "
+                f"({nb / times[-1] / 1e9:.2f} GB/s; first {times[0]:.3f}s)")
+        t0 = time.perf_counter()
+        W.quantize_checkpoint(paths["bf16"], tmp / "q.safetensors")
+        res["quantize_checkpoint_s"] = time.perf_counter() - t0
+        # plain pinned H2D copy of the same byte count
+        nb = res["int8"]["bytes"]
+        src = torch.empty(nb, dtype=torch.uint8, pin_memory=True)
+        dst = torch.empty(nb, dtype=torch.uint8, device="cuda")
+        dst.copy_(src, non_blocking=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        dst.copy_(src, non_blocking=True)
+        torch.cuda.synchronize()
+        res["h2d_pinned_GBs"] = nb / (time.perf_counter() - t0) / 1e9
+        del src, dst
+        # the reference loader over the BF16 file (its byte-count dispatch reads
+        # the 2-byte tensors as F16: the same work, different values)
+        res["cpu"] = _ref_loader_time(paths["bf16"])
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    return res
+
+
+def _ref_loader_time(path):
+    import ctypes
+    import numpy as np
+    import oracle
+    lib_path = oracle.HERE / "_ref" / "libsafetensors_ref.so"
+    if not lib_path.exists():
+        return None
+    from oracle import safetensors_ref as stref
+    L = ctypes.CDLL(str(lib_path))
+    L.open_safetensors.restype = ctypes.c_void_p
+    L.open_safetensors.argtypes = [ctypes.c_char_p]
+    L.load_tensor_data.restype = ctypes.c_int
+    L.load_tensor_data.argtypes = [ctypes.c_void_p, ctypes.c_char_p,
+                                   ctypes.POINTER(ctypes.c_float), ctypes.c_int]
+    L.close_safetensors.argtypes = [ctypes.c_void_p]
+    entries, _ = stref.read_header(path)
+    t0 = time.perf_counter()
+    ctx = L.open_safetensors(str(path).encode())
+    ok = 0
+    for name, (dt, shape, b, e) in entries.items():
+        n = int(np.prod(shape))
+        buf = np.empty(n, np.float32)
+        ok += L.load_tensor_data(ctx, name.encode(), buf.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), n)
+    L.close_safetensors(ctx)
+    dt_s = time.perf_counter() - t0
+    nb = Path(path).stat().st_size
+    return {"value": nb / dt_s / 1e9, "unit": "GB/s", "cores": int(os.environ.get("OMP_NUM_THREADS", 0))
+            or os.cpu_count(), "kind": "reference",
+            "sample": (f"reference load_tensor_data (safetensors_loader.c:147-243, built from its "
+                       f"source) of all {len(entries)} tensors of the BF16 checkpoint into host "
+                       f"fp32 buffers ({ok} loaded; its F16 conversion loop runs under OpenMP); "
+                       f"the host-to-device copy the reference does next is not included"),
+            "s": dt_s}
+
+
 # ----------------------------------------------------------------- traffic
 TRAFFIC_PROFILE = ROOT / "profiles" / "decode_loop_kernel_traffic.txt"
 
@@ -377,6 +509,9 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (three times), for scaling "
                          "the FETCH_SIZE / WRITE_SIZE counters of the traffic measurement")
+    ap.add_argument("--weights", action="store_true",
+                    help="only time checkpoint loading (config-2 decoder weights, int8 and BF16 "
+                         "safetensors from the page cache into HBM) and print its own JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: the int8 path has no multi-GPU component in this "
@@ -397,6 +532,24 @@ def main():
         return 0
     from mod_amd import ops
     log(f"[bench] {ops.version()}  lib={ops.LIB_FILE}")
+    if args.weights:
+        r = bench_weights(torch)
+        cpu = r.pop("cpu")
+        rnd = lambda d: {k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}  # noqa: E731
+        print(json.dumps({
+            "metric": "int8 checkpoint load, page cache -> HBM",
+            "value": round(r["int8"]["GBs"], 3), "unit": "GB/s", "n_gpus": 1,
+            "higher_is_better": True, "dtype": "int8 weights, fp32 scales, bf16 embedding",
+            "data": "synthetic: random-init config-2 decoder weights written as safetensors",
+            "config": {"workload": "Qwen3-0.6B-shaped decoder checkpoint (28 layers, vocab "
+                                   "151936) loaded by qwen3.weights_from_checkpoint"},
+            "int8": rnd(r["int8"]), "bf16_quantized_on_load": rnd(r["bf16"]),
+            "quantize_checkpoint_s": round(r["quantize_checkpoint_s"], 3),
+            "h2d_pinned_GBs": round(r["h2d_pinned_GBs"], 2),
+            "frac_of_pinned_h2d": round(r["int8"]["GBs"] / r["h2d_pinned_GBs"], 4),
+            "cpu_baseline": cpu and rnd(cpu),
+        }), flush=True)
+        return 0
     timer = Timer(torch)
 
     cfg, w, dec, st, dall = bench_decode(torch, args)

@@ -297,6 +297,72 @@ int pio_qwen3_read(void* dec, int32_t* ids, int n, float* logits);
 /* Device pointer of the last step's logits ([vocab] fp32). */
 const float* pio_qwen3_logits(void* dec);
 
+/* ---------------------------------------------------------------------------
+ * int8 on-disk weights: safetensors reading.
+ *
+ * The reference loads checkpoints through plugins/cpu/c_src/safetensors_loader.c
+ * (bound at core/engine/backend.py:120-126, driven by load_safetensors,
+ * backend.py:812-835). That loader searches the header text for the name and
+ * picks F32 or F16 from the byte count, so BF16 is misread and I8 is refused.
+ * Here the header is parsed into a table and conversions follow the stored
+ * dtype; the three reference entry points keep their signatures and return
+ * conventions. A context is read-only after open and may be shared by threads.
+ * ------------------------------------------------------------------------- */
+
+/* safetensors_loader.c:40-120. Maps the file read-only and parses its header;
+ * NULL on any error (missing file, header length beyond the file, malformed
+ * JSON, an entry whose offsets leave the data region or whose byte count is
+ * not dtype size x shape, a duplicate name); the reason is in
+ * tensor_last_error. */
+void* open_safetensors(const char* filepath);
+/* safetensors_loader.c:147-243. Converts tensor `name` to fp32 into `buffer`
+ * (`size` fp32 elements, which must equal the tensor's element count). Reads
+ * F32, F16, BF16, I8, U8, BOOL, I16 and I32 by their stored dtype (the
+ * reference reads only F32 and, by byte count, F16). 1 on success, 0 if the
+ * name is absent, the size differs or the dtype has no fp32 conversion. */
+int load_tensor_data(void* ctx, const char* name, float* buffer, int size);
+/* safetensors_loader.c:245-265. Unmaps the file; NULL is a no-op. */
+void close_safetensors(void* ctx);
+
+/* Stored dtype codes reported by pio_safetensors_info. */
+enum {
+    PIO_ST_F64 = 0, PIO_ST_F32 = 1, PIO_ST_F16 = 2, PIO_ST_BF16 = 3, PIO_ST_I64 = 4,
+    PIO_ST_I32 = 5, PIO_ST_I16 = 6, PIO_ST_I8 = 7, PIO_ST_U8 = 8, PIO_ST_BOOL = 9,
+    PIO_ST_U16 = 10, PIO_ST_U32 = 11, PIO_ST_U64 = 12,
+};
+/* Number of tensors in the file (__metadata__ excluded); the i-th name in
+ * header order (NULL when out of range; valid until close). No reference
+ * counterpart: the reference can only probe names it already knows. */
+int pio_safetensors_count(void* ctx);
+const char* pio_safetensors_name(void* ctx, int i);
+/* Stored dtype (PIO_ST_*), rank, up to max_dims dims and byte count of
+ * `name`; any output pointer may be NULL. PIO_OK or PIO_ERR_INVALID. */
+int pio_safetensors_info(void* ctx, const char* name, int* dtype, int64_t* shape, int max_dims,
+                         int* ndim, int64_t* nbytes);
+/* The stored bytes of `name` into host memory; nbytes must equal the stored
+ * size. */
+int pio_safetensors_read(void* ctx, const char* name, void* dst, int64_t nbytes);
+/* The stored bytes of `name` into device memory `dst` on `stream` (NULL =
+ * current); returns once the bytes have landed. The bytes are read with
+ * pread by up to 8 threads into two pinned 16 MiB staging buffers, one
+ * filling while the other's DMA runs; the buffers and threads are
+ * process-wide, made on first use and kept until exit, and device loads
+ * serialize on them. */
+int pio_safetensors_to_device(void* ctx, const char* name, void* dst, int64_t nbytes,
+                              void* stream);
+/* `name` converted to fp32 into device memory (`count` elements, which must
+ * equal the tensor's): F32 is copied; BF16, F16, I8, U8, BOOL, I16 and I32
+ * land raw in device scratch and are widened on the GPU (bit-exact; a
+ * signalling F16 NaN comes back quiet). Returns once done. */
+int pio_safetensors_to_device_f32(void* ctx, const char* name, float* dst, int64_t count,
+                                  void* stream);
+/* Drop-in load of `name` into a device Tensor (the tensor_load_data step of
+ * backend.py:822-826 without the host fp32 round trip): an int8 tensor takes
+ * I8 / U8 bytes, an fp16 tensor F16 bytes, an fp32 tensor any dtype
+ * pio_safetensors_to_device_f32 converts. Element counts must match. */
+void tensor_load_safetensors(void* ctx, const char* name, Tensor* out);
+int tensor_load_safetensors_status(void* ctx, const char* name, Tensor* out);
+
 /* Library version string and the gfx target it was built for. */
 const char* pio_version(void);
 

@@ -225,16 +225,6 @@ class Module:
         return destination
 
 
-def quantize_weight_per_channel(w: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
-    """Offline per-output-channel symmetric quantization of an fp weight [N,K]:
-    s = amax_row / 127 (1 for all-zero rows), q = clamp(rint(w / s), -127, 127)."""
-    w = np.asarray(w, dtype=np.float32)
-    amax = np.abs(w).max(axis=1)
-    s = np.where(amax == 0, np.float32(1), amax / np.float32(127)).astype(np.float32)
-    q = np.clip(np.rint(w / s[:, None]), -127, 127).astype(np.int8)
-    return q, s
-
-
 class W8Linear(Module):
     """Drop-in for the reference Linear (backend.py:695-702) with int8 weights
     [out, in] and per-output-channel fp32 scales; forward(x) = x.linear_w8(...)."""
@@ -259,7 +249,10 @@ class W8Linear(Module):
             self.bias.load(b)
 
     def load_float(self, w: np.ndarray, b: Optional[np.ndarray] = None):
-        q, s = quantize_weight_per_channel(w)
+        """Quantize an fp weight [out, in] per output channel on the GPU
+        (s = amax_row / 127, q = rint(w / s)) and load it."""
+        from .weights import quantize_array
+        q, s = quantize_array(w, self.weight.device)
         self.load_quantized(q, s, b)
 
     def forward(self, x: Tensor) -> Tensor:

@@ -102,6 +102,19 @@ SIGNATURES: dict[str, tuple] = {
     "pio_qwen3_persistent_supported": (_i, [_vp]),
     "pio_qwen3_read": (_i, [_vp, _vp, _i, _vp]),
     "pio_qwen3_logits": (_vp, [_vp]),
+    "open_safetensors": (_vp, [ctypes.c_char_p]),
+    "load_tensor_data": (_i, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float), _i]),
+    "close_safetensors": (None, [_vp]),
+    "pio_safetensors_count": (_i, [_vp]),
+    "pio_safetensors_name": (ctypes.c_char_p, [_vp, _i]),
+    "pio_safetensors_info": (_i, [_vp, ctypes.c_char_p, ctypes.POINTER(_i),
+                                  ctypes.POINTER(ctypes.c_int64), _i, ctypes.POINTER(_i),
+                                  ctypes.POINTER(ctypes.c_int64)]),
+    "pio_safetensors_read": (_i, [_vp, ctypes.c_char_p, _vp, ctypes.c_int64]),
+    "pio_safetensors_to_device": (_i, [_vp, ctypes.c_char_p, _vp, ctypes.c_int64, _vp]),
+    "pio_safetensors_to_device_f32": (_i, [_vp, ctypes.c_char_p, _vp, ctypes.c_int64, _vp]),
+    "tensor_load_safetensors": (None, [_vp, ctypes.c_char_p, TP]),
+    "tensor_load_safetensors_status": (_i, [_vp, ctypes.c_char_p, TP]),
     "pio_version": (ctypes.c_char_p, []),
 }
 

@@ -100,6 +100,134 @@ def random_weights(cfg: Qwen3Config, seed: int = 0, qkv_bias: bool = True) -> di
             "s_lm_head": (s_lm * 10).astype(np.float32), "layers": layers}
 
 
+def _hf(i: int, leaf: str) -> str:
+    return f"model.layers.{i}.{leaf}"
+
+
+def weights_from_checkpoint(path, cfg: Qwen3Config, device: str = "rocm:0",
+                            strict: bool = True) -> dict:
+    """Decoder weights from a safetensors checkpoint under the Hugging Face
+    Qwen names (``model.layers.{i}.self_attn.q_proj.weight`` ...), as device
+    tensors for ``Qwen3Int8Decoder``.
+
+    Each linear is read either in the int8 format (I8 ``.weight`` plus F32
+    ``.weight_scale``) or as F32 / F16 / BF16 and quantized per output channel
+    on the GPU. q/k/v and gate/up are fused by stacking rows (q, k, v; gate,
+    up), or read fused from ``qkv_proj`` / ``gate_up_proj`` (the reference
+    layout, ip/models/qwen3_0_6b/architecture.py:24,47). Per-channel scales make
+    stacking rows before or after quantization give the same int8 weights.
+    ``lm_head`` falls back to the embedding (tied weights). With ``strict``,
+    a checkpoint tensor the decoder has no place for (e.g. per-head q/k norms,
+    which this decoder does not apply) is an error rather than silently unused.
+    """
+    from .weights import Checkpoint, FLOAT_DTYPES, SCALE_SUFFIX, quantize_rows
+
+    H, D, I, V = cfg.hidden, cfg.head_dim, cfg.intermediate, cfg.vocab
+    nq, nkv = cfg.n_heads * D, cfg.n_kv_heads * D
+    used = set()
+
+    with Checkpoint(path) as ck:
+        def need(name):
+            if name not in ck:
+                raise RocmError(f"checkpoint lacks '{name}'")
+            used.add(name)
+            return name
+
+        def vec(name, n):
+            inf = ck.info(need(name))
+            if inf.shape != (n,):
+                raise RocmError(f"{name}: shape {inf.shape}, expected ({n},)")
+            t = Tensor([n], device=device)
+            ck.load_into(name, t)
+            return t
+
+        def linear(blocks, k):
+            """blocks: [(name, rows)] stacked in order -> (int8 [sum rows, k], fp32 scales).
+            Each block lands in its row slice of the device tensors."""
+            infos = [(n, ck.info(need(n)), r) for n, r in blocks]
+            for n, inf, r in infos:
+                if inf.shape != (r, k):
+                    raise RocmError(f"{n}: shape {inf.shape}, expected ({r}, {k})")
+            rows = sum(r for _, r in blocks)
+            kinds = {inf.dtype in FLOAT_DTYPES for _, inf, _ in infos}
+            if len(kinds) != 1:
+                raise RocmError(f"{[n for n, _ in blocks]}: mixed int8 and fp storage")
+            q = Tensor([rows, k], device=device, dtype="int8")
+            s = Tensor([rows], device=device)
+            if kinds == {True}:
+                w = Tensor([rows, k], device=device)
+                off = 0
+                for n, _, r in infos:
+                    ck.to_device_f32(n, w.data_ptr() + 4 * off * k, r * k)
+                    off += r
+                quantize_rows(w, q, s)
+                return q, s
+            off = 0
+            for n, inf, r in infos:
+                if inf.dtype != "I8":
+                    raise RocmError(f"{n}: stored {inf.dtype}, expected I8 or fp")
+                sn = need(n + SCALE_SUFFIX)
+                if ck.info(sn).shape != (r,):
+                    raise RocmError(f"{sn}: shape {ck.info(sn).shape}, expected ({r},)")
+                ck.to_device(n, q.data_ptr() + off * k, r * k)
+                ck.to_device_f32(sn, s.data_ptr() + 4 * off, r)
+                off += r
+            return q, s
+
+        def fused_or_split(fused, split, k):
+            if fused in ck:
+                return linear([(fused, sum(r for _, r in split))], k)
+            return linear(split, k)
+
+        def bias(fused, split):
+            if fused in ck:
+                return vec(fused, sum(r for _, r in split))
+            present = [n in ck for n, _ in split]
+            if not any(present):
+                return None
+            if not all(present):
+                raise RocmError(f"only some of {[n for n, _ in split]} are present")
+            t = Tensor([sum(r for _, r in split)], device=device)
+            off = 0
+            for n, r in split:
+                if ck.info(need(n)).shape != (r,):
+                    raise RocmError(f"{n}: shape {ck.info(n).shape}, expected ({r},)")
+                ck.to_device_f32(n, t.data_ptr() + 4 * off, r)
+                off += r
+            return t
+
+        layers = []
+        for i in range(cfg.n_layers):
+            L = {}
+            L["in_norm"] = vec(_hf(i, "input_layernorm.weight"), H)
+            L["post_norm"] = vec(_hf(i, "post_attention_layernorm.weight"), H)
+            qkv = [(_hf(i, f"self_attn.{p}_proj.weight"), r) for p, r in (("q", nq), ("k", nkv),
+                                                                           ("v", nkv))]
+            L["w_qkv"], L["s_qkv"] = fused_or_split(_hf(i, "self_attn.qkv_proj.weight"), qkv, H)
+            L["b_qkv"] = bias(_hf(i, "self_attn.qkv_proj.bias"),
+                              [(n[:-len("weight")] + "bias", r) for n, r in qkv])
+            L["w_o"], L["s_o"] = linear([(_hf(i, "self_attn.o_proj.weight"), H)], nq)
+            gu = [(_hf(i, "mlp.gate_proj.weight"), I), (_hf(i, "mlp.up_proj.weight"), I)]
+            L["w_gu"], L["s_gu"] = fused_or_split(_hf(i, "mlp.gate_up_proj.weight"), gu, H)
+            L["w_down"], L["s_down"] = linear([(_hf(i, "mlp.down_proj.weight"), H)], I)
+            layers.append(L)
+        emb_name = need("model.embed_tokens.weight")
+        if ck.info(emb_name).shape != (V, H):
+            raise RocmError(f"{emb_name}: shape {ck.info(emb_name).shape}, expected ({V}, {H})")
+        embed = Tensor([V, H], device=device)
+        ck.load_into(emb_name, embed)
+        lm_name = "lm_head.weight" if "lm_head.weight" in ck else emb_name
+        lm, s_lm = linear([(lm_name, V)], H)
+        final = vec("model.norm.weight", H)
+        if strict:
+            extra = sorted(set(ck.names()) - used)
+            if extra:
+                raise RocmError(f"checkpoint tensors this decoder does not use: {extra[:8]}"
+                                + (" ..." if len(extra) > 8 else ""))
+    return {"embed": embed, "final_norm": final, "lm_head": lm, "s_lm_head": s_lm,
+            "layers": layers}
+
+
 MODES = {"eager": 0, "graph": 1, "persistent": 2}
 
 
@@ -122,6 +250,9 @@ class Qwen3Int8Decoder:
         def up(a):
             if a is None:
                 return None
+            if isinstance(a, Tensor):   # already on the device (checkpoint loads)
+                self._keep.append(a)
+                return a.data_ptr()
             t = Tensor.from_numpy(np.ascontiguousarray(a), device)
             self._keep.append(t)
             return t.data_ptr()

@@ -290,6 +290,190 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const int32_t* __res
     }
 }
 
+// ---------------------------------------------------------- skinny ---
+// W8A8 with few activation rows (M <= 64: decode batches, small prefills).
+// Such a product is bound by streaming the weights once (N*K bytes), not by
+// the MFMA, so the kernel is built like the GEMV: each wave owns 16 weight
+// rows and streams them from HBM straight into registers, SK_D blocks of 256 K
+// ahead, already in the operand layout of v_mfma_i32_16x16x64_i8 (lane: row
+// r = lane % 16 and K chunk q = lane / 16, i.e. the 16 bytes at 64*i + 16*q of
+// MFMA i's 64-K step), so each load instruction reads 64 contiguous bytes of
+// each of 16 rows. The workgroup's whole activation slice (MT*16 rows x the
+// slice's K) is copied into LDS once, up front, with direct-to-LDS loads, and
+// read there with the same per-lane K chunks, so each product pairs the same
+// K. After that the loop only streams weights: no barriers, and the waits on
+// the weight registers are exact (the K loop is unrolled per block count NB;
+// vector-memory loads complete in order, so any activation load inside the
+// loop would make its wait drain the weight prefetch). Grid x: weight row
+// tiles of 16*WV; grid y: K slices (int32 partials for splitk_reduce_kernel
+// when there is more than one).
+constexpr int SK_KB = 256;                // K per block: 4 MFMAs of 64
+constexpr int SK_D = 4;                   // weight blocks in flight per wave
+
+typedef __attribute__((address_space(1))) const v4i sk_gv4i;
+
+// LDS row pitch of the activation slice: K + 16, so rows start 4 banks apart.
+template <int NB>
+constexpr int sk_pitch() { return NB * SK_KB + 16; }
+template <int MT, int NB>
+constexpr size_t sk_lds_bytes() { return (size_t)MT * 16 * sk_pitch<NB>(); }
+
+template <int WV, int MT, int NB, int OUT>
+__global__ __launch_bounds__(64 * WV) void skinny_w8a8_kernel(GemmParams p) {
+    typedef __attribute__((address_space(3))) void lds_t;
+    constexpr int D = NB < SK_D ? NB : SK_D;
+    constexpr int P = sk_pitch<NB>();
+    constexpr int SEG = NB * SK_KB / 1024;         // 1 KB segments per activation row
+    constexpr int NCP = MT * 16 * SEG;             // copies (wave instructions) of the slice
+    extern __shared__ __attribute__((aligned(16))) int8_t sk_lds[];
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int r = lane & 15, q = lane >> 4;
+    const int n0 = blockIdx.x * (16 * WV) + w * 16;
+    const int64_t k0 = (int64_t)blockIdx.y * p.K;          // p.K is the K of one slice
+
+    // Activation slice -> LDS: copy u moves row u / SEG, segment u % SEG (lane l
+    // lands 16 B at LDS offset 16*l of the segment). Rows >= M re-read row M-1;
+    // they only feed accumulator rows that are never stored.
+#pragma unroll
+    for (int j = 0; j < (NCP + WV - 1) / WV; j++) {
+        const int u = w + WV * j;
+        if (NCP % WV == 0 || u < NCP) {
+            const int row = u / SEG, seg = u % SEG;
+            const int8_t* src = p.A + (int64_t)min(row, p.M - 1) * p.lda + k0 + seg * 1024 + 16 * lane;
+            __builtin_amdgcn_global_load_lds((const void*)src, (lds_t*)(sk_lds + row * P + seg * 1024), 16, 0, 0);
+        }
+    }
+    // The copies must be issued before the weight prefetch: loads complete in
+    // order, and the wait below (at most 4*D loads outstanding) covers the
+    // copies only if the 4*D weight loads are the youngest. Without this fence
+    // the scheduler may hoist weight loads above the copies.
+    __builtin_amdgcn_sched_barrier(0);
+    // This lane's weight row, clamped: rows past N are computed, never stored.
+    const int8_t* wp = p.B + (int64_t)min(n0 + r, p.N - 1) * p.ldb + k0 + 16 * q;
+    v4i wr[D][4];
+    auto load_w = [&](int b, v4i (&dst)[4]) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) dst[i] = __builtin_nontemporal_load((sk_gv4i*)(wp + b * SK_KB + 64 * i));
+    };
+#pragma unroll
+    for (int b = 0; b < D; b++) load_w(b, wr[b]);
+    // The slice copies are older than the weight prefetch: wait for them only.
+    stage_barrier<4 * D>();
+
+    v4i acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) acc[t] = v4i{0, 0, 0, 0};
+    const int8_t* as = sk_lds + r * P + 16 * q;
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const v4i a = *(const v4i*)(as + t * 16 * P + b * SK_KB + 64 * i);
+                acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, wr[b % D][i], acc[t], 0, 0, 0);
+            }
+        }
+        if (b + D < NB) load_w(b + D, wr[b % D]);
+        // Keep the reload here, right after the block that freed its
+        // registers: left alone, the scheduler sinks it next to its use (to
+        // save registers), which leaves no weight loads in flight.
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // 16x16 accumulator: lane holds rows 4*q + v (v < 4) of M tile t, column r.
+    const int n = n0 + r;
+    if (n >= p.N) return;
+    const float sw = OUT == OUT_I32 ? 0.f : p.s_w[n];
+    const float bn = (OUT != OUT_I32 && p.bias) ? p.bias[n] : 0.f;
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int m = t * 16 + 4 * q + v;
+            if (m >= p.M) continue;
+            const int64_t o = (int64_t)blockIdx.y * p.c_batch + (int64_t)m * p.ldc + n;
+            if constexpr (OUT == OUT_I32) {
+                ((int32_t*)p.C)[o] = acc[t][v];
+            } else {
+                const float val = scaled_value<OUT>(acc[t][v], p.s_a[m], sw, bn, p.bias != nullptr);
+                if constexpr (OUT == OUT_F32) ((float*)p.C)[o] = val;
+                else ((_Float16*)p.C)[o] = (_Float16)val;
+            }
+        }
+    }
+}
+
+struct SkinnyPlan {
+    int wv = 0, nb = 0, splits = 1;
+};
+
+// Plan for the skinny kernel, or wv == 0 when it does not apply (M > 64, K not
+// a multiple of 1024, or unaligned operands). Cost model: the weights stream
+// at ~6 TB/s when every CU has a workgroup (proportionally less on a partly
+// filled grid), a workgroup moves its 16*WV rows x NB blocks at ~32 GB/s at
+// most (its loads in flight over the HBM latency), and split K adds the
+// partials' write + read and the reduce launch.
+static SkinnyPlan plan_skinny(const GemmParams& p) {
+    SkinnyPlan best;
+    if (p.M < 1 || p.M > 64 || p.K % 1024 || !aligned16(p.A) || !aligned16(p.B) || p.lda % 16 || p.ldb % 16)
+        return best;
+    const int kb = p.K / SK_KB;
+    double best_t = 0;
+    for (int wv : {4, 3}) {
+        for (int nb : {16, 8, 4}) {
+            // the activation slice lives in LDS: 64 rows x 2 KB at most
+            if (kb % nb || kb / nb > 16 || (p.M > 16 && nb > 8)) continue;
+            const int sp = kb / nb;
+            const int64_t units = (int64_t)ceil_div(p.N, 16 * wv) * sp;
+            const double rounds = (double)((units + 255) / 256);
+            const double fill = std::min(1.0, (double)units / 256.0);
+            double t = std::max((double)p.N * p.K / (6.0e12 * fill), rounds * 16.0 * wv * nb * SK_KB / 32.0e9);
+            if (sp > 1) t += (double)sp * p.M * p.N * 8.0 / 4.0e12 + 2.0e-6;
+            if (best.wv == 0 || t < best_t * 0.98) {
+                best_t = t;
+                best.wv = wv; best.nb = nb; best.splits = sp;
+            }
+        }
+    }
+    return best;
+}
+
+template <int WV, int MT, int NB, int OUT>
+static int launch_skinny_out(const GemmParams& p, int splits, hipStream_t st) {
+    constexpr size_t lds = sk_lds_bytes<MT, NB>();
+    PIO_TRY(allow_lds(skinny_w8a8_kernel<WV, MT, NB, OUT>, lds));
+    skinny_w8a8_kernel<WV, MT, NB, OUT><<<dim3(ceil_div(p.N, 16 * WV), splits), 64 * WV, lds, st>>>(p);
+    PIO_LAUNCHED();
+    return PIO_OK;
+}
+
+template <int WV, int MT, int NB>
+static int launch_skinny_nb(const GemmParams& p, int out_mode, int splits, hipStream_t st) {
+    switch (out_mode) {
+    case OUT_I32: return launch_skinny_out<WV, MT, NB, OUT_I32>(p, splits, st);
+    case OUT_F32: return launch_skinny_out<WV, MT, NB, OUT_F32>(p, splits, st);
+    case OUT_F16: return launch_skinny_out<WV, MT, NB, OUT_F16>(p, splits, st);
+    default: return set_error(PIO_ERR_INVALID, "gemm: bad output mode");
+    }
+}
+
+template <int WV, int MT>
+static int launch_skinny_mt(const GemmParams& p, int out_mode, const SkinnyPlan& sp, hipStream_t st) {
+    if constexpr (MT == 1) {
+        if (sp.nb == 16) return launch_skinny_nb<WV, MT, 16>(p, out_mode, sp.splits, st);
+    }
+    if (sp.nb == 8) return launch_skinny_nb<WV, MT, 8>(p, out_mode, sp.splits, st);
+    if (sp.nb == 4) return launch_skinny_nb<WV, MT, 4>(p, out_mode, sp.splits, st);
+    return set_error(PIO_ERR_INVALID, "gemm: skinny plan with %d blocks for %d rows", sp.nb, p.M);
+}
+
+static int launch_skinny_one(const GemmParams& p, int out_mode, const SkinnyPlan& sp, hipStream_t st) {
+    if (sp.wv == 4)
+        return p.M <= 16 ? launch_skinny_mt<4, 1>(p, out_mode, sp, st) : launch_skinny_mt<4, 4>(p, out_mode, sp, st);
+    return p.M <= 16 ? launch_skinny_mt<3, 1>(p, out_mode, sp, st) : launch_skinny_mt<3, 4>(p, out_mode, sp, st);
+}
+
 // Split-K plan: block tile (WMT x WNT waves of 32 x 32) and slice count.
 struct SplitPlan {
     int wmt = 0, wnt = 0, splits = 1;
@@ -346,6 +530,8 @@ static int launch_split_tiles(const GemmParams& p, int splits, hipStream_t st) {
     return launch_v2_out<WMT, WNT, OUT_I32, 5, v5_stages<WMT, WNT>()>(p, dim3(tm * tn, 1, splits), tn, st);
 }
 
+static int splitk_reduce(const int32_t* w, int splits, const GemmParams& p0, int out_mode, hipStream_t st);
+
 static int launch_splitk(const GemmParams& p0, int out_mode, const SplitPlan& sp, hipStream_t st) {
     Scratch ws;
     PIO_TRY(ws.get((size_t)sp.splits * p0.M * p0.N * sizeof(int32_t)));
@@ -368,17 +554,39 @@ static int launch_splitk(const GemmParams& p0, int out_mode, const SplitPlan& sp
                          : launch_split_tiles<2, 1>(p, sp.splits, st);
     }
     if (rc != PIO_OK) return rc;
+    return splitk_reduce((const int32_t*)ws.ptr, sp.splits, p0, out_mode, st);
+}
+
+// Sums the int32 partials ws[splits][M][N] in slice order and applies the
+// epilogue into p0.C (ldc == N).
+static int splitk_reduce(const int32_t* w, int splits, const GemmParams& p0, int out_mode, hipStream_t st) {
     const int64_t MN = (int64_t)p0.M * p0.N;
     const int blocks = (int)ceil_div(MN, (int64_t)1024);
-    const int32_t* w = (const int32_t*)ws.ptr;
     switch (out_mode) {
-    case OUT_I32: splitk_reduce_kernel<OUT_I32><<<blocks, 256, 0, st>>>(w, sp.splits, p0.M, p0.N, nullptr, nullptr, nullptr, p0.C); break;
-    case OUT_F32: splitk_reduce_kernel<OUT_F32><<<blocks, 256, 0, st>>>(w, sp.splits, p0.M, p0.N, p0.s_a, p0.s_w, p0.bias, p0.C); break;
-    case OUT_F16: splitk_reduce_kernel<OUT_F16><<<blocks, 256, 0, st>>>(w, sp.splits, p0.M, p0.N, p0.s_a, p0.s_w, p0.bias, p0.C); break;
+    case OUT_I32: splitk_reduce_kernel<OUT_I32><<<blocks, 256, 0, st>>>(w, splits, p0.M, p0.N, nullptr, nullptr, nullptr, p0.C); break;
+    case OUT_F32: splitk_reduce_kernel<OUT_F32><<<blocks, 256, 0, st>>>(w, splits, p0.M, p0.N, p0.s_a, p0.s_w, p0.bias, p0.C); break;
+    case OUT_F16: splitk_reduce_kernel<OUT_F16><<<blocks, 256, 0, st>>>(w, splits, p0.M, p0.N, p0.s_a, p0.s_w, p0.bias, p0.C); break;
     default: return set_error(PIO_ERR_INVALID, "gemm: bad output mode");
     }
     PIO_LAUNCHED();
     return PIO_OK;
+}
+
+// Skinny product: one pass, or K slices into int32 partials plus the reduce.
+static int launch_skinny(const GemmParams& p0, int out_mode, const SkinnyPlan& sp, hipStream_t st) {
+    GemmParams p = p0;
+    p.K = p0.K / sp.splits;
+    if (sp.splits == 1) {
+        p.c_batch = 0;
+        return launch_skinny_one(p, out_mode, sp, st);
+    }
+    Scratch ws;
+    PIO_TRY(ws.get((size_t)sp.splits * p0.M * p0.N * sizeof(int32_t)));
+    p.C = ws.ptr;
+    p.ldc = p0.N;
+    p.c_batch = (int64_t)p0.M * p0.N;
+    PIO_TRY(launch_skinny_one(p, OUT_I32, sp, st));
+    return splitk_reduce((const int32_t*)ws.ptr, sp.splits, p0, out_mode, st);
 }
 
 int gemm_w8a8(const int8_t* q, const float* s_a, const int8_t* w, const float* s_w,
@@ -400,6 +608,8 @@ int gemm_w8a8(const int8_t* q, const float* s_a, const int8_t* w, const float* s
     p.s_a = s_a; p.s_w = s_w; p.bias = bias;
     p.C = y; p.ldc = N;
     p.M = M; p.N = N; p.K = K;
+    const SkinnyPlan kp = plan_skinny(p);
+    if (kp.wv) return launch_skinny(p, mode, kp, st);
     const SplitPlan sp = plan_split(p, 256);
     if (sp.splits > 1) return launch_splitk(p, mode, sp, st);
     return launch_dense(p, mode, 1, st);

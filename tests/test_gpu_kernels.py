@@ -269,6 +269,47 @@ def test_gemm_split_k(env, M, N, K):
         assert np.array_equal(host(y32).view(np.uint32), yr32.view(np.uint32)), f"f32 call {rep}"
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 12288, 4096), (16, 12288, 4096), (64, 12288, 4096),
+                                   (1, 4096, 12288), (64, 4096, 12288), (16, 3072, 1024),
+                                   (64, 3072, 1024), (1, 1024, 3072), (5, 1000, 2048),
+                                   (17, 1000, 2048), (20, 200, 12288), (3, 48, 4096),
+                                   (64, 130, 1024)])
+def test_gemm_skinny(env, M, N, K):
+    """M <= 64 with K % 1024 == 0 takes the skinny kernel (weights streamed
+    into registers, the activation slice in LDS, 16x16x64 MFMAs; one pass or
+    K slices into int32 partials). The shapes cover both row tilings (M <= 16
+    and up to 64), both workgroup widths, 4/8/16 blocks per slice, one to
+    twelve slices and ragged N. int32 bit-exact, fp16 / fp32 (with and
+    without bias) byte-equal to the oracle, two calls in a row."""
+    torch, ops, d = env
+    _say(f"skinny M={M} N={N} K={K}")
+    rng = np.random.default_rng(M * 131 + N + 3 * K)
+    q = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    W = rng.integers(-127, 127, size=(N, K), dtype=np.int8)
+    sa = rng.uniform(0.001, 0.05, size=M).astype(np.float32)
+    sw = rng.uniform(0.001, 0.02, size=N).astype(np.float32)
+    b = rng.standard_normal(N, dtype=np.float32)
+    qd, Wd, sad, swd, bd = (dev(torch, a, d) for a in (q, W, sa, sw, b))
+    acc_ref = oracle.matmul_nt_i32(q, W)
+    yr16 = oracle.w8a8(q, sa, W, sw, b, out="f16")
+    yr32 = oracle.w8a8(q, sa, W, sw, None, out="f32")
+    yr32b = oracle.w8a8(q, sa, W, sw, b, out="f32")
+    for rep in range(2):
+        acc = torch.full((M, N), 7, dtype=torch.int32, device=d)
+        y16 = torch.full((M, N), float("nan"), dtype=torch.float16, device=d)
+        y32 = torch.full((M, N), float("nan"), dtype=torch.float32, device=d)
+        y32b = torch.full((M, N), float("nan"), dtype=torch.float32, device=d)
+        ops.gemm_w8a8(qd, None, Wd, None, None, acc, M, N, K)
+        ops.gemm_w8a8(qd, sad, Wd, swd, bd, y16, M, N, K)
+        ops.gemm_w8a8(qd, sad, Wd, swd, None, y32, M, N, K)
+        ops.gemm_w8a8(qd, sad, Wd, swd, bd, y32b, M, N, K)
+        sync(torch)
+        assert np.array_equal(host(acc), acc_ref), f"int32 call {rep}"
+        assert np.array_equal(host(y16).view(np.uint16), yr16.view(np.uint16)), f"f16 call {rep}"
+        assert np.array_equal(host(y32).view(np.uint32), yr32.view(np.uint32)), f"f32 call {rep}"
+        assert np.array_equal(host(y32b).view(np.uint32), yr32b.view(np.uint32)), f"f32+bias call {rep}"
+
+
 @pytest.mark.parametrize("K,N", [(1024, 3072), (3072, 1024), (1024, 2048)])
 def test_gemm_c3_fp16_pipeline(env, K, N):
     """C3: x fp16 -> per-token quant -> W8A8 GEMM -> fp16, vs the oracle."""

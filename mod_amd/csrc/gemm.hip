@@ -308,7 +308,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const int32_t* __res
 // tiles of 16*WV; grid y: K slices (int32 partials for splitk_reduce_kernel
 // when there is more than one).
 constexpr int SK_KB = 256;                // K per block: 4 MFMAs of 64
-constexpr int SK_D = 4;                   // weight blocks in flight per wave
+constexpr int SK_D = 4;                   // weight blocks in flight per wave (8 measured no faster)
 
 typedef __attribute__((address_space(1))) const v4i sk_gv4i;
 
@@ -421,7 +421,7 @@ static SkinnyPlan plan_skinny(const GemmParams& p) {
     const int kb = p.K / SK_KB;
     double best_t = 0;
     for (int wv : {4, 3}) {
-        for (int nb : {16, 8, 4}) {
+        for (int nb : {16, 12, 8, 4}) {
             // the activation slice lives in LDS: 64 rows x 2 KB at most
             if (kb % nb || kb / nb > 16 || (p.M > 16 && nb > 8)) continue;
             const int sp = kb / nb;
@@ -462,6 +462,7 @@ template <int WV, int MT>
 static int launch_skinny_mt(const GemmParams& p, int out_mode, const SkinnyPlan& sp, hipStream_t st) {
     if constexpr (MT == 1) {
         if (sp.nb == 16) return launch_skinny_nb<WV, MT, 16>(p, out_mode, sp.splits, st);
+        if (sp.nb == 12) return launch_skinny_nb<WV, MT, 12>(p, out_mode, sp.splits, st);
     }
     if (sp.nb == 8) return launch_skinny_nb<WV, MT, 8>(p, out_mode, sp.splits, st);
     if (sp.nb == 4) return launch_skinny_nb<WV, MT, 4>(p, out_mode, sp.splits, st);

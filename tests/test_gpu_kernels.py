@@ -270,7 +270,8 @@ def test_gemm_split_k(env, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 12288, 4096), (16, 12288, 4096), (64, 12288, 4096),
-                                   (1, 4096, 12288), (64, 4096, 12288), (16, 3072, 1024),
+                                   (1, 4096, 12288), (16, 4096, 12288), (64, 4096, 12288),
+                                   (16, 3072, 1024),
                                    (64, 3072, 1024), (1, 1024, 3072), (5, 1000, 2048),
                                    (17, 1000, 2048), (20, 200, 12288), (3, 48, 4096),
                                    (64, 130, 1024)])
@@ -278,7 +279,7 @@ def test_gemm_skinny(env, M, N, K):
     """M <= 64 with K % 1024 == 0 takes the skinny kernel (weights streamed
     into registers, the activation slice in LDS, 16x16x64 MFMAs; one pass or
     K slices into int32 partials). The shapes cover both row tilings (M <= 16
-    and up to 64), both workgroup widths, 4/8/16 blocks per slice, one to
+    and up to 64), both workgroup widths, 4/8/12/16 blocks per slice, one to
     twelve slices and ragged N. int32 bit-exact, fp16 / fp32 (with and
     without bias) byte-equal to the oracle, two calls in a row."""
     torch, ops, d = env

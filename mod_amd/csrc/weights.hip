@@ -116,9 +116,10 @@ struct Json {
                     unsigned v = 0;
                     for (int i = 0; i < 4; i++) {
                         const char h = p[i];
-                        v = v * 16 + (h >= '0' && h <= '9' ? h - '0' : h >= 'a' && h <= 'f' ? h - 'a' + 10
-                                      : h >= 'A' && h <= 'F' ? h - 'A' + 10 : 99);
-                        if (v > 0xFFFF) return ok = false;
+                        const int d = h >= '0' && h <= '9' ? h - '0' : h >= 'a' && h <= 'f' ? h - 'a' + 10
+                                    : h >= 'A' && h <= 'F' ? h - 'A' + 10 : -1;
+                        if (d < 0) return ok = false;
+                        v = v * 16 + (unsigned)d;
                     }
                     p += 4;
                     c = v < 0x80 ? (char)v : '?';

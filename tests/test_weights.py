@@ -176,7 +176,7 @@ def _raw(p, hdr_bytes, payload=b""):
 
 @pytest.mark.parametrize("case", [
     "too_short", "hdr_len_beyond", "not_json", "offsets_beyond", "bytes_vs_shape", "dup",
-    "neg_dim", "bad_dtype", "missing_field", "reversed_offsets", "float_offset",
+    "neg_dim", "bad_dtype", "missing_field", "reversed_offsets", "float_offset", "bad_escape",
 ])
 def test_malformed_files_rejected(tmp_path, case, W):
     from mod_amd import ops
@@ -206,6 +206,8 @@ def test_malformed_files_rejected(tmp_path, case, W):
         _raw(p, json.dumps({"a": ent("I8", [0], 8, 4)}).encode(), payload)
     elif case == "float_offset":
         _raw(p, b'{"a": {"dtype": "I8", "shape": [4], "data_offsets": [0.0, 4]}}', payload)
+    elif case == "bad_escape":
+        _raw(p, b'{"a\\u00zz": {"dtype": "I8", "shape": [4], "data_offsets": [0, 4]}}', payload)
     assert not ops.lib.open_safetensors(str(p).encode())
     assert ops.last_error()
     with pytest.raises(ops.RocmError):

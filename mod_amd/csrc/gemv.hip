@@ -11,8 +11,10 @@
 // per output after the cross-lane reduction. Requires K % 16 == 0 and 16 B
 // aligned x and W rows.
 #include "pio_common.hpp"
+#include "gemm_core.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace pio {
 
@@ -342,6 +344,249 @@ static void launch_direct_rows(const XT* x, const int8_t* w, const float* s_w, c
     }
 }
 
+// ------------------------------------------------------------- MFMA ---
+// fp16 activations with 2 <= M <= 64 rows. The FMA kernels above spend M
+// fp32 FMAs per weight byte, which makes them VALU-bound from M ~ 4 (M = 64:
+// 2% of HBM). Here the products go to v_mfma_f32_16x16x32_f16: an int8 weight
+// is exact in fp16, an fp16 x int8 product is exact in fp32, and the MFMA
+// accumulates in fp32 -- the same result as the FMA kernels up to the order
+// of the fp32 additions. The structure is the skinny W8A8 kernel's (gemm.hip):
+// each wave owns 16 weight rows streamed from HBM into registers 4 blocks of
+// 256 K ahead (lane: row r = lane % 16, K chunk q = lane / 16, 16 bytes at
+// 64*i + 16*q), each 16-byte chunk widened to two 8 x fp16 operands; the
+// workgroup's x slice (MT*16 rows x the slice's K, fp16) is copied once into
+// LDS with direct-to-LDS loads and read with the same per-lane K chunks.
+// Widening: byte b becomes the fp16 whose bits are 0x64 | (b ^ 0x80), i.e.
+// 1024 + (b + 128) exactly, minus 1152 (one byte permute per two values and
+// one packed fp16 subtract per two values; all values exact). K slices
+// (grid y) write fp32 partials that gemv_split_reduce_kernel sums in slice
+// order before the scale.
+typedef _Float16 gm_v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 gm_v2h __attribute__((ext_vector_type(2)));
+typedef float gm_v4f __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const v4i gm_gv4i;
+
+constexpr int GM_KB = 256;   // K per block: 4 x 64 (8 MFMAs of 32)
+constexpr int GM_D = 4;      // weight blocks in flight per wave
+
+template <int NB>
+constexpr int gm_pitch() { return NB * GM_KB * 2 + 16; }   // LDS row pitch in bytes (fp16 x)
+template <int MT, int NB>
+constexpr size_t gm_lds_bytes() { return (size_t)MT * 16 * gm_pitch<NB>(); }
+
+// Two fp16 (k and k+1 of dword d's bytes sel) from a dword of four int8.
+__device__ __forceinline__ gm_v2h gm_widen2(uint32_t t, uint32_t sel) {
+    const uint32_t u = __builtin_amdgcn_perm(0x64646464u, t, sel);
+    return __builtin_bit_cast(gm_v2h, u) - gm_v2h{(_Float16)1152.0f, (_Float16)1152.0f};
+}
+// 16 int8 -> two operands of 8 fp16 (bytes 0..7, 8..15).
+__device__ __forceinline__ void gm_widen16(v4i w, gm_v8h& lo, gm_v8h& hi) {
+    gm_v2h h[8];
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        const uint32_t t = (uint32_t)w[d] ^ 0x80808080u;
+        h[2 * d] = gm_widen2(t, 0x04010400u);       // bytes 0, 1
+        h[2 * d + 1] = gm_widen2(t, 0x04030402u);   // bytes 2, 3
+    }
+    lo = gm_v8h{h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
+    hi = gm_v8h{h[4][0], h[4][1], h[5][0], h[5][1], h[6][0], h[6][1], h[7][0], h[7][1]};
+}
+
+struct GemvMfma {
+    const _Float16* x;
+    const int8_t* w;
+    const float* s_w;
+    const float* bias;
+    void* y;          // YT [M][N], or fp32 partials [S][M][N] when split
+    int M, N, K;      // K of one slice
+    int ldx;          // row pitch of x and W (the full K)
+};
+
+template <int WV, int MT, int NB, typename YT, bool SPLIT>
+__global__ __launch_bounds__(64 * WV) void gemv_w8_mfma_kernel(GemvMfma p) {
+    typedef __attribute__((address_space(3))) void lds_t;
+    constexpr int D = NB < GM_D ? NB : GM_D;
+    constexpr int P = gm_pitch<NB>();
+    constexpr int SEG = NB * GM_KB * 2 / 1024;   // 1 KB segments per x row
+    constexpr int NCP = MT * 16 * SEG;
+    extern __shared__ __attribute__((aligned(16))) int8_t gm_lds[];
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int r = lane & 15, q = lane >> 4;
+    const int n0 = blockIdx.x * (16 * WV) + w * 16;
+    const int64_t k0 = (int64_t)blockIdx.y * p.K;
+
+    // x slice -> LDS (rows >= M re-read row M-1; their outputs are dropped)
+#pragma unroll
+    for (int j = 0; j < (NCP + WV - 1) / WV; j++) {
+        const int u = w + WV * j;
+        if (NCP % WV == 0 || u < NCP) {
+            const int row = u / SEG, seg = u % SEG;
+            const int8_t* src = (const int8_t*)(p.x + (int64_t)min(row, p.M - 1) * p.ldx + k0) + seg * 1024 + 16 * lane;
+            __builtin_amdgcn_global_load_lds((const void*)src, (lds_t*)(gm_lds + row * P + seg * 1024), 16, 0, 0);
+        }
+    }
+    // the copies must stay older than the weight prefetch (see the wait below)
+    __builtin_amdgcn_sched_barrier(0);
+    const int8_t* wp = p.w + (int64_t)min(n0 + r, p.N - 1) * p.ldx + k0 + 16 * q;
+    v4i wr[D][4];
+    auto load_w = [&](int b, v4i (&dst)[4]) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) dst[i] = __builtin_nontemporal_load((gm_gv4i*)(wp + b * GM_KB + 64 * i));
+    };
+#pragma unroll
+    for (int b = 0; b < D; b++) load_w(b, wr[b]);
+    stage_barrier<4 * D>();   // the copies have landed; the weight loads stay in flight
+    // The widening is register work the scheduler would hoist above the
+    // barrier, with a full wait on every load issued so far.
+    __builtin_amdgcn_sched_barrier(0);
+
+    gm_v4f acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) acc[t] = gm_v4f{0.f, 0.f, 0.f, 0.f};
+    const int8_t* xs = gm_lds + r * P + 32 * q;   // fp16 element 16*q of the K chunk
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            gm_v8h wlo, whi;
+            gm_widen16(wr[b % D][i], wlo, whi);
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const int8_t* a = xs + t * 16 * P + (b * GM_KB + 64 * i) * 2;
+                const gm_v8h alo = *(const gm_v8h*)a, ahi = *(const gm_v8h*)(a + 16);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, wlo, acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, whi, acc[t], 0, 0, 0);
+            }
+        }
+        if (b + D < NB) load_w(b + D, wr[b % D]);
+        __builtin_amdgcn_sched_barrier(0);   // keep the reload here (see gemm.hip's skinny kernel)
+    }
+
+    // 16x16 accumulator: lane holds rows 4*q + v of M tile t, column r.
+    const int n = n0 + r;
+    if (n >= p.N) return;
+    const float sw = SPLIT ? 0.f : p.s_w[n];
+    const float bn = (!SPLIT && p.bias) ? p.bias[n] : 0.f;
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int m = t * 16 + 4 * q + v;
+            if (m >= p.M) continue;
+            if constexpr (SPLIT) {
+                ((float*)p.y)[((int64_t)blockIdx.y * p.M + m) * p.N + n] = acc[t][v];
+            } else {
+                float val = acc[t][v] * sw;
+                if (p.bias) val += bn;
+                ((YT*)p.y)[(int64_t)m * p.N + n] = from_f32<YT>(val);
+            }
+        }
+    }
+}
+
+// y[m,n] = (sum over slices in order of ws[z][m][n]) * s_w[n] (+ bias[n]).
+template <typename YT>
+__global__ __launch_bounds__(256) void gemv_split_reduce_kernel(const float* __restrict__ ws, int splits, int M,
+                                                                int N, const float* __restrict__ s_w,
+                                                                const float* __restrict__ bias, YT* __restrict__ y) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x, MN = (int64_t)M * N;
+    if (i >= MN) return;
+    float acc = 0.f;
+    for (int z = 0; z < splits; z++) acc += ws[z * MN + i];
+    const int n = (int)(i % N);
+    float val = acc * s_w[n];
+    if (bias) val += bias[n];
+    y[i] = from_f32<YT>(val);
+}
+
+struct GemvMfmaPlan {
+    int wv = 0, nb = 0, splits = 1;
+};
+
+// Same cost model as the skinny W8A8 plan; the fp16 x slice must fit the LDS
+// (16 rows x 8 KB, or 64 rows x 2 KB).
+static GemvMfmaPlan plan_gemv_mfma(int M, int N, int K) {
+    GemvMfmaPlan best;
+    if (M < 2 || M > 64 || K % 1024) return best;
+    const int kb = K / GM_KB;
+    double best_t = 0;
+    for (int wv : {4, 3}) {
+        for (int nb : {16, 12, 8, 4}) {
+            if (kb % nb || kb / nb > 16 || (M > 16 && nb > 4)) continue;
+            const int sp = kb / nb;
+            const int64_t units = (int64_t)ceil_div(N, 16 * wv) * sp;
+            const double rounds = (double)((units + 255) / 256);
+            const double fill = std::min(1.0, (double)units / 256.0);
+            double t = std::max((double)N * K / (6.0e12 * fill), rounds * 16.0 * wv * nb * GM_KB / 32.0e9);
+            if (sp > 1) t += (double)sp * M * N * 8.0 / 4.0e12 + 2.0e-6;
+            if (best.wv == 0 || t < best_t * 0.98) {
+                best_t = t;
+                best.wv = wv; best.nb = nb; best.splits = sp;
+            }
+        }
+    }
+    return best;
+}
+
+template <int WV, int MT, int NB, typename YT>
+static int launch_gemv_mfma_nb(const GemvMfma& p, int splits, hipStream_t st) {
+    constexpr size_t lds = gm_lds_bytes<MT, NB>();
+    const dim3 grid(ceil_div(p.N, 16 * WV), splits);
+    if (splits > 1) {
+        static bool done = false;
+        if (!done && lds > 65536) {
+            PIO_HIP(hipFuncSetAttribute((const void*)gemv_w8_mfma_kernel<WV, MT, NB, YT, true>,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+            done = true;
+        }
+        gemv_w8_mfma_kernel<WV, MT, NB, YT, true><<<grid, 64 * WV, lds, st>>>(p);
+    } else {
+        static bool done = false;
+        if (!done && lds > 65536) {
+            PIO_HIP(hipFuncSetAttribute((const void*)gemv_w8_mfma_kernel<WV, MT, NB, YT, false>,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+            done = true;
+        }
+        gemv_w8_mfma_kernel<WV, MT, NB, YT, false><<<grid, 64 * WV, lds, st>>>(p);
+    }
+    PIO_LAUNCHED();
+    return PIO_OK;
+}
+
+template <int WV, typename YT>
+static int launch_gemv_mfma_wv(const GemvMfma& p, const GemvMfmaPlan& pl, hipStream_t st) {
+    if (p.M <= 16) {
+        switch (pl.nb) {
+        case 16: return launch_gemv_mfma_nb<WV, 1, 16, YT>(p, pl.splits, st);
+        case 12: return launch_gemv_mfma_nb<WV, 1, 12, YT>(p, pl.splits, st);
+        case 8: return launch_gemv_mfma_nb<WV, 1, 8, YT>(p, pl.splits, st);
+        default: return launch_gemv_mfma_nb<WV, 1, 4, YT>(p, pl.splits, st);
+        }
+    }
+    if (pl.nb != 4) return set_error(PIO_ERR_INVALID, "gemv: MFMA plan with %d blocks for %d rows", pl.nb, p.M);
+    return launch_gemv_mfma_nb<WV, 4, 4, YT>(p, pl.splits, st);
+}
+
+template <typename YT>
+static int launch_gemv_mfma(const _Float16* x, const int8_t* w, const float* s_w, const float* bias, YT* y,
+                            int M, int N, int K, const GemvMfmaPlan& pl, hipStream_t st) {
+    GemvMfma p{x, w, s_w, bias, y, M, N, K / pl.splits, K};
+    Scratch ws;
+    if (pl.splits > 1) {
+        PIO_TRY(ws.get((size_t)pl.splits * M * N * sizeof(float)));
+        p.y = ws.ptr;
+    }
+    const int rc = pl.wv == 4 ? launch_gemv_mfma_wv<4, YT>(p, pl, st) : launch_gemv_mfma_wv<3, YT>(p, pl, st);
+    if (rc != PIO_OK) return rc;
+    if (pl.splits > 1) {
+        const int64_t MN = (int64_t)M * N;
+        gemv_split_reduce_kernel<YT><<<(int)ceil_div(MN, (int64_t)256), 256, 0, st>>>((const float*)ws.ptr, pl.splits,
+                                                                                      M, N, s_w, bias, y);
+        PIO_LAUNCHED();
+    }
+    return PIO_OK;
+}
+
 // Below this weight size a launch is bounded by its start-up (one HBM round
 // trip), not by streaming: the direct kernel's one-wave-per-row-group grid
 // reaches its first weight bytes sooner than the stream kernel, which first
@@ -351,6 +596,10 @@ constexpr size_t GEMV_STREAM_MIN_BYTES = 16u << 20;
 template <typename XT, typename YT>
 static int dispatch(const XT* x, const int8_t* w, const float* s_w, const float* bias, YT* y,
                     int M, int N, int K, hipStream_t st) {
+    if constexpr (std::is_same<XT, _Float16>::value) {
+        const GemvMfmaPlan pl = plan_gemv_mfma(M, N, K);
+        if (pl.wv) return launch_gemv_mfma(x, w, s_w, bias, y, M, N, K, pl, st);
+    }
     if ((size_t)N * K >= GEMV_STREAM_MIN_BYTES && stream_pick(1, N, K)) {
         // x rows in launches of up to 4 (as many as the LDS takes); each launch re-streams W
         for (int m0 = 0; m0 < M;) {

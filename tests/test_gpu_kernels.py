@@ -91,6 +91,38 @@ def test_gemv_shapes(env, M, N, K, xdt, ydt, bias):
                1e-2 if (ydt == np.float16 or xdt == np.float16) else 1e-3, "gemv")
 
 
+@pytest.mark.parametrize("M,N,K,ydt,bias", [
+    (2, 12288, 4096, np.float16, False),   # 1 row tile, 16 blocks, one pass
+    (4, 4096, 12288, np.float32, True),    # 12-block K slices + fp32 partials reduce
+    (16, 12288, 4096, np.float32, False),
+    (16, 3072, 1024, np.float16, True),    # 4 blocks
+    (7, 1000, 2048, np.float32, True),     # 8 blocks, ragged N
+    (17, 4096, 4096, np.float32, False),   # 4 row tiles (rows 17..63 padded), K slices
+    (64, 12288, 4096, np.float16, True),
+    (64, 130, 1024, np.float32, True),
+    (33, 2048, 12288, np.float16, False),
+])
+def test_gemv_mfma_fp16(env, M, N, K, ydt, bias):
+    """fp16 activations with 2 <= M <= 64 and K % 1024 == 0 take the MFMA GEMV
+    (int8 weights widened exactly to fp16, fp32 accumulation). Every product
+    is exact, so the fp32 output is held to rel 1e-3 against the oracle (the
+    fp16-input bar is 1e-2); fp16 output to 1e-2. Two calls in a row."""
+    torch, ops, d = env
+    _say(f"gemv mfma M={M} N={N} K={K}")
+    x, W, s = _inputs(M * 5 + N + K, M, N, K, np.float16)
+    b = np.random.default_rng(2).standard_normal(N, dtype=np.float32) if bias else None
+    ref = oracle.gemv_w8(x, W, s, b, out_dtype=ydt)
+    xd, wd, sd = dev(torch, x, d), dev(torch, W, d), dev(torch, s, d)
+    bd = None if b is None else dev(torch, b, d)
+    for rep in range(2):
+        y = torch.full((M, N), float("nan"), dtype=torch.float16 if ydt == np.float16 else torch.float32,
+                       device=d)
+        ops.gemv_w8(xd, wd, sd, bd, y, M, N, K, stream(torch))
+        sync(torch)
+        assert_rel(host(y).astype(np.float64), ref.astype(np.float64),
+                   1e-2 if ydt == np.float16 else 1e-3, f"gemv mfma call {rep}")
+
+
 @pytest.mark.parametrize("M,N,K,xdt", [
     (1, 151936, 1024, np.float16),   # lm_head-sized N: many row groups per wave
     (5, 20000, 4096, np.float16),    # 4 + 1 x rows

@@ -8,8 +8,10 @@
 // takes small weights and the shapes whose x does not fit the LDS. Both
 // convert each weight byte to fp32 once (v_cvt_f32_i32_sdwa, sign-extended
 // byte select), accumulate in fp32 FMA, and apply the per-channel scale once
-// per output after the cross-lane reduction. Requires K % 16 == 0 and 16 B
-// aligned x and W rows.
+// per output after the cross-lane reduction. fp16 activations with
+// 2 <= M <= 64 and K % 1024 == 0 go to the MFMA kernel (gemv_w8_mfma_kernel,
+// below), where the FMA kernels would be VALU-bound. Requires K % 16 == 0 and
+// 16 B aligned x and W rows.
 #include "pio_common.hpp"
 #include "gemm_core.hpp"
 

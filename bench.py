@@ -509,6 +509,9 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (three times), for scaling "
                          "the FETCH_SIZE / WRITE_SIZE counters of the traffic measurement")
+    ap.add_argument("--gemm-launches", nargs="+", metavar="MxKxN",
+                    help="only run 10 plain (ungraphed) W8A8 GEMM launches per shape, fp16 out, "
+                         "then exit -- the command the MFMA counter passes profile")
     ap.add_argument("--weights", action="store_true",
                     help="only time checkpoint loading (config-2 decoder weights, int8 and BF16 "
                          "safetensors from the page cache into HBM) and print its own JSON line")
@@ -532,6 +535,19 @@ def main():
         return 0
     from mod_amd import ops
     log(f"[bench] {ops.version()}  lib={ops.LIB_FILE}")
+    if args.gemm_launches:
+        for shape in args.gemm_launches:
+            M, K, N = (int(v) for v in shape.split("x"))
+            A = torch.randint(-127, 127, (M, K), dtype=torch.int8, device="cuda")
+            W = torch.randint(-127, 127, (N, K), dtype=torch.int8, device="cuda")
+            sa = torch.rand(M, device="cuda")
+            sw = torch.rand(N, device="cuda")
+            y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+            for _ in range(10):
+                ops.gemm_w8a8(A, sa, W, sw, None, y, M, N, K)
+            torch.cuda.synchronize()
+            print(f"done {shape}", flush=True)
+        return 0
     if args.weights:
         r = bench_weights(torch)
         cpu = r.pop("cpu")

@@ -512,6 +512,10 @@ def main():
     ap.add_argument("--gemm-launches", nargs="+", metavar="MxKxN",
                     help="only run 10 plain (ungraphed) W8A8 GEMM launches per shape, fp16 out, "
                          "then exit -- the command the MFMA counter passes profile")
+    ap.add_argument("--gemv-launches", nargs="+", metavar="MxKxN[:f16]",
+                    help="only run 10 plain (ungraphed) W8 GEMV launches per shape (fp32 x and y, "
+                         "or fp16 with ':f16'), each on its own weight copy, then exit -- the "
+                         "command the GEMV traffic counter passes profile")
     ap.add_argument("--weights", action="store_true",
                     help="only time checkpoint loading (config-2 decoder weights, int8 and BF16 "
                          "safetensors from the page cache into HBM) and print its own JSON line")
@@ -547,6 +551,20 @@ def main():
                 ops.gemm_w8a8(A, sa, W, sw, None, y, M, N, K)
             torch.cuda.synchronize()
             print(f"done {shape}", flush=True)
+        return 0
+    if args.gemv_launches:
+        for spec in args.gemv_launches:
+            shape, _, kind = spec.partition(":")
+            M, K, N = (int(v) for v in shape.split("x"))
+            dt = torch.float16 if kind == "f16" else torch.float32
+            Ws = [torch.randint(-127, 127, (N, K), dtype=torch.int8, device="cuda") for _ in range(2)]
+            sw = torch.rand(N, device="cuda") * 0.019 + 0.001
+            x = torch.randn((M, K), device="cuda").to(dt)
+            y = torch.empty((M, N), dtype=dt, device="cuda")
+            for i in range(10):   # alternate two weight copies so no launch reads a warm cache
+                ops.gemv_w8(x, Ws[i % 2], sw, None, y, M, N, K)
+            torch.cuda.synchronize()
+            print(f"done {spec}", flush=True)
         return 0
     if args.weights:
         r = bench_weights(torch)

@@ -199,7 +199,10 @@ int tensor_moe_w8a8_status(Tensor* x, Tensor* logits, Tensor* w_gu, Tensor* s_gu
  * ------------------------------------------------------------------------- */
 
 /* y[m,n] = s_w[n]*sum_k x[m,k]*W[n,k] (+bias[n]); x_dtype, y_dtype in {F32,F16}.
- * Requirements: K % 16 == 0, pointers 16-byte aligned. Any M >= 1. */
+ * Requirements: K % 16 == 0, pointers 16-byte aligned. Any M >= 1. Products
+ * and sums in fp32 on every path: fp32 FMA kernels in general; fp16 x with
+ * 2 <= M <= 64 and K % 1024 == 0 runs on fp16 MFMAs with exact products and
+ * fp32 accumulation (results differ only in the order of fp32 additions). */
 int pio_gemv_w8(const void* x, int x_dtype, const int8_t* w, const float* s_w, const float* bias,
                 void* y, int y_dtype, int M, int N, int K, void* stream);
 

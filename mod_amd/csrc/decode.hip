@@ -618,7 +618,7 @@ PIO_EXPORT void* pio_qwen3_create(const pio_qwen3_config* cfg, const float* embe
         al256((size_t)d->lm_blocks * 8)};                 // argmax partial keys
     size_t total = 0;
     for (size_t sz : sizes) total += sz;
-    if (device_alloc(&d->block, total) != PIO_OK) {
+    if (device_alloc(&d->block, total, d->st) != PIO_OK) {
         destroy(d);
         return nullptr;
     }

@@ -1258,7 +1258,7 @@ static int loop_build(Qwen3Dec* d) {
 
     // source line table
     void* zero = nullptr;
-    PIO_TRY(device_alloc(&zero, 1024));
+    PIO_TRY(device_alloc(&zero, 1024, d->st));
     Scratch zero_guard;
     zero_guard.ptr = zero;
     PIO_HIP(hipMemsetAsync(zero, 0, 1024, d->st));
@@ -1299,9 +1299,9 @@ static int loop_build(Qwen3Dec* d) {
                     tab[lb + s->off_dn + ub * CI + ch] = L.w_down + (int64_t)(u0 + ub) * I + ch * 1024;
         }
     }
-    PIO_TRY(device_alloc(&s->stream, (size_t)nlines * 1024));
+    PIO_TRY(device_alloc(&s->stream, (size_t)nlines * 1024, d->st));
     void* dtab = nullptr;
-    PIO_TRY(device_alloc(&dtab, (size_t)nlines * sizeof(void*)));
+    PIO_TRY(device_alloc(&dtab, (size_t)nlines * sizeof(void*), d->st));
     Scratch tab_guard;
     tab_guard.ptr = dtab;
     PIO_HIP(hipMemcpyAsync(dtab, tab.data(), (size_t)nlines * sizeof(void*), hipMemcpyHostToDevice,
@@ -1322,7 +1322,7 @@ static int loop_build(Qwen3Dec* d) {
     const size_t lay_off = s->ll_bytes;
     const size_t err_off = lay_off + (c.n_layers * sizeof(LoopLayer) + 255) / 256 * 256;
     s->small_bytes = err_off + 256;
-    PIO_TRY(device_alloc(&s->small, s->small_bytes));
+    PIO_TRY(device_alloc(&s->small, s->small_bytes, d->st));
     char* sp = (char*)s->small;
     u64** dst[] = {&s->xa, &s->xb, &s->q, &s->kv, &s->part, &s->merged, &s->act, &s->keys};
     for (int i = 0; i < 8; i++) *dst[i] = (u64*)(sp + off[i]);

@@ -535,7 +535,7 @@ static int splitk_reduce(const int32_t* w, int splits, const GemmParams& p0, int
 
 static int launch_splitk(const GemmParams& p0, int out_mode, const SplitPlan& sp, hipStream_t st) {
     Scratch ws;
-    PIO_TRY(ws.get((size_t)sp.splits * p0.M * p0.N * sizeof(int32_t)));
+    PIO_TRY(ws.get((size_t)sp.splits * p0.M * p0.N * sizeof(int32_t), st));
     GemmParams p = p0;
     p.a_batch = p.b_batch = p0.K / sp.splits;   // slice z starts at column z*Kc
     p.K = p0.K / sp.splits;
@@ -582,7 +582,7 @@ static int launch_skinny(const GemmParams& p0, int out_mode, const SkinnyPlan& s
         return launch_skinny_one(p, out_mode, sp, st);
     }
     Scratch ws;
-    PIO_TRY(ws.get((size_t)sp.splits * p0.M * p0.N * sizeof(int32_t)));
+    PIO_TRY(ws.get((size_t)sp.splits * p0.M * p0.N * sizeof(int32_t), st));
     p.C = ws.ptr;
     p.ldc = p0.N;
     p.c_batch = (int64_t)p0.M * p0.N;
@@ -682,7 +682,7 @@ static int matmul_int8_impl(const int8_t* a, const int8_t* b, void* c, int out_i
     const int Kp = padded_k(K);
     Scratch own;
     if (!ws) {
-        PIO_TRY(own.get(matmul_ws(batch, M, K, N)));
+        PIO_TRY(own.get(matmul_ws(batch, M, K, N), st));
         ws = own.ptr;
     }
     int8_t* bt = (int8_t*)ws;

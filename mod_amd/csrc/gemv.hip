@@ -575,7 +575,7 @@ static int launch_gemv_mfma(const _Float16* x, const int8_t* w, const float* s_w
     GemvMfma p{x, w, s_w, bias, y, M, N, K / pl.splits, K};
     Scratch ws;
     if (pl.splits > 1) {
-        PIO_TRY(ws.get((size_t)pl.splits * M * N * sizeof(float)));
+        PIO_TRY(ws.get((size_t)pl.splits * M * N * sizeof(float), st));
         p.y = ws.ptr;
     }
     const int rc = pl.wv == 4 ? launch_gemv_mfma_wv<4, YT>(p, pl, st) : launch_gemv_mfma_wv<3, YT>(p, pl, st);

@@ -449,7 +449,7 @@ int moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* w_gu
     if (T == 0) return PIO_OK;
     Scratch own;
     if (!ws) {
-        PIO_TRY(own.get(moe_layout(nullptr, T, H, I, E, top_k).total));
+        PIO_TRY(own.get(moe_layout(nullptr, T, H, I, E, top_k).total, st));
         ws = own.ptr;
     }
     MoeWs w = moe_layout((char*)ws, T, H, I, E, top_k);

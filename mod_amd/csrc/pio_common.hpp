@@ -62,14 +62,19 @@ inline size_t dtype_bytes(int dt) {
 }
 
 // ---- device allocation (caching allocator, runtime.hip) -------------------
-int device_alloc(void** p, size_t bytes);   // on the current device
+// On the current device. A freed block is cached and handed out again only
+// to a request for the same stream (`stream`, NULL = the current stream), so
+// stream order makes the reuse safe: the new owner's work is queued behind
+// the old owner's last kernel.
+int device_alloc(void** p, size_t bytes, hipStream_t stream = nullptr);
 void device_free(void* p);                  // back to the cache (or no-op for pool memory)
 
-// Scoped device scratch from the caching allocator.
+// Scoped device scratch from the caching allocator, for work queued on `st`;
+// freed when the scope ends, possibly while that work is still running.
 struct Scratch {
     void* ptr = nullptr;
     ~Scratch() { if (ptr) device_free(ptr); }
-    int get(size_t bytes) { return bytes ? device_alloc(&ptr, bytes) : PIO_OK; }
+    int get(size_t bytes, hipStream_t st) { return bytes ? device_alloc(&ptr, bytes, st) : PIO_OK; }
 };
 
 // ---- Tensor metadata -------------------------------------------------------

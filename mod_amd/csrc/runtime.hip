@@ -10,11 +10,15 @@
 // free list and are reused by the next request of that size. init_memory_pool()
 // adds the reference's arena on top: while it has room, device tensors are
 // bump-allocated from it and freeing them is a no-op (tensor_ops.c:135-162).
-// Everything is ordered on one in-order stream per device, so a block freed
-// after its last kernel was enqueued can be handed out again immediately.
+// A block remembers the stream it was allocated for and, once freed, is handed
+// out again only for that stream: a block freed right after its last kernel
+// was enqueued is then safe to reuse, because the next owner's work queues
+// behind that kernel. (Blocks move between streams only through
+// tensor_empty_cache / an out-of-memory retry, whose hipFree synchronizes.)
 #include "pio_common.hpp"
 
 #include <mutex>
+#include <tuple>
 #include <map>
 #include <unordered_map>
 #include <vector>
@@ -64,9 +68,15 @@ struct Arena {
 
 struct Alloc {
     std::mutex mu;
-    std::unordered_map<void*, std::pair<size_t, int>> live;   // ptr -> (rounded bytes, device)
+    struct Live {
+        size_t bytes;        // rounded
+        int dev;
+        hipStream_t stream;  // the stream whose order protects reuse
+    };
+    std::unordered_map<void*, Live> live;
     std::unordered_map<void*, int> arena_live;                // ptr -> device
-    std::map<std::pair<int, size_t>, std::vector<void*>> free_lists;
+    // (device, rounded bytes, stream) -> cached blocks
+    std::map<std::tuple<int, size_t, hipStream_t>, std::vector<void*>> free_lists;
     std::map<int, Arena> arenas;
     size_t reserved = 0, in_use = 0, cached = 0, peak = 0, n_malloc = 0;
 };
@@ -86,20 +96,21 @@ static void empty_cache_locked(Alloc& a) {
         for (void* p : kv.second) {
             int cur = 0;
             (void)hipGetDevice(&cur);
-            (void)hipSetDevice(kv.first.first);
+            (void)hipSetDevice(std::get<0>(kv.first));
             (void)hipFree(p);
             (void)hipSetDevice(cur);
-            a.reserved -= kv.first.second;
-            a.cached -= kv.first.second;
+            a.reserved -= std::get<1>(kv.first);
+            a.cached -= std::get<1>(kv.first);
         }
     }
     a.free_lists.clear();
 }
 
-int device_alloc(void** out, size_t bytes) {
+int device_alloc(void** out, size_t bytes, hipStream_t stream) {
     *out = nullptr;
     int dev = 0;
     PIO_HIP(hipGetDevice(&dev));
+    if (!stream) stream = current_stream();
     Alloc& a = A();
     std::lock_guard<std::mutex> lk(a.mu);
     size_t r = round_bytes(bytes);
@@ -114,7 +125,7 @@ int device_alloc(void** out, size_t bytes) {
             return PIO_OK;
         }
     }
-    auto fit = a.free_lists.find({dev, r});
+    auto fit = a.free_lists.find(std::make_tuple(dev, r, stream));
     if (fit != a.free_lists.end() && !fit->second.empty()) {
         *out = fit->second.back();
         fit->second.pop_back();
@@ -136,7 +147,7 @@ int device_alloc(void** out, size_t bytes) {
         a.n_malloc++;
         *out = p;
     }
-    a.live[*out] = {r, dev};
+    a.live[*out] = {r, dev, stream};
     a.in_use += r;
     if (a.in_use > a.peak) a.peak = a.in_use;
     return PIO_OK;
@@ -149,12 +160,11 @@ void device_free(void* p) {
     if (a.arena_live.erase(p)) return;   // pool memory: reclaimed by reset_memory_pool
     auto it = a.live.find(p);
     if (it == a.live.end()) return;
-    size_t r = it->second.first;
-    int dev = it->second.second;
+    const Alloc::Live l = it->second;
     a.live.erase(it);
-    a.in_use -= r;
-    a.cached += r;
-    a.free_lists[{dev, r}].push_back(p);
+    a.in_use -= l.bytes;
+    a.cached += l.bytes;
+    a.free_lists[std::make_tuple(l.dev, l.bytes, l.stream)].push_back(p);
 }
 
 // ------------------------------------------------------ tensor metadata ---

@@ -606,7 +606,7 @@ PIO_EXPORT int pio_safetensors_to_device_f32(void* ctx, const char* name, float*
     if (count == 0) return PIO_OK;
     hipStream_t st = pick_stream(stream);
     Scratch raw;
-    PIO_TRY(raw.get((size_t)nbytes));
+    PIO_TRY(raw.get((size_t)nbytes, st));
     {
         std::lock_guard<std::mutex> lk(g_stager.mu);
         PIO_TRY(stage_to_device((const StFile*)ctx, (size_t)en->begin, (size_t)nbytes, raw.ptr, st));

@@ -108,3 +108,44 @@ def test_unified_manager_evicts_lru_and_restores_bytes():
     assert id(big) in mm.evicted
     np.testing.assert_array_equal(ts[0].numpy(), data[0])
     assert mm.stats()["registered"] == len(mm.tensors)
+
+
+@pytest.mark.gpu
+def test_allocator_reuses_a_block_only_on_its_stream():
+    """A freed block goes back to the cache tagged with the stream it was
+    allocated for and is handed out again only for that stream, so work still
+    queued on the old stream can never see its memory taken by another
+    stream. Checked through the public pool statistics (stats[4] counts
+    hipMalloc calls): same stream -> reuse, other stream -> a new block."""
+    from mod_amd import ops
+    from mod_amd.backend import Tensor
+    lib = ops.lib
+    stats = (ctypes.c_size_t * 7)()
+
+    def mallocs():
+        lib.tensor_pool_stats(stats)
+        return stats[4]
+
+    sa, sb = lib.create_stream(), lib.create_stream()
+    try:
+        shape = [3, 1000, 77]            # an odd size no other test allocates
+        lib.set_current_stream(sa)
+        t = Tensor(shape)
+        del t                            # cached for stream A
+        n0 = mallocs()
+        t = Tensor(shape)                # same stream: the cached block
+        assert mallocs() == n0
+        del t
+        lib.set_current_stream(sb)
+        t = Tensor(shape)                # other stream: never the block cached for A
+        assert mallocs() == n0 + 1
+        del t
+        lib.set_current_stream(sa)
+        t = Tensor(shape)
+        assert mallocs() == n0 + 1       # A's block again
+        del t
+    finally:
+        lib.set_current_stream(None)
+        lib.device_synchronize()
+        lib.destroy_stream(sa)
+        lib.destroy_stream(sb)

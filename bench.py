@@ -29,6 +29,16 @@ Also in the same line:
                 token, on the host cores, extrapolated per token.
   kernels       the other BASELINE configs' kernels: C1 GEMV, C3 W8A8 GEMMs +
                 quantizer, C4 skinny-M sweep and lm_head, C5 MoE layer.
+
+Other modes (each prints its own line and exits):
+  --weights             checkpoint loading: config-2 decoder weights as int8 and
+                        BF16 safetensors, page cache -> HBM, with the reference
+                        loader timed beside it.
+  --gemm-launches S..   10 plain W8A8 GEMM launches per MxKxN shape (the command
+                        the MFMA counter passes profile).
+  --gemv-launches S..   10 plain W8 GEMV launches per MxKxN[:f16] shape (the
+                        command the HBM traffic counter passes profile).
+  --decode-only, --calibrate-copy: see --help.
 """
 from __future__ import annotations
 

@@ -77,7 +77,10 @@ class SafetensorsFile:
         self.close()
 
     def __del__(self):
-        self.close()
+        try:
+            self.close()
+        except Exception:   # interpreter shutdown: the library may already be gone
+            pass
 
     def _c(self):
         if not self._ctx:
@@ -371,12 +374,17 @@ def save_safetensors(path, tensors: Dict[str, np.ndarray], dtypes: Optional[Dict
     meta.update(metadata or {})
     hdr = _header(entries, meta)
     tmp = os.fspath(path) + ".tmp"
-    with open(tmp, "wb") as out:
-        out.write(struct.pack("<Q", len(hdr)))
-        out.write(hdr)
-        for a in arrays:
-            a.tofile(out)
-    os.replace(tmp, os.fspath(path))
+    try:
+        with open(tmp, "wb") as out:
+            out.write(struct.pack("<Q", len(hdr)))
+            out.write(hdr)
+            for a in arrays:
+                a.tofile(out)
+        os.replace(tmp, os.fspath(path))
+    except BaseException:
+        if os.path.exists(tmp):
+            os.remove(tmp)
+        raise
 
 
 def quantize_checkpoint(src_path, dst_path, select: Callable[[str, TensorInfo], bool] = None,
@@ -407,22 +415,33 @@ def quantize_checkpoint(src_path, dst_path, select: Callable[[str, TensorInfo], 
         hdr = _header(entries, meta)
         tmp = os.fspath(dst_path) + ".tmp"
         quantized = []
-        with open(tmp, "wb") as out:
-            out.write(struct.pack("<Q", len(hdr)))
-            out.write(hdr)
-            for name, quant in plan:
-                if quant:
-                    inf = ck.info(name)
-                    q = Tensor(list(inf.shape), device=device, dtype="int8")
-                    s = Tensor([inf.shape[0]], device=device)
-                    load_int8_weight(ck, name, q, s)
-                    out.write(q.numpy().tobytes())
-                    out.write(s.numpy().tobytes())
-                    quantized.append(name)
-                else:
-                    out.write(ck.read(name).tobytes())
-        os.replace(tmp, os.fspath(dst_path))
+        try:
+            _write_quantized(ck, plan, hdr, tmp, device, quantized)
+            os.replace(tmp, os.fspath(dst_path))
+        except BaseException:
+            if os.path.exists(tmp):
+                os.remove(tmp)
+            raise
     return quantized
+
+
+def _write_quantized(ck, plan, hdr: bytes, tmp: str, device: str, quantized: List[str]) -> None:
+    """Header, then each planned tensor in order: quantized ones as int8 rows
+    followed by their fp32 scales (quantized on the GPU), the rest as stored."""
+    with open(tmp, "wb") as out:
+        out.write(struct.pack("<Q", len(hdr)))
+        out.write(hdr)
+        for name, quant in plan:
+            if quant:
+                inf = ck.info(name)
+                q = Tensor(list(inf.shape), device=device, dtype="int8")
+                s = Tensor([inf.shape[0]], device=device)
+                load_int8_weight(ck, name, q, s)
+                out.write(q.numpy().tobytes())
+                out.write(s.numpy().tobytes())
+                quantized.append(name)
+            else:
+                out.write(ck.read(name).tobytes())
 
 
 def quantize_array(w: np.ndarray, device: str = "rocm:0") -> Tuple[np.ndarray, np.ndarray]:

@@ -202,7 +202,9 @@ int tensor_moe_w8a8_status(Tensor* x, Tensor* logits, Tensor* w_gu, Tensor* s_gu
  * Requirements: K % 16 == 0, pointers 16-byte aligned. Any M >= 1. Products
  * and sums in fp32 on every path: fp32 FMA kernels in general; fp16 x with
  * 2 <= M <= 64 and K % 1024 == 0 runs on fp16 MFMAs with exact products and
- * fp32 accumulation (results differ only in the order of fp32 additions). */
+ * fp32 accumulation inside the matrix core, whose rounding is not
+ * round-to-nearest-even (measured: results within a few ulp of the FMA
+ * kernels'; deterministic run to run). */
 int pio_gemv_w8(const void* x, int x_dtype, const int8_t* w, const float* s_w, const float* bias,
                 void* y, int y_dtype, int M, int N, int K, void* stream);
 

@@ -351,8 +351,10 @@ static void launch_direct_rows(const XT* x, const int8_t* w, const float* s_w, c
 // fp32 FMAs per weight byte, which makes them VALU-bound from M ~ 4 (M = 64:
 // 2% of HBM). Here the products go to v_mfma_f32_16x16x32_f16: an int8 weight
 // is exact in fp16, an fp16 x int8 product is exact in fp32, and the MFMA
-// accumulates in fp32 -- the same result as the FMA kernels up to the order
-// of the fp32 additions. The structure is the skinny W8A8 kernel's (gemm.hip):
+// accumulates in fp32. The matrix core's accumulation does not round to
+// nearest-even (a sign flip of W moves ~0.06% of outputs by 1-4 ulp, the
+// negative side larger), so results match the FMA kernels to a few ulp, not
+// bit for bit; they are deterministic run to run. The structure is the skinny W8A8 kernel's (gemm.hip):
 // each wave owns 16 weight rows streamed from HBM into registers 4 blocks of
 // 256 K ahead (lane: row r = lane % 16, K chunk q = lane / 16, 16 bytes at
 // 64*i + 16*q), each 16-byte chunk widened to two 8 x fp16 operands; the

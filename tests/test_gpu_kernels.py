@@ -472,3 +472,46 @@ def test_moe_tiny_golden(env):
                  out, T, H, I2 // 2, E, 2, False)
     sync(torch)
     assert_rel(host(out), g["y"], 1e-2, "moe golden")
+
+
+def test_skinny_paths_full_size_properties(env):
+    """At the Qwen3-8B lm_head size (M = 16, N = 151936, K = 4096), where the
+    oracle would take minutes, properties the arithmetic fixes:
+    - MFMA GEMV (fp16 x, fp32 y): products are exact and the accumulation
+      scales exactly by 2, so y(2x) == 2 y(x) bit for bit. Under a sign flip
+      of W the result mirrors only to within a few ulp: the f16 MFMA's fp32
+      accumulation does not round to nearest-even (measured: about 0.06% of
+      outputs move by 1-4 ulp, the negative side larger, as rounding toward
+      -inf does), so y(x; -W) == -y(x; W) is held to 8 ulp of max |y|;
+    - skinny W8A8 (int32 out): acc(q; -W) == -acc(q; W) exactly, and a few
+      rows equal the oracle's int32 dot products."""
+    torch, ops, d = env
+    M, N, K = 16, 151936, 4096
+    _say(f"skinny full-size properties M={M} N={N} K={K}")
+    rng = np.random.default_rng(99)
+    W = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    Wd, Wn = dev(torch, W, d), dev(torch, -W, d)
+    s = dev(torch, rng.uniform(0.001, 0.02, size=N).astype(np.float32), d)
+    x = rng.standard_normal((M, K), dtype=np.float32).astype(np.float16)
+    xd, x2d = dev(torch, x, d), dev(torch, (x.astype(np.float32) * 2).astype(np.float16), d)
+    y, y2, yn = (torch.empty((M, N), dtype=torch.float32, device=d) for _ in range(3))
+    ops.gemv_w8(xd, Wd, s, None, y, M, N, K)
+    ops.gemv_w8(x2d, Wd, s, None, y2, M, N, K)
+    ops.gemv_w8(xd, Wn, s, None, yn, M, N, K)
+    sync(torch)
+    hy = host(y)
+    assert np.isfinite(hy).all()
+    assert np.array_equal(host(y2), 2 * hy)
+    # the accumulation error scales with the partial sums, not with outputs
+    # that cancel to near zero: bound it by 8 ulp of the largest output
+    assert np.abs(host(yn) + hy).max() <= 8 * np.spacing(np.float32(np.abs(hy).max()))
+    q = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    qd = dev(torch, q, d)
+    acc, accn = (torch.empty((M, N), dtype=torch.int32, device=d) for _ in range(2))
+    ops.gemm_w8a8(qd, None, Wd, None, None, acc, M, N, K)
+    ops.gemm_w8a8(qd, None, Wn, None, None, accn, M, N, K)
+    sync(torch)
+    ha = host(acc)
+    assert np.array_equal(host(accn), -ha)
+    rows = [0, 1, 77, 4095, 100000, N - 1]
+    assert np.array_equal(ha[:, rows], oracle.matmul_nt_i32(q, W[rows]))

@@ -3,32 +3,38 @@
 
 Headline (BASELINE.json metric, config 2): greedy int8 decode tok/s of a
 Qwen3-0.6B-shaped decoder (28 layers, hidden 1024, 16/8 heads, head_dim 128,
-SwiGLU 3072, vocab 151936, int8 lm_head), batch 1, 128-token random prompt then
-256 generated tokens. A "step" is one generated token. Random-init int8 weights
-(no checkpoint is available offline) and random prompt ids; every input is
-resident in HBM before the timed region; the timed region is exactly `--steps`
-decode steps bracketed by device synchronization. The steps run in the
-persistent decode kernel (one cooperative launch for all timed steps) when the
-config supports it; the captured-graph step path is timed the same way and
-reported next to it.
+SwiGLU 3072, vocab 151936, int8 lm_head), batch 1. A "step" is one whole
+config-2 generation: reset to a 128-token random prompt, run the prompt
+positions, then 256 greedy tokens. `--steps K` times K generations after
+`--warmup W` untimed ones, bracketed by device synchronization; HIP events on
+the decoder's stream split each generation into prefill and decode, and
+`value` = generated tokens / decode time (so every step decodes at the
+config's mean context of 255.5 positions whatever K is). Random-init int8
+weights (no checkpoint is available offline) and random prompt ids; every
+input is resident in HBM before the timed region. The tokens run in the
+persistent decode kernel (one cooperative launch per generation's 256 tokens)
+when the config supports it; the captured-graph step path is timed on one
+generation and reported next to it.
 
 Also in the same line:
   roofline      the dominant kernel: the persistent decode kernel (algorithmic
-                bytes of all timed tokens / its launch time, HIP events on the
-                decoder's stream); on the graph path, the per-layer W8 GEMV
-                replayed alone from a graph. `traffic` is the HBM bytes of that
-                launch measured with rocprofv3 counters (FETCH_SIZE and
-                WRITE_SIZE passes over this same command, each scaled by what
-                the counter reads for a plain 1 GiB device copy, see
+                bytes of a generation's 256 tokens / its launch time, HIP
+                events on the decoder's stream); on the graph path, the
+                per-layer W8 GEMV replayed alone from a graph. `traffic` is the
+                HBM bytes of that launch measured with rocprofv3 counters
+                (FETCH_SIZE and WRITE_SIZE passes, each scaled by what the
+                counter reads for a plain 1 GiB device copy, see
                 --calibrate-copy), read from the profile summary
-                profiles/decode_loop_kernel_traffic.txt when its step count
-                matches; null otherwise.
+                profiles/decode_loop_kernel_traffic.txt.
   cpu_baseline  the reference CPU path (oracle/_ref/libtensor_ops_ref.so, built
                 from the reference's own tensor_ops.c): its fp32 tensor_linear on
                 per-channel-dequantized weights over every linear of one decode
-                token, on the host cores, extrapolated per token.
+                token, on the host cores.
   kernels       the other BASELINE configs' kernels: C1 GEMV, C3 W8A8 GEMMs +
-                quantizer, C4 skinny-M sweep and lm_head, C5 MoE layer.
+                quantizer, C4 skinny-M sweep and lm_head, C5 MoE layer; each
+                entry carries a `cpu` leg: the reference's tensor_matmul_int8
+                (tensor_linear for C1's fp32 path, plus tensor_softmax /
+                tensor_topk routing for C5) on a bounded sample, scaled.
 
 Other modes (each prints its own line and exits):
   --weights             checkpoint loading: config-2 decoder weights as int8 and
@@ -96,12 +102,21 @@ class Timer:
 
 
 # ------------------------------------------------------------------ decode
+PROMPT_LEN = 128     # 128-token random-id prompt ...
+GEN_LEN = 256        # ... then 256 greedy tokens
+
+
 def bench_decode(torch, args):
+    """BASELINE config 2, as stated: every step is one whole generation --
+    reset to a 128-token prompt, the prompt positions, then 256 greedy tokens
+    -- so each timed step decodes at mean context 255.5 whatever --steps is.
+    HIP events on the decoder's stream split each generation into prefill and
+    decode; `value` is generated tokens / decode time."""
     import numpy as np
     from mod_amd.qwen3 import Qwen3Config, Qwen3Int8Decoder, random_weights
 
-    P = 128
-    cfg = Qwen3Config(max_seq=max(384, P + args.steps))
+    P, NG = PROMPT_LEN, GEN_LEN
+    cfg = Qwen3Config(max_seq=P + NG)
     t0 = time.time()
     w = random_weights(cfg, seed=0)
     log(f"[decode] random weights built in {time.time() - t0:.1f}s")
@@ -112,47 +127,62 @@ def bench_decode(torch, args):
     if args.decode_only:
         modes = modes[:1]
 
-    def timed_run(mode):
-        # Warmup: builds the mode's resources (graph / weight stream), untimed.
-        dec.reset(prompt)
-        dec.run(P - 1 + min(args.warmup, cfg.max_seq - P + 1), mode=mode)
-        torch.cuda.synchronize()
-        # Timed: the exact config-2 run. Prefill (P-1 prompt steps) is timed apart.
-        dec.reset(prompt)
+    def generation(mode):
+        dec.reset(prompt)                 # host-synchronous upload of the prompt
         e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-        torch.cuda.synchronize()
         e[0].record(st)
         dec.run(P - 1, mode=mode)
         e[1].record(st)
-        dec.run(args.steps, mode=mode)
+        dec.run(NG, mode=mode)
         e[2].record(st)
-        e[2].synchronize()
+        return e
+
+    def run_mode(mode, steps, warmup):
+        for _ in range(warmup):
+            generation(mode)
         torch.cuda.synchronize()
-        ids = dec.read(P + args.steps)
+        t_wall = time.perf_counter()
+        evs = [generation(mode) for _ in range(steps)]
+        torch.cuda.synchronize()
+        t_wall = time.perf_counter() - t_wall
+        ids = dec.read(P + NG)
         assert np.array_equal(ids[:P], prompt)
-        return e[0].elapsed_time(e[1]) * 1e-3, e[1].elapsed_time(e[2]) * 1e-3, ids
+        pre = [e[0].elapsed_time(e[1]) * 1e-3 for e in evs]
+        dcd = [e[1].elapsed_time(e[2]) * 1e-3 for e in evs]
+        return t_wall, pre, dcd, ids
 
     wb = cfg.weight_bytes()
-    mean_ctx = P + (args.steps - 1) / 2.0
+    mean_ctx = P + (NG - 1) / 2.0
     bytes_tok = wb["int8"] + wb["scales"] + wb["bias_norms"] + cfg.kv_bytes_per_pos() * mean_ctx
     res = {}
-    for mode in modes:
-        prefill_s, decode_s, ids = timed_run(mode)
+    for i, mode in enumerate(modes):
+        # the first mode is the headline (all --steps); the other one is timed
+        # on a single generation for comparison
+        steps, warmup = (args.steps, args.warmup) if i == 0 else (1, 1)
+        t_wall, pre, dcd, ids = run_mode(mode, steps, warmup)
+        dsum = float(sum(dcd))
         res[mode] = {
-            "tok_s": args.steps / decode_s,
-            "ms_per_token": decode_s / args.steps * 1e3,
-            "prefill_ms": prefill_s * 1e3,
-            "prefill_tok_s": (P - 1) / prefill_s,
+            "generations": steps,
+            "tok_s": NG * steps / dsum,
+            "ms_per_token": dsum / (NG * steps) * 1e3,
+            "decode_ms_per_generation": dsum / steps * 1e3,
+            "prefill_ms_per_generation": float(sum(pre)) / steps * 1e3,
+            "wall_ms_per_generation": t_wall / steps * 1e3,
+            "decode_ms_min_max": [min(dcd) * 1e3, max(dcd) * 1e3],
             "bytes_per_token": bytes_tok,
-            "hbm_frac": bytes_tok * args.steps / decode_s / (HBM_PEAK_GBS * 1e9),
+            "hbm_frac": bytes_tok * NG * steps / dsum / (HBM_PEAK_GBS * 1e9),
             "ceiling_tok_s": HBM_PEAK_GBS * 1e9 / bytes_tok,
             "generated_head": ids[P:P + 8].tolist(),
         }
-        log(f"[decode:{mode}] {res[mode]['tok_s']:.1f} tok/s ({res[mode]['ms_per_token']:.3f} ms/token), "
-            f"prefill {res[mode]['prefill_ms']:.1f} ms")
+        log(f"[decode:{mode}] {res[mode]['tok_s']:.1f} tok/s over {steps} generation(s) of {NG} "
+            f"tokens ({res[mode]['ms_per_token']:.3f} ms/token), prefill "
+            f"{res[mode]['prefill_ms_per_generation']:.1f} ms")
+        res[mode]["_ids"] = ids
     if len(modes) == 2:
-        same = res["persistent"]["generated_head"] == res["graph"]["generated_head"]
-        res["persistent"]["same_tokens_as_graph"] = same
+        res["persistent"]["same_tokens_as_graph"] = bool(
+            np.array_equal(res["persistent"]["_ids"], res["graph"]["_ids"]))
+    for m in modes:
+        res[m].pop("_ids")
     res["mode"] = modes[0]
     return cfg, w, dec, st, res
 
@@ -298,9 +328,31 @@ def bench_kernels(torch, timer):
 
 
 # ------------------------------------------------------------ CPU baseline
+CPU_NOTE = ("reference CPU backend built from its own source (tensor_ops.c, Makefile:15 flags); "
+            "it parallelizes over the batch dimension only (tensor_ops.c:225, 306), so a 2-D "
+            "product runs on one core")
+
+
+def _median_time(fn, reps=5, budget_s=5.0):
+    """Median wall time of fn over up to `reps` calls within `budget_s`; the
+    first call warms up, and counts as a sample when it is long (>= 0.2 s)."""
+    import numpy as np
+    t0 = time.perf_counter()
+    fn()
+    first = time.perf_counter() - t0
+    times = [first] if first >= 0.2 else []
+    t_start = time.perf_counter()
+    while len(times) < reps and (time.perf_counter() - t_start) < budget_s:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
+
+
 def cpu_baseline(cfg, w, budget_s=20.0):
-    """The reference CPU path on the host: tensor_linear (fp32, tensor_ops.c:
-    323-335) over one decode token's linears, weights dequantized per channel."""
+    """Config 2 on the host: the reference's fp32 tensor_linear (tensor_ops.c:
+    323-335) over one decode token's linears, weights dequantized per channel
+    (what the reference model runs today)."""
     import numpy as np
     import oracle
     if not oracle.ref_available():
@@ -330,28 +382,163 @@ def cpu_baseline(cfg, w, budget_s=20.0):
         for (tw, tb, n, k) in mats:
             L.tensor_linear(x[k].h, tw.h, tb.h if tb else None, outs[n].h)
 
-    one_token()    # warm
-    times = []
-    t_start = time.time()
-    while len(times) < 5 and (time.time() - t_start) < budget_s:
-        t0 = time.perf_counter()
-        one_token()
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
+    med, n = _median_time(one_token, reps=5, budget_s=budget_s)
+    del mats
     return {
         "value": 1.0 / med,
         "unit": "tok/s",
         "cores": 1,
         "kind": "reference",
-        "sample": (f"reference tensor_linear (fp32, tensor_ops.c:301-335, built from the reference "
-                   f"source with Makefile:15 flags) over one decode token's {len(mats)} linears of "
-                   f"the config-2 model (weights dequantized per channel), median of {len(times)} "
-                   f"tokens; attention/norm ops excluded. The reference parallelizes over batch "
-                   f"only (tensor_ops.c:306), so at batch 1 one core works "
+        "sample": (f"reference tensor_linear (fp32, tensor_ops.c:301-335) over one decode token's "
+                   f"113 linears of the config-2 model (weights dequantized per channel), median "
+                   f"of {n} tokens; attention/norm ops excluded. {CPU_NOTE} "
                    f"(OMP_NUM_THREADS={os.environ.get('OMP_NUM_THREADS', 'default')}, "
                    f"host cores={os.cpu_count()})."),
         "ms_per_token": med * 1e3,
     }
+
+
+def cpu_kernel_baselines():
+    """The other configs on the host, with the reference's own functions:
+    tensor_matmul_int8 (tensor_ops.c:217-246, B given [K,N]) for every int8
+    product plus the per-token / per-channel scale epilogue in numpy, and
+    tensor_linear for C1's fp32 path; C5 adds the reference routing
+    (tensor_softmax, tensor_topk). Each leg runs a bounded sample and is scaled
+    to the full workload (rows and experts are independent work in these
+    loops); the sample is stated per leg."""
+    import numpy as np
+    import oracle
+    if not oracle.ref_available():
+        return {}
+    L = oracle.ref_lib()
+    RT = oracle.RefTensor
+    out = {}
+
+    def mm_leg(q, WT, s_a, s_w, out_f16):
+        """Reference int8 matmul q[M,K] x WT[K,N] then the scale epilogue."""
+        M, K = q.shape
+        N = WT.shape[1]
+        ta, tb, to = RT((M, K), q), RT((K, N), WT), RT((M, N))
+
+        def f():
+            L.tensor_matmul_int8(ta.h, tb.h, to.h)
+            y = to.f32() * s_a[:, None] * s_w[None, :]
+            return y.astype(np.float16) if out_f16 else y
+        return f
+
+    rng = np.random.default_rng(5)
+
+    # C1: (i) fp32 tensor_linear on per-channel dequantized W (what the model runs);
+    #     (ii) tensor_matmul_int8 at M=1 on the per-token quantized x.
+    N, K = 3072, 1024
+    W = rng.integers(-127, 127, size=(N, K), dtype=np.int8)
+    s = rng.uniform(0.001, 0.02, size=N).astype(np.float32)
+    x = rng.standard_normal((1, K), dtype=np.float32)
+    tx, tw, ty = RT((1, K), x), RT((N, K), W.astype(np.float32) * s[:, None]), RT((1, N))
+    t_lin, n1 = _median_time(lambda: L.tensor_linear(tx.h, tw.h, None, ty.h))
+    q, sa = oracle.quant_per_token(x)
+    t_i8, n2 = _median_time(mm_leg(q, np.ascontiguousarray(W.T), sa, s, False))
+    out["c1_gemv"] = {"us": t_lin * 1e6, "kind": "reference", "cores": 1,
+                      "int8_matmul_us": t_i8 * 1e6,
+                      "sample": f"full C1: tensor_linear fp32 [1,1024]x[3072,1024]^T median of {n1}; "
+                                f"int8 leg tensor_matmul_int8 [1,1024]x[1024,3072] + epilogue, median of {n2}"}
+    del tw
+
+    # C3: M=2048 rows; an 8-row sample of the int8 matmul (time is linear in M).
+    c3 = {}
+    for (K, N) in [(1024, 3072), (3072, 1024), (1024, 2048)]:
+        Ms = 8
+        xs = rng.standard_normal((Ms, K), dtype=np.float32).astype(np.float16)
+        q, sa = oracle.quant_per_token(xs)
+        W = rng.integers(-127, 127, size=(N, K), dtype=np.int8)
+        sw = rng.uniform(0.001, 0.02, size=N).astype(np.float32)
+        t, n = _median_time(mm_leg(q, np.ascontiguousarray(W.T), sa, sw, True), reps=2)
+        c3[f"K{K}_N{N}"] = {"gemm_us": t * 2048 / Ms * 1e6,
+                            "TOPS": 2 * 2048 * N * K / (t * 2048 / Ms) / 1e12,
+                            "kind": "reference", "cores": 1,
+                            "sample": f"{Ms} of 2048 rows (median of {n}), scaled x{2048 // Ms}"}
+    out["c3_w8a8"] = c3
+
+    # C4: Qwen3-8B linears; M=1 measured, larger M from its time x M (the
+    # reference loop redoes the whole B sweep per row).
+    c4 = {}
+    for (N, K) in [(12288, 4096), (4096, 12288)]:
+        W = rng.integers(-127, 127, size=(N, K), dtype=np.int8)
+        WT = np.ascontiguousarray(W.T)
+        del W
+        sw = rng.uniform(0.001, 0.02, size=N).astype(np.float32)
+        q, sa = oracle.quant_per_token(rng.standard_normal((1, K), dtype=np.float32).astype(np.float16))
+        t, n = _median_time(mm_leg(q, WT, sa, sw, True), reps=2)
+        for M in (1, 4, 16, 64):
+            c4[f"N{N}_K{K}_M{M}"] = {
+                "us": t * M * 1e6, "kind": "reference", "cores": 1,
+                "sample": (f"full, median of {n}" if M == 1 else
+                           f"the measured M=1 time x {M} (rows are independent passes over B)")}
+        del WT
+    N, K, Ns = 151936, 4096, 8192
+    WT = rng.integers(-127, 127, size=(K, Ns), dtype=np.int8)
+    sw = rng.uniform(0.001, 0.02, size=Ns).astype(np.float32)
+    q, sa = oracle.quant_per_token(rng.standard_normal((1, K), dtype=np.float32).astype(np.float16))
+    t, n = _median_time(mm_leg(q, WT, sa, sw, True), reps=3)
+    c4["lm_head_8b_M1"] = {"us": t * N / Ns * 1e6, "kind": "reference", "cores": 1,
+                           "sample": f"{Ns} of {N} output columns (median of {n}), scaled x{N / Ns:.2f}"}
+    del WT
+    out["c4_skinny"] = c4
+
+    # C5: reference routing over all 512 tokens; then per expert gather, per-token
+    # quant, tensor_matmul_int8 gate_up, SwiGLU, requant, tensor_matmul_int8 down
+    # and the k-ordered combine, on a sample of 8 experts scaled by routed rows.
+    T, H, I, E, k, Es = 512, 2048, 768, 128, 8, 4
+    logits = rng.standard_normal((T, E), dtype=np.float32)
+    xm = rng.standard_normal((T, H), dtype=np.float32).astype(np.float16)
+    tl, tp = RT((T, E), logits), RT((T, E))
+    tv, ti = RT((T, k)), RT((T, k))
+
+    def route():
+        L.tensor_softmax(tl.h, tp.h)
+        L.tensor_topk(tp.h, k, tv.h, ti.h)
+        return tv.f32(), ti.f32().astype(np.int32)
+    t_route, _ = _median_time(route, reps=3)
+    wts, ids = route()
+    experts = []
+    for e in range(Es):
+        wgu = rng.integers(-127, 127, size=(2 * I, H), dtype=np.int8)
+        wdn = rng.integers(-127, 127, size=(H, I), dtype=np.int8)
+        experts.append((RT((H, 2 * I), np.ascontiguousarray(wgu.T)), RT((I, H), np.ascontiguousarray(wdn.T)),
+                        rng.uniform(0.001, 0.02, size=2 * I).astype(np.float32),
+                        rng.uniform(0.001, 0.02, size=H).astype(np.float32)))
+
+    def experts_run():
+        y = np.zeros((T, H), np.float32)
+        for e in range(Es):
+            tok, slot = np.nonzero(ids == e)
+            n_e = tok.size
+            if n_e == 0:
+                continue
+            tg, td, sgu, sdn = experts[e]
+            q, sa = oracle.quant_per_token(xm[tok])
+            tq, tgo = RT((n_e, H), q), RT((n_e, 2 * I))
+            L.tensor_matmul_int8(tq.h, tg.h, tgo.h)
+            gu = tgo.f32() * sa[:, None] * sgu[None, :]
+            g, u = gu[:, :I], gu[:, I:]
+            with np.errstate(over="ignore"):
+                h = g / (1.0 + np.exp(-g)) * u
+            qh, sh = oracle.quant_per_token(h.astype(np.float32))
+            th, tdo = RT((n_e, I), qh), RT((n_e, H))
+            L.tensor_matmul_int8(th.h, td.h, tdo.h)
+            dn = tdo.f32() * sh[:, None] * sdn[None, :]
+            y[tok] += wts[tok, slot][:, None] * dn
+        return y
+    t_exp, n = _median_time(experts_run, reps=2)
+    rows_sample = int(np.isin(ids, np.arange(Es)).sum())
+    t_total = t_route + t_exp * (T * k) / max(rows_sample, 1)
+    ops_ = T * k * (2 * H * 2 * I + 2 * I * H)
+    out["c5_moe"] = {"us": t_total * 1e6, "TOPS": ops_ / t_total / 1e12, "kind": "reference",
+                     "cores": 1, "route_us": t_route * 1e6,
+                     "sample": (f"reference tensor_softmax + tensor_topk over all {T} tokens; the "
+                                f"expert pipeline on {Es} of {E} experts ({rows_sample} of {T * k} "
+                                f"routed rows, median of {n}), scaled by routed rows")}
+    return out
 
 
 # ----------------------------------------------------------- checkpoint load
@@ -508,8 +695,9 @@ def measured_traffic(steps):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
-    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--steps", type=int, default=3,
+                    help="timed generations (each: 128-token prompt + 256 generated tokens)")
+    ap.add_argument("--warmup", type=int, default=1, help="untimed generations before them")
     ap.add_argument("--no-kernels", action="store_true", help="skip the C1/C3/C4/C5 kernel suite")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--decode-only", action="store_true",
@@ -605,6 +793,7 @@ def main():
         g = bench_decode_gemv(torch, timer, cfg, dec)
         log(f"[gemv] layer GEMV {g['layer_gemv_us_per_launch']:.2f} us/launch "
             f"{g['layer_gemv_GBs']:.0f} GB/s; lm_head {g['lm_head_us']:.1f} us {g['lm_head_GBs']:.0f} GB/s")
+    dec.close()
     kern = {}
     if not args.no_kernels:
         kern = bench_kernels(torch, timer)
@@ -613,25 +802,40 @@ def main():
     if not args.no_cpu:
         try:
             cpu = cpu_baseline(cfg, w)
+            if cpu:
+                log(f"[cpu] config 2: {cpu['value']:.3f} tok/s ({cpu['ms_per_token']:.1f} ms/token)")
+            t0 = time.time()
+            legs = cpu_kernel_baselines()
+            log(f"[cpu] kernel legs in {time.time() - t0:.1f}s: " + json.dumps(legs))
+            for key, leg in legs.items():
+                if key not in kern:
+                    continue
+                if key in ("c3_w8a8", "c4_skinny"):
+                    for sub, v in leg.items():
+                        for tgt in (sub, f"gemv_{sub}", f"w8a8_{sub}"):
+                            if tgt in kern[key]:
+                                kern[key][tgt]["cpu"] = v
+                else:
+                    kern[key]["cpu"] = leg
         except Exception as e:  # the GPU result stands without the baseline
             log(f"[cpu] baseline failed: {e!r}")
-        if cpu:
-            log(f"[cpu] {cpu['value']:.3f} tok/s ({cpu['ms_per_token']:.1f} ms/token)")
 
+    NG = GEN_LEN
     if dall["mode"] == "persistent" or g is None:
         # Dominant kernel = the persistent decode kernel itself: one launch runs
-        # all timed tokens, so bytes per launch = bytes per token x steps.
+        # a generation's 256 tokens, so bytes per launch = bytes per token x 256.
         roof = {
             "bound": "hbm",
-            "kernel": ("decode_loop_kernel (persistent decode: every timed token in one launch)"
-                       if dall["mode"] == "persistent" else "decode step graph (all timed tokens)"),
+            "kernel": ("decode_loop_kernel (persistent decode: one launch per generation's "
+                       f"{NG} tokens)" if dall["mode"] == "persistent"
+                       else "decode step graph (all generated tokens)"),
             "achieved": round(dres["bytes_per_token"] * dres["tok_s"] / 1e9, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dres["hbm_frac"], 4),
-            "traffic": measured_traffic(args.steps) if dall["mode"] == "persistent" else None,
-            "bytes_per_launch": round(dres["bytes_per_token"] * args.steps),
-            "us_per_launch": round(dres["ms_per_token"] * args.steps * 1e3, 1),
+            "traffic": measured_traffic(NG) if dall["mode"] == "persistent" else None,
+            "bytes_per_launch": round(dres["bytes_per_token"] * NG),
+            "us_per_launch": round(dres["decode_ms_per_generation"] * 1e3, 1),
         }
     else:
         achieved = g["layer_gemv_GBs"]
@@ -646,6 +850,7 @@ def main():
             "bytes_per_launch": round(g["layer_gemv_bytes_per_launch"]),
             "us_per_launch": round(g["layer_gemv_us_per_launch"], 3),
         }
+    rnd = lambda d: {k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}  # noqa: E731
     line = {
         "metric": METRIC,
         "value": round(dres["tok_s"], 2),
@@ -653,7 +858,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(dres["ms_per_token"], 4),
+        "ms_per_step": round(dres["wall_ms_per_generation"], 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -661,33 +866,24 @@ def main():
         "data": "synthetic: random-init int8 weights (seed 0), random 128-token prompt",
         "decode_mode": dall["mode"],
         "config": {
-            "workload": "BASELINE config 2: Qwen3-0.6B-shaped int8 greedy decode, batch 1, "
-                        "128-token prompt + 256 generated tokens (steps = generated tokens)",
-            "global_batch": 1, "seq_len": 128 + args.steps, "layers": cfg.n_layers,
+            "workload": (f"BASELINE config 2: Qwen3-0.6B-shaped int8 greedy decode, batch 1; one "
+                         f"step = one generation: {PROMPT_LEN}-token prompt then {NG} generated "
+                         f"tokens; value = generated tokens / decode time (prefill timed apart)"),
+            "global_batch": 1, "prompt_len": PROMPT_LEN, "generated": NG,
+            "seq_len": PROMPT_LEN + NG, "layers": cfg.n_layers,
             "hidden": cfg.hidden, "heads": f"{cfg.n_heads}q/{cfg.n_kv_heads}kv",
             "head_dim": cfg.head_dim, "intermediate": cfg.intermediate, "vocab": cfg.vocab,
             "parallelism": "single GPU",
         },
         "roofline": roof,
-        "cpu_baseline": cpu and {k: (round(v, 4) if isinstance(v, float) else v)
-                                 for k, v in cpu.items()},
-        "decode": {m: ({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
-                       if isinstance(r, dict) else r) for m, r in dall.items()},
+        "cpu_baseline": cpu and rnd(cpu),
+        "decode": {m: (rnd(r) if isinstance(r, dict) else r) for m, r in dall.items()},
         "decode_gemv": g and {k: (round(v, 3) if isinstance(v, float) else v) for k, v in g.items()},
         "kernels": kern,
     }
     print(json.dumps(line), flush=True)
-    if not args.decode_only:
-        # (a decode-only run leaves the decoder to process exit: under a counter
-        # profiler, tearing it down first has crashed the profiler's own exit)
-        dec.close()
     return 0
 
 
 if __name__ == "__main__":
-    # A clean run returns normally instead of raising SystemExit: under
-    # rocprofv3 the SystemExit teardown path has crashed the profiler before
-    # it wrote its results.
-    rc = main()
-    if rc:
-        sys.exit(rc)
+    sys.exit(main())

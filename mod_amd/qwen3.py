@@ -349,6 +349,5 @@ def _main(argv=None) -> int:
 
 
 if __name__ == "__main__":
-    # returns normally (no SystemExit): a counter profiler's exit hook then
-    # writes its results (with sys.exit it has crashed before writing them)
-    _main()
+    import sys
+    sys.exit(_main())

@@ -12,7 +12,7 @@ the decoder's stream split each generation into prefill and decode, and
 config's mean context of 255.5 positions whatever K is). Random-init int8
 weights (no checkpoint is available offline) and random prompt ids; every
 input is resident in HBM before the timed region. The tokens run in the
-persistent decode kernel (one cooperative launch per generation's 256 tokens)
+persistent decode kernel (one launch per generation's 256 tokens)
 when the config supports it; the captured-graph step path is timed on one
 generation and reported next to it.
 

@@ -116,11 +116,19 @@ void free_pinned_memory(void* ptr);
 void tensor_pool_stats(size_t* stats7);
 /* New: hipFree every cached (not live) block. */
 void tensor_empty_cache(void);
+/* New: bytes of op workspaces freed while their stream was capturing a graph
+ * and still held for that graph's replays. begin_capture/end_capture's graph
+ * returns them to the cache when it is replaced; graphs captured by other
+ * means keep them for the life of the process. */
+size_t tensor_pool_graph_bytes(void);
 
 /* ---------------------------------------------------------------------------
  * Drop-in: streams and graphs (probed by hasattr at backend.py:82-87, 139-149;
  * CUDAGraph wrapper backend.py:801-810). One in-order HIP stream per device is
- * the library default; set_current_stream(NULL) restores it.
+ * the library default; set_current_stream(NULL) restores it. destroy_stream
+ * drains the stream and releases the memory cached for it. A workspace an op
+ * frees while its stream captures stays reserved for the captured graph (see
+ * tensor_pool_graph_bytes), so no later tensor can alias it.
  * ------------------------------------------------------------------------- */
 void* create_stream(void);
 void destroy_stream(void* stream);
@@ -281,7 +289,7 @@ void pio_qwen3_destroy(void* dec);
 int pio_qwen3_reset(void* dec, const int32_t* ids, int prompt_len);
 /* Enqueues n decode steps. mode PIO_DECODE_EAGER launches the step kernels,
  * PIO_DECODE_GRAPH replays one captured step graph per token, and
- * PIO_DECODE_PERSISTENT runs all n steps in one cooperative kernel (one
+ * PIO_DECODE_PERSISTENT runs all n steps in one kernel launch (one
  * workgroup per CU; weights stream through LDS while each phase waits for its
  * input). The modes share the KV cache and position, so they can alternate.
  * Persistent mode builds a per-workgroup copy of the weights on first use

@@ -533,13 +533,20 @@ static int enqueue_step(Qwen3Dec* d) {
 
 static size_t al256(size_t b) { return (b + 255) / 256 * 256; }
 
+// Frees the decoder's memory into the cache of its stream. A stream the
+// decoder created is drained first and its cached blocks (the state block and
+// the persistent kernel's weight copy among them) are released with it, so
+// nothing stays cached under a stream that no longer exists.
 static void destroy(Qwen3Dec* d) {
     if (!d) return;
     loop_destroy(d);
     if (d->exec) (void)hipGraphExecDestroy(d->exec);
     if (d->graph) (void)hipGraphDestroy(d->graph);
     if (d->block) device_free(d->block);
-    if (d->own_stream && d->st) (void)hipStreamDestroy(d->st);
+    if (d->own_stream && d->st) {
+        release_stream(d->st);
+        (void)hipStreamDestroy(d->st);
+    }
     delete d;
 }
 

@@ -35,7 +35,7 @@ struct Qwen3Dec {
     LoopState* loop = nullptr;   // persistent-loop resources, built on first use
 };
 
-// Persistent decode loop (decode_loop.hip): one cooperative launch runs
+// Persistent decode loop (decode_loop.hip): one launch (a workgroup per CU) runs
 // n_steps tokens. loop_check() says whether the config fits its kernel.
 int loop_check(const Qwen3Dec* d);
 int loop_run(Qwen3Dec* d, int n_steps);

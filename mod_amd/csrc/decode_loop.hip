@@ -1,7 +1,7 @@
-// Persistent int8 decode loop: one cooperative launch (one workgroup per CU)
-// runs n greedy decode steps of the Qwen3-style decoder, replacing the 143
-// kernel launches per token of the step graph (decode.hip) with in-kernel
-// data flow. Same semantics as the step kernels (reference decode loop:
+// Persistent int8 decode loop: one launch of one workgroup per CU runs n
+// greedy decode steps of the Qwen3-style decoder, replacing the 143 kernel
+// launches per token of the step graph (decode.hip) with in-kernel data flow.
+// Same semantics as the step kernels (reference decode loop:
 // ip/models/qwen3_0_6b/architecture.py:124-221, with the defects listed in
 // decode.hip fixed).
 //
@@ -10,6 +10,15 @@
 // of launch overhead plus a full HBM latency before its first weight arrives.
 // Here the weights of the next phases stream into LDS while the current phase
 // waits for its input, and phases hand data to each other directly.
+//
+// Co-residency. The grid has exactly as many workgroups as the device has
+// CUs, and each workgroup takes 131 KB of a CU's 160 KB of LDS, so on an idle
+// device all of them are resident at once. The kernel needs no grid barrier,
+// only that residency, so it is launched as an ordinary kernel: a cooperative
+// launch would claim the device's global wave-sync resource, which only one
+// process at a time can hold (a second process's cooperative launch fails).
+// If other work holds some CUs, the workgroups waiting for them start when it
+// drains; every wait below is bounded, so the kernel ends in any case.
 //
 // Workgroup = 8 waves:
 //   waves 4-7 ("stream waves") copy this workgroup's weight lines, in the order
@@ -1204,13 +1213,24 @@ struct PhaseShape {
 
 static int seg_lines(const PhaseShape& s, int nblk) { return ceil_div(s.U, nblk) * s.lpu; }
 
+// The kernel's dynamic LDS exceeds the 64 KB default limit.
+static int loop_lds_attr() {
+    PIO_HIP(hipFuncSetAttribute((const void*)decode_loop_kernel<LP_CH, LP_CO, LP_CI>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)LP_LDS_BYTES));
+    return PIO_OK;
+}
+
 int loop_check(const Qwen3Dec* d) {
     const pio_qwen3_config& c = d->c;
-    int dev = 0, cus = 0, coop = 0;
+    int dev = 0, cus = 0, per_cu = 0;
     PIO_HIP(hipGetDevice(&dev));
     PIO_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    PIO_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
-    if (!coop) return set_error(PIO_ERR_UNSUPPORTED, "persistent decode: no cooperative launch");
+    PIO_TRY(loop_lds_attr());
+    PIO_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &per_cu, decode_loop_kernel<LP_CH, LP_CO, LP_CI>, LP_THREADS, LP_LDS_BYTES));
+    if (per_cu < 1)
+        return set_error(PIO_ERR_UNSUPPORTED, "persistent decode: a %d-thread workgroup with %zu B "
+                         "of LDS does not fit a CU", LP_THREADS, LP_LDS_BYTES);
     const int G = c.n_heads / c.n_kv_heads;
     const bool ok = c.head_dim == 128 && c.hidden == LP_CH * 1024 &&
                     c.n_heads * 128 == LP_CO * 1024 && c.intermediate == LP_CI * 1024 && G == LP_G &&
@@ -1351,11 +1371,9 @@ void loop_destroy(Qwen3Dec* d) {
 
 template <int CH, int CO, int CI>
 static int launch_loop(LoopParams& p, hipStream_t st) {
-    const void* k = (const void*)decode_loop_kernel<CH, CO, CI>;
-    PIO_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LP_LDS_BYTES));
-    void* args[] = {&p};
-    PIO_HIP(hipLaunchCooperativeKernel(k, dim3(p.nblk), dim3(LP_THREADS), args, (unsigned)LP_LDS_BYTES,
-                                       st));
+    PIO_TRY(loop_lds_attr());
+    decode_loop_kernel<CH, CO, CI><<<dim3(p.nblk), dim3(LP_THREADS), LP_LDS_BYTES, st>>>(p);
+    PIO_LAUNCHED();
     return PIO_OK;
 }
 

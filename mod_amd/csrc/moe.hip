@@ -282,8 +282,10 @@ static void launch_grouped(const GroupedParams& g, dim3 grid, int nk, hipStream_
 }
 
 // ------------------------------------------------------ swiglu + requant ---
+// silu(g) * u with the deterministic exp (the host oracle evaluates the same
+// operations, so h and its requantized bytes are bit-identical).
 __device__ __forceinline__ float silu_mul(float g, float u) {
-    return g * (1.0f / (1.0f + expf(-g))) * u;
+    return g * (1.0f / (1.0f + exp_det(-g))) * u;
 }
 
 // One pass: a lane keeps its h values in registers (4 consecutive columns per
@@ -357,7 +359,8 @@ __global__ __launch_bounds__(256) void moe_swiglu_quant_kernel(const float* __re
 }
 
 // ---------------------------------------------------------------- combine ---
-// Four consecutive columns per thread (H % 4 == 0), summed in k order.
+// Four consecutive columns per thread (H % 4 == 0), summed in k order with
+// one fused multiply-add per term.
 template <typename OT>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ d,
                                                           const float* __restrict__ topk_w,
@@ -372,10 +375,10 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
         const int pr = t * top_k + kk;
         const float wk = topk_w[pr];
         const float4 v = *(const float4*)(d + (int64_t)pos_of_pair[pr] * H + n);
-        acc[0] += wk * v.x;
-        acc[1] += wk * v.y;
-        acc[2] += wk * v.z;
-        acc[3] += wk * v.w;
+        acc[0] = __builtin_fmaf(wk, v.x, acc[0]);
+        acc[1] = __builtin_fmaf(wk, v.y, acc[1]);
+        acc[2] = __builtin_fmaf(wk, v.z, acc[2]);
+        acc[3] = __builtin_fmaf(wk, v.w, acc[3]);
     }
 #pragma unroll
     for (int e = 0; e < 4; e++) out[(int64_t)t * H + n + e] = from_f32<OT>(acc[e]);

@@ -67,7 +67,14 @@ inline size_t dtype_bytes(int dt) {
 // stream order makes the reuse safe: the new owner's work is queued behind
 // the old owner's last kernel.
 int device_alloc(void** p, size_t bytes, hipStream_t stream = nullptr);
-void device_free(void* p);                  // back to the cache (or no-op for pool memory)
+// Back to the cache (a no-op for pool memory). A block whose stream is
+// capturing is parked with the capture instead: the graph keeps using it.
+void device_free(void* p);
+// Drains `s`, releases the blocks cached for it and retires its cache id; call
+// before destroying a stream the library created.
+void release_stream(hipStream_t s);
+// Id of the capture `s` is recording (0 when it is not capturing).
+unsigned long long capture_id(hipStream_t s);
 
 // Scoped device scratch from the caching allocator, for work queued on `st`;
 // freed when the scope ends, possibly while that work is still running.
@@ -147,5 +154,29 @@ template <> __device__ __forceinline__ float from_f32<float>(float v) { return v
 template <> __device__ __forceinline__ _Float16 from_f32<_Float16>(float v) { return (_Float16)v; }
 
 inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+// e^x by a fixed sequence of IEEE fp32 operations (Cody-Waite reduction by
+// ln2 in two parts, degree-7 Taylor polynomial in Horner form with explicit
+// fmaf, scaling by ldexp), so that the host oracle's identical C function
+// gives the same bits: within 2 ulp of e^x, exact 1 at 0, +inf above the
+// overflow bound, +0 below -103.98, NaN propagated. The MoE SwiGLU uses it
+// where a last-ulp difference of expf between libm and the device library
+// could move a requantized byte.
+__device__ __forceinline__ float exp_det(float x) {
+    if (!(x < 88.72283935546875f)) return x != x ? x : __builtin_inff();
+    if (x < -103.97208f) return 0.0f;
+    const float n = __builtin_rintf(x * 1.44269502162933349609375f);
+    float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+    r = __builtin_fmaf(-n, 1.428606765330187045e-06f, r);
+    float p = 1.98412698e-4f;
+    p = __builtin_fmaf(p, r, 1.38888889e-3f);
+    p = __builtin_fmaf(p, r, 8.33333377e-3f);
+    p = __builtin_fmaf(p, r, 4.16666679e-2f);
+    p = __builtin_fmaf(p, r, 1.66666672e-1f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return __builtin_ldexpf(p, (int)n);
+}
 
 }  // namespace pio

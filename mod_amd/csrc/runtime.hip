@@ -15,6 +15,20 @@
 // was enqueued is then safe to reuse, because the next owner's work queues
 // behind that kernel. (Blocks move between streams only through
 // tensor_empty_cache / an out-of-memory retry, whose hipFree synchronizes.)
+// Streams are known to the cache by a generation id, not by their handle: a
+// destroyed stream's id is retired (its cached blocks are released after the
+// stream drains), so a later stream that receives the same handle value starts
+// with an empty cache.
+//
+// Graph capture. A block freed while its stream is capturing (an op's
+// workspace, freed once its kernels are recorded) is still used by every
+// replay of the graph being built, so it is not cached: it is parked under the
+// capture's id. end_capture hands the parked blocks to the graph it
+// instantiates and returns them to the cache only when that graph is replaced
+// (their stream then orders any new owner after the old replays). Blocks of
+// captures made by other means (the caller's own hipStreamBeginCapture,
+// torch.cuda.graph) stay parked for the life of the process, since the library
+// cannot see when such a graph dies; tensor_pool_graph_bytes() reports them.
 #include "pio_common.hpp"
 
 #include <mutex>
@@ -72,13 +86,20 @@ struct Alloc {
         size_t bytes;        // rounded
         int dev;
         hipStream_t stream;  // the stream whose order protects reuse
+        uint64_t sid;        // that stream's generation id
     };
     std::unordered_map<void*, Live> live;
     std::unordered_map<void*, int> arena_live;                // ptr -> device
-    // (device, rounded bytes, stream) -> cached blocks
-    std::map<std::tuple<int, size_t, hipStream_t>, std::vector<void*>> free_lists;
+    // (device, rounded bytes, stream id) -> cached blocks
+    std::map<std::tuple<int, size_t, uint64_t>, std::vector<void*>> free_lists;
     std::map<int, Arena> arenas;
-    size_t reserved = 0, in_use = 0, cached = 0, peak = 0, n_malloc = 0;
+    std::unordered_map<hipStream_t, uint64_t> stream_ids;     // live streams -> generation id
+    uint64_t next_sid = 1;
+    // blocks freed during a capture, by capture id; and those the library's
+    // own captured graph (begin_capture / end_capture) holds
+    std::map<unsigned long long, std::vector<std::pair<void*, Live>>> parked;
+    std::vector<std::pair<void*, Live>> graph_held;
+    size_t reserved = 0, in_use = 0, cached = 0, peak = 0, n_malloc = 0, held = 0;
 };
 static Alloc& A() {
     static Alloc* a = new Alloc();   // never destroyed: frees after exit are no-ops
@@ -89,6 +110,19 @@ static size_t round_bytes(size_t b) {
     if (b == 0) b = 1;
     const size_t small = 256, big = size_t(2) << 20;
     return b <= (size_t(1) << 20) ? (b + small - 1) / small * small : (b + big - 1) / big * big;
+}
+
+static uint64_t stream_id_locked(Alloc& a, hipStream_t s) {
+    auto it = a.stream_ids.find(s);
+    if (it != a.stream_ids.end()) return it->second;
+    const uint64_t id = a.next_sid++;
+    a.stream_ids[s] = id;
+    return id;
+}
+
+static void cache_block_locked(Alloc& a, void* p, const Alloc::Live& l) {
+    a.cached += l.bytes;
+    a.free_lists[std::make_tuple(l.dev, l.bytes, l.sid)].push_back(p);
 }
 
 static void empty_cache_locked(Alloc& a) {
@@ -125,7 +159,8 @@ int device_alloc(void** out, size_t bytes, hipStream_t stream) {
             return PIO_OK;
         }
     }
-    auto fit = a.free_lists.find(std::make_tuple(dev, r, stream));
+    const uint64_t sid = stream_id_locked(a, stream);
+    auto fit = a.free_lists.find(std::make_tuple(dev, r, sid));
     if (fit != a.free_lists.end() && !fit->second.empty()) {
         *out = fit->second.back();
         fit->second.pop_back();
@@ -147,7 +182,7 @@ int device_alloc(void** out, size_t bytes, hipStream_t stream) {
         a.n_malloc++;
         *out = p;
     }
-    a.live[*out] = {r, dev, stream};
+    a.live[*out] = {r, dev, stream, sid};
     a.in_use += r;
     if (a.in_use > a.peak) a.peak = a.in_use;
     return PIO_OK;
@@ -163,8 +198,75 @@ void device_free(void* p) {
     const Alloc::Live l = it->second;
     a.live.erase(it);
     a.in_use -= l.bytes;
-    a.cached += l.bytes;
-    a.free_lists[std::make_tuple(l.dev, l.bytes, l.stream)].push_back(p);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    unsigned long long cid = 0;
+    if (a.stream_ids.count(l.stream) && a.stream_ids[l.stream] == l.sid &&
+        hipStreamGetCaptureInfo(l.stream, &cs, &cid) == hipSuccess &&
+        cs != hipStreamCaptureStatusNone) {
+        // recorded into a graph that is still being built: keep it out of reach
+        a.parked[cid].emplace_back(p, l);
+        a.held += l.bytes;
+        return;
+    }
+    (void)hipGetLastError();
+    cache_block_locked(a, p, l);
+}
+
+unsigned long long capture_id(hipStream_t s) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    unsigned long long cid = 0;
+    if (hipStreamGetCaptureInfo(s, &cs, &cid) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return cs == hipStreamCaptureStatusNone ? 0 : cid;
+}
+
+// end_capture's hand-over: the blocks parked under capture `cid` now belong to
+// the library's graph; the ones the replaced graph held return to the cache.
+static void graph_replaced(unsigned long long cid) {
+    Alloc& a = A();
+    std::lock_guard<std::mutex> lk(a.mu);
+    for (auto& pl : a.graph_held) {
+        a.held -= pl.second.bytes;
+        cache_block_locked(a, pl.first, pl.second);
+    }
+    a.graph_held.clear();
+    auto it = cid ? a.parked.find(cid) : a.parked.end();
+    if (it != a.parked.end()) {
+        a.graph_held = std::move(it->second);
+        a.parked.erase(it);
+    }
+}
+
+// Before a stream is destroyed: drain it, release the blocks cached for it and
+// retire its id (blocks still live keep the old id and are only reclaimed by
+// tensor_empty_cache or an out-of-memory retry once freed).
+void release_stream(hipStream_t s) {
+    if (!s) return;
+    (void)hipStreamSynchronize(s);
+    Alloc& a = A();
+    std::lock_guard<std::mutex> lk(a.mu);
+    auto it = a.stream_ids.find(s);
+    if (it == a.stream_ids.end()) return;
+    const uint64_t sid = it->second;
+    a.stream_ids.erase(it);
+    int cur = 0;
+    (void)hipGetDevice(&cur);
+    for (auto f = a.free_lists.begin(); f != a.free_lists.end();) {
+        if (std::get<2>(f->first) != sid) {
+            ++f;
+            continue;
+        }
+        (void)hipSetDevice(std::get<0>(f->first));
+        for (void* p : f->second) {
+            (void)hipFree(p);
+            a.reserved -= std::get<1>(f->first);
+            a.cached -= std::get<1>(f->first);
+        }
+        f = a.free_lists.erase(f);
+    }
+    (void)hipSetDevice(cur);
 }
 
 // ------------------------------------------------------ tensor metadata ---
@@ -462,6 +564,12 @@ PIO_EXPORT void tensor_pool_stats(size_t* s) {
     s[6] = it == a.arenas.end() ? 0 : it->second.used;
 }
 
+PIO_EXPORT size_t tensor_pool_graph_bytes(void) {
+    Alloc& a = A();
+    std::lock_guard<std::mutex> lk(a.mu);
+    return a.held;
+}
+
 PIO_EXPORT void tensor_empty_cache(void) {
     Alloc& a = A();
     std::lock_guard<std::mutex> lk(a.mu);
@@ -496,6 +604,7 @@ PIO_EXPORT void destroy_stream(void* s) {
         std::lock_guard<std::mutex> lk(g_mu);
         if (g_user_stream == (hipStream_t)s) g_user_stream = nullptr;
     }
+    release_stream((hipStream_t)s);
     (void)hipStreamDestroy((hipStream_t)s);
 }
 PIO_EXPORT void stream_synchronize(void* s) {
@@ -522,6 +631,7 @@ PIO_EXPORT void begin_capture(void) {
 }
 PIO_EXPORT void end_capture(void) {
     if (!g_capture_stream) return;
+    const unsigned long long cid = capture_id(g_capture_stream);
     if (g_graph_exec) {
         (void)hipGraphExecDestroy(g_graph_exec);
         g_graph_exec = nullptr;
@@ -532,8 +642,10 @@ PIO_EXPORT void end_capture(void) {
     }
     if (hipStreamEndCapture(g_capture_stream, &g_graph) != hipSuccess) {
         set_error(PIO_ERR_HIP, "end_capture failed");
+        graph_replaced(0);
         return;
     }
+    graph_replaced(cid);
     if (hipGraphInstantiate(&g_graph_exec, g_graph, nullptr, nullptr, 0) != hipSuccess)
         set_error(PIO_ERR_HIP, "hipGraphInstantiate failed");
 }

@@ -61,6 +61,7 @@ SIGNATURES: dict[str, tuple] = {
     "free_pinned_memory": (None, [_vp]),
     "tensor_pool_stats": (None, [ctypes.POINTER(ctypes.c_size_t)]),
     "tensor_empty_cache": (None, []),
+    "tensor_pool_graph_bytes": (_sz, []),
     "create_stream": (_vp, []),
     "destroy_stream": (None, [_vp]),
     "stream_synchronize": (None, [_vp]),

@@ -6,7 +6,7 @@ Three ways to run steps, sharing one KV cache and position:
   "eager"       the step's kernels launched one by one,
   "graph"       one device-driven step captured once as a HIP graph and
                 replayed per token,
-  "persistent"  every step of the call in one cooperative kernel (Qwen3-0.6B
+  "persistent"  every step of the call in one kernel launch (Qwen3-0.6B
                 layer shape only; see ``persistent_supported``).
 Replaces Qwen3ForCausalLM.generate (ip/models/qwen3_0_6b/architecture.py:
 183-221), whose loop makes ~30 ctypes calls and allocations per layer per token.

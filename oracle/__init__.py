@@ -84,6 +84,9 @@ def lib() -> ctypes.CDLL:
         L.ref_moe_group.argtypes = [_c_i32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_i32p,
                                     _c_i32p, _c_i32p]
         L.ref_num_threads.restype = ctypes.c_int
+        L.ref_exp_det.restype = ctypes.c_float
+        L.ref_exp_det.argtypes = [ctypes.c_float]
+        L.ref_exp_det_array.argtypes = [_c_f32p, _c_f32p, ctypes.c_int64]
     return _lib
 
 
@@ -102,6 +105,15 @@ def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     out = np.empty(x.shape, dtype=np.uint16)
     lib().ref_f32_to_f16_array(_p(x, _c_f32p), _p(out, _c_u16p), x.size)
+    return out
+
+
+def exp_det(x: np.ndarray) -> np.ndarray:
+    """The deterministic fp32 e^x of the MoE SwiGLU (int8_ref.c ref_exp_det).
+    Pinned against float64 exp (<= 2 ulp) and special values."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().ref_exp_det_array(_p(x, _c_f32p), _p(out, _c_f32p), x.size)
     return out
 
 

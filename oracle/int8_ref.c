@@ -254,9 +254,36 @@ void ref_moe_route(const float* logits, int T, int E, int k, int renorm, float* 
     free(p);
 }
 
-/* tensor_ops.c:588-604 (tensor_fused_gate_up_swiglu): h = g*(1/(1+expf(-g)))*u
- * for the halves [g | u] of one gate_up row. */
-static inline float silu_mul(float g, float u) { return g * (1.0f / (1.0f + expf(-g))) * u; }
+/* e^x as a fixed sequence of fp32 operations (Cody-Waite reduction by ln2 in
+ * two parts, degree-7 Taylor polynomial, Horner with explicit fmaf, ldexpf),
+ * the same steps as the GPU's exp_det, so both give the same bits. Pinned in
+ * tests against float64 exp (<= 2 ulp) and special values. */
+float ref_exp_det(float x) {
+    if (!(x < 88.72283935546875f)) return x != x ? x : INFINITY;
+    if (x < -103.97208f) return 0.0f;
+    const float n = rintf(x * 1.44269502162933349609375f);
+    float r = fmaf(-n, 0.693145751953125f, x);
+    r = fmaf(-n, 1.428606765330187045e-06f, r);
+    float p = 1.98412698e-4f;
+    p = fmaf(p, r, 1.38888889e-3f);
+    p = fmaf(p, r, 8.33333377e-3f);
+    p = fmaf(p, r, 4.16666679e-2f);
+    p = fmaf(p, r, 1.66666672e-1f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return ldexpf(p, (int)n);
+}
+void ref_exp_det_array(const float* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) y[i] = ref_exp_det(x[i]);
+}
+
+/* tensor_ops.c:588-604 (tensor_fused_gate_up_swiglu): h = g*(1/(1+exp(-g)))*u
+ * for the halves [g | u] of one gate_up row, with the reference's expf
+ * replaced by ref_exp_det (same value to 2 ulp; bit-reproducible on the GPU). */
+static inline float silu_mul(float g, float u) {
+    return g * (1.0f / (1.0f + ref_exp_det(-g))) * u;
+}
 
 /* --------------------------------------------------- MoE layer (a9/a10) --- */
 /* For every token t and slot kk (expert e = id[t,kk], weight w[t,kk]):
@@ -264,7 +291,8 @@ static inline float silu_mul(float g, float u) { return g * (1.0f / (1.0f + expf
  *   h   = silu(gu[:I]) * gu[I:]                                      (fp32, [I])
  *   q_h, s_h = per-token quantization of h
  *   d   = float(int32(q_h . W_down[e]^T)) * s_h * s_down[e]          (fp32, [H])
- *   out[t] = sum over kk = 0..k-1, in order, of w[t,kk] * d          (fp32)
+ *   out[t] = sum over kk = 0..k-1, in order, of w[t,kk] * d          (fp32,
+ *            one fmaf per term)
  * q_x, s_x = per-token quantization of x. The reference's own combine
  * (model.py:348, elementwise tensor_mul of [n,H] by [n,1]) reads out of bounds
  * and scatter-adds atomically, so this deterministic definition replaces it. */
@@ -305,7 +333,7 @@ void ref_moe_w8a8(const void* x, int x_f16, const float* logits, const int8_t* w
                 const float wt = tw[(int64_t)t * k + kk];
                 for (int n = 0; n < H; n++) {
                     d[n] = (float)acc[n] * sh * sd[n];
-                    o[n] = o[n] + wt * d[n];
+                    o[n] = fmaf(wt, d[n], o[n]);
                 }
             }
             for (int n = 0; n < H; n++) store_out(out, out_f16, (int64_t)t * H + n, o[n]);

@@ -105,6 +105,50 @@ class Qwen3Ref:
         return logits
 
 
+def forward_all(cfg: Qwen3Config, w: dict, ids, want, dtype=np.float64) -> np.ndarray:
+    """Teacher-forced logits of a whole id sequence in one batched pass:
+    position i sees ids[0..i] (causal attention), exactly the computation of
+    Qwen3Ref.step at every position, done as matrix products over all
+    positions at once. Returns the logits of the positions in `want`
+    ([len(want), vocab]); pinned against step() in the oracle tests."""
+    c, dt = cfg, dtype
+    H, D, nq, nkv, I = c.hidden, c.head_dim, c.n_heads, c.n_kv_heads, c.intermediate
+    ids = np.asarray(ids)
+    T = len(ids)
+    cos, sin = rope_tables(c, dt)
+    cos, sin = cos[:T][:, None, :], sin[:T][:, None, :]
+    causal = np.triu(np.ones((T, T), bool), 1)
+
+    def lin(x, W, s, b):
+        y = (x @ W.astype(dt).T) * s.astype(dt)
+        return y if b is None else y + b.astype(dt)
+
+    def rms(x, g):
+        return x * (1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + c.rms_eps)) * g.astype(dt)
+
+    x = w["embed"][ids].astype(dt)
+    grp = nq // nkv
+    for Lw in w["layers"]:
+        qkv = lin(rms(x, Lw["in_norm"]), Lw["w_qkv"], Lw["s_qkv"], Lw.get("b_qkv"))
+        q = _rope(qkv[:, : nq * D].reshape(T, nq, D), cos, sin)
+        k = _rope(qkv[:, nq * D: (nq + nkv) * D].reshape(T, nkv, D), cos, sin)
+        v = qkv[:, (nq + nkv) * D:].reshape(T, nkv, D)
+        out = np.empty((T, nq, D), dt)
+        for hh in range(nq):
+            kv = hh // grp
+            sc = (q[:, hh, :] @ k[:, kv, :].T) / np.sqrt(D)
+            sc[causal] = -np.inf
+            p = np.exp(sc - sc.max(axis=1, keepdims=True))
+            p = p / p.sum(axis=1, keepdims=True)
+            out[:, hh, :] = p @ v[:, kv, :]
+        x = x + lin(out.reshape(T, nq * D), Lw["w_o"], Lw["s_o"], None)
+        gu = lin(rms(x, Lw["post_norm"]), Lw["w_gu"], Lw["s_gu"], None)
+        g, u = gu[:, :I], gu[:, I:]
+        x = x + lin(g / (1.0 + np.exp(-g)) * u, Lw["w_down"], Lw["s_down"], None)
+    h = rms(x[np.asarray(want)], w["final_norm"])
+    return lin(h, w["lm_head"], w["s_lm_head"], None)
+
+
 def greedy(cfg: Qwen3Config, w: dict, prompt, n_new: int, dtype=np.float64):
     """Greedy decode: returns (ids, logits of every step)."""
     ref = Qwen3Ref(cfg, w, dtype)

@@ -1,5 +1,5 @@
 """GPU parity of the persistent decode loop (pio_qwen3_run with
-PIO_DECODE_PERSISTENT): all steps of a call run in one cooperative kernel that
+PIO_DECODE_PERSISTENT): all steps of a call run in one kernel launch that
 hands data between workgroups through tagged words instead of kernel launches.
 
 Same bar as the step-kernel decoder (test_gpu_decode.py): teacher-forced logits
@@ -133,6 +133,68 @@ def test_persistent_c2_shape(torch_dev):
     match = float(np.mean(a == b))
     _say(f"persistent vs graph greedy token match {match:.2f}")
     assert match >= 0.9
+
+
+def _check_against_batched_oracle(got, ids, pos, rcfg, w, what):
+    """got[i] = GPU logits after position pos[i] of the id sequence `ids`
+    (teacher forcing on the GPU's own tokens): the bar of _check_logits, with
+    the oracle evaluated in one batched pass (float64, and numpy float32 for
+    the fp32 error scale)."""
+    from tests.test_gpu_decode import _check_argmax
+    seq = ids[:max(pos) + 1]
+    e64 = qwen3_ref.forward_all(rcfg, w, seq, pos, np.float64)
+    e32 = qwen3_ref.forward_all(rcfg, w, seq, pos, np.float32).astype(np.float64)
+    worst = 0.0
+    for i, p in enumerate(pos):
+        rms = float(np.sqrt(np.mean(e64[i] * e64[i])))
+        err = float(np.abs(got[i] - e64[i]).max()) / rms
+        err32 = float(np.abs(e32[i] - e64[i]).max()) / rms
+        worst = max(worst, err)
+        _say(f"{what}: position {p}: err {err:.2e} (numpy fp32 {err32:.2e})")
+        assert err <= max(1e-4, 4 * err32), (what, p, err, err32)
+        _check_argmax(got[i:i + 1], e64[i:i + 1], 1e-3)
+    _say(f"{what}: worst logit err {worst:.2e} x rms")
+
+
+def test_persistent_c2_full_generation_vs_oracle(torch_dev):
+    """BASELINE config 2 end to end: 28 layers, vocab 151936, a 128-token
+    prompt and 256 greedy tokens (KV to 384 positions). The generation runs in
+    chunks (1, 7 x 32, 31 tokens) so the logits of the first generated token,
+    of every 32nd after it and of the last are read; they must meet the
+    teacher-forced bar against the oracle on the GPU's own ids, the GPU's
+    argmax at each of them must be the id it then generated, and the chunked
+    run must produce the same 384 ids as one launch."""
+    from mod_amd.qwen3 import Qwen3Config, Qwen3Int8Decoder, random_weights
+    P, NG = 128, 256
+    cfg = Qwen3Config(max_seq=P + NG)
+    rcfg = qwen3_ref.Qwen3Config(max_seq=P + NG)
+    _say("C2 full generation: building weights")
+    w = random_weights(cfg, seed=0)
+    dec = Qwen3Int8Decoder(cfg, w)
+    if not dec.persistent_supported():
+        from mod_amd import ops
+        pytest.fail(f"persistent mode unsupported: {ops.last_error()}")
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab, size=P).astype(np.int32)
+    _say("C2 full generation: chunked")
+    dec.reset(prompt)
+    dec.run(P - 1, mode="persistent")
+    pos, logits, done = [], [], 0
+    for n in [1] + [32] * 7 + [31]:
+        dec.run(n, mode="persistent")
+        done += n
+        pos.append(P - 2 + done)          # the position the chunk's last step ran
+        logits.append(dec.read(0, with_logits=True)[1].copy())
+    assert done == NG
+    ids = dec.read(P + NG)
+    assert np.array_equal(ids[:P], prompt)
+    for p, lg in zip(pos, logits):
+        assert int(np.argmax(lg)) == int(ids[p + 1]), p
+    _say("C2 full generation: one launch")
+    dec.reset(prompt)
+    dec.run(P - 1 + NG, mode="persistent")
+    assert np.array_equal(dec.read(P + NG), ids)
+    _say("C2 full generation: oracle (batched, teacher forced)")
+    _check_against_batched_oracle(np.stack(logits), ids, pos, rcfg, w, "C2 full generation")
 
 
 def test_persistent_rejects_other_shapes(torch_dev):

@@ -125,8 +125,11 @@ def test_gemv_mfma_fp16(env, M, N, K, ydt, bias):
 
 @pytest.mark.parametrize("M,N,K,xdt", [
     (1, 151936, 1024, np.float16),   # lm_head-sized N: many row groups per wave
-    (5, 20000, 4096, np.float16),    # 4 + 1 x rows
+    (5, 20000, 4096, np.float16),    # fp16 x at 2 <= M <= 64: the MFMA GEMV
     (1, 50001, 3072, np.float32),    # 4-row groups, ragged last group
+    (5, 20000, 4096, np.float32),    # stream kernel: a 4-x-row launch, then 1 row
+    (2, 4096, 12288, np.float32),    # stream kernel: one 2-x-row launch
+    (9, 12288, 4096, np.float32),    # stream kernel: 4 + 4 + 1 x rows
 ])
 def test_gemv_many_row_groups(env, M, N, K, xdt):
     """Large N: every persistent wave walks many row groups; every output must
@@ -140,6 +143,29 @@ def test_gemv_many_row_groups(env, M, N, K, xdt):
     got = host(y)
     assert np.isfinite(got).all(), "an output row was never written"
     assert_rel(got, oracle.gemv_w8(x, W, s), 1e-2 if xdt == np.float16 else 1e-3, "gemv many groups")
+
+
+@pytest.mark.parametrize("N,K", [(12288, 4096), (4096, 12288), (151936, 4096)])
+def test_gemv_stream_fp16_in_out(env, N, K):
+    """The fp16-in / fp16-out stream GEMV at M = 1 (the
+    Qwen3-8B linears and lm_head), against the oracle at the fp16 bar. For the
+    lm_head the oracle runs on a subset of rows (first, last and 4096 random
+    ones): each output row depends only on its weight row."""
+    torch, ops, d = env
+    M = 1
+    _say(f"gemv fp16 stream M=1 N={N} K={K}")
+    x, W, s = _inputs(N + 3 * K, M, N, K, np.float16)
+    y = torch.full((M, N), float("nan"), dtype=torch.float16, device=d)
+    ops.gemv_w8(dev(torch, x, d), dev(torch, W, d), dev(torch, s, d), None, y, M, N, K)
+    sync(torch)
+    got = host(y).astype(np.float64)
+    assert np.isfinite(got).all(), "an output row was never written"
+    if N > 20000:
+        rows = np.unique(np.concatenate([[0, 1, N - 1],
+                                         np.random.default_rng(5).integers(0, N, 4096)]))
+        W, s, got = W[rows], s[rows], got[:, rows]
+    ref = oracle.gemv_w8(x, W, s, out_dtype=np.float16).astype(np.float64)
+    assert_rel(got, ref, 1e-2, "gemv fp16 stream")
 
 
 def test_gemv_repeated_launches_identical(env):
@@ -455,9 +481,12 @@ def test_moe_layer_matches_oracle(env, T, H, I, E, k, xdt):
                  dev(torch, wd, d), dev(torch, sd, d), out, T, H, I, E, k, False)
     sync(torch)
     ref = oracle.moe_w8a8(x, lg, wgu, sgu, wd, sd, k)
-    # silu's expf differs by ulps between libm and the GPU, which can move a
-    # requantized byte by one; the fp16-level bar covers that.
-    assert_rel(host(out), ref, 1e-2, "moe")
+    # quantized x, the expert GEMMs' int32 sums, SwiGLU (deterministic exp)
+    # and the requantized h are bit-identical to the oracle's (a flipped byte
+    # would show as ~1e-3); what remains is the router's expf (libm vs device
+    # library, last ulp of a routing weight), amplified where the k-sum
+    # cancels (observed up to 1.7e-5 at the 1e-2 * rms floor)
+    assert_rel(host(out), ref, 1e-4, "moe")
 
 
 def test_moe_tiny_golden(env):
@@ -471,7 +500,7 @@ def test_moe_tiny_golden(env):
                  dev(torch, g["s_gu"], d), dev(torch, g["w_down"], d), dev(torch, g["s_down"], d),
                  out, T, H, I2 // 2, E, 2, False)
     sync(torch)
-    assert_rel(host(out), g["y"], 1e-2, "moe golden")
+    assert_rel(host(out), g["y"], 1e-4, "moe golden")
 
 
 def test_skinny_paths_full_size_properties(env):

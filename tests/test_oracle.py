@@ -294,6 +294,30 @@ def test_group_bruteforce():
             assert rows[p] == t and off[ids[t, kk]] <= p < off[ids[t, kk] + 1]
 
 
+def test_exp_det_against_float64_exp():
+    """The MoE SwiGLU's deterministic e^x: within 1 ulp of float64 exp over the
+    whole finite range (dense sweep plus random points), and its special
+    cases: exact 1 at 0, +inf past the overflow bound and for +inf, +0 below
+    -103.98 and for -inf, NaN in, NaN out."""
+    rng = np.random.default_rng(0)
+    x = np.concatenate([np.linspace(-103.9, 88.72, 2_000_001, dtype=np.float32),
+                        (rng.standard_normal(1_000_000) * 20).astype(np.float32),
+                        np.float32([-1e-8, 1e-8, -0.5, 0.5, 1.0, -1.0, 0.34657359, -0.34657359])])
+    x = x[(x > -103.9) & (x < 88.72)]
+    y = oracle.exp_det(x).astype(np.float64)
+    ref = np.exp(x.astype(np.float64))
+    normal = ref > np.finfo(np.float32).tiny
+    ulp = np.abs(y[normal] - ref[normal]) / np.spacing(ref[normal].astype(np.float32))
+    assert ulp.max() <= 1.0, ulp.max()
+    sub = ~normal   # subnormal results: within one subnormal step
+    assert np.all(np.abs(y[sub] - ref[sub]) <= np.float64(2.0 ** -149))
+    sp = oracle.exp_det(np.float32([0.0, -0.0, 88.73, 1e30, np.inf, -104.0, -1e30, -np.inf, np.nan]))
+    assert sp[0] == 1.0 and sp[1] == 1.0
+    assert np.all(np.isposinf(sp[2:5]))
+    assert np.all(sp[5:8] == 0.0) and not np.any(np.signbit(sp[5:8]))
+    assert np.isnan(sp[8])
+
+
 def _numpy_moe(x, logits, wgu, sgu, wd, sd, k, renorm=False):
     """Independent numpy composition of the MoE definition (float64 epilogues
     rounded to fp32 at the same points as the definition)."""
@@ -423,3 +447,23 @@ def test_decoder_oracle_pin_resolves_a_rope_slip(monkeypatch):
     ours, hf = _qwen2_logits_and_oracle()
     err = np.abs(ours - hf).max() / np.sqrt(np.mean(hf * hf))
     assert err > 1e-2, err
+
+
+def test_decoder_oracle_batched_forward_equals_steps():
+    """qwen3_ref.forward_all (every position at once, causal mask) computes
+    what Qwen3Ref.step computes position by position: float64 logits agree to
+    1e-12 of their rms at every position, GQA (4 query heads on 2 KV heads)
+    and the qkv bias included."""
+    import oracle.qwen3_ref as q3
+    from mod_amd.qwen3 import random_weights, Qwen3Config
+    kw = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=128, intermediate=512,
+              vocab=500, max_seq=64)
+    w = random_weights(Qwen3Config(**kw), seed=9)
+    cfg = q3.Qwen3Config(**kw)
+    ids = np.random.default_rng(10).integers(0, cfg.vocab, 40)
+    ref = q3.Qwen3Ref(cfg, w, np.float64)
+    steps = np.stack([ref.step(int(t)) for t in ids])
+    want = [0, 1, 17, 39]
+    got = q3.forward_all(cfg, w, ids, want)
+    err = np.abs(got - steps[want]).max() / np.sqrt(np.mean(steps * steps))
+    assert err < 1e-12, err

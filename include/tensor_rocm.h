@@ -226,6 +226,19 @@ int pio_quantize_per_token(const void* x, int x_dtype, int8_t* q, float* s, int 
 int pio_gemm_w8a8(const int8_t* q, const float* s_a, const int8_t* w, const float* s_w,
                   const float* bias, void* y, int y_dtype, int M, int N, int K, void* stream);
 
+/* No counterpart in the reference. pio_gemm_w8a8 for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): the same kernels and bit-identical
+ * results, with the K-slice int32 partials kept in the library's per-GPU
+ * static scratch array (16 MiB, held until the process ends) instead of
+ * allocator memory. It calls no hipMalloc/hipFree. Shapes whose plan needs
+ * more than 16 MiB of partials (splits x M x N x 4 B) are refused with an
+ * error. Every call on a GPU shares that GPU's array: calls that overlap on
+ * one GPU (different streams, no ordering between them) race. */
+int pio_gemm_w8a8_static(const int8_t* q, const float* s_a, const int8_t* w, const float* s_w,
+                         const float* bias, void* y, int y_dtype, int M, int N, int K,
+                         void* stream);
+
 /* tensor_matmul_int8 semantics on raw pointers (B is [K,N]); `out_i32` != 0
  * writes int32 instead of fp32. `workspace` needs pio_matmul_int8_workspace()
  * bytes (B is repacked to [N,K] there). */

@@ -9,6 +9,7 @@
 #include "gemm_core.hpp"
 
 #include <stdlib.h>
+#include <mutex>
 
 namespace pio {
 
@@ -533,8 +534,30 @@ static int launch_split_tiles(const GemmParams& p, int splits, hipStream_t st) {
 
 static int splitk_reduce(const int32_t* w, int splits, const GemmParams& p0, int out_mode, hipStream_t st);
 
-static int launch_splitk(const GemmParams& p0, int out_mode, const SplitPlan& sp, hipStream_t st) {
-    Scratch ws;
+// Workspace of one GEMM call: the caller's buffer when it brings one (`ext`,
+// `cap` bytes), else a block from the caching allocator for the call's scope.
+struct GemmWs {
+    void* ext = nullptr;
+    size_t cap = 0;
+    const char* ext_name = "";
+    Scratch own;
+    void* ptr = nullptr;
+    int get(size_t bytes, hipStream_t st) {
+        if (!ext) {
+            PIO_TRY(own.get(bytes, st));
+            ptr = own.ptr;
+            return PIO_OK;
+        }
+        if (bytes > cap)
+            return set_error(PIO_ERR_INVALID, "%s: this shape's plan needs %zu B of workspace, "
+                             "more than the %zu B it has", ext_name, bytes, cap);
+        ptr = ext;
+        return PIO_OK;
+    }
+};
+
+static int launch_splitk(const GemmParams& p0, int out_mode, const SplitPlan& sp, GemmWs& ws,
+                         hipStream_t st) {
     PIO_TRY(ws.get((size_t)sp.splits * p0.M * p0.N * sizeof(int32_t), st));
     GemmParams p = p0;
     p.a_batch = p.b_batch = p0.K / sp.splits;   // slice z starts at column z*Kc
@@ -574,14 +597,14 @@ static int splitk_reduce(const int32_t* w, int splits, const GemmParams& p0, int
 }
 
 // Skinny product: one pass, or K slices into int32 partials plus the reduce.
-static int launch_skinny(const GemmParams& p0, int out_mode, const SkinnyPlan& sp, hipStream_t st) {
+static int launch_skinny(const GemmParams& p0, int out_mode, const SkinnyPlan& sp, GemmWs& ws,
+                         hipStream_t st) {
     GemmParams p = p0;
     p.K = p0.K / sp.splits;
     if (sp.splits == 1) {
         p.c_batch = 0;
         return launch_skinny_one(p, out_mode, sp, st);
     }
-    Scratch ws;
     PIO_TRY(ws.get((size_t)sp.splits * p0.M * p0.N * sizeof(int32_t), st));
     p.C = ws.ptr;
     p.ldc = p0.N;
@@ -590,8 +613,12 @@ static int launch_skinny(const GemmParams& p0, int out_mode, const SkinnyPlan& s
     return splitk_reduce((const int32_t*)ws.ptr, sp.splits, p0, out_mode, st);
 }
 
-int gemm_w8a8(const int8_t* q, const float* s_a, const int8_t* w, const float* s_w,
-              const float* bias, void* y, int y_dtype, int M, int N, int K, hipStream_t st) {
+// The W8A8 product with its workspace from `ws_ext` (`ws_cap` bytes) when
+// given, else from the caching allocator; the plan (and so every output bit)
+// is the same either way.
+static int gemm_w8a8_ws(const int8_t* q, const float* s_a, const int8_t* w, const float* s_w,
+                        const float* bias, void* y, int y_dtype, int M, int N, int K,
+                        void* ws_ext, size_t ws_cap, const char* ws_name, hipStream_t st) {
     PIO_REQUIRE(q && w && y, "gemm_w8a8: null pointer");
     PIO_REQUIRE(M >= 0 && N >= 0 && K >= 0, "gemm_w8a8: negative shape");
     PIO_REQUIRE(K % 16 == 0, "gemm_w8a8: K=%d must be a multiple of 16", K);
@@ -609,11 +636,48 @@ int gemm_w8a8(const int8_t* q, const float* s_a, const int8_t* w, const float* s
     p.s_a = s_a; p.s_w = s_w; p.bias = bias;
     p.C = y; p.ldc = N;
     p.M = M; p.N = N; p.K = K;
+    GemmWs ws;
+    ws.ext = ws_ext;
+    ws.cap = ws_cap;
+    ws.ext_name = ws_name;
     const SkinnyPlan kp = plan_skinny(p);
-    if (kp.wv) return launch_skinny(p, mode, kp, st);
+    if (kp.wv) return launch_skinny(p, mode, kp, ws, st);
     const SplitPlan sp = plan_split(p, 256);
-    if (sp.splits > 1) return launch_splitk(p, mode, sp, st);
+    if (sp.splits > 1) return launch_splitk(p, mode, sp, ws, st);
     return launch_dense(p, mode, 1, st);
+}
+
+int gemm_w8a8(const int8_t* q, const float* s_a, const int8_t* w, const float* s_w,
+              const float* bias, void* y, int y_dtype, int M, int N, int K, hipStream_t st) {
+    return gemm_w8a8_ws(q, s_a, w, s_w, bias, y, y_dtype, M, N, K, nullptr, 0, "", st);
+}
+
+// ---- the allocation-free variant ------------------------------------------
+// Workspace of pio_gemm_w8a8_static: one array per GPU, loaded with this code
+// object and held until the process ends. Host code uses the device address
+// that hipGetSymbolAddress returns for it (per device), never the name.
+constexpr size_t STATIC_SCRATCH_BYTES = size_t(16) << 20;
+static __device__ __align__(256) char scratch[STATIC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[MAX_DEVICES];
+
+// Device address of this GPU's scratch array (looked up on the first call on
+// each device, with that device current).
+static int static_scratch(void** out) {
+    int dev = 0;
+    PIO_HIP(hipGetDevice(&dev));
+    PIO_REQUIRE(dev >= 0 && dev < MAX_DEVICES, "gemm_w8a8_static: device %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        PIO_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        PIO_REQUIRE(ptr, "gemm_w8a8_static: no device address for the scratch array");
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return PIO_OK;
 }
 
 // [K,N] -> [N,K] int8 transpose through a 64x64 LDS tile (per batch z).
@@ -648,6 +712,19 @@ PIO_EXPORT int pio_gemm_w8a8(const int8_t* q, const float* s_a, const int8_t* w,
                              const float* bias, void* y, int y_dtype, int M, int N, int K,
                              void* stream) {
     return gemm_w8a8(q, s_a, w, s_w, bias, y, y_dtype, M, N, K, pick_stream(stream));
+}
+
+// pio_gemm_w8a8 without any allocation: the K-slice partials live in the
+// library's per-GPU static scratch array (16 MiB). Same kernels, same bits.
+// Calls that overlap on one GPU (different streams) share that array and race.
+PIO_EXPORT int pio_gemm_w8a8_static(const int8_t* q, const float* s_a, const int8_t* w,
+                                    const float* s_w, const float* bias, void* y, int y_dtype,
+                                    int M, int N, int K, void* stream) {
+    void* ptr = nullptr;
+    PIO_TRY(static_scratch(&ptr));
+    return gemm_w8a8_ws(q, s_a, w, s_w, bias, y, y_dtype, M, N, K, ptr, STATIC_SCRATCH_BYTES,
+                        "pio_gemm_w8a8_static (static scratch; pio_gemm_w8a8 serves larger shapes)",
+                        pick_stream(stream));
 }
 
 // Workspace: B repacked to [batch][N][Kp] (Kp = K rounded up to 16, zero

@@ -90,6 +90,7 @@ SIGNATURES: dict[str, tuple] = {
     "pio_gemv_w8": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "pio_quantize_per_token": (_i, [_vp, _i, _vp, _vp, _i, _i, _vp]),
     "pio_gemm_w8a8": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "pio_gemm_w8a8_static": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "pio_matmul_int8_workspace": (_sz, [_i, _i, _i, _i]),
     "pio_matmul_int8": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp]),
     "pio_moe_route": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),

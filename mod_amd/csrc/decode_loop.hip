@@ -11,42 +11,61 @@
 // Here the weights of the next phases stream into LDS while the current phase
 // waits for its input, and phases hand data to each other directly.
 //
-// Co-residency. The grid has exactly as many workgroups as the device has
-// CUs, and each workgroup takes 131 KB of a CU's 160 KB of LDS, so on an idle
-// device all of them are resident at once. The kernel needs no grid barrier,
-// only that residency, so it is launched as an ordinary kernel: a cooperative
-// launch would claim the device's global wave-sync resource, which only one
-// process at a time can hold (a second process's cooperative launch fails).
-// If other work holds some CUs, the workgroups waiting for them start when it
-// drains; every wait below is bounded, so the kernel ends in any case.
+// Partitioning by XCD. MI355X has 8 XCDs of 32 CUs, each XCD with its own L2.
+// The dispatcher deals a launch's workgroups to the XCDs round-robin, but from
+// wherever the previous launch left off, so each workgroup reads its XCD from
+// the hardware XCC id at start and takes the next free slot j of that XCD; the
+// role (g, j) then fixes all its work. A value handed to another XCD travels
+// through the memory side
+// (~0.75 us one way, measured), one handed within an XCD stays closer. The
+// layer is split so that only two hand-offs per layer cross XCDs:
+//   XCD g owns KV head g (8 KV heads, 8 XCDs) and slice g of the MLP:
+//   P1  x''[e] = x'[e] + sum_h dpart[h][e]   reduce the previous layer's 8
+//       down partials; workgroup (g, j) reduces elements [32j, 32j+32) for
+//       its XCD (every XCD keeps the full residual stream)        [cross-XCD]
+//   P2  every workgroup of XCD g gathers the full x'', RMSNorm, and computes
+//       8 of the 256 (row, row+64) pairs of KV head g's q/k/v rows, bias,
+//       RoPE, KV-cache row                                        [intra-XCD]
+//   P3  attention of KV head g (both query heads) in 8 position splits on
+//       workgroups j < 8                                          [intra-XCD]
+//   P4  every workgroup merges the 8 splits into the head output o_g (256
+//       values) and computes the o_proj partial of rows [32j, 32j+32) over
+//       o_g's 256 columns                                         [cross-XCD]
+//   P5  x'[e] = x''[e] + sum_h opart[h][e] (like P1)
+//   P6  gather x', RMSNorm, gate_up for 12 of XCD g's 384 intermediate
+//       channels, SwiGLU                                          [intra-XCD]
+//   P7  down partial of rows [32j, 32j+32) over XCD g's 384 channels
+// After the last layer: P1, gather, final RMSNorm, lm_head rows + argmax key.
+// The o_proj and down outputs are thus sums of 8 per-XCD partials, added in a
+// fixed order (deterministic); each workgroup streams 60 KB of weights per
+// layer, as evenly as before.
 //
 // Workgroup = 8 waves:
 //   waves 4-7 ("stream waves") copy this workgroup's weight lines, in the order
 //     the compute waves consume them, from a per-workgroup contiguous copy of
 //     the weights (built once) into an LDS ring of 1 KB lines with
 //     global_load_lds_dwordx4; a line is published when its copy has landed.
-//   waves 0-3 ("compute waves") run the phases of every token:
-//       qkv -> attention -> merge -> o_proj -> gate_up -> down   (per layer)
-//       -> lm_head + argmax
-//     reading x from LDS, weights from the ring, and writing outputs.
+//   waves 0-3 ("compute waves") run the phases; each polls whole input vectors
+//     itself (no cross-wave rendezvous except around attention and the merge).
 //
-// Cross-workgroup hand-off uses tagged 64-bit words: every value a phase
-// produces for other workgroups is stored as {tag:32 | fp32 bits:32} with a
-// device-scope (L2-bypassing) store; a consumer polls the words it needs with
-// device-scope loads until every tag equals the producing phase's tag. Tags
-// grow monotonically over the decoder's lifetime, so no buffer is ever reset
-// and no barrier is needed: one memory round trip per hand-off. A buffer is
-// rewritten only one layer later, by which time every consumer has read it
-// (each phase needs all of the previous phase's outputs, so no workgroup can
-// be two phases ahead of any other's reads).
+// Hand-off: every value a phase produces for other workgroups is stored as a
+// tagged 64-bit word {tag:32 | fp32 bits:32} with a device-scope store; a
+// consumer polls the words it needs with device-scope loads until every tag
+// equals the producing phase's tag. Tags grow monotonically over the
+// decoder's lifetime, so no buffer is ever reset and no barrier is needed. A
+// buffer is rewritten one layer later, when every workgroup of every XCD has
+// consumed it: each layer's gathers (P2, P6) need all workgroups of the XCD,
+// and the cross-XCD reductions need all XCDs.
 //
-// The KV cache rows are written with device-scope stores; rows are read only
-// after the token that wrote them (the current row is read from the tagged
-// copy), so ordinary cached loads never see a stale line.
-//
-// Every wait is bounded: a wait that exceeds its limit records an error
-// (read back by pio_qwen3_read) and makes every wave leave its loops, so the
-// kernel always terminates.
+// Co-residency. The grid has exactly as many workgroups as the device has
+// CUs, and each workgroup takes most of a CU's 160 KB of LDS, so on an idle
+// device all of them are resident at once. The kernel needs no grid barrier,
+// only that residency, so it is launched as an ordinary kernel: a cooperative
+// launch would claim the device's global wave-sync resource, which only one
+// process at a time can hold (a second process's cooperative launch fails).
+// If other work holds some CUs, the workgroups waiting for them start when it
+// drains; every wait below is bounded (a timeout records an error, read back
+// by pio_qwen3_read, and makes every wave leave), so the kernel ends in any case.
 #include "decode.hpp"
 
 #include <math.h>
@@ -63,34 +82,44 @@ constexpr int LP_SW = 4;                   // stream waves
 constexpr int LP_THREADS = 64 * (LP_CW + LP_SW);
 constexpr int LP_RING = 64;                // LDS ring of 1 KB weight lines (power of two)
 constexpr int LP_INFL = 12;                // lines in flight per stream wave
-constexpr int LP_S = ATT_SPLITS;           // attention splits over positions
+// The shape the kernel is built for (Qwen3-0.6B on an 8-XCD, 256-CU MI355X)
+constexpr int LP_NX = 8;                   // XCDs = KV heads
+constexpr int LP_WPX = 32;                 // workgroups per XCD
+constexpr int LP_NBLK = LP_NX * LP_WPX;
+constexpr int LP_D = 128;                  // head_dim
+constexpr int LP_G = 2;                    // query heads per KV head
+constexpr int LP_H = 1024;                 // hidden
+constexpr int LP_KO = 2048;                // n_heads * head_dim
+constexpr int LP_I = 3072;                 // intermediate
+constexpr int LP_IX = LP_I / LP_NX;        // 384 intermediate channels per XCD
+constexpr int LP_QKVX = (LP_G + 2) * LP_D; // 512 q/k/v values per KV head
+constexpr int LP_S = 8;                    // attention splits over positions
 constexpr int LP_NPF = 2;                  // attention passes whose K/V are prefetched
 constexpr int LP_NPMAX = 8;                // attention passes (8 positions each) per wave
-constexpr int LP_CMAX = 3;                 // K <= 3 * 1024
-// The layer shape the kernel is instantiated for, in 1 KB weight lines per
-// row: hidden (qkv, gate_up, lm_head rows), n_heads*head_dim (o_proj rows),
-// intermediate (down rows). Qwen3-0.6B: 1024, 2048, 3072.
-constexpr int LP_CH = 1, LP_CO = 2, LP_CI = 3;
-constexpr int LP_G = 2;                    // query heads per KV head the kernel is built for
-// Units per wave and phase the kernel is unrolled for (Qwen3-0.6B on 256 CUs:
-// qkv 2048 pairs, gate_up 3072 pairs, o_proj/down 1024 rows over 1024 waves).
-constexpr int LP_MU_QKV = 2, LP_MU_GU = 3, LP_MU_ROW = 1;
-constexpr int LP_LM_B = 6;                 // lm_head rows per wave and batch (double-buffered)
-constexpr int LP_PH = 6;                   // tagged phases per layer
 constexpr int LP_MAX_SEQ = LP_S * LP_CW * 8 * LP_NPMAX;   // 2048
-constexpr int LP_PART = 2 + 128;           // (max, sum, o[128]) per split and head
+constexpr int LP_PART = 2 + LP_D;          // (max, sum, o[128]) per split and head
+static_assert(LP_S == 8, "the merge loads the partials of 8 splits in one batch");
+constexpr int LP_LM_B = 6;                 // lm_head rows per wave and batch (double-buffered)
+constexpr int LP_PH = 7;                   // tagged phases per layer
+// weight lines per workgroup and layer, in consumption order
+constexpr int LP_L_QKV = 16;               // 8 (row, row+64) pairs of 1 KB rows
+constexpr int LP_L_O = 8;                  // 32 rows x 256 B (4 rows per line)
+constexpr int LP_L_GU = 24;                // 12 (gate, up) pairs of 1 KB rows
+constexpr int LP_L_DN = 12;                // 32 rows x 384 B (8 rows x 128 B per line)
+constexpr int LP_OFF_O = LP_L_QKV, LP_OFF_GU = LP_OFF_O + LP_L_O, LP_OFF_DN = LP_OFF_GU + LP_L_GU;
+constexpr int LP_LPL = LP_OFF_DN + LP_L_DN;   // 60
 constexpr uint32_t LP_POLL_LIMIT = 1u << 21;   // device-scope polls (~0.5-1 us each)
 constexpr uint32_t LP_LDS_LIMIT = 1u << 24;    // LDS polls
 
-enum { PH_QKV = 0, PH_ATT = 1, PH_MERGE = 2, PH_O = 3, PH_GU = 4, PH_DN = 5 };
-enum { LP_ERR_TIMEOUT = 1 };
+enum { PH_XR = 0, PH_QKV = 1, PH_ATT = 2, PH_OP = 3, PH_XR2 = 4, PH_ACT = 5, PH_DP = 6 };
+enum { LP_ERR_TIMEOUT = 1, LP_ERR_XCD = 2 };
 
 struct LoopLayer {
     const float *in_norm, *s_qkv, *b_qkv, *s_o, *post_norm, *s_gu, *s_down;
 };
 
 struct LoopParams {
-    int L, H, nq, nkv, I, V, max_seq, nblk;
+    int L, V, max_seq;
     float eps, att_scale;
     const float* embed;
     const float* final_norm;
@@ -98,31 +127,38 @@ struct LoopParams {
     const int8_t* lm_head;     // [V][H] int8, read directly by the lm phase
     const LoopLayer* layers;
     const int8_t* stream;      // [nblk][lpt][1024] weight lines in consumption order
-    int lpl;                   // lines per layer (per workgroup)
-    int off_o, off_gu, off_dn; // phase offsets inside a layer
-    int lpt;                   // weight lines per token (n_layers * lpl)
+    int lpt;                   // weight lines per token (n_layers * LP_LPL)
     float* kc;
     float* vc;
     const float* cos_t;
     const float* sin_t;
-    u64 *xa, *xb, *q, *kv, *part, *merged, *act, *keys;
+    // tagged hand-off buffers
+    u64* xr;      // [8][H]    P1 output, per XCD
+    u64* xr2;     // [8][H]    P5 output, per XCD
+    u64* qkv;     // [8][512]  q (2 heads), k, v of KV head g
+    u64* att;     // [8][S][2][LP_PART] attention partials
+    u64* act;     // [8][384]  SwiGLU output, XCD g's channels
+    u64* opart;   // [8][H]    o_proj partials, per XCD
+    u64* dpart;   // [8][H]    down partials, per XCD
+    u64* keys;    // [nblk]    argmax keys
     int32_t* ids;
     float* logits;
     int32_t* state;
     int pos0, prompt_len, n_steps;
     uint32_t epoch0;
-    int* err;                  // [0] code, [1] where, [2] abort flag
+    int* err;                  // [0] code, [1] where, [2] abort flag, [8 + g] XCD g's next slot
 };
 
-// LDS layout (dynamic): ring | xs[2][3072] | att partials | per-wave staging
-constexpr int LP_XS = LP_CMAX * 1024;
+// LDS layout (dynamic): ring | per-wave x copies | merged head output |
+// per-wave act copies | attention partials | attention staging
 constexpr size_t LP_LDS_RING = (size_t)LP_RING * 1024;
-constexpr size_t LP_LDS_XS = 2 * LP_XS * 4;
-// attention partials: [wave][head][lane group][128] + per (wave, head) max and sum
-constexpr size_t LP_LDS_ATT = (size_t)LP_CW * LP_G * 8 * 128 * 4 + 2 * LP_CW * LP_G * 4;
-constexpr size_t LP_STG = LP_G * 128 + 256;   // floats per wave: q heads + current k,v
+constexpr size_t LP_LDS_XW = (size_t)LP_CW * LP_H * 4;
+constexpr size_t LP_LDS_OS = (size_t)LP_G * LP_D * 4;
+constexpr size_t LP_LDS_ACT = (size_t)LP_CW * LP_IX * 4;
+constexpr size_t LP_LDS_ATT = (size_t)LP_CW * LP_G * 8 * LP_D * 4 + 2 * LP_CW * LP_G * 4;
+constexpr size_t LP_STG = LP_G * LP_D + 256;   // floats per wave: q heads + current k,v
 constexpr size_t LP_LDS_STG = (size_t)LP_CW * LP_STG * 4;
-constexpr size_t LP_LDS_BYTES = LP_LDS_RING + LP_LDS_XS + LP_LDS_ATT + LP_LDS_STG;
+constexpr size_t LP_LDS_BYTES = LP_LDS_RING + LP_LDS_XW + LP_LDS_OS + LP_LDS_ACT + LP_LDS_ATT + LP_LDS_STG;
 
 // ------------------------------------------------------------------ helpers
 __device__ __forceinline__ u64 ll_load(const u64* p) {
@@ -139,6 +175,76 @@ __device__ __forceinline__ void ll_store(u64* p, float v, uint32_t tag) {
 template <typename T>
 __device__ __forceinline__ T gld(const T* p) {
     return *(const __attribute__((address_space(1))) T*)p;
+}
+
+// Hand-offs within one XCD go through that XCD's L2: the producer's store
+// (sc0) lands in the L2, and the consumer's load (sc0 nt) misses the CU's L1
+// and reads the L2 (~0.45 us one way between two CUs of an XCD, against ~0.75
+// us through the memory side, measured). Every batch of polling loads is one
+// asm statement that also waits for them, so no output register is used
+// before its load has landed.
+__device__ __forceinline__ void st_l2(u64* p, float v, uint32_t tag) {
+    const u64 w = ((u64)tag << 32) | (u64)__float_as_uint(v);
+    asm volatile("global_store_dwordx2 %0, %1, off sc0" ::"v"(p), "v"(w) : "memory");
+}
+#define LP_LD(i, off) "global_load_dwordx2 %" #i ", %[a], off offset:" #off " sc0 nt\n"
+#define LP_LDB(i, off) "global_load_dwordx2 %" #i ", %[b], off offset:" #off " sc0 nt\n"
+#define LP_LDC(i, off) "global_load_dwordx2 %" #i ", %[c], off offset:" #off " sc0 nt\n"
+#define LP_LDD(i, off) "global_load_dwordx2 %" #i ", %[d], off offset:" #off " sc0 nt\n"
+// 16 tagged words 64 words apart (lane-consecutive: coalesced), from two
+// bases 512 words apart (immediate offsets reach 4 KB)
+__device__ __forceinline__ void ld_l2_16s(const u64* a, const u64* b, u64 (&v)[16]) {
+    asm volatile(LP_LD(0, 0) LP_LD(1, 512) LP_LD(2, 1024) LP_LD(3, 1536) LP_LD(4, 2048)
+                 LP_LD(5, 2560) LP_LD(6, 3072) LP_LD(7, 3584) LP_LDB(8, 0) LP_LDB(9, 512)
+                 LP_LDB(10, 1024) LP_LDB(11, 1536) LP_LDB(12, 2048) LP_LDB(13, 2560)
+                 LP_LDB(14, 3072) LP_LDB(15, 3584) "s_waitcnt vmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+                   "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]),
+                   "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15])
+                 : [a] "v"(a), [b] "v"(b)
+                 : "memory");
+}
+// 8 tagged words 64 words apart
+__device__ __forceinline__ void ld_l2_8s(const u64* p, u64 (&v)[8]) {
+    asm volatile(LP_LD(0, 0) LP_LD(1, 512) LP_LD(2, 1024) LP_LD(3, 1536) LP_LD(4, 2048)
+                 LP_LD(5, 2560) LP_LD(6, 3072) LP_LD(7, 3584) "s_waitcnt vmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+                   "=&v"(v[6]), "=&v"(v[7])
+                 : [a] "v"(p)
+                 : "memory");
+}
+// 6 tagged words 64 words apart
+__device__ __forceinline__ void ld_l2_6s(const u64* p, u64 (&v)[6]) {
+    asm volatile(LP_LD(0, 0) LP_LD(1, 512) LP_LD(2, 1024) LP_LD(3, 1536) LP_LD(4, 2048)
+                 LP_LD(5, 2560) "s_waitcnt vmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5])
+                 : [a] "v"(p)
+                 : "memory");
+}
+// The merge's words of 8 attention splits (split stride 130 words): max and
+// sum of splits 0-3 from a, 4-7 from b (the same address in every lane), and
+// o[d] of splits 0-3 from c, 4-7 from d (lane-consecutive d).
+__device__ __forceinline__ void ld_l2_merge(const u64* a, const u64* b, const u64* c, const u64* d,
+                                            u64 (&ml)[16], u64 (&o)[8]) {
+    asm volatile(LP_LD(0, 0) LP_LD(1, 8) LP_LD(2, 1040) LP_LD(3, 1048) LP_LD(4, 2080) LP_LD(5, 2088)
+                 LP_LD(6, 3120) LP_LD(7, 3128) LP_LDB(8, 0) LP_LDB(9, 8) LP_LDB(10, 1040)
+                 LP_LDB(11, 1048) LP_LDB(12, 2080) LP_LDB(13, 2088) LP_LDB(14, 3120) LP_LDB(15, 3128)
+                 LP_LDC(16, 0) LP_LDC(17, 1040) LP_LDC(18, 2080) LP_LDC(19, 3120)
+                 LP_LDD(20, 0) LP_LDD(21, 1040) LP_LDD(22, 2080) LP_LDD(23, 3120) "s_waitcnt vmcnt(0)"
+                 : "=&v"(ml[0]), "=&v"(ml[1]), "=&v"(ml[2]), "=&v"(ml[3]), "=&v"(ml[4]), "=&v"(ml[5]),
+                   "=&v"(ml[6]), "=&v"(ml[7]), "=&v"(ml[8]), "=&v"(ml[9]), "=&v"(ml[10]),
+                   "=&v"(ml[11]), "=&v"(ml[12]), "=&v"(ml[13]), "=&v"(ml[14]), "=&v"(ml[15]),
+                   "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(o[4]), "=&v"(o[5]),
+                   "=&v"(o[6]), "=&v"(o[7])
+                 : [a] "v"(a), [b] "v"(b), [c] "v"(c), [d] "v"(d)
+                 : "memory");
+}
+template <int N>
+__device__ __forceinline__ bool tags_ok(const u64 (&v)[N], uint32_t tag) {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < N; i++) ok &= (uint32_t)(v[i] >> 32) == tag;
+    return ok;
 }
 
 __device__ __forceinline__ void dev_store(float* p, float v) {
@@ -273,20 +379,21 @@ __device__ __forceinline__ bool lm_needed(const LoopParams& p, int t) {
     return p.pos0 + t + 1 >= p.prompt_len || t == p.n_steps - 1;
 }
 __device__ __forceinline__ uint32_t tag_of(const LoopParams& p, int t, int l, int ph) {
-    return p.epoch0 + (uint32_t)t * (uint32_t)(p.L * LP_PH + 1) + (uint32_t)(l * LP_PH + ph);
+    return p.epoch0 + (uint32_t)t * (uint32_t)(p.L * LP_PH + 2) + (uint32_t)(l * LP_PH + ph);
 }
 
-struct Units;
 struct Cx {
     int lane, w, nsync, fail_where;
-    int uq0, nuq, uh0, nuh, ui0, nui, uv0, nuv;   // unit ranges: qkv pairs, H rows, I pairs, V rows
+    int g, j, role;  // XCD, slot within it, role index j * 8 + g
+    int uv0, nuv;    // lm_head rows of this workgroup
     int* ready;      // [LP_SW] lines landed per stream wave
     int* done;       // [LP_CW] first line each compute wave may still need
     int* csync;      // compute-wave rendezvous counter
     int* abort;      // workgroup abort flag
     int8_t* ring;
-    float* xs;       // [2][LP_XS]
-    float* ss;       // [2][LP_CW] partial sums of squares
+    float* xw;       // [LP_CW][H] each wave's copy of the current input vector
+    float* os;       // [256] merged attention output of KV head g
+    float* acts;     // [LP_CW][384] each wave's copy of XCD g's act slice
     float* attp;     // [LP_CW][LP_G][8][128] attention partials
     float* attm;     // [2][LP_CW][LP_G] wave max, wave sum
     float* stg;      // [LP_CW][LP_STG]
@@ -294,16 +401,16 @@ struct Cx {
 };
 
 // Records a timed-out wait (site `where`) and tells every workgroup to stop.
-__device__ void lp_fail(const LoopParams& p, int where) {
-    if (atomicCAS(&p.err[0], 0, LP_ERR_TIMEOUT) == 0) atomicExch(&p.err[1], where);
+__device__ void lp_fail(const LoopParams& p, int code, int where) {
+    if (atomicCAS(&p.err[0], 0, code) == 0) atomicExch(&p.err[1], where);
     __hip_atomic_store(&p.err[2], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // One more iteration of a bounded wait? Also leaves when another wave or
 // workgroup gave up. A wave that runs out of patience only notes where (and
-// raises the workgroup's abort flag); its role function reports the error
-// once, on the way out -- the kernel has to fit the instruction cache, so no
-// calls or long paths sit inside the wait loops.
+// raises the workgroup's abort flag); the kernel reports it once on the way
+// out -- the kernel has to fit the instruction cache, so no calls or long
+// paths sit inside the wait loops.
 __device__ __forceinline__ bool keep_waiting(const LoopParams& p, Cx& c, uint32_t it, uint32_t limit,
                                              int where) {
     if (lds_ld_u(c.abort)) return false;
@@ -316,34 +423,21 @@ __device__ __forceinline__ bool keep_waiting(const LoopParams& p, Cx& c, uint32_
     return true;
 }
 
-// Polls n tagged words per lane (src[lane + 64 i], i < n) until every tag
+// Polls N tagged words per lane (addr(i), i < N) until every tag of the wave
 // matches; returns their values.
-template <int NMAX>
-__device__ __forceinline__ bool ll_poll(const LoopParams& p, Cx& c, const u64* src, int n,
-                                        uint32_t tag, float (&out)[NMAX], int where) {
+template <int N, typename F>
+__device__ __forceinline__ bool poll(const LoopParams& p, Cx& c, F addr, uint32_t tag,
+                                     float (&out)[N], int where) {
     for (uint32_t it = 0;; it++) {
-        u64 v[NMAX];
+        u64 v[N];
 #pragma unroll
-        for (int i = 0; i < NMAX; i++) v[i] = i < n ? ll_load(src + c.lane + 64 * i) : ((u64)tag << 32);
+        for (int i = 0; i < N; i++) v[i] = ll_load(addr(i));
         bool ok = true;
 #pragma unroll
-        for (int i = 0; i < NMAX; i++) ok &= (uint32_t)(v[i] >> 32) == tag;
+        for (int i = 0; i < N; i++) ok &= (uint32_t)(v[i] >> 32) == tag;
         if (__all(ok)) {
 #pragma unroll
-            for (int i = 0; i < NMAX; i++) out[i] = __uint_as_float((uint32_t)v[i]);
-            return true;
-        }
-        if (!keep_waiting(p, c, it, LP_POLL_LIMIT, where)) return false;
-    }
-}
-
-// One tagged word (same address in every lane).
-__device__ __forceinline__ bool ll_poll1(const LoopParams& p, Cx& c, const u64* src, uint32_t tag,
-                                         float& out, int where) {
-    for (uint32_t it = 0;; it++) {
-        const u64 v = ll_load(src);
-        if ((uint32_t)(v >> 32) == tag) {
-            out = __uint_as_float((uint32_t)v);
+            for (int i = 0; i < N; i++) out[i] = __uint_as_float((uint32_t)v[i]);
             return true;
         }
         if (!keep_waiting(p, c, it, LP_POLL_LIMIT, where)) return false;
@@ -389,227 +483,459 @@ __device__ __forceinline__ lp_v4i ring_line(const Cx& c, int line) {
     return *(const lp_v4i*)(c.ring + (size_t)(line % LP_RING) * 1024 + c.lane * 16);
 }
 
-// Stage one quarter of a K-vector (this wave's values v[i] = x[w*K/4 + lane + 64 i])
-// into LDS buffer `buf`, times gamma if given, with this wave's partial sum of
-// squares; after the rendezvous load the whole vector into the lane layout
-// xr[c][j] = x[c*1024 + 16 lane + j] and return the RMSNorm scale (1 without gamma).
-template <int NMAX, int C>
-__device__ __forceinline__ bool stage_x(const LoopParams& p, Cx& c, int buf, int K,
-                                        const float (&v)[NMAX], const float (&g)[NMAX], bool norm,
-                                        float (&xr)[LP_CMAX][16], float& nscale, int where) {
-    const int n = K / 256;
-    float* xs = c.xs + buf * LP_XS;
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < NMAX; i++) {
-        if (i >= n) continue;
-        const int e = c.w * (K / 4) + c.lane + 64 * i;
-        s += v[i] * v[i];
-        xs[e] = norm ? v[i] * g[i] : v[i];
-    }
-    if (norm) {
-        s = wsum(s);
-        if (c.lane == 0) c.ss[buf * LP_CW + c.w] = s;
-    }
-    if (!csync(p, c, where)) return false;
-#pragma unroll
-    for (int ch = 0; ch < C; ch++) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float4 a = *(const float4*)&xs[ch * 1024 + c.lane * 16 + 4 * i];
-            xr[ch][4 * i] = a.x; xr[ch][4 * i + 1] = a.y; xr[ch][4 * i + 2] = a.z; xr[ch][4 * i + 3] = a.w;
-        }
-    }
-    nscale = 1.f;
-    if (norm) {
-        const float* ss = c.ss + buf * LP_CW;
-        nscale = rsqrtf((ss[0] + ss[1] + ss[2] + ss[3]) * (1.0f / (float)K) + p.eps);
-    }
-    return true;
-}
-
-// Units of a phase owned by this workgroup: [u0, u0 + nu), u0 = b*U/nblk.
-// Computed once per kernel (a division is a long instruction sequence).
-struct Units {
-    int u0, nu;
-};
-__device__ __forceinline__ Units blk_units(int U, int nblk) {
-    const uint32_t b = blockIdx.x;
-    const int u0 = (int)((b * (uint32_t)U) / (uint32_t)nblk);
-    return Units{u0, (int)(((b + 1) * (uint32_t)U) / (uint32_t)nblk) - u0};
-}
-
-// Dot products of this wave's units of a phase: units ub = w + 4m (m < MU,
-// ub < nu), each R rows of C 1 KB lines at ring lines line0 + ub*R*C + r*C + ch.
-// One wait covers all of them; every ring read is issued before the first dot
-// product, and the reductions are independent chains.
-template <int C, int R, int MU>
-__device__ __forceinline__ bool phase_dots(const LoopParams& p, Cx& c, int line0, int nu,
-                                           const float (&xr)[LP_CMAX][16], float (&acc)[MU][R],
-                                           int& nmy, int where) {
-    const int lpu = R * C;
-    nmy = nu > c.w ? min(MU, (nu - c.w + LP_CW - 1) / LP_CW) : 0;
-    if (nmy == 0) return true;
-    if (!wait_upto(p, c, line0 + (c.w + LP_CW * (nmy - 1)) * lpu + lpu - 1, where)) return false;
-    // Every MU unit is computed (a unit past nmy reads a stale ring line, and
-    // its result is never used): straight-line code, no per-unit branches.
-    lp_v4i wv[MU][R][C];
-#pragma unroll
-    for (int m = 0; m < MU; m++)
-#pragma unroll
-        for (int r = 0; r < R; r++)
-#pragma unroll
-            for (int ch = 0; ch < C; ch++)
-                wv[m][r][ch] = ring_line(c, line0 + (c.w + LP_CW * m) * lpu + r * C + ch);
-#pragma unroll
-    for (int m = 0; m < MU; m++) {
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            float s[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ch = 0; ch < C; ch++) lp_dot16s(xr[ch], wv[m][r][ch], s);
-            acc[m][r] = (s[0] + s[1]) + (s[2] + s[3]);
-        }
-    }
-    wsum_n<MU * R>(&acc[0][0]);
-    return true;
+// Sum over each group of 16 consecutive lanes, in every lane of the group.
+__device__ __forceinline__ float sum16(float x) {
+    x = sum8(x);
+    return x + dpp<DPP_ROR8>(x);
 }
 
 // ------------------------------------------------------------ phase bodies
+__device__ __forceinline__ void load_row16(const float* src, float (&d)[16]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 a = *(const float4*)(src + 4 * i);
+        d[4 * i] = a.x; d[4 * i + 1] = a.y; d[4 * i + 2] = a.z; d[4 * i + 3] = a.w;
+    }
+}
+// The same from global memory (the KV cache), through the global address space.
+typedef float lp_f4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void load_row16g(const float* src, float (&d)[16]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const lp_f4 a = gld((const lp_f4*)(src + 4 * i));
+        d[4 * i] = a[0]; d[4 * i + 1] = a[1]; d[4 * i + 2] = a[2]; d[4 * i + 3] = a[3];
+    }
+}
+
+// The full input vector (H values), polled by this wave into the lane layout
+// of a 1 KB weight line (lane l holds x[16 l .. 16 l + 15]) and copied to the
+// wave's own LDS vector; returns the RMSNorm scale of g * x (g = gamma).
+__device__ __forceinline__ bool gather_x(const LoopParams& p, Cx& c, const u64* src, uint32_t tag,
+                                         const float (&gam)[16], float (&xv)[16], float& nscale,
+                                         int where) {
+    // coalesced poll (word lane + 64 i), transposed through the wave's LDS copy
+    // into the line layout (lane l: x[16 l .. 16 l + 15])
+    const u64* base = src + c.g * LP_H + c.lane;
+    float* xw = c.xw + c.w * LP_H;
+    for (uint32_t it = 0;; it++) {
+        u64 v[16];
+        ld_l2_16s(base, base + 512, v);
+        if (__all(tags_ok(v, tag))) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) xw[c.lane + 64 * i] = __uint_as_float((uint32_t)v[i]);
+            break;
+        }
+        if (!keep_waiting(p, c, it, LP_POLL_LIMIT, where)) return false;
+    }
+    load_row16(xw + 16 * c.lane, xv);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i += 4)
+        ss += xv[i] * xv[i] + xv[i + 1] * xv[i + 1] + xv[i + 2] * xv[i + 2] + xv[i + 3] * xv[i + 3];
+#pragma unroll
+    for (int i = 0; i < 16; i++) xv[i] *= gam[i];
+    nscale = rsqrtf(wsum(ss) * (1.0f / (float)LP_H) + p.eps);
+    return true;
+}
+
+// Cross-XCD reduction (P1 / P5): x_new[e] = base[e] + sum over the 8 XCDs'
+// partials part[h][e], for this wave's 8 elements e = 32 j + 8 w + (lane >> 3)
+// (lane & 7 = h); the 8-lane sum has one fixed order. base is the wave's own
+// copy of the previous input vector. Stored tagged for the XCD's gather.
+__device__ __forceinline__ bool reduce_x(const LoopParams& p, Cx& c, const u64* part, uint32_t ptag,
+                                         u64* out, uint32_t otag, int where) {
+    const int e = 32 * c.j + 8 * c.w + (c.lane >> 3);
+    const u64* src = part + (c.lane & 7) * LP_H + e;
+    float v[1];
+    if (!poll<1>(p, c, [&](int) { return src; }, ptag, v, where)) return false;
+    const float s = sum8(v[0]);
+    if ((c.lane & 7) == 0) st_l2(out + c.g * LP_H + e, c.xw[c.w * LP_H + e] + s, otag);
+    return true;
+}
+
 // Per-unit constants of a phase are loaded one per lane before the phase
-// waits for its input (lane k holds the value of this wave's unit k, or of
-// row k&1 of unit k>>1 for paired units) and read back with readlane.
+// waits for its input and read back with readlane.
 struct Pre {
     float a = 0.f, b = 0.f, cs = 0.f, sn = 0.f;
-    u64 r = 0;
 };
 
-// qkv: pairs (n, n + 64) of one head; bias + rotate-half RoPE at pos;
-// q -> tagged q, k/v -> tagged current row + cache row pos.
+// q/k/v unit u (0..255) of KV head g: the row pair (r, r + 64) of a 128-row
+// head block: u < 128: query head 2g + u/64; u < 192: key head g; else value
+// head g. Returns the first row of the pair in W_qkv.
+__device__ __forceinline__ int qkv_row(int g, int u) {
+    if (u < 128) return (LP_G * g + (u >> 6)) * LP_D + (u & 63);
+    if (u < 192) return LP_KO + g * LP_D + (u - 128);
+    return LP_KO + LP_NX * LP_D + g * LP_D + (u - 192);
+}
+
 __device__ __forceinline__ Pre pre_qkv(const LoopParams& p, const Cx& c, int l, int pos) {
     const LoopLayer& Lw = p.layers[l];
-    const int u0 = c.uq0, nu = c.nuq;
     Pre q;
-    const int ub = c.w + LP_CW * (c.lane >> 1);
-    if (ub < nu) {
-        const int u = u0 + ub, row = (u >> 6) * 128 + (u & 63) + (c.lane & 1) * 64;
+    if (c.lane < 4) {   // lane 2m + r: row r of this wave's unit m
+        const int u = 8 * c.j + c.w + LP_CW * (c.lane >> 1);
+        const int row = qkv_row(c.g, u) + (c.lane & 1) * 64;
         q.a = gld(Lw.s_qkv + row);
         q.b = Lw.b_qkv ? gld(Lw.b_qkv + row) : 0.f;
     }
-    const int ubc = c.w + LP_CW * c.lane;
-    if (ubc < nu) {
-        const int i = (u0 + ubc) & 63;
-        q.cs = gld(p.cos_t + (int64_t)pos * 64 + i);
-        q.sn = gld(p.sin_t + (int64_t)pos * 64 + i);
+    if (c.lane < 2) {   // lane m: RoPE angle of unit m
+        const int u = 8 * c.j + c.w + LP_CW * c.lane;
+        q.cs = gld(p.cos_t + (int64_t)pos * 64 + (u & 63));
+        q.sn = gld(p.sin_t + (int64_t)pos * 64 + (u & 63));
     }
     return q;
 }
 
-template <int C>
+// qkv (P2): this wave's 2 units, from ring lines line0 + 2 (w + 4 m) + r.
 __device__ bool phase_qkv(const LoopParams& p, Cx& c, int l, int pos, int line0, uint32_t tag,
-                          const float (&xr)[LP_CMAX][16], float nscale, const Pre& pre) {
-    int nmy;
-    const int u0 = c.uq0, nu = c.nuq;
-    float acc[LP_MU_QKV][2];
-    if (!phase_dots<C, 2, LP_MU_QKV>(p, c, line0, nu, xr, acc, nmy, 10)) return false;
+                          const float (&xv)[16], float nscale, const Pre& pre) {
+    if (!wait_upto(p, c, line0 + 2 * (c.w + LP_CW) + 1, 10)) return false;
+    lp_v4i wv[2][2];
 #pragma unroll
-    for (int m = 0; m < LP_MU_QKV; m++) {
-        if (m >= nmy) break;
-        const int u = u0 + c.w + LP_CW * m, hd = u >> 6, i = u & 63;
-        const float v0 = acc[m][0] * rlane(pre.a, 2 * m) * nscale + rlane(pre.b, 2 * m);
-        const float v1 = acc[m][1] * rlane(pre.a, 2 * m + 1) * nscale + rlane(pre.b, 2 * m + 1);
+    for (int m = 0; m < 2; m++)
+#pragma unroll
+        for (int r = 0; r < 2; r++) wv[m][r] = ring_line(c, line0 + 2 * (c.w + LP_CW * m) + r);
+    float acc[4];
+#pragma unroll
+    for (int m = 0; m < 2; m++)
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            float s[4] = {0.f, 0.f, 0.f, 0.f};
+            lp_dot16s(xv, wv[m][r], s);
+            acc[2 * m + r] = (s[0] + s[1]) + (s[2] + s[3]);
+        }
+    wsum4(acc[0], acc[1], acc[2], acc[3]);
+    u64* dst = p.qkv + c.g * LP_QKVX;
+#pragma unroll
+    for (int m = 0; m < 2; m++) {
+        const int u = 8 * c.j + c.w + LP_CW * m, i = u & 63;
+        const float v0 = acc[2 * m] * rlane(pre.a, 2 * m) * nscale + rlane(pre.b, 2 * m);
+        const float v1 = acc[2 * m + 1] * rlane(pre.a, 2 * m + 1) * nscale + rlane(pre.b, 2 * m + 1);
         const float cs = rlane(pre.cs, m), sn = rlane(pre.sn, m);
         if (c.lane != 0) continue;
-        if (hd < p.nq + p.nkv) {
+        if (u < 192) {
             const float o0 = v0 * cs - v1 * sn, o1 = v0 * sn + v1 * cs;
-            if (hd < p.nq) {
-                ll_store(p.q + hd * 128 + i, o0, tag);
-                ll_store(p.q + hd * 128 + i + 64, o1, tag);
+            if (u < 128) {
+                st_l2(dst + (u >> 6) * LP_D + i, o0, tag);
+                st_l2(dst + (u >> 6) * LP_D + i + 64, o1, tag);
             } else {
-                const int kvh = hd - p.nq;
-                float* kr = p.kc + (((int64_t)l * p.nkv + kvh) * p.max_seq + pos) * 128;
+                float* kr = p.kc + (((int64_t)l * LP_NX + c.g) * p.max_seq + pos) * LP_D;
                 dev_store(kr + i, o0);
                 dev_store(kr + i + 64, o1);
-                ll_store(p.kv + kvh * 256 + i, o0, tag);
-                ll_store(p.kv + kvh * 256 + i + 64, o1, tag);
+                st_l2(dst + 256 + i, o0, tag);
+                st_l2(dst + 256 + i + 64, o1, tag);
             }
         } else {
-            const int kvh = hd - p.nq - p.nkv;
-            float* vr = p.vc + (((int64_t)l * p.nkv + kvh) * p.max_seq + pos) * 128;
+            float* vr = p.vc + (((int64_t)l * LP_NX + c.g) * p.max_seq + pos) * LP_D;
             dev_store(vr + i, v0);
             dev_store(vr + i + 64, v1);
-            ll_store(p.kv + kvh * 256 + 128 + i, v0, tag);
-            ll_store(p.kv + kvh * 256 + 128 + i + 64, v1, tag);
+            st_l2(dst + 384 + i, v0, tag);
+            st_l2(dst + 384 + i + 64, v1, tag);
         }
     }
     return true;
 }
 
-// Residual row phase: y[n] = res[n] + s[n] * (W x)[n] for this wave's rows.
-// res comes from the tagged vector `rin` (tag rtag) or, when rin is null, from
-// the embedding row emb.
-__device__ __forceinline__ Pre pre_resid(const LoopParams& p, const Cx& c, const float* s_w,
-                                         const u64* rin) {
-    const int u0 = c.uh0, nu = c.nuh;
-    Pre q;
-    const int ub = c.w + LP_CW * c.lane;
-    if (ub < nu) {
-        q.a = gld(s_w + u0 + ub);
-        if (rin) q.r = ll_load(rin + u0 + ub);
-    }
-    return q;
-}
-
-template <int C>
-__device__ bool phase_resid(const LoopParams& p, Cx& c, int line0, const u64* rin, uint32_t rtag,
-                            const float* emb, u64* out, uint32_t tag,
-                            const float (&xr)[LP_CMAX][16], const Pre& pre, int where) {
-    int nmy;
-    const int u0 = c.uh0, nu = c.nuh;
-    float acc[LP_MU_ROW][1];
-    if (!phase_dots<C, 1, LP_MU_ROW>(p, c, line0, nu, xr, acc, nmy, where)) return false;
-#pragma unroll
-    for (int m = 0; m < LP_MU_ROW; m++) {
-        if (m >= nmy) break;
-        const int n = u0 + c.w + LP_CW * m;
-        float res;
-        if (rin) {
-            const uint32_t rt = (uint32_t)__builtin_amdgcn_readlane((int)(pre.r >> 32), m);
-            res = __int_as_float(__builtin_amdgcn_readlane((int)(uint32_t)pre.r, m));
-            if (rt != rtag && !ll_poll1(p, c, rin + n, rtag, res, where + 1)) return false;
-        } else {
-            res = gld(emb + n);
-        }
-        const float v = res + acc[m][0] * rlane(pre.a, m);
-        if (c.lane == 0) ll_store(out + n, v, tag);
-    }
-    return true;
-}
-
-// gate_up: pairs (i, i + I) -> act[i] = silu(g) * u.
+// gate_up (P6): this wave's 3 pairs (i, i + I), i = 384 g + 12 j + w + 4 m,
+// lines line0 + 2 (w + 4 m) + r -> act = silu(g) * u.
 __device__ __forceinline__ Pre pre_gu(const LoopParams& p, const Cx& c, int l) {
-    const int u0 = c.ui0, nu = c.nui;
     Pre q;
-    const int ub = c.w + LP_CW * (c.lane >> 1);
-    if (ub < nu) q.a = gld(p.layers[l].s_gu + u0 + ub + (c.lane & 1) * p.I);
+    if (c.lane < 6) {
+        const int i = LP_IX * c.g + 12 * c.j + c.w + LP_CW * (c.lane >> 1);
+        q.a = gld(p.layers[l].s_gu + i + (c.lane & 1) * LP_I);
+    }
     return q;
 }
 
-template <int C>
-__device__ bool phase_gu(const LoopParams& p, Cx& c, int line0, uint32_t tag,
-                         const float (&xr)[LP_CMAX][16], float nscale, const Pre& pre) {
-    int nmy;
-    const int u0 = c.ui0, nu = c.nui;
-    float acc[LP_MU_GU][2];
-    if (!phase_dots<C, 2, LP_MU_GU>(p, c, line0, nu, xr, acc, nmy, 40)) return false;
+__device__ bool phase_gu(const LoopParams& p, Cx& c, int line0, uint32_t tag, const float (&xv)[16],
+                         float nscale, const Pre& pre) {
+    if (!wait_upto(p, c, line0 + 2 * (c.w + 2 * LP_CW) + 1, 40)) return false;
+    lp_v4i wv[3][2];
 #pragma unroll
-    for (int m = 0; m < LP_MU_GU; m++) {
-        if (m >= nmy) break;
-        const float g = acc[m][0] * rlane(pre.a, 2 * m) * nscale;
-        const float up = acc[m][1] * rlane(pre.a, 2 * m + 1) * nscale;
-        if (c.lane == 0) ll_store(p.act + u0 + c.w + LP_CW * m, g * __frcp_rn(1.0f + __expf(-g)) * up, tag);
+    for (int m = 0; m < 3; m++)
+#pragma unroll
+        for (int r = 0; r < 2; r++) wv[m][r] = ring_line(c, line0 + 2 * (c.w + LP_CW * m) + r);
+    float acc[6];
+#pragma unroll
+    for (int m = 0; m < 3; m++)
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            float s[4] = {0.f, 0.f, 0.f, 0.f};
+            lp_dot16s(xv, wv[m][r], s);
+            acc[2 * m + r] = (s[0] + s[1]) + (s[2] + s[3]);
+        }
+    wsum_n<6>(acc);
+#pragma unroll
+    for (int m = 0; m < 3; m++) {
+        const float g = acc[2 * m] * rlane(pre.a, 2 * m) * nscale;
+        const float up = acc[2 * m + 1] * rlane(pre.a, 2 * m + 1) * nscale;
+        if (c.lane == 0)
+            st_l2(p.act + c.g * LP_IX + 12 * c.j + c.w + LP_CW * m,
+                  g * __frcp_rn(1.0f + __expf(-g)) * up, tag);
     }
     return true;
+}
+
+// o_proj partial (P4): rows 32 j + 8 w + 4 c' + (lane >> 4) (c' = 0, 1) over the
+// 256 columns of KV head g's query heads; lane holds columns 16 (lane & 15) ..
+// +16 of its row in line line0 + 2 w + c'. x = the merged head output in LDS;
+// so[c'] = the row's output scale.
+__device__ bool phase_opart(const LoopParams& p, Cx& c, int line0, uint32_t tag, const float (&so)[2]) {
+    if (!wait_upto(p, c, line0 + 2 * c.w + 1, 32)) return false;
+    float xv[16];
+    load_row16(c.os + 16 * (c.lane & 15), xv);
+    float acc[2];
+#pragma unroll
+    for (int cc = 0; cc < 2; cc++) {
+        const lp_v4i wv = ring_line(c, line0 + 2 * c.w + cc);
+        float s[4] = {0.f, 0.f, 0.f, 0.f};
+        lp_dot16s(xv, wv, s);
+        acc[cc] = sum16((s[0] + s[1]) + (s[2] + s[3]));
+    }
+#pragma unroll
+    for (int cc = 0; cc < 2; cc++) {
+        const int r = 4 * cc + (c.lane >> 4);                 // row within the wave's 8
+        const float v = acc[cc] * so[cc];
+        if ((c.lane & 15) == 0) ll_store(p.opart + c.g * LP_H + 32 * c.j + 8 * c.w + r, v, tag);
+    }
+    return true;
+}
+
+// down partial (P7): rows 32 j + 8 w + (lane >> 3) over XCD g's 384 channels;
+// line line0 + 3 w + cc holds channels 128 cc .. +128 of the wave's 8 rows,
+// lane: 16 channels 128 cc + 16 (lane & 7).
+__device__ bool phase_dpart(const LoopParams& p, Cx& c, int line0, uint32_t atag, uint32_t tag,
+                            float sd) {
+    float av[6];
+    const u64* src = p.act + c.g * LP_IX + c.lane;
+    for (uint32_t it = 0;; it++) {
+        u64 v[6];
+        ld_l2_6s(src, v);
+        if (__all(tags_ok(v, atag))) {
+#pragma unroll
+            for (int i = 0; i < 6; i++) av[i] = __uint_as_float((uint32_t)v[i]);
+            break;
+        }
+        if (!keep_waiting(p, c, it, LP_POLL_LIMIT, 7)) return false;
+    }
+    float* aw = c.acts + c.w * LP_IX;
+#pragma unroll
+    for (int i = 0; i < 6; i++) aw[c.lane + 64 * i] = av[i];
+    if (!wait_upto(p, c, line0 + 3 * c.w + 2, 50)) return false;
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int cc = 0; cc < 3; cc++) {
+        float xv[16];
+        load_row16(aw + 128 * cc + 16 * (c.lane & 7), xv);
+        lp_dot16s(xv, ring_line(c, line0 + 3 * c.w + cc), s);
+    }
+    const float v = sum8((s[0] + s[1]) + (s[2] + s[3])) * sd;
+    if ((c.lane & 7) == 0) ll_store(p.dpart + c.g * LP_H + 32 * c.j + 8 * c.w + (c.lane >> 3), v, tag);
+    return true;
+}
+
+// ------------------------------------------------------------- attention
+struct AttRange {
+    int t0, n, tw0, tw1;
+};
+
+// Positions of attention split s (workgroup j = s of XCD g) and of wave w in it.
+__device__ __forceinline__ AttRange att_range(int s, int w, int pos) {
+    AttRange r;
+    const int Lc = pos + 1, cs = (Lc + LP_S - 1) / LP_S;
+    r.t0 = s * cs;
+    r.n = min(cs, Lc - r.t0);
+    const int nw = r.n > 0 ? (r.n + LP_CW - 1) / LP_CW : 0;
+    r.tw0 = r.t0 + w * nw;
+    r.tw1 = r.n > 0 ? min(r.t0 + r.n, r.tw0 + nw) : r.tw0;
+    return r;
+}
+
+// Partial attention (P3) of split s = j over this workgroup's positions, for
+// both query heads of KV head g. Lane layout: 8 lanes per position (16 dims
+// each), 8 positions per pass; online softmax per lane group. The current
+// position's k/v (this step's, from the tagged copy) is one extra step, done by
+// lane group 0 of the wave whose range holds it. The per-lane-group partials
+// (scaled to the wave's max) go to LDS and one pass over them combines the 32
+// lane groups of the workgroup; the split's (max, sum, o) is stored tagged.
+__device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t qtag, uint32_t tag) {
+    constexpr int G = LP_G;
+    const AttRange r = att_range(c.j, c.w, pos);
+    if (r.n <= 0) return true;
+    const int jj = c.lane >> 3, part = c.lane & 7;
+    const int npos = max(0, r.tw1 - r.tw0), passes = (npos + 7) / 8;
+    float* stg = c.stg + c.w * LP_STG;
+    const bool has_cur = pos >= r.tw0 && pos < r.tw1;
+    // Keys/values of the earlier positions (final since the steps that wrote
+    // them): issued before the q poll, so their latency hides behind it.
+    const float* kb = p.kc + ((int64_t)l * LP_NX + c.g) * p.max_seq * LP_D;
+    const float* vb = p.vc + ((int64_t)l * LP_NX + c.g) * p.max_seq * LP_D;
+    float kp[LP_NPF][16], vp[LP_NPF][16];
+#pragma unroll
+    for (int ps = 0; ps < LP_NPF; ps++) {
+        const int tp = r.tw0 + ps * 8 + jj;
+        if (tp < r.tw1 && tp != pos) {
+            load_row16g(kb + (int64_t)tp * LP_D + part * 16, kp[ps]);
+            load_row16g(vb + (int64_t)tp * LP_D + part * 16, vp[ps]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) { kp[ps][i] = 0.f; vp[ps][i] = 0.f; }
+        }
+    }
+    {
+        // q of the two query heads and the current k/v row, in one poll
+        // (words lane + 64 i: q for i < 4, then k, v)
+        const u64* src = p.qkv + c.g * LP_QKVX + c.lane;
+        for (uint32_t it = 0;; it++) {
+            u64 v[8];
+            ld_l2_8s(src, v);
+            bool ok = true;
+#pragma unroll
+            for (int i = 0; i < 8; i++) ok &= (i < 2 * G || has_cur) ? (uint32_t)(v[i] >> 32) == qtag : true;
+            if (__all(ok)) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) stg[c.lane + 64 * i] = __uint_as_float((uint32_t)v[i]);
+                break;
+            }
+            if (!keep_waiting(p, c, it, LP_POLL_LIMIT, 20)) return false;
+        }
+    }
+    cbar();
+    float qv[G][16];
+#pragma unroll
+    for (int h = 0; h < G; h++) load_row16(stg + h * LP_D + part * 16, qv[h]);
+    float m[G], lsum[G], o[G][16];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        m[h] = -INFINITY;
+        lsum[h] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) o[h][i] = 0.f;
+    }
+    auto step = [&](const float (&kk)[16], const float (&vv)[16], bool valid) {
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            float d4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < 16; i++) d4[i & 3] = fmaf(qv[h][i], kk[i], d4[i & 3]);
+            float s = sum8((d4[0] + d4[1]) + (d4[2] + d4[3])) * p.att_scale;
+            s = valid ? s : -INFINITY;
+            const float mn = fmaxf(m[h], s);
+            const float corr = mn == -INFINITY ? 1.f : __expf(m[h] - mn);
+            const float e = s == -INFINITY ? 0.f : __expf(s - mn);
+            lsum[h] = fmaf(lsum[h], corr, e);
+#pragma unroll
+            for (int i = 0; i < 16; i++) o[h][i] = fmaf(o[h][i], corr, e * vv[i]);
+            m[h] = mn;
+        }
+    };
+#pragma unroll
+    for (int ps = 0; ps < LP_NPF; ps++) {
+        const int tp = r.tw0 + ps * 8 + jj;
+        step(kp[ps], vp[ps], ps < passes && tp < r.tw1 && tp != pos);
+    }
+    for (int ps = LP_NPF; ps < passes; ps++) {
+        const int tp = r.tw0 + ps * 8 + jj;
+        const bool valid = tp < r.tw1 && tp != pos;
+        float kk[16], vv[16];
+        if (valid) {
+            load_row16g(kb + (int64_t)tp * LP_D + part * 16, kk);
+            load_row16g(vb + (int64_t)tp * LP_D + part * 16, vv);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) { kk[i] = 0.f; vv[i] = 0.f; }
+        }
+        step(kk, vv, valid);
+    }
+    if (has_cur) {
+        float kk[16], vv[16];
+        load_row16(stg + G * LP_D + part * 16, kk);
+        load_row16(stg + G * LP_D + LP_D + part * 16, vv);
+        step(kk, vv, jj == 0);
+    }
+    // Scale every lane group to the wave's max; partials to LDS:
+    // po[w][h][jj][128], wave max / sum in pm / pl.
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        const float mw = wmax(m[h]);
+        const float f = m[h] == -INFINITY ? 0.f : __expf(m[h] - mw);
+        const float lw = wsum(part == 0 ? lsum[h] * f : 0.f);
+        float* dst = c.attp + ((c.w * G + h) * 8 + jj) * LP_D + part * 16;
+#pragma unroll
+        for (int i = 0; i < 16; i += 4)
+            *(float4*)(dst + i) = make_float4(o[h][i] * f, o[h][i + 1] * f, o[h][i + 2] * f, o[h][i + 3] * f);
+        if (c.lane == 0) {
+            c.attm[c.w * G + h] = mw;
+            c.attm[LP_CW * G + c.w * G + h] = lw;
+        }
+    }
+    if (!csync(p, c, 22)) return false;
+    // combine: one (head, dim) per thread of the four waves; partial layout
+    // att[g][h][split][max, sum, o[128]]
+    u64* dst = p.att + ((int64_t)c.g * G * LP_S + c.j) * LP_PART;
+    for (int e = c.w * 64 + c.lane; e < G * LP_D; e += LP_CW * 64) {
+        const int h = e >> 7, d = e & 127;
+        float M = -INFINITY;
+#pragma unroll
+        for (int wv = 0; wv < LP_CW; wv++) M = fmaxf(M, c.attm[wv * G + h]);
+        float acc = 0.f, den = 0.f;
+#pragma unroll
+        for (int wv = 0; wv < LP_CW; wv++) {
+            const float mw = c.attm[wv * G + h];
+            const float F = mw == -INFINITY ? 0.f : __expf(mw - M);
+            const float* src = c.attp + (wv * G + h) * 8 * LP_D + d;
+            float sj = 0.f;
+#pragma unroll
+            for (int q = 0; q < 8; q++) sj += src[q * LP_D];
+            acc = fmaf(F, sj, acc);
+            den = fmaf(F, c.attm[LP_CW * G + wv * G + h], den);
+        }
+        st_l2(dst + h * LP_S * LP_PART + 2 + d, acc, tag);
+        if (d == 0) {
+            st_l2(dst + h * LP_S * LP_PART, M, tag);
+            st_l2(dst + h * LP_S * LP_PART + 1, den, tag);
+        }
+    }
+    return true;
+}
+
+// Merge (start of P4) of the active splits of KV head g's query heads into the
+// head output o_g [2][128] in LDS: wave w merges head w >> 1, dims
+// 64 (w & 1) + lane, in split order; then the four waves meet.
+__device__ bool merge_heads(const LoopParams& p, Cx& c, int pos, uint32_t ptag) {
+    const int hh = c.w >> 1, d = 64 * (c.w & 1) + c.lane;
+    const int Lc = pos + 1, cs = (Lc + LP_S - 1) / LP_S, sact = (Lc + cs - 1) / cs;
+    float mm[LP_S], ll[LP_S], oo[LP_S];
+    const u64* base = p.att + (int64_t)(c.g * LP_G + hh) * LP_S * LP_PART;
+    for (uint32_t it = 0;; it++) {
+        u64 ml[16], ov[8];   // (max, sum) of split s at ml[2s], ml[2s+1]; o[d] of split s at ov[s]
+        ld_l2_merge(base, base + 4 * LP_PART, base + 2 + d, base + 4 * LP_PART + 2 + d, ml, ov);
+        bool ok = true;
+#pragma unroll
+        for (int s = 0; s < LP_S; s++) {
+            if (s >= sact) continue;
+            ok &= (uint32_t)(ml[2 * s] >> 32) == ptag && (uint32_t)(ml[2 * s + 1] >> 32) == ptag &&
+                  (uint32_t)(ov[s] >> 32) == ptag;
+            mm[s] = __uint_as_float((uint32_t)ml[2 * s]);
+            ll[s] = __uint_as_float((uint32_t)ml[2 * s + 1]);
+            oo[s] = __uint_as_float((uint32_t)ov[s]);
+        }
+        if (__all(ok)) break;
+        if (!keep_waiting(p, c, it, LP_POLL_LIMIT, 30)) return false;
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < LP_S; s++)
+        if (s < sact) M = fmaxf(M, mm[s]);
+    float den = 0.f, a = 0.f;
+#pragma unroll
+    for (int s = 0; s < LP_S; s++) {
+        if (s >= sact) continue;
+        const float f = mm[s] == -INFINITY ? 0.f : __expf(mm[s] - M);
+        den += f * ll[s];
+        a += f * oo[s];
+    }
+    c.os[hh * LP_D + d] = a * __frcp_rn(den);
+    return csync(p, c, 31);
 }
 
 typedef __attribute__((address_space(3))) float lds_f32;
@@ -707,13 +1033,13 @@ __device__ __noinline__ void phase_lm(const int8_t* lm, const float* s_lm, float
 // Argmax over the workgroups' keys of the lm phase tagged `tag` (first max,
 // tensor_ops.c:649-662).
 __device__ bool argmax_id(const LoopParams& p, Cx& c, uint32_t tag, int& id) {
-    const int n = (p.nblk + 63) / 64;
+    const int n = (LP_NBLK + 63) / 64;
     for (uint32_t it = 0;; it++) {
         u64 best = 0;
         bool ok = true;
         for (int i = 0; i < n; i++) {
             const int j = c.lane + 64 * i;
-            if (j >= p.nblk) continue;
+            if (j >= LP_NBLK) continue;
             const u64 k = ll_load(p.keys + j);
             ok &= (uint32_t)(k & 0x3FFF) == (tag & 0x3FFFu);
             best = k > best ? k : best;
@@ -727,249 +1053,9 @@ __device__ bool argmax_id(const LoopParams& p, Cx& c, uint32_t tag, int& id) {
     }
 }
 
-// ------------------------------------------------------------- attention
-struct AttRange {
-    int s, kvh, t0, n, tw0, tw1;
-};
-
-__device__ __forceinline__ AttRange att_range(const LoopParams& p, int w, int pos) {
-    AttRange r;
-    r.kvh = blockIdx.x / LP_S;
-    r.s = blockIdx.x % LP_S;
-    const int Lc = pos + 1, cs = (Lc + LP_S - 1) / LP_S;
-    r.t0 = r.s * cs;
-    r.n = min(cs, Lc - r.t0);
-    const int nw = r.n > 0 ? (r.n + LP_CW - 1) / LP_CW : 0;
-    r.tw0 = r.t0 + w * nw;
-    r.tw1 = r.n > 0 ? min(r.t0 + r.n, r.tw0 + nw) : r.tw0;
-    return r;
-}
-
-__device__ __forceinline__ void load_row16(const float* src, float (&d)[16]) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float4 a = *(const float4*)(src + 4 * i);
-        d[4 * i] = a.x; d[4 * i + 1] = a.y; d[4 * i + 2] = a.z; d[4 * i + 3] = a.w;
-    }
-}
-// The same from global memory (the KV cache), through the global address space.
-typedef float lp_f4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ void load_row16g(const float* src, float (&d)[16]) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const lp_f4 a = gld((const lp_f4*)(src + 4 * i));
-        d[4 * i] = a[0]; d[4 * i + 1] = a[1]; d[4 * i + 2] = a[2]; d[4 * i + 3] = a[3];
-    }
-}
-
-// Partial attention of split s over this workgroup's positions. Lane layout:
-// 8 lanes per position (16 dims each), 8 positions per pass, both query heads
-// of the KV head per pass; online softmax per lane group. The current
-// position's k/v (this step's, from the tagged copy) is one extra step, done by
-// lane group 0 of the wave whose range holds it. The per-lane-group partials
-// (scaled to the wave's max) go to LDS and one pass over them combines the 32
-// lane groups of the workgroup; the split's (max, sum, o) is stored tagged.
-__device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t qtag, uint32_t tag) {
-    constexpr int G = LP_G;
-    const AttRange r = att_range(p, c.w, pos);
-    if (r.n <= 0) return true;
-    const int j = c.lane >> 3, part = c.lane & 7;
-    const int npos = max(0, r.tw1 - r.tw0), passes = (npos + 7) / 8;
-    float* stg = c.stg + c.w * LP_STG;
-    const bool has_cur = pos >= r.tw0 && pos < r.tw1;
-    // Keys/values of the earlier positions (final since the steps that wrote
-    // them): issued before the q poll, so their latency hides behind it.
-    const float* kb = p.kc + ((int64_t)l * p.nkv + r.kvh) * p.max_seq * 128;
-    const float* vb = p.vc + ((int64_t)l * p.nkv + r.kvh) * p.max_seq * 128;
-    float kp[LP_NPF][16], vp[LP_NPF][16];
-#pragma unroll
-    for (int ps = 0; ps < LP_NPF; ps++) {
-        const int tp = r.tw0 + ps * 8 + j;
-        if (tp < r.tw1 && tp != pos) {
-            load_row16g(kb + (int64_t)tp * 128 + part * 16, kp[ps]);
-            load_row16g(vb + (int64_t)tp * 128 + part * 16, vp[ps]);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; i++) { kp[ps][i] = 0.f; vp[ps][i] = 0.f; }
-        }
-    }
-    {
-        // q of this KV head's G query heads, and the current k/v row, in one poll
-        for (uint32_t it = 0;; it++) {
-            u64 v[2 * G + 4];
-            bool ok = true;
-#pragma unroll
-            for (int i = 0; i < 2 * G; i++) {
-                v[i] = ll_load(p.q + r.kvh * G * 128 + c.lane + 64 * i);
-                ok &= (uint32_t)(v[i] >> 32) == qtag;
-            }
-            if (has_cur) {
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    v[2 * G + i] = ll_load(p.kv + r.kvh * 256 + c.lane + 64 * i);
-                    ok &= (uint32_t)(v[2 * G + i] >> 32) == qtag;
-                }
-            }
-            if (__all(ok)) {
-#pragma unroll
-                for (int i = 0; i < 2 * G; i++) stg[c.lane + 64 * i] = __uint_as_float((uint32_t)v[i]);
-                if (has_cur) {
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        stg[G * 128 + c.lane + 64 * i] = __uint_as_float((uint32_t)v[2 * G + i]);
-                }
-                break;
-            }
-            if (!keep_waiting(p, c, it, LP_POLL_LIMIT, 20)) return false;
-        }
-    }
-    cbar();
-    float qv[G][16];
-#pragma unroll
-    for (int h = 0; h < G; h++) load_row16(stg + h * 128 + part * 16, qv[h]);
-    float m[G], lsum[G], o[G][16];
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        m[h] = -INFINITY;
-        lsum[h] = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; i++) o[h][i] = 0.f;
-    }
-    auto step = [&](const float (&kk)[16], const float (&vv)[16], bool valid) {
-#pragma unroll
-        for (int h = 0; h < G; h++) {
-            float d4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int i = 0; i < 16; i++) d4[i & 3] = fmaf(qv[h][i], kk[i], d4[i & 3]);
-            float s = sum8((d4[0] + d4[1]) + (d4[2] + d4[3])) * p.att_scale;
-            s = valid ? s : -INFINITY;
-            const float mn = fmaxf(m[h], s);
-            const float corr = mn == -INFINITY ? 1.f : __expf(m[h] - mn);
-            const float e = s == -INFINITY ? 0.f : __expf(s - mn);
-            lsum[h] = fmaf(lsum[h], corr, e);
-#pragma unroll
-            for (int i = 0; i < 16; i++) o[h][i] = fmaf(o[h][i], corr, e * vv[i]);
-            m[h] = mn;
-        }
-    };
-#pragma unroll
-    for (int ps = 0; ps < LP_NPF; ps++) {
-        const int tp = r.tw0 + ps * 8 + j;
-        step(kp[ps], vp[ps], ps < passes && tp < r.tw1 && tp != pos);
-    }
-    for (int ps = LP_NPF; ps < passes; ps++) {
-        const int tp = r.tw0 + ps * 8 + j;
-        const bool valid = tp < r.tw1 && tp != pos;
-        float kk[16], vv[16];
-        if (valid) {
-            load_row16g(kb + (int64_t)tp * 128 + part * 16, kk);
-            load_row16g(vb + (int64_t)tp * 128 + part * 16, vv);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; i++) { kk[i] = 0.f; vv[i] = 0.f; }
-        }
-        step(kk, vv, valid);
-    }
-    if (has_cur) {
-        float kk[16], vv[16];
-        load_row16(stg + G * 128 + part * 16, kk);
-        load_row16(stg + G * 128 + 128 + part * 16, vv);
-        step(kk, vv, j == 0);
-    }
-    // Scale every lane group to the wave's max; partials to LDS:
-    // po[w][h][j][128], wave max / sum in pm / pl.
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        const float mw = wmax(m[h]);
-        const float f = m[h] == -INFINITY ? 0.f : __expf(m[h] - mw);
-        const float lw = wsum(part == 0 ? lsum[h] * f : 0.f);
-        float* dst = c.attp + ((c.w * G + h) * 8 + j) * 128 + part * 16;
-#pragma unroll
-        for (int i = 0; i < 16; i += 4)
-            *(float4*)(dst + i) = make_float4(o[h][i] * f, o[h][i + 1] * f, o[h][i + 2] * f, o[h][i + 3] * f);
-        if (c.lane == 0) {
-            c.attm[c.w * G + h] = mw;
-            c.attm[LP_CW * G + c.w * G + h] = lw;
-        }
-    }
-    if (!csync(p, c, 22)) return false;
-    // combine: one (head, dim) per thread of the four waves
-    u64* dst = p.part + (int64_t)(r.kvh * LP_S + r.s) * G * LP_PART;
-    for (int e = c.w * 64 + c.lane; e < G * 128; e += LP_CW * 64) {
-        const int h = e >> 7, d = e & 127;
-        float M = -INFINITY;
-#pragma unroll
-        for (int wv = 0; wv < LP_CW; wv++) M = fmaxf(M, c.attm[wv * G + h]);
-        float acc = 0.f, den = 0.f;
-#pragma unroll
-        for (int wv = 0; wv < LP_CW; wv++) {
-            const float mw = c.attm[wv * G + h];
-            const float F = mw == -INFINITY ? 0.f : __expf(mw - M);
-            const float* src = c.attp + (wv * G + h) * 8 * 128 + d;
-            float sj = 0.f;
-#pragma unroll
-            for (int jj = 0; jj < 8; jj++) sj += src[jj * 128];
-            acc = fmaf(F, sj, acc);
-            den = fmaf(F, c.attm[LP_CW * G + wv * G + h], den);
-        }
-        ll_store(dst + h * LP_PART + 2 + d, acc, tag);
-        if (d == 0) {
-            ll_store(dst + h * LP_PART, M, tag);
-            ll_store(dst + h * LP_PART + 1, den, tag);
-        }
-    }
-    return true;
-}
-
-// Merge of the active splits of query head h = kvh*G + w (wave w < G of the
-// split-0 workgroup of each KV head), in split order; tagged head output.
-__device__ bool phase_merge(const LoopParams& p, Cx& c, int pos, uint32_t ptag, uint32_t tag) {
-    const int G = p.nq / p.nkv;
-    const int kvh = blockIdx.x / LP_S;
-    const int h = kvh * G + c.w;
-    const int Lc = pos + 1, cs = (Lc + LP_S - 1) / LP_S, sact = (Lc + cs - 1) / cs;
-    float mm[LP_S], ll[LP_S], o0[LP_S], o1[LP_S];
-    for (uint32_t it = 0;; it++) {
-        bool ok = true;
-#pragma unroll
-        for (int s = 0; s < LP_S; s++) {
-            if (s >= sact) continue;
-            const u64* src = p.part + ((int64_t)(kvh * LP_S + s) * G + c.w) * LP_PART;
-            const u64 a = ll_load(src), b = ll_load(src + 1), x0 = ll_load(src + 2 + c.lane),
-                      x1 = ll_load(src + 2 + 64 + c.lane);
-            ok &= (uint32_t)(a >> 32) == ptag && (uint32_t)(b >> 32) == ptag &&
-                  (uint32_t)(x0 >> 32) == ptag && (uint32_t)(x1 >> 32) == ptag;
-            mm[s] = __uint_as_float((uint32_t)a);
-            ll[s] = __uint_as_float((uint32_t)b);
-            o0[s] = __uint_as_float((uint32_t)x0);
-            o1[s] = __uint_as_float((uint32_t)x1);
-        }
-        if (__all(ok)) break;
-        if (!keep_waiting(p, c, it, LP_POLL_LIMIT, 30)) return false;
-    }
-    float M = -INFINITY;
-#pragma unroll
-    for (int s = 0; s < LP_S; s++)
-        if (s < sact) M = fmaxf(M, mm[s]);
-    float den = 0.f, a0 = 0.f, a1 = 0.f;
-#pragma unroll
-    for (int s = 0; s < LP_S; s++) {
-        if (s >= sact) continue;
-        const float f = mm[s] == -INFINITY ? 0.f : __expf(mm[s] - M);
-        den += f * ll[s];
-        a0 += f * o0[s];
-        a1 += f * o1[s];
-    }
-    const float inv = __frcp_rn(den);
-    ll_store(p.merged + h * 128 + c.lane, a0 * inv, tag);
-    ll_store(p.merged + h * 128 + 64 + c.lane, a1 * inv, tag);
-    return true;
-}
-
-// ----------------------------------------------------------- wave roles
 __device__ void stream_role(const LoopParams& p, Cx& c) {
     const int sw = c.w - LP_CW;
-    const int8_t* src = p.stream + (int64_t)blockIdx.x * p.lpt * 1024 + c.lane * 16;
+    const int8_t* src = p.stream + (int64_t)c.role * p.lpt * 1024 + c.lane * 16;
     typedef __attribute__((address_space(3))) void lds_t;
     int G = 0, inflight = 0, published = 0;
     bool ok = true;
@@ -1015,14 +1101,19 @@ __device__ void stream_role(const LoopParams& p, Cx& c) {
     lds_st(&c.ready[sw], published + inflight);
 }
 
-template <int CH, int CO, int CI>
+// ----------------------------------------------------------- compute waves
+__device__ __forceinline__ void gld16(const float* src, float (&d)[16]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const lp_f4 a = gld((const lp_f4*)(src + 4 * i));
+        d[4 * i] = a[0]; d[4 * i + 1] = a[1]; d[4 * i + 2] = a[2]; d[4 * i + 3] = a[3];
+    }
+}
+
 __device__ void compute_role(const LoopParams& p, Cx& c) {
     __builtin_amdgcn_s_setprio(2);
-    const int H = p.H, KO = p.nq * 128, I = p.I;
-    const bool att_blk = (int)blockIdx.x < p.nkv * LP_S;
-    const bool merger = att_blk && (blockIdx.x % LP_S) == 0 && c.w < p.nq / p.nkv;
+    const bool att_blk = c.j < LP_S;
     int Gl = 0;        // first ring line of the current token
-    int buf = 0;
     int id = 0;
     for (int t = 0; t < p.n_steps; t++) {
         asm volatile("" : "+v"(c.lane));
@@ -1031,115 +1122,107 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
         if (t == 0 || pos < p.prompt_len) {
             id = p.ids[pos];
         } else {
-            if (!argmax_id(p, c, tag_of(p, t - 1, p.L, 0), id)) return;
-            if (blockIdx.x == 0 && c.w == 0 && c.lane == 0) p.ids[pos] = id;
+            if (!argmax_id(p, c, tag_of(p, t - 1, p.L, 1), id)) return;
+            if (c.role == 0 && c.w == 0 && c.lane == 0) p.ids[pos] = id;
         }
         if (id < 0 || id >= p.V) id = 0;
-        const float* emb = p.embed + (int64_t)id * H;
+        const float* emb = p.embed + (int64_t)id * LP_H;
         for (int l = 0; l < p.L; l++) {
             // Opaque per-iteration copy of the lane id: keeps the compiler from
             // hoisting every per-lane address of the loop body out of the loop
             // (they would stay live across all phases and spill).
             asm volatile("" : "+v"(c.lane));
             const LoopLayer& Lw = p.layers[l];
-            const int lb = Gl + l * p.lpl;
-            const uint32_t tq = tag_of(p, t, l, PH_QKV);
-            // ---- qkv: x = embed row (layer 0) or the previous layer's output
+            const int lb = Gl + l * LP_LPL;
+            // ---- P1 + P2: x'' (embedding row or reduced), RMSNorm, q/k/v of head g
             {
-                constexpr int NX = CH * 4;
                 cbar();   // the preloads must not move above the previous phase
                 const Pre pq = pre_qkv(p, c, l, pos);
-                float v[NX], g[NX], xr[LP_CMAX][16], nscale;
-#pragma unroll
-                for (int i = 0; i < NX; i++) g[i] = gld(Lw.in_norm + c.w * (H / 4) + c.lane + 64 * i);
+                float gam[16], xv[16], nscale;
+                gld16(Lw.in_norm + 16 * c.lane, gam);
                 if (l == 0) {
+                    gld16(emb + 16 * c.lane, xv);
+                    float ss = 0.f;
+                    float* xw = c.xw + c.w * LP_H + 16 * c.lane;
 #pragma unroll
-                    for (int i = 0; i < NX; i++) v[i] = gld(emb + c.w * (H / 4) + c.lane + 64 * i);
-                } else if (!ll_poll<NX>(p, c, p.xa + c.w * (H / 4), NX, tag_of(p, t, l - 1, PH_DN), v, 1)) {
-                    return;
+                    for (int i = 0; i < 16; i += 4) {
+                        *(float4*)(xw + i) = make_float4(xv[i], xv[i + 1], xv[i + 2], xv[i + 3]);
+                        ss += xv[i] * xv[i] + xv[i + 1] * xv[i + 1] + xv[i + 2] * xv[i + 2] +
+                              xv[i + 3] * xv[i + 3];
+                    }
+#pragma unroll
+                    for (int i = 0; i < 16; i++) xv[i] *= gam[i];
+                    nscale = rsqrtf(wsum(ss) * (1.0f / (float)LP_H) + p.eps);
+                } else {
+                    if (!reduce_x(p, c, p.dpart, tag_of(p, t, l - 1, PH_DP), p.xr, tag_of(p, t, l, PH_XR), 1))
+                        return;
+                    if (!gather_x(p, c, p.xr, tag_of(p, t, l, PH_XR), gam, xv, nscale, 2)) return;
                 }
-                if (!stage_x<NX, CH>(p, c, buf, H, v, g, true, xr, nscale, 2)) return;
-                buf ^= 1;
-                if (!phase_qkv<CH>(p, c, l, pos, lb, tq, xr, nscale, pq)) return;
-                set_done(c, lb + p.off_o);
+                if (!phase_qkv(p, c, l, pos, lb, tag_of(p, t, l, PH_QKV), xv, nscale, pq)) return;
+                set_done(c, lb + LP_OFF_O);
             }
-            // ---- attention partials and merge
-            if (att_blk && !phase_att(p, c, l, pos, tq, tag_of(p, t, l, PH_ATT))) return;
-            if (merger && !phase_merge(p, c, pos, tag_of(p, t, l, PH_ATT), tag_of(p, t, l, PH_MERGE)))
+            // ---- P3: attention partials of head g's splits
+            if (att_blk && !phase_att(p, c, l, pos, tag_of(p, t, l, PH_QKV), tag_of(p, t, l, PH_ATT)))
                 return;
-            // ---- o_proj (+ residual)
+            // ---- P4: merge, o_proj partial over head g's columns
             {
-                constexpr int NX = CO * 4;
-                float v[NX], g[NX], xr[LP_CMAX][16], nscale;
-                const u64* rin = l == 0 ? nullptr : p.xa;
-                cbar();   // the preloads must not move above the previous phase
-                const Pre pr = pre_resid(p, c, Lw.s_o, rin);
-                if (!ll_poll<NX>(p, c, p.merged + c.w * (KO / 4), NX, tag_of(p, t, l, PH_MERGE), v, 3))
-                    return;
-                if (!stage_x<NX, CO>(p, c, buf, KO, v, g, false, xr, nscale, 4)) return;
-                buf ^= 1;
-                if (!phase_resid<CO>(p, c, lb + p.off_o, rin, tag_of(p, t, l - 1, PH_DN), emb, p.xb,
-                                     tag_of(p, t, l, PH_O), xr, pr, 32))
-                    return;
-                set_done(c, lb + p.off_gu);
+                const int r0 = 32 * c.j + 8 * c.w + (c.lane >> 4);
+                const float so[2] = {gld(Lw.s_o + r0), gld(Lw.s_o + r0 + 4)};
+                if (!merge_heads(p, c, pos, tag_of(p, t, l, PH_ATT))) return;
+                if (!phase_opart(p, c, lb + LP_OFF_O, tag_of(p, t, l, PH_OP), so)) return;
+                set_done(c, lb + LP_OFF_GU);
             }
-            // ---- gate_up + SwiGLU
+            // ---- P5 + P6: x' (reduced), RMSNorm, gate_up + SwiGLU for XCD g's channels
             {
-                constexpr int NX = CH * 4;
-                float v[NX], g[NX], xr[LP_CMAX][16], nscale;
-#pragma unroll
-                for (int i = 0; i < NX; i++) g[i] = gld(Lw.post_norm + c.w * (H / 4) + c.lane + 64 * i);
-                cbar();   // the preloads must not move above the previous phase
+                cbar();
                 const Pre pg = pre_gu(p, c, l);
-                if (!ll_poll<NX>(p, c, p.xb + c.w * (H / 4), NX, tag_of(p, t, l, PH_O), v, 5)) return;
-                if (!stage_x<NX, CH>(p, c, buf, H, v, g, true, xr, nscale, 6)) return;
-                buf ^= 1;
-                if (!phase_gu<CH>(p, c, lb + p.off_gu, tag_of(p, t, l, PH_GU), xr, nscale, pg)) return;
-                set_done(c, lb + p.off_dn);
-            }
-            // ---- down (+ residual)
-            {
-                constexpr int NX = CI * 4;
-                float v[NX], g[NX], xr[LP_CMAX][16], nscale;
-                cbar();   // the preloads must not move above the previous phase
-                const Pre pd = pre_resid(p, c, Lw.s_down, p.xb);
-                if (!ll_poll<NX>(p, c, p.act + c.w * (I / 4), NX, tag_of(p, t, l, PH_GU), v, 7)) return;
-                if (!stage_x<NX, CI>(p, c, buf, I, v, g, false, xr, nscale, 8)) return;
-                buf ^= 1;
-                if (!phase_resid<CI>(p, c, lb + p.off_dn, p.xb, tag_of(p, t, l, PH_O), nullptr, p.xa,
-                                     tag_of(p, t, l, PH_DN), xr, pd, 50))
+                float gam[16], xv[16], nscale;
+                gld16(Lw.post_norm + 16 * c.lane, gam);
+                if (!reduce_x(p, c, p.opart, tag_of(p, t, l, PH_OP), p.xr2, tag_of(p, t, l, PH_XR2), 3))
                     return;
-                set_done(c, lb + p.lpl);
+                if (!gather_x(p, c, p.xr2, tag_of(p, t, l, PH_XR2), gam, xv, nscale, 4)) return;
+                if (!phase_gu(p, c, lb + LP_OFF_GU, tag_of(p, t, l, PH_ACT), xv, nscale, pg)) return;
+                set_done(c, lb + LP_OFF_DN);
+            }
+            // ---- P7: down partial over XCD g's channels
+            {
+                const float sd = gld(Lw.s_down + 32 * c.j + 8 * c.w + (c.lane >> 3));
+                if (!phase_dpart(p, c, lb + LP_OFF_DN, tag_of(p, t, l, PH_ACT), tag_of(p, t, l, PH_DP), sd))
+                    return;
+                set_done(c, lb + LP_LPL);
             }
         }
         if (lm) {
-            constexpr int NX = CH * 4;
-            float v[NX], g[NX], xr[LP_CMAX][16], nscale;
+            float gam[16], xv[16], nscale;
+            gld16(p.final_norm + 16 * c.lane, gam);
+            if (!reduce_x(p, c, p.dpart, tag_of(p, t, p.L - 1, PH_DP), p.xr, tag_of(p, t, p.L, PH_XR), 9))
+                return;
+            if (!gather_x(p, c, p.xr, tag_of(p, t, p.L, PH_XR), gam, xv, nscale, 11)) return;
+            // the lm phase reads gamma * x from the wave's LDS copy
+            float* xw = c.xw + c.w * LP_H + 16 * c.lane;
 #pragma unroll
-            for (int i = 0; i < NX; i++) g[i] = gld(p.final_norm + c.w * (H / 4) + c.lane + 64 * i);
-            if (!ll_poll<NX>(p, c, p.xa + c.w * (H / 4), NX, tag_of(p, t, p.L - 1, PH_DN), v, 9)) return;
-            if (!stage_x<NX, CH>(p, c, buf, H, v, g, true, xr, nscale, 11)) return;
-            const uint32_t tl = tag_of(p, t, p.L, 0);
-            phase_lm<CH>(p.lm_head, p.s_lm, t == p.n_steps - 1 ? p.logits : nullptr, H, c.uv0, c.nuv,
-                         c.w, c.lane, (const lds_f32*)(c.xs + buf * LP_XS), nscale, tl,
-                         (lds_u64*)(c.wkeys + c.w));
-            buf ^= 1;
+            for (int i = 0; i < 16; i += 4) *(float4*)(xw + i) = make_float4(xv[i], xv[i + 1], xv[i + 2], xv[i + 3]);
+            cbar();
+            const uint32_t tl = tag_of(p, t, p.L, 1);
+            phase_lm<1>(p.lm_head, p.s_lm, t == p.n_steps - 1 ? p.logits : nullptr, LP_H, c.uv0, c.nuv,
+                        c.w, c.lane, (const lds_f32*)(c.xw + c.w * LP_H), nscale, tl,
+                        (lds_u64*)(c.wkeys + c.w));
             if (!csync(p, c, 61)) return;
             if (c.w == 0 && c.lane == 0) {
                 u64 b = c.wkeys[0];
                 for (int i = 1; i < LP_CW; i++) b = c.wkeys[i] > b ? c.wkeys[i] : b;
                 b = (b & ~(u64)0x3FFF) | (u64)(tl & 0x3FFFu);
-                __hip_atomic_store(p.keys + blockIdx.x, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(p.keys + c.role, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
         Gl += p.lpt;
     }
     // The last step's argmax -> ids[pos+1] and the device position/state.
-    if (blockIdx.x == 0 && c.w == 0) {
+    if (c.role == 0 && c.w == 0) {
         const int pos = p.pos0 + p.n_steps - 1;
         int last = id;
         if (pos + 1 >= p.prompt_len) {
-            if (!argmax_id(p, c, tag_of(p, p.n_steps - 1, p.L, 0), last)) return;
+            if (!argmax_id(p, c, tag_of(p, p.n_steps - 1, p.L, 1), last)) return;
             if (c.lane == 0 && pos + 1 < p.max_seq + 1) p.ids[pos + 1] = last;
         }
         if (c.lane == 0) {
@@ -1149,24 +1232,36 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
     }
 }
 
-template <int CH, int CO, int CI>
 __global__ __launch_bounds__(LP_THREADS, 1) void decode_loop_kernel(LoopParams p) {
     extern __shared__ __attribute__((aligned(16))) int8_t lp_lds[];
-    __shared__ int ready[LP_SW], done[LP_CW], sync_ctr, abort_flag;
+    __shared__ int ready[LP_SW], done[LP_CW], sync_ctr, abort_flag, role;
     __shared__ u64 wkeys[LP_CW];
-    __shared__ float ss[2 * LP_CW];
     if (threadIdx.x < LP_SW) ready[threadIdx.x] = 0;
     if (threadIdx.x < LP_CW) done[threadIdx.x] = 0;
-    if (threadIdx.x == 0) { sync_ctr = 0; abort_flag = 0; }
+    if (threadIdx.x == 0) {
+        sync_ctr = 0;
+        abort_flag = 0;
+        // this workgroup's XCD and the next free slot in it
+        unsigned xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 16)" : "=s"(xcc));
+        int slot = LP_WPX;
+        if (xcc < (unsigned)LP_NX)
+            slot = __hip_atomic_fetch_add(p.err + 8 + xcc, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        role = slot < LP_WPX ? slot * LP_NX + (int)xcc : -1;
+        if (role < 0) lp_fail(p, LP_ERR_XCD, 100 + (int)xcc);
+    }
     __syncthreads();
+    if (role < 0) return;   // every wave of the workgroup leaves together
     Cx c;
     c.lane = threadIdx.x & 63;
     c.w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar branches
+    c.role = __builtin_amdgcn_readfirstlane(role);
+    c.g = c.role % LP_NX;
+    c.j = c.role / LP_NX;
     {
-        const Units q = blk_units((p.nq + 2 * p.nkv) * 64, p.nblk), h = blk_units(p.H, p.nblk),
-                    i = blk_units(p.I, p.nblk), v = blk_units(p.V, p.nblk);
-        c.uq0 = q.u0; c.nuq = q.nu; c.uh0 = h.u0; c.nuh = h.nu;
-        c.ui0 = i.u0; c.nui = i.nu; c.uv0 = v.u0; c.nuv = v.nu;
+        const int V = p.V;
+        c.uv0 = (int)(((uint32_t)c.role * (uint32_t)V) / (uint32_t)LP_NBLK);
+        c.nuv = (int)(((uint32_t)(c.role + 1) * (uint32_t)V) / (uint32_t)LP_NBLK) - c.uv0;
     }
     c.nsync = 0;
     c.fail_where = 0;
@@ -1175,47 +1270,41 @@ __global__ __launch_bounds__(LP_THREADS, 1) void decode_loop_kernel(LoopParams p
     c.csync = &sync_ctr;
     c.abort = &abort_flag;
     c.ring = lp_lds;
-    c.xs = (float*)(lp_lds + LP_LDS_RING);
-    c.ss = ss;
-    c.attp = (float*)(lp_lds + LP_LDS_RING + LP_LDS_XS);
-    c.attm = c.attp + LP_CW * LP_G * 8 * 128;
-    c.stg = (float*)(lp_lds + LP_LDS_RING + LP_LDS_XS + LP_LDS_ATT);
+    c.xw = (float*)(lp_lds + LP_LDS_RING);
+    c.os = (float*)(lp_lds + LP_LDS_RING + LP_LDS_XW);
+    c.acts = (float*)(lp_lds + LP_LDS_RING + LP_LDS_XW + LP_LDS_OS);
+    c.attp = (float*)(lp_lds + LP_LDS_RING + LP_LDS_XW + LP_LDS_OS + LP_LDS_ACT);
+    c.attm = c.attp + LP_CW * LP_G * 8 * LP_D;
+    c.stg = (float*)(lp_lds + LP_LDS_RING + LP_LDS_XW + LP_LDS_OS + LP_LDS_ACT + LP_LDS_ATT);
     c.wkeys = wkeys;
     if (c.w >= LP_CW) {
         stream_role(p, c);
     } else {
-        compute_role<CH, CO, CI>(p, c);
+        compute_role(p, c);
         // a compute wave that leaves early must not hold the ring
         cbar();
         if (c.lane == 0) lds_st(&done[c.w], 0x7fffffff);
     }
-    if (c.fail_where && c.lane == 0) lp_fail(p, c.fail_where);
+    if (c.fail_where && c.lane == 0) lp_fail(p, LP_ERR_TIMEOUT, c.fail_where);
 }
 
 // ------------------------------------------------------------------ host
 struct LoopState {
     int nblk = 0;
-    int lpl = 0, off_o = 0, off_gu = 0, off_dn = 0, lpt = 0;
+    int lpt = 0;
     void* stream = nullptr;      // relaid weights
     void* small = nullptr;       // tagged buffers + layer table + error words
     size_t small_bytes = 0, ll_bytes = 0;
     LoopLayer* layers = nullptr;
-    u64 *xa, *xb, *q, *kv, *part, *merged, *act, *keys;
+    u64 *xr, *xr2, *qkv, *att, *act, *opart, *dpart, *keys;
     int* err = nullptr;
     uint32_t epoch = 1;
     bool ran = false;
 };
 
-// Unit counts and lines per unit of the five weight phases.
-struct PhaseShape {
-    int U, lpu;
-};
-
-static int seg_lines(const PhaseShape& s, int nblk) { return ceil_div(s.U, nblk) * s.lpu; }
-
 // The kernel's dynamic LDS exceeds the 64 KB default limit.
 static int loop_lds_attr() {
-    PIO_HIP(hipFuncSetAttribute((const void*)decode_loop_kernel<LP_CH, LP_CO, LP_CI>,
+    PIO_HIP(hipFuncSetAttribute((const void*)decode_loop_kernel,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)LP_LDS_BYTES));
     return PIO_OK;
 }
@@ -1226,126 +1315,109 @@ int loop_check(const Qwen3Dec* d) {
     PIO_HIP(hipGetDevice(&dev));
     PIO_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
     PIO_TRY(loop_lds_attr());
-    PIO_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &per_cu, decode_loop_kernel<LP_CH, LP_CO, LP_CI>, LP_THREADS, LP_LDS_BYTES));
-    if (per_cu < 1)
-        return set_error(PIO_ERR_UNSUPPORTED, "persistent decode: a %d-thread workgroup with %zu B "
-                         "of LDS does not fit a CU", LP_THREADS, LP_LDS_BYTES);
-    const int G = c.n_heads / c.n_kv_heads;
-    const bool ok = c.head_dim == 128 && c.hidden == LP_CH * 1024 &&
-                    c.n_heads * 128 == LP_CO * 1024 && c.intermediate == LP_CI * 1024 && G == LP_G &&
-                    c.n_kv_heads * LP_S <= cus && c.max_seq <= LP_MAX_SEQ && c.vocab <= (1 << 18);
-    // per-wave unit counts must fit the one-value-per-lane preloads
-    auto per_wave = [&](int U) { return ceil_div(ceil_div(U, cus), LP_CW); };
-    const bool fits = per_wave((c.n_heads + 2 * c.n_kv_heads) * 64) <= LP_MU_QKV &&
-                      per_wave(c.intermediate) <= LP_MU_GU && per_wave(c.hidden) <= LP_MU_ROW;
-    if (!ok || !fits)
+    PIO_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_loop_kernel, LP_THREADS,
+                                                         LP_LDS_BYTES));
+    const bool ok = c.head_dim == LP_D && c.hidden == LP_H && c.n_heads * LP_D == LP_KO &&
+                    c.n_kv_heads == LP_NX && c.intermediate == LP_I && cus == LP_NBLK &&
+                    c.max_seq <= LP_MAX_SEQ && c.vocab <= (1 << 18) && per_cu >= 1;
+    if (!ok)
         return set_error(PIO_ERR_UNSUPPORTED,
-                         "persistent decode is built for the Qwen3-0.6B layer shape: head_dim 128, "
-                         "hidden %d, n_heads*head_dim %d, intermediate %d, %d query heads per KV "
-                         "head, n_kv_heads*%d <= %d CUs, max_seq <= %d, vocab <= 262144",
-                         LP_CH * 1024, LP_CO * 1024, LP_CI * 1024, LP_G, LP_S, cus, LP_MAX_SEQ);
+                         "persistent decode is built for the Qwen3-0.6B layer shape on a %d-CU, "
+                         "%d-XCD device: head_dim %d, hidden %d, %d query / %d KV heads, "
+                         "intermediate %d, max_seq <= %d, vocab <= 262144 (device has %d CUs)",
+                         LP_NBLK, LP_NX, LP_D, LP_H, LP_KO / LP_D, LP_NX, LP_I, LP_MAX_SEQ, cus);
     return PIO_OK;
 }
 
+// One 1 KB line per 64 threads from 8 sources of 128 B each (chunk k of the
+// line = lanes 8k .. 8k+7).
 __global__ void loop_gather_kernel(const int8_t* const* __restrict__ src, int8_t* __restrict__ dst,
                                    int64_t nlines) {
     const int64_t line = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (line >= nlines) return;
     const int lane = threadIdx.x & 63;
-    const lp_v4i v = *(const lp_v4i*)(src[line] + lane * 16);
+    const lp_v4i v = *(const lp_v4i*)(src[line * 8 + (lane >> 3)] + (lane & 7) * 16);
     *(lp_v4i*)(dst + line * 1024 + lane * 16) = v;
 }
 
 // Lays every workgroup's weight lines out contiguously, in the order its
-// compute waves consume them (the same unit split as the kernel's blk_units).
+// compute waves consume them (the partition of the kernel above).
 static int loop_build(Qwen3Dec* d) {
     const pio_qwen3_config& c = d->c;
     LoopState* s = new LoopState();
     d->loop = s;
-    int dev = 0;
-    PIO_HIP(hipGetDevice(&dev));
-    PIO_HIP(hipDeviceGetAttribute(&s->nblk, hipDeviceAttributeMultiprocessorCount, dev));
-    const int nb = s->nblk, H = c.hidden, I = c.intermediate, KO = c.n_heads * 128;
-    const int CH = H / 1024, CO = KO / 1024, CI = I / 1024;
-    const PhaseShape qkv{(c.n_heads + 2 * c.n_kv_heads) * 64, 2 * CH}, o{H, CO}, gu{I, 2 * CH},
-        dn{H, CI};
-    s->off_o = seg_lines(qkv, nb);
-    s->off_gu = s->off_o + seg_lines(o, nb);
-    s->off_dn = s->off_gu + seg_lines(gu, nb);
-    s->lpl = s->off_dn + seg_lines(dn, nb);
-    s->lpt = c.n_layers * s->lpl;
-
-    // source line table
-    void* zero = nullptr;
-    PIO_TRY(device_alloc(&zero, 1024, d->st));
-    Scratch zero_guard;
-    zero_guard.ptr = zero;
-    PIO_HIP(hipMemsetAsync(zero, 0, 1024, d->st));
-    const int64_t nlines = (int64_t)nb * s->lpt;
-    std::vector<const int8_t*> tab((size_t)nlines, (const int8_t*)zero);
-    auto blk = [&](int U, int b, int& u0, int& nu) {
-        u0 = (int)(((int64_t)b * U) / nb);
-        nu = (int)(((int64_t)(b + 1) * U) / nb) - u0;
-    };
-    for (int b = 0; b < nb; b++) {
-        const int64_t base = (int64_t)b * s->lpt;
-        int u0, nu;
+    s->nblk = LP_NBLK;
+    s->lpt = c.n_layers * LP_LPL;
+    const int64_t nlines = (int64_t)LP_NBLK * s->lpt;
+    std::vector<const int8_t*> tab((size_t)nlines * 8);
+    for (int b = 0; b < LP_NBLK; b++) {
+        const int g = b % LP_NX, j = b / LP_NX;
         for (int l = 0; l < c.n_layers; l++) {
             const pio_qwen3_layer& L = d->layers[l];
-            const int64_t lb = base + (int64_t)l * s->lpl;
-            blk(qkv.U, b, u0, nu);
-            for (int ub = 0; ub < nu; ub++) {
-                const int u = u0 + ub, r0 = (u >> 6) * 128 + (u & 63), r1 = r0 + 64;
-                for (int ch = 0; ch < CH; ch++) {
-                    tab[lb + ub * qkv.lpu + ch] = L.w_qkv + (int64_t)r0 * H + ch * 1024;
-                    tab[lb + ub * qkv.lpu + CH + ch] = L.w_qkv + (int64_t)r1 * H + ch * 1024;
-                }
+            const int64_t lb = ((int64_t)b * s->lpt + (int64_t)l * LP_LPL) * 8;
+            auto row_line = [&](int64_t line, const int8_t* row) {   // a whole 1 KB row
+                for (int k = 0; k < 8; k++) tab[lb + line * 8 + k] = row + 128 * k;
+            };
+            // qkv: unit ub = w + 4m of this workgroup's 8 -> lines 2 ub (+1 for row + 64)
+            for (int ub = 0; ub < 8; ub++) {
+                const int u = 8 * j + ub;
+                int r0;
+                if (u < 128) r0 = (LP_G * g + (u >> 6)) * LP_D + (u & 63);
+                else if (u < 192) r0 = LP_KO + g * LP_D + (u - 128);
+                else r0 = LP_KO + LP_NX * LP_D + g * LP_D + (u - 192);
+                row_line(2 * ub, L.w_qkv + (int64_t)r0 * LP_H);
+                row_line(2 * ub + 1, L.w_qkv + (int64_t)(r0 + 64) * LP_H);
             }
-            blk(o.U, b, u0, nu);
-            for (int ub = 0; ub < nu; ub++)
-                for (int ch = 0; ch < CO; ch++)
-                    tab[lb + s->off_o + ub * CO + ch] = L.w_o + (int64_t)(u0 + ub) * KO + ch * 1024;
-            blk(gu.U, b, u0, nu);
-            for (int ub = 0; ub < nu; ub++)
-                for (int ch = 0; ch < CH; ch++) {
-                    tab[lb + s->off_gu + ub * gu.lpu + ch] = L.w_gu + (int64_t)(u0 + ub) * H + ch * 1024;
-                    tab[lb + s->off_gu + ub * gu.lpu + CH + ch] =
-                        L.w_gu + (int64_t)(u0 + ub + I) * H + ch * 1024;
+            // o_proj partial: line c holds rows 32 j + 4 c + r (r < 4), columns 256 g .. +256
+            for (int cc = 0; cc < LP_L_O; cc++)
+                for (int k = 0; k < 8; k++) {
+                    const int row = 32 * j + 4 * cc + (k >> 1);
+                    tab[lb + (LP_OFF_O + cc) * 8 + k] =
+                        L.w_o + (int64_t)row * LP_KO + 256 * g + 128 * (k & 1);
                 }
-            blk(dn.U, b, u0, nu);
-            for (int ub = 0; ub < nu; ub++)
-                for (int ch = 0; ch < CI; ch++)
-                    tab[lb + s->off_dn + ub * CI + ch] = L.w_down + (int64_t)(u0 + ub) * I + ch * 1024;
+            // gate_up: unit ub -> channel i = 384 g + 12 j + ub; lines gate row i, up row i + I
+            for (int ub = 0; ub < 12; ub++) {
+                const int i = LP_IX * g + 12 * j + ub;
+                row_line(LP_OFF_GU + 2 * ub, L.w_gu + (int64_t)i * LP_H);
+                row_line(LP_OFF_GU + 2 * ub + 1, L.w_gu + (int64_t)(i + LP_I) * LP_H);
+            }
+            // down partial: wave w, line 3 w + cc, chunk k = row 32 j + 8 w + k,
+            // channels 384 g + 128 cc .. +128
+            for (int w = 0; w < LP_CW; w++)
+                for (int cc = 0; cc < 3; cc++)
+                    for (int k = 0; k < 8; k++) {
+                        const int row = 32 * j + 8 * w + k;
+                        tab[lb + (LP_OFF_DN + 3 * w + cc) * 8 + k] =
+                            L.w_down + (int64_t)row * LP_I + LP_IX * g + 128 * cc;
+                    }
         }
     }
     PIO_TRY(device_alloc(&s->stream, (size_t)nlines * 1024, d->st));
     void* dtab = nullptr;
-    PIO_TRY(device_alloc(&dtab, (size_t)nlines * sizeof(void*), d->st));
+    PIO_TRY(device_alloc(&dtab, tab.size() * sizeof(void*), d->st));
     Scratch tab_guard;
     tab_guard.ptr = dtab;
-    PIO_HIP(hipMemcpyAsync(dtab, tab.data(), (size_t)nlines * sizeof(void*), hipMemcpyHostToDevice,
-                           d->st));
+    PIO_HIP(hipMemcpyAsync(dtab, tab.data(), tab.size() * sizeof(void*), hipMemcpyHostToDevice, d->st));
     loop_gather_kernel<<<(unsigned)((nlines + 3) / 4), 256, 0, d->st>>>((const int8_t* const*)dtab,
                                                                         (int8_t*)s->stream, nlines);
     PIO_LAUNCHED();
 
     // tagged buffers, layer table, error words
-    const int G = c.n_heads / c.n_kv_heads;
-    const size_t n_ll[] = {(size_t)H, (size_t)H, (size_t)KO, (size_t)c.n_kv_heads * 256,
-                           (size_t)c.n_kv_heads * LP_S * G * LP_PART, (size_t)KO, (size_t)I,
-                           (size_t)nb};
-    size_t off[9];
+    const size_t n_ll[] = {(size_t)LP_NX * LP_H, (size_t)LP_NX * LP_H, (size_t)LP_NX * LP_QKVX,
+                           (size_t)LP_NX * LP_S * LP_G * LP_PART, (size_t)LP_NX * LP_IX,
+                           (size_t)LP_NX * LP_H, (size_t)LP_NX * LP_H, (size_t)LP_NBLK};
+    constexpr int NB = 8;
+    size_t off[NB + 1];
     off[0] = 0;
-    for (int i = 0; i < 8; i++) off[i + 1] = off[i] + (n_ll[i] * 8 + 255) / 256 * 256;
-    s->ll_bytes = off[8];
+    for (int i = 0; i < NB; i++) off[i + 1] = off[i] + (n_ll[i] * 8 + 255) / 256 * 256;
+    s->ll_bytes = off[NB];
     const size_t lay_off = s->ll_bytes;
     const size_t err_off = lay_off + (c.n_layers * sizeof(LoopLayer) + 255) / 256 * 256;
     s->small_bytes = err_off + 256;
     PIO_TRY(device_alloc(&s->small, s->small_bytes, d->st));
     char* sp = (char*)s->small;
-    u64** dst[] = {&s->xa, &s->xb, &s->q, &s->kv, &s->part, &s->merged, &s->act, &s->keys};
-    for (int i = 0; i < 8; i++) *dst[i] = (u64*)(sp + off[i]);
+    u64** dst[] = {&s->xr, &s->xr2, &s->qkv, &s->att, &s->act, &s->opart, &s->dpart, &s->keys};
+    for (int i = 0; i < NB; i++) *dst[i] = (u64*)(sp + off[i]);
     s->layers = (LoopLayer*)(sp + lay_off);
     s->err = (int*)(sp + err_off);
     std::vector<LoopLayer> lt(c.n_layers);
@@ -1356,7 +1428,7 @@ static int loop_build(Qwen3Dec* d) {
     PIO_HIP(hipMemsetAsync(s->small, 0, s->small_bytes, d->st));
     PIO_HIP(hipMemcpyAsync(s->layers, lt.data(), lt.size() * sizeof(LoopLayer), hipMemcpyHostToDevice,
                            d->st));
-    PIO_HIP(hipStreamSynchronize(d->st));   // the host table and guards go out of scope
+    PIO_HIP(hipStreamSynchronize(d->st));   // the host table and the guard go out of scope
     s->epoch = 1;
     return PIO_OK;
 }
@@ -1367,14 +1439,6 @@ void loop_destroy(Qwen3Dec* d) {
     if (d->loop->small) device_free(d->loop->small);
     delete d->loop;
     d->loop = nullptr;
-}
-
-template <int CH, int CO, int CI>
-static int launch_loop(LoopParams& p, hipStream_t st) {
-    PIO_TRY(loop_lds_attr());
-    decode_loop_kernel<CH, CO, CI><<<dim3(p.nblk), dim3(LP_THREADS), LP_LDS_BYTES, st>>>(p);
-    PIO_LAUNCHED();
-    return PIO_OK;
 }
 
 int loop_run(Qwen3Dec* d, int n_steps) {
@@ -1389,34 +1453,34 @@ int loop_run(Qwen3Dec* d, int n_steps) {
     }
     LoopState* s = d->loop;
     const pio_qwen3_config& c = d->c;
-    const uint32_t per_tok = (uint32_t)(c.n_layers * LP_PH + 1);
+    const uint32_t per_tok = (uint32_t)(c.n_layers * LP_PH + 2);
     if ((uint64_t)s->epoch + (uint64_t)n_steps * per_tok + 1 >= 0xFFFFFFFFull) {
         // tags would wrap: clear every tagged word and start over
         PIO_HIP(hipMemsetAsync(s->small, 0, s->ll_bytes, d->st));
         s->epoch = 1;
     }
-    PIO_HIP(hipMemsetAsync(s->err, 0, 16, d->st));
+    PIO_HIP(hipMemsetAsync(s->err, 0, 64, d->st));   // error words and XCD slot counters
     LoopParams p{};
-    p.L = c.n_layers; p.H = c.hidden; p.nq = c.n_heads; p.nkv = c.n_kv_heads;
-    p.I = c.intermediate; p.V = c.vocab; p.max_seq = c.max_seq; p.nblk = s->nblk;
+    p.L = c.n_layers; p.V = c.vocab; p.max_seq = c.max_seq;
     p.eps = c.rms_eps;
     p.att_scale = 1.0f / sqrtf((float)c.head_dim);
     p.embed = d->embed; p.final_norm = d->final_norm; p.s_lm = d->s_lm;
     p.layers = s->layers;
     p.stream = (const int8_t*)s->stream;
-    p.lpl = s->lpl; p.off_o = s->off_o; p.off_gu = s->off_gu; p.off_dn = s->off_dn;
     p.lpt = s->lpt;
     p.lm_head = d->lm_head;
     p.kc = d->kc; p.vc = d->vc; p.cos_t = d->cos_t; p.sin_t = d->sin_t;
-    p.xa = s->xa; p.xb = s->xb; p.q = s->q; p.kv = s->kv; p.part = s->part; p.merged = s->merged;
-    p.act = s->act; p.keys = s->keys;
+    p.xr = s->xr; p.xr2 = s->xr2; p.qkv = s->qkv; p.att = s->att; p.act = s->act;
+    p.opart = s->opart; p.dpart = s->dpart; p.keys = s->keys;
     p.ids = d->ids; p.logits = d->logits; p.state = d->state;
     p.pos0 = d->host_pos;
     p.prompt_len = d->prompt_len;
     p.n_steps = n_steps;
     p.epoch0 = s->epoch;
     p.err = s->err;
-    PIO_TRY((launch_loop<LP_CH, LP_CO, LP_CI>(p, d->st)));
+    PIO_TRY(loop_lds_attr());
+    decode_loop_kernel<<<dim3(LP_NBLK), dim3(LP_THREADS), LP_LDS_BYTES, d->st>>>(p);
+    PIO_LAUNCHED();
     s->epoch += (uint32_t)n_steps * per_tok;
     s->ran = true;
     return PIO_OK;
@@ -1428,6 +1492,10 @@ int loop_status(Qwen3Dec* d) {
     int e[2] = {0, 0};
     PIO_HIP(hipMemcpy(e, d->loop->err, sizeof(e), hipMemcpyDeviceToHost));
     d->loop->ran = false;
+    if (e[0] == LP_ERR_XCD)
+        return set_error(PIO_ERR_HIP, "persistent decode: more than %d workgroups on XCD %d (or no "
+                                      "such XCD); results of that run are invalid",
+                         LP_WPX, e[1] - 100);
     if (e[0])
         return set_error(PIO_ERR_HIP, "persistent decode: a wait timed out (site %d); results of "
                                       "that run are invalid", e[1]);

@@ -155,7 +155,7 @@ constexpr size_t LP_LDS_RING = (size_t)LP_RING * 1024;
 constexpr size_t LP_LDS_XW = (size_t)LP_CW * LP_H * 4;
 constexpr size_t LP_LDS_OS = (size_t)LP_G * LP_D * 4;
 constexpr size_t LP_LDS_ACT = (size_t)LP_CW * LP_IX * 4;
-constexpr size_t LP_LDS_ATT = (size_t)LP_CW * LP_G * 8 * LP_D * 4 + 2 * LP_CW * LP_G * 4;
+constexpr size_t LP_LDS_ATT = (size_t)LP_CW * LP_G * LP_D * 4 + 2 * LP_CW * LP_G * 4;
 constexpr size_t LP_STG = LP_G * LP_D + 256;   // floats per wave: q heads + current k,v
 constexpr size_t LP_LDS_STG = (size_t)LP_CW * LP_STG * 4;
 constexpr size_t LP_LDS_BYTES = LP_LDS_RING + LP_LDS_XW + LP_LDS_OS + LP_LDS_ACT + LP_LDS_ATT + LP_LDS_STG;
@@ -394,7 +394,7 @@ struct Cx {
     float* xw;       // [LP_CW][H] each wave's copy of the current input vector
     float* os;       // [256] merged attention output of KV head g
     float* acts;     // [LP_CW][384] each wave's copy of XCD g's act slice
-    float* attp;     // [LP_CW][LP_G][8][128] attention partials
+    float* attp;     // [LP_CW][LP_G][128] attention partials
     float* attm;     // [2][LP_CW][LP_G] wave max, wave sum
     float* stg;      // [LP_CW][LP_STG]
     u64* wkeys;      // [LP_CW]
@@ -852,17 +852,22 @@ __device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t q
         load_row16(stg + G * LP_D + LP_D + part * 16, vv);
         step(kk, vv, jj == 0);
     }
-    // Scale every lane group to the wave's max; partials to LDS:
-    // po[w][h][jj][128], wave max / sum in pm / pl.
+    // Scale every lane group to the wave's max and sum the 8 lane groups in
+    // registers (lanes with equal lane & 7 hold the same 16 dims); the wave's
+    // partial po[w][h][128] and its max / sum go to LDS.
 #pragma unroll
     for (int h = 0; h < G; h++) {
         const float mw = wmax(m[h]);
         const float f = m[h] == -INFINITY ? 0.f : __expf(m[h] - mw);
         const float lw = wsum(part == 0 ? lsum[h] * f : 0.f);
-        float* dst = c.attp + ((c.w * G + h) * 8 + jj) * LP_D + part * 16;
+        float os[16];
 #pragma unroll
-        for (int i = 0; i < 16; i += 4)
-            *(float4*)(dst + i) = make_float4(o[h][i] * f, o[h][i + 1] * f, o[h][i + 2] * f, o[h][i + 3] * f);
+        for (int i = 0; i < 16; i++) os[i] = sum_stride8(o[h][i] * f);
+        if (jj == 0) {
+            float* dst = c.attp + (c.w * G + h) * LP_D + part * 16;
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) *(float4*)(dst + i) = make_float4(os[i], os[i + 1], os[i + 2], os[i + 3]);
+        }
         if (c.lane == 0) {
             c.attm[c.w * G + h] = mw;
             c.attm[LP_CW * G + c.w * G + h] = lw;
@@ -882,11 +887,7 @@ __device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t q
         for (int wv = 0; wv < LP_CW; wv++) {
             const float mw = c.attm[wv * G + h];
             const float F = mw == -INFINITY ? 0.f : __expf(mw - M);
-            const float* src = c.attp + (wv * G + h) * 8 * LP_D + d;
-            float sj = 0.f;
-#pragma unroll
-            for (int q = 0; q < 8; q++) sj += src[q * LP_D];
-            acc = fmaf(F, sj, acc);
+            acc = fmaf(F, c.attp[(wv * G + h) * LP_D + d], acc);
             den = fmaf(F, c.attm[LP_CW * G + wv * G + h], den);
         }
         st_l2(dst + h * LP_S * LP_PART + 2 + d, acc, tag);
@@ -1274,7 +1275,7 @@ __global__ __launch_bounds__(LP_THREADS, 1) void decode_loop_kernel(LoopParams p
     c.os = (float*)(lp_lds + LP_LDS_RING + LP_LDS_XW);
     c.acts = (float*)(lp_lds + LP_LDS_RING + LP_LDS_XW + LP_LDS_OS);
     c.attp = (float*)(lp_lds + LP_LDS_RING + LP_LDS_XW + LP_LDS_OS + LP_LDS_ACT);
-    c.attm = c.attp + LP_CW * LP_G * 8 * LP_D;
+    c.attm = c.attp + LP_CW * LP_G * LP_D;
     c.stg = (float*)(lp_lds + LP_LDS_RING + LP_LDS_XW + LP_LDS_OS + LP_LDS_ACT + LP_LDS_ATT);
     c.wkeys = wkeys;
     if (c.w >= LP_CW) {

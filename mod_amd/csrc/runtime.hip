@@ -23,7 +23,10 @@
 // Graph capture. A block freed while its stream is capturing (an op's
 // workspace, freed once its kernels are recorded) is still used by every
 // replay of the graph being built, so it is not cached: it is parked under the
-// capture's id. end_capture hands the parked blocks to the graph it
+// capture's id, where only later ops of the same capture on the same stream
+// may take it again (the graph orders them after the op that freed it; this
+// also keeps a capture of many ops from calling hipMalloc, which some capture
+// modes forbid). end_capture hands the parked blocks to the graph it
 // instantiates and returns them to the cache only when that graph is replaced
 // (their stream then orders any new owner after the old replays). Blocks of
 // captures made by other means (the caller's own hipStreamBeginCapture,
@@ -160,6 +163,25 @@ int device_alloc(void** out, size_t bytes, hipStream_t stream) {
         }
     }
     const uint64_t sid = stream_id_locked(a, stream);
+    // While the stream captures, first reuse a block an earlier op of the same
+    // capture freed: the graph orders that op's kernels before this one's.
+    const unsigned long long cid = capture_id(stream);
+    if (cid) {
+        auto pit = a.parked.find(cid);
+        if (pit != a.parked.end()) {
+            auto& v = pit->second;
+            for (size_t i = 0; i < v.size(); i++) {
+                if (v[i].second.bytes != r || v[i].second.sid != sid || v[i].second.dev != dev) continue;
+                *out = v[i].first;
+                v.erase(v.begin() + (std::ptrdiff_t)i);
+                a.held -= r;
+                a.live[*out] = {r, dev, stream, sid};
+                a.in_use += r;
+                if (a.in_use > a.peak) a.peak = a.in_use;
+                return PIO_OK;
+            }
+        }
+    }
     auto fit = a.free_lists.find(std::make_tuple(dev, r, sid));
     if (fit != a.free_lists.end() && !fit->second.empty()) {
         *out = fit->second.back();

@@ -179,6 +179,51 @@ def test_capture_keeps_workspace_from_later_tensors(T):
     assert int(lib.tensor_pool_graph_bytes()) == held0
 
 
+def test_torch_graph_of_several_ops_with_workspaces(torch_dev):
+    """The capture pattern of bench.py: one warm call outside the capture, then
+    a torch.cuda.graph holding several ops whose plans need workspaces (the
+    MFMA GEMV in K slices, the skinny W8A8 in K slices). Inside one capture the
+    later ops reuse the workspace the earlier ones freed (no hipMalloc while
+    capturing); every replay, with eager work and a synchronization between
+    replays, gives the eager result."""
+    import torch
+    from mod_amd import ops
+    d = torch_dev
+    rng = np.random.default_rng(8)
+    M, N, K = 16, 4096, 12288
+    xh = torch.from_numpy(rng.standard_normal((M, K), dtype=np.float32).astype(np.float16)).to(d)
+    q = torch.from_numpy(rng.integers(-127, 128, size=(M, K), dtype=np.int8)).to(d)
+    sa = torch.from_numpy(rng.uniform(0.001, 0.05, size=M).astype(np.float32)).to(d)
+    Ws = [torch.from_numpy(rng.integers(-127, 128, size=(N, K), dtype=np.int8)).to(d) for _ in range(3)]
+    sw = torch.from_numpy(rng.uniform(0.001, 0.02, size=N).astype(np.float32)).to(d)
+    ys = [torch.empty((M, N), dtype=torch.float32, device=d) for _ in range(6)]
+    st = torch.cuda.Stream()
+
+    def work(s):
+        for i in range(3):
+            ops.gemv_w8(xh, Ws[i], sw, None, ys[i], M, N, K, s)
+            ops.gemm_w8a8(q, sa, Ws[i], sw, None, ys[3 + i], M, N, K, s)
+
+    with torch.cuda.stream(st):
+        work(st.cuda_stream)
+    st.synchronize()
+    ref = [y.clone() for y in ys]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(st):
+        with torch.cuda.graph(g, stream=st):
+            work(st.cuda_stream)
+    for r in range(3):
+        for y in ys:
+            y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (y, e) in enumerate(zip(ys, ref)):
+            assert torch.equal(y, e), f"replay {r}, output {i}"
+        junk = torch.randn(1 << 20, device=d) * 2   # eager work between replays
+        del junk
+
+
 def test_destroy_stream_releases_its_cache(T):
     from mod_amd import ops
     from mod_amd.ops import lib

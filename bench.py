@@ -181,6 +181,28 @@ def bench_decode(torch, args):
     if len(modes) == 2:
         res["persistent"]["same_tokens_as_graph"] = bool(
             np.array_equal(res["persistent"]["_ids"], res["graph"]["_ids"]))
+    if not args.decode_only:
+        # the same generation with an fp16 KV cache (its own decoder), one
+        # timed generation in the fastest mode
+        from dataclasses import replace
+        cfg16 = replace(cfg, kv_dtype="float16")
+        dec16 = Qwen3Int8Decoder(cfg16, w, stream=st.cuda_stream)
+        m16 = "persistent" if dec16.persistent_supported() else "graph"
+        dec_main = dec
+        dec = dec16
+        try:
+            t_wall, pre, dcd, ids = run_mode(m16, 1, 1)
+        finally:
+            dec = dec_main
+        b16 = wb["int8"] + wb["scales"] + wb["bias_norms"] + cfg16.kv_bytes_per_pos() * mean_ctx
+        res["kv_fp16"] = {
+            "mode": m16, "tok_s": NG / dcd[0], "ms_per_token": dcd[0] / NG * 1e3,
+            "bytes_per_token": b16, "hbm_frac": b16 * NG / dcd[0] / (HBM_PEAK_GBS * 1e9),
+            "generated_head": ids[P:P + 8].tolist(),
+        }
+        log(f"[decode:kv fp16] {res['kv_fp16']['tok_s']:.1f} tok/s ({m16})")
+        dec16.close()
+        del dec16
     for m in modes:
         res[m].pop("_ids")
     res["mode"] = modes[0]

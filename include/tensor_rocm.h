@@ -269,13 +269,18 @@ int pio_moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* 
  *   logits = W8_lm_head(rmsnorm(x)*w_final); id[pos+1] = argmax (first max,
  *   tensor_ops.c:649-662) unless pos+1 is still inside the prompt; pos += 1.
  * Position and token ids live in device memory, so a step is replayable as a
- * captured HIP graph. The handle owns activations, KV cache (fp32,
- * [layer][kv_head][max_seq][head_dim]) and the RoPE table; weights are the
- * caller's device pointers and must outlive the handle.
+ * captured HIP graph. The handle owns activations, KV cache
+ * ([layer][kv_head][max_seq][head_dim], fp32 or fp16 by `kv_dtype`) and the
+ * RoPE table; weights are the caller's device pointers and must outlive the
+ * handle.
  * ------------------------------------------------------------------------- */
 typedef struct {
     int n_layers, hidden, n_heads, n_kv_heads, head_dim, intermediate, vocab, max_seq;
     float rms_eps, rope_theta;
+    /* KV cache element type: PIO_F32 (0, the reference's) or PIO_F16 (1: k and
+     * v rounded to fp16 when they are written, half the cache bytes read per
+     * token). A caller that zero-initializes the struct gets fp32. */
+    int kv_dtype;
 } pio_qwen3_config;
 
 typedef struct {

@@ -63,8 +63,9 @@ struct DecGemv {
     const float* sin_t;
     const int32_t* state;
     float* q_out;
-    float* kc;
-    float* vc;
+    void* kc;              // KV cache rows of this layer: fp32, or fp16 when kv16
+    void* vc;
+    int kv16;
     int nq, nkv, max_seq;
     unsigned long long* part_keys;
     // o_proj prologue: merge the attention splits into x (x must be nullptr)
@@ -84,6 +85,20 @@ __device__ __forceinline__ float dot16i8(const float (&x)[16], v4i_t w, float ac
         acc = fmaf(x[4 * d + 3], (float)(int8_t)(u >> 24), acc);
     }
     return acc;
+}
+
+// Two elements (i, i + half) of a KV cache row starting at element `row`.
+__device__ __forceinline__ void kv_store(void* base, int64_t row, int i, int half, float a, float b,
+                                         int kv16) {
+    if (kv16) {
+        _Float16* d = (_Float16*)base + row;
+        d[i] = (_Float16)a;
+        d[i + half] = (_Float16)b;
+    } else {
+        float* d = (float*)base + row;
+        d[i] = a;
+        d[i + half] = b;
+    }
 }
 
 __device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
@@ -260,15 +275,16 @@ __global__ __launch_bounds__(256) void dec_gemv_kernel(DecGemv p) {
                     const float c = p.cos_t[(int64_t)pos * p.half + i];
                     const float sn = p.sin_t[(int64_t)pos * p.half + i];
                     const float o0 = re * c - im * sn, o1 = re * sn + im * c;
-                    float* dst = head < p.nq
-                                     ? p.q_out + (int64_t)head * D
-                                     : p.kc + ((int64_t)(head - p.nq) * p.max_seq + pos) * D;
-                    dst[i] = o0;
-                    dst[i + p.half] = o1;
+                    if (head < p.nq) {
+                        float* dst = p.q_out + (int64_t)head * D;
+                        dst[i] = o0;
+                        dst[i + p.half] = o1;
+                    } else {
+                        kv_store(p.kc, ((int64_t)(head - p.nq) * p.max_seq + pos) * D, i, p.half, o0, o1, p.kv16);
+                    }
                 } else {
-                    float* dst = p.vc + ((int64_t)(head - p.nq - p.nkv) * p.max_seq + pos) * D;
-                    dst[i] = re;
-                    dst[i + p.half] = im;
+                    kv_store(p.vc, ((int64_t)(head - p.nq - p.nkv) * p.max_seq + pos) * D, i, p.half, re, im,
+                             p.kv16);
                 }
             }
         }
@@ -303,8 +319,17 @@ __global__ __launch_bounds__(256) void dec_gemv_kernel(DecGemv p) {
 //   values  32 dim-groups (float4) x 8 position-groups, LDS reduction.
 constexpr int ATT_MAX_G = 4;
 
+// Four consecutive cache elements as fp32.
+__device__ __forceinline__ float4 kv_ld4(const float* p) { return *(const float4*)p; }
+__device__ __forceinline__ float4 kv_ld4(const _Float16* p) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 h = *(const h4*)p;
+    return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+}
+
+template <typename KT>
 __global__ __launch_bounds__(256) void dec_attn_kernel(
-    const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
+    const float* __restrict__ q, const KT* __restrict__ kc, const KT* __restrict__ vc,
     const int32_t* __restrict__ state, float* __restrict__ att_o, float* __restrict__ att_ml,
     int nq, int nkv, int max_seq, float scale) {
     constexpr int D = 128;
@@ -329,8 +354,8 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(
         }
         return;
     }
-    const float* kb = kc + ((int64_t)kvh * max_seq + t0) * D;
-    const float* vb = vc + ((int64_t)kvh * max_seq + t0) * D;
+    const KT* kb = kc + ((int64_t)kvh * max_seq + t0) * D;
+    const KT* vb = vc + ((int64_t)kvh * max_seq + t0) * D;
     const float* qg = q + (int64_t)kvh * G * D;
 
     {
@@ -352,7 +377,7 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (t < n) a = *(const float4*)(kb + (int64_t)t * D + part * 16 + 4 * i);
+                    if (t < n) a = kv_ld4(kb + (int64_t)t * D + part * 16 + 4 * i);
                     kv[u][4 * i] = a.x; kv[u][4 * i + 1] = a.y; kv[u][4 * i + 2] = a.z; kv[u][4 * i + 3] = a.w;
                 }
             }
@@ -403,7 +428,7 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 const int t = tb + 8 * u;
-                vv[u] = t < n ? *(const float4*)(vb + (int64_t)t * D + 4 * dg) : make_float4(0.f, 0.f, 0.f, 0.f);
+                vv[u] = t < n ? kv_ld4(vb + (int64_t)t * D + 4 * dg) : make_float4(0.f, 0.f, 0.f, 0.f);
             }
 #pragma unroll
             for (int u = 0; u < 4; u++) {
@@ -497,15 +522,22 @@ static int enqueue_step(Qwen3Dec* d) {
     base.max_seq = c.max_seq;
     for (int l = 0; l < c.n_layers; l++) {
         const pio_qwen3_layer& L = d->layers[l];
-        float* kc = d->kc + (int64_t)l * nkv * c.max_seq * D;
-        float* vc = d->vc + (int64_t)l * nkv * c.max_seq * D;
+        const int64_t lkv = (int64_t)l * nkv * c.max_seq * D * (d->kv16 ? 2 : 4);   // bytes
+        void* kc = (char*)d->kc + lkv;
+        void* vc = (char*)d->vc + lkv;
         // qkv: rmsnorm(x) -> W8 + bias -> RoPE -> q, k/v cache
         DecGemv g = base;
         g.x = d->x; g.norm_w = L.in_norm; g.W = L.w_qkv; g.s_w = L.s_qkv; g.bias = L.b_qkv;
-        g.N = nqkv; g.K = H; g.half = D / 2; g.q_out = d->q; g.kc = kc; g.vc = vc;
+        g.N = nqkv; g.K = H; g.half = D / 2; g.q_out = d->q; g.kc = kc; g.vc = vc; g.kv16 = d->kv16;
         PIO_TRY((launch_dec_gemv<EPI_ROPE, 2>(g, ceil_div(g.N, 8), st)));
-        dec_attn_kernel<<<dim3(ATT_SPLITS, nkv), 256, d->att_lds, st>>>(
-            d->q, kc, vc, d->state, d->att_o, d->att_ml, nq, nkv, c.max_seq, scale);
+        if (d->kv16)
+            dec_attn_kernel<_Float16><<<dim3(ATT_SPLITS, nkv), 256, d->att_lds, st>>>(
+                d->q, (const _Float16*)kc, (const _Float16*)vc, d->state, d->att_o, d->att_ml, nq, nkv,
+                c.max_seq, scale);
+        else
+            dec_attn_kernel<float><<<dim3(ATT_SPLITS, nkv), 256, d->att_lds, st>>>(
+                d->q, (const float*)kc, (const float*)vc, d->state, d->att_o, d->att_ml, nq, nkv,
+                c.max_seq, scale);
         PIO_LAUNCHED();
         // o_proj: x += W8(attn)
         g = base;
@@ -567,9 +599,11 @@ PIO_EXPORT void* pio_qwen3_create(const pio_qwen3_config* cfg, const float* embe
     // every GEMV K (hidden, heads*head_dim, intermediate) must be a multiple of 16.
     if (c.n_layers < 1 || c.hidden < 16 || c.hidden % 16 || c.n_heads < 1 || c.n_kv_heads < 1 ||
         c.n_heads % c.n_kv_heads || c.head_dim != 128 || c.intermediate % 16 ||
-        c.intermediate < 16 || c.vocab < 1 || c.max_seq < 1 || c.max_seq > DEC_MAX_SEQ) {
+        c.intermediate < 16 || c.vocab < 1 || c.max_seq < 1 || c.max_seq > DEC_MAX_SEQ ||
+        (c.kv_dtype != PIO_F32 && c.kv_dtype != PIO_F16)) {
         set_error(PIO_ERR_INVALID, "pio_qwen3_create: unsupported config (head_dim must be 128; "
-                                   "hidden and intermediate multiples of 16; max_seq <= %d)",
+                                   "hidden and intermediate multiples of 16; max_seq <= %d; "
+                                   "kv_dtype PIO_F32 or PIO_F16)",
                   DEC_MAX_SEQ);
         return nullptr;
     }
@@ -618,7 +652,8 @@ PIO_EXPORT void* pio_qwen3_create(const pio_qwen3_config* cfg, const float* embe
         al256((size_t)ATT_SPLITS * nq * 2 * 4),           // attention partial (max, sum)
         al256((size_t)c.intermediate * 4),                // act
         al256((size_t)c.vocab * 4),                       // logits
-        al256(kv * 4), al256(kv * 4),                     // k, v cache
+        al256(kv * (c.kv_dtype == PIO_F16 ? 2 : 4)),      // k cache
+        al256(kv * (c.kv_dtype == PIO_F16 ? 2 : 4)),      // v cache
         al256(c.max_seq * half * 4), al256(c.max_seq * half * 4),   // cos, sin
         al256(16 * 4),                                    // state
         al256((size_t)(c.max_seq + 1) * 4),               // ids
@@ -638,8 +673,9 @@ PIO_EXPORT void* pio_qwen3_create(const pio_qwen3_config* cfg, const float* embe
     d->att_ml = (float*)take(3);
     d->act = (float*)take(4);
     d->logits = (float*)take(5);
-    d->kc = (float*)take(6);
-    d->vc = (float*)take(7);
+    d->kc = take(6);
+    d->vc = take(7);
+    d->kv16 = c.kv_dtype == PIO_F16;
     d->cos_t = (float*)take(8);
     d->sin_t = (float*)take(9);
     d->state = (int32_t*)take(10);

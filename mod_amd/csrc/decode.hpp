@@ -23,7 +23,9 @@ struct Qwen3Dec {
     hipStream_t st = nullptr;
     bool own_stream = false;
     void* block = nullptr;
-    float *x, *q, *att_o, *att_ml, *act, *logits, *kc, *vc, *cos_t, *sin_t;
+    float *x, *q, *att_o, *att_ml, *act, *logits, *cos_t, *sin_t;
+    void *kc, *vc;         // KV cache, fp32 or fp16 elements (kv16)
+    bool kv16 = false;
     int32_t *state, *ids;
     unsigned long long* part_keys;
     int lm_blocks = 0;

@@ -128,8 +128,8 @@ struct LoopParams {
     const LoopLayer* layers;
     const int8_t* stream;      // [nblk][lpt][1024] weight lines in consumption order
     int lpt;                   // weight lines per token (n_layers * LP_LPL)
-    float* kc;
-    float* vc;
+    void* kc;                  // KV cache [L][8][max_seq][128], fp32 or fp16 (kernel's KV16)
+    void* vc;
     const float* cos_t;
     const float* sin_t;
     // tagged hand-off buffers
@@ -506,6 +506,25 @@ __device__ __forceinline__ void load_row16g(const float* src, float (&d)[16]) {
         d[4 * i] = a[0]; d[4 * i + 1] = a[1]; d[4 * i + 2] = a[2]; d[4 * i + 3] = a[3];
     }
 }
+typedef _Float16 lp_h8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ void load_row16g(const _Float16* src, float (&d)[16]) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const lp_h8 a = gld((const lp_h8*)(src + 8 * i));
+#pragma unroll
+        for (int k = 0; k < 8; k++) d[8 * i + k] = (float)a[k];
+    }
+}
+// A KV cache element, stored with device scope (read by other workgroups'
+// attention in later tokens of the same launch).
+__device__ __forceinline__ void kv_put(float* p, float v) { dev_store(p, v); }
+__device__ __forceinline__ void kv_put(_Float16* p, float v) {
+    __hip_atomic_store((unsigned short*)p, __builtin_bit_cast(unsigned short, (_Float16)v),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// The value the cache holds for v.
+__device__ __forceinline__ float kv_round(float v, float*) { return v; }
+__device__ __forceinline__ float kv_round(float v, _Float16*) { return (float)(_Float16)v; }
 
 // The full input vector (H values), polled by this wave into the lane layout
 // of a 1 KB weight line (lane l holds x[16 l .. 16 l + 15]) and copied to the
@@ -586,6 +605,8 @@ __device__ __forceinline__ Pre pre_qkv(const LoopParams& p, const Cx& c, int l, 
 }
 
 // qkv (P2): this wave's 2 units, from ring lines line0 + 2 (w + 4 m) + r.
+// KT = the KV cache element type.
+template <typename KT>
 __device__ bool phase_qkv(const LoopParams& p, Cx& c, int l, int pos, int line0, uint32_t tag,
                           const float (&xv)[16], float nscale, const Pre& pre) {
     if (!wait_upto(p, c, line0 + 2 * (c.w + LP_CW) + 1, 10)) return false;
@@ -618,16 +639,16 @@ __device__ bool phase_qkv(const LoopParams& p, Cx& c, int l, int pos, int line0,
                 st_l2(dst + (u >> 6) * LP_D + i, o0, tag);
                 st_l2(dst + (u >> 6) * LP_D + i + 64, o1, tag);
             } else {
-                float* kr = p.kc + (((int64_t)l * LP_NX + c.g) * p.max_seq + pos) * LP_D;
-                dev_store(kr + i, o0);
-                dev_store(kr + i + 64, o1);
+                KT* kr = (KT*)p.kc + (((int64_t)l * LP_NX + c.g) * p.max_seq + pos) * LP_D;
+                kv_put(kr + i, o0);
+                kv_put(kr + i + 64, o1);
                 st_l2(dst + 256 + i, o0, tag);
                 st_l2(dst + 256 + i + 64, o1, tag);
             }
         } else {
-            float* vr = p.vc + (((int64_t)l * LP_NX + c.g) * p.max_seq + pos) * LP_D;
-            dev_store(vr + i, v0);
-            dev_store(vr + i + 64, v1);
+            KT* vr = (KT*)p.vc + (((int64_t)l * LP_NX + c.g) * p.max_seq + pos) * LP_D;
+            kv_put(vr + i, v0);
+            kv_put(vr + i + 64, v1);
             st_l2(dst + 384 + i, v0, tag);
             st_l2(dst + 384 + i + 64, v1, tag);
         }
@@ -757,6 +778,7 @@ __device__ __forceinline__ AttRange att_range(int s, int w, int pos) {
 // lane group 0 of the wave whose range holds it. The per-lane-group partials
 // (scaled to the wave's max) go to LDS and one pass over them combines the 32
 // lane groups of the workgroup; the split's (max, sum, o) is stored tagged.
+template <typename KT>
 __device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t qtag, uint32_t tag) {
     constexpr int G = LP_G;
     const AttRange r = att_range(c.j, c.w, pos);
@@ -767,8 +789,8 @@ __device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t q
     const bool has_cur = pos >= r.tw0 && pos < r.tw1;
     // Keys/values of the earlier positions (final since the steps that wrote
     // them): issued before the q poll, so their latency hides behind it.
-    const float* kb = p.kc + ((int64_t)l * LP_NX + c.g) * p.max_seq * LP_D;
-    const float* vb = p.vc + ((int64_t)l * LP_NX + c.g) * p.max_seq * LP_D;
+    const KT* kb = (const KT*)p.kc + ((int64_t)l * LP_NX + c.g) * p.max_seq * LP_D;
+    const KT* vb = (const KT*)p.vc + ((int64_t)l * LP_NX + c.g) * p.max_seq * LP_D;
     float kp[LP_NPF][16], vp[LP_NPF][16];
 #pragma unroll
     for (int ps = 0; ps < LP_NPF; ps++) {
@@ -847,9 +869,15 @@ __device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t q
         step(kk, vv, valid);
     }
     if (has_cur) {
+        // this step's k/v as the cache holds them
         float kk[16], vv[16];
         load_row16(stg + G * LP_D + part * 16, kk);
         load_row16(stg + G * LP_D + LP_D + part * 16, vv);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            kk[i] = kv_round(kk[i], (KT*)nullptr);
+            vv[i] = kv_round(vv[i], (KT*)nullptr);
+        }
         step(kk, vv, jj == 0);
     }
     // Scale every lane group to the wave's max and sum the 8 lane groups in
@@ -1111,6 +1139,7 @@ __device__ __forceinline__ void gld16(const float* src, float (&d)[16]) {
     }
 }
 
+template <typename KT>
 __device__ void compute_role(const LoopParams& p, Cx& c) {
     __builtin_amdgcn_s_setprio(2);
     const bool att_blk = c.j < LP_S;
@@ -1159,11 +1188,11 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
                         return;
                     if (!gather_x(p, c, p.xr, tag_of(p, t, l, PH_XR), gam, xv, nscale, 2)) return;
                 }
-                if (!phase_qkv(p, c, l, pos, lb, tag_of(p, t, l, PH_QKV), xv, nscale, pq)) return;
+                if (!phase_qkv<KT>(p, c, l, pos, lb, tag_of(p, t, l, PH_QKV), xv, nscale, pq)) return;
                 set_done(c, lb + LP_OFF_O);
             }
             // ---- P3: attention partials of head g's splits
-            if (att_blk && !phase_att(p, c, l, pos, tag_of(p, t, l, PH_QKV), tag_of(p, t, l, PH_ATT)))
+            if (att_blk && !phase_att<KT>(p, c, l, pos, tag_of(p, t, l, PH_QKV), tag_of(p, t, l, PH_ATT)))
                 return;
             // ---- P4: merge, o_proj partial over head g's columns
             {
@@ -1233,6 +1262,7 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
     }
 }
 
+template <typename KT>
 __global__ __launch_bounds__(LP_THREADS, 1) void decode_loop_kernel(LoopParams p) {
     extern __shared__ __attribute__((aligned(16))) int8_t lp_lds[];
     __shared__ int ready[LP_SW], done[LP_CW], sync_ctr, abort_flag, role;
@@ -1281,7 +1311,7 @@ __global__ __launch_bounds__(LP_THREADS, 1) void decode_loop_kernel(LoopParams p
     if (c.w >= LP_CW) {
         stream_role(p, c);
     } else {
-        compute_role(p, c);
+        compute_role<KT>(p, c);
         // a compute wave that leaves early must not hold the ring
         cbar();
         if (c.lane == 0) lds_st(&done[c.w], 0x7fffffff);
@@ -1305,7 +1335,9 @@ struct LoopState {
 
 // The kernel's dynamic LDS exceeds the 64 KB default limit.
 static int loop_lds_attr() {
-    PIO_HIP(hipFuncSetAttribute((const void*)decode_loop_kernel,
+    PIO_HIP(hipFuncSetAttribute((const void*)decode_loop_kernel<float>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)LP_LDS_BYTES));
+    PIO_HIP(hipFuncSetAttribute((const void*)decode_loop_kernel<_Float16>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)LP_LDS_BYTES));
     return PIO_OK;
 }
@@ -1316,8 +1348,12 @@ int loop_check(const Qwen3Dec* d) {
     PIO_HIP(hipGetDevice(&dev));
     PIO_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
     PIO_TRY(loop_lds_attr());
-    PIO_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_loop_kernel, LP_THREADS,
-                                                         LP_LDS_BYTES));
+    if (d->kv16)
+        PIO_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_loop_kernel<_Float16>,
+                                                             LP_THREADS, LP_LDS_BYTES));
+    else
+        PIO_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_loop_kernel<float>,
+                                                             LP_THREADS, LP_LDS_BYTES));
     const bool ok = c.head_dim == LP_D && c.hidden == LP_H && c.n_heads * LP_D == LP_KO &&
                     c.n_kv_heads == LP_NX && c.intermediate == LP_I && cus == LP_NBLK &&
                     c.max_seq <= LP_MAX_SEQ && c.vocab <= (1 << 18) && per_cu >= 1;
@@ -1480,7 +1516,8 @@ int loop_run(Qwen3Dec* d, int n_steps) {
     p.epoch0 = s->epoch;
     p.err = s->err;
     PIO_TRY(loop_lds_attr());
-    decode_loop_kernel<<<dim3(LP_NBLK), dim3(LP_THREADS), LP_LDS_BYTES, d->st>>>(p);
+    if (d->kv16) decode_loop_kernel<_Float16><<<dim3(LP_NBLK), dim3(LP_THREADS), LP_LDS_BYTES, d->st>>>(p);
+    else decode_loop_kernel<float><<<dim3(LP_NBLK), dim3(LP_THREADS), LP_LDS_BYTES, d->st>>>(p);
     PIO_LAUNCHED();
     s->epoch += (uint32_t)n_steps * per_tok;
     s->ran = true;

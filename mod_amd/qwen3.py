@@ -37,6 +37,7 @@ class Qwen3Config:
     max_seq: int = 384
     rms_eps: float = 1e-6
     rope_theta: float = 10000.0
+    kv_dtype: str = "float32"     # KV cache element type: "float32" or "float16"
 
     def weight_bytes(self) -> Dict[str, int]:
         """Int8 weight and fp32 scale bytes streamed per decode token."""
@@ -51,14 +52,17 @@ class Qwen3Config:
         }
 
     def kv_bytes_per_pos(self) -> int:
-        """fp32 K and V bytes read per cached position per token."""
-        return self.n_layers * 2 * self.n_kv_heads * self.head_dim * 4
+        """K and V bytes read per cached position per token."""
+        return self.n_layers * 2 * self.n_kv_heads * self.head_dim * (2 if self.kv_dtype == "float16" else 4)
 
 
 class _CConfig(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in ("n_layers", "hidden", "n_heads", "n_kv_heads",
                                               "head_dim", "intermediate", "vocab", "max_seq")] + \
-               [("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_float)]
+               [("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_float), ("kv_dtype", ctypes.c_int)]
+
+
+_KV_CODES = {"float32": 0, "float16": 1}
 
 
 class _CLayer(ctypes.Structure):
@@ -265,7 +269,11 @@ class Qwen3Int8Decoder:
         for i, L in enumerate(weights["layers"]):
             for k in LAYER_KEYS:
                 setattr(layers[i], k, up(L.get(k)))
-        c = _CConfig(**{k: v for k, v in asdict(cfg).items()})
+        if cfg.kv_dtype not in _KV_CODES:
+            raise ValueError(f"kv_dtype must be one of {sorted(_KV_CODES)}, not {cfg.kv_dtype!r}")
+        fields = asdict(cfg)
+        fields["kv_dtype"] = _KV_CODES[cfg.kv_dtype]
+        c = _CConfig(**fields)
         self._cfg_c, self._layers_c = c, layers
         self._h = lib.pio_qwen3_create(ctypes.addressof(c), self._embed, self._final, self._lm,
                                        self._slm, ctypes.addressof(layers), stream)

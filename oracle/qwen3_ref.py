@@ -30,6 +30,12 @@ class Qwen3Config:
     max_seq: int = 384
     rms_eps: float = 1e-6
     rope_theta: float = 10000.0
+    kv_dtype: str = "float32"     # "float16": k and v rounded to fp16 (RNE) when cached
+
+
+def _kv_round(v, cfg):
+    """The value the KV cache holds: v itself, or v rounded to fp16."""
+    return v.astype(np.float16).astype(v.dtype) if cfg.kv_dtype == "float16" else v
 
 
 def rope_tables(cfg: Qwen3Config, dtype=np.float64):
@@ -81,8 +87,8 @@ class Qwen3Ref:
             v = qkv[(nq + nkv) * D:].reshape(nkv, D)
             q = _rope(q, self.cos[pos], self.sin[pos])
             k = _rope(k, self.cos[pos], self.sin[pos])
-            self.kc[l, pos] = k
-            self.vc[l, pos] = v
+            self.kc[l, pos] = _kv_round(k, c)
+            self.vc[l, pos] = _kv_round(v, c)
             K = self.kc[l, : pos + 1]            # [t, nkv, D]
             V = self.vc[l, : pos + 1]
             grp = nq // nkv
@@ -131,8 +137,8 @@ def forward_all(cfg: Qwen3Config, w: dict, ids, want, dtype=np.float64) -> np.nd
     for Lw in w["layers"]:
         qkv = lin(rms(x, Lw["in_norm"]), Lw["w_qkv"], Lw["s_qkv"], Lw.get("b_qkv"))
         q = _rope(qkv[:, : nq * D].reshape(T, nq, D), cos, sin)
-        k = _rope(qkv[:, nq * D: (nq + nkv) * D].reshape(T, nkv, D), cos, sin)
-        v = qkv[:, (nq + nkv) * D:].reshape(T, nkv, D)
+        k = _kv_round(_rope(qkv[:, nq * D: (nq + nkv) * D].reshape(T, nkv, D), cos, sin), c)
+        v = _kv_round(qkv[:, (nq + nkv) * D:].reshape(T, nkv, D), c)
         out = np.empty((T, nq, D), dt)
         for hh in range(nq):
             kv = hh // grp

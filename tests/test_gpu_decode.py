@@ -23,13 +23,14 @@ def _say(m):
     sys.stdout.flush()
 
 
-def _cfgs(small: bool):
+def _cfgs(small: bool, **over):
     from mod_amd.qwen3 import Qwen3Config
     if small:
         kw = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=128, intermediate=512,
                   vocab=1000, max_seq=192)
     else:
         kw = dict(max_seq=384)
+    kw.update(over)
     return Qwen3Config(**kw), qwen3_ref.Qwen3Config(**kw)
 
 
@@ -45,22 +46,56 @@ def _check_argmax(got_logits, ref_logits, rtol):
 def _check_logits(got, ids, rcfg, w, what):
     r64 = qwen3_ref.Qwen3Ref(rcfg, w, np.float64)
     r32 = qwen3_ref.Qwen3Ref(rcfg, w, np.float32)
-    worst = 0.0
+    errs, errs32 = [], []
     for i, t in enumerate(ids[:len(got)]):
         e64 = r64.step(int(t))
         e32 = r32.step(int(t)).astype(np.float64)
         rms = float(np.sqrt(np.mean(e64 * e64)))
-        err_gpu = float(np.abs(got[i] - e64).max()) / rms
-        err_np32 = float(np.abs(e32 - e64).max()) / rms
-        worst = max(worst, err_gpu)
-        assert err_gpu <= max(1e-4, 4 * err_np32), (what, i, err_gpu, err_np32)
+        errs.append(float(np.abs(got[i] - e64).max()) / rms)
+        errs32.append(float(np.abs(e32 - e64).max()) / rms)
         _check_argmax(got[i:i + 1], e64[None], 1e-3)
-    _say(f"{what}: worst logit err {worst:.2e} x rms")
+    _assert_logit_bar(errs, errs32, rcfg, what)
+    if rcfg.kv_dtype == "float16":
+        # the GPU must sit nearer the fp16-KV oracle than the fp32-KV one:
+        # this fails if k/v were not rounded (or rounded differently)
+        from dataclasses import replace
+        r_f32kv = qwen3_ref.Qwen3Ref(replace(rcfg, kv_dtype="float32"), w, np.float64)
+        rh = qwen3_ref.Qwen3Ref(rcfg, w, np.float64)
+        effect = []
+        for i, t in enumerate(ids[:len(got)]):
+            a, b = rh.step(int(t)), r_f32kv.step(int(t))
+            effect.append(float(np.abs(a - b).max()) / float(np.sqrt(np.mean(a * a))))
+        _say(f"{what}: mean err {np.mean(errs):.2e}, mean fp16-KV effect {np.mean(effect):.2e}")
+        assert np.mean(errs) <= 0.25 * np.mean(effect), (np.mean(errs), np.mean(effect))
+    _say(f"{what}: worst logit err {max(errs):.2e} x rms")
+    return max(errs32)
 
 
-def test_decoder_small_teacher_forced(torch_dev):
+def _assert_logit_bar(errs, errs32, rcfg, what):
+    """fp32 KV: per position, err <= max(1e-4, 4x numpy fp32's error there).
+    fp16 KV: a k or v element whose fp32 value lies within fp32 rounding of an
+    fp16 rounding boundary rounds to a neighbouring fp16 value in one fp32
+    implementation and not in another; such flips are rare and stay in the
+    cache, so two correct fp32 paths differ at other positions by up to a few
+    1e-3 of the logit rms (numpy fp32 vs float64: up to 2.3e-3 on the small
+    config). The bar is therefore taken over the whole sequence: every
+    position's err <= max(1e-4, 4x numpy fp32's worst error on the sequence)."""
+    if rcfg.kv_dtype == "float16":
+        bar = max(1e-4, 4 * max(errs32))
+        for i, e in enumerate(errs):
+            assert e <= bar, (what, i, e, bar)
+    else:
+        for i, (e, e32) in enumerate(zip(errs, errs32)):
+            assert e <= max(1e-4, 4 * e32), (what, i, e, e32)
+
+
+@pytest.mark.parametrize("kv_dtype", ["float32", "float16"])
+def test_decoder_small_teacher_forced(torch_dev, kv_dtype):
+    """With an fp16 KV cache the oracle rounds k and v to fp16 the same way
+    (round to nearest even when they are cached); the bar is then taken over
+    the sequence (_assert_logit_bar)."""
     from mod_amd.qwen3 import Qwen3Int8Decoder, random_weights
-    cfg, rcfg = _cfgs(True)
+    cfg, rcfg = _cfgs(True, kv_dtype=kv_dtype)
     w = random_weights(cfg, seed=0)
     dec = Qwen3Int8Decoder(cfg, w)
     rng = np.random.default_rng(1)

@@ -43,19 +43,22 @@ def _decoder(cfg, seed):
     return dec, w
 
 
-def test_persistent_teacher_forced_small(torch_dev):
-    cfg, rcfg = _cfgs()
+@pytest.mark.parametrize("kv_dtype", ["float32", "float16"])
+def test_persistent_teacher_forced_small(torch_dev, kv_dtype):
+    cfg, rcfg = _cfgs(kv_dtype=kv_dtype)
     dec, w = _decoder(cfg, seed=11)
     ids = np.random.default_rng(12).integers(0, cfg.vocab, size=72).astype(np.int32)
     _say("persistent small: teacher forced, one launch per position")
     got = dec.teacher_forced_logits(ids, mode="persistent")
-    _check_logits(got, ids, rcfg, w, "persistent small teacher-forced")
+    np32_worst = _check_logits(got, ids, rcfg, w, "persistent small teacher-forced")
     _say("persistent small: graph path on the same ids")
     ref = dec.teacher_forced_logits(ids, mode="graph")
     rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
     diff = float(np.abs(got - ref).max()) / rms
     _say(f"persistent vs graph: max diff {diff:.2e} x rms")
-    assert diff <= 1e-4, diff
+    # fp16 KV: the two paths sum k and v in different orders, so fp16
+    # rounding flips differ between them as between any two fp32 paths
+    assert diff <= (1e-4 if kv_dtype == "float32" else max(1e-4, 8 * np32_worst)), diff
 
 
 def test_persistent_one_launch_equals_many(torch_dev):
@@ -144,19 +147,20 @@ def _check_against_batched_oracle(got, ids, pos, rcfg, w, what):
     seq = ids[:max(pos) + 1]
     e64 = qwen3_ref.forward_all(rcfg, w, seq, pos, np.float64)
     e32 = qwen3_ref.forward_all(rcfg, w, seq, pos, np.float32).astype(np.float64)
-    worst = 0.0
+    from tests.test_gpu_decode import _assert_logit_bar
+    errs, errs32 = [], []
     for i, p in enumerate(pos):
         rms = float(np.sqrt(np.mean(e64[i] * e64[i])))
-        err = float(np.abs(got[i] - e64[i]).max()) / rms
-        err32 = float(np.abs(e32[i] - e64[i]).max()) / rms
-        worst = max(worst, err)
-        _say(f"{what}: position {p}: err {err:.2e} (numpy fp32 {err32:.2e})")
-        assert err <= max(1e-4, 4 * err32), (what, p, err, err32)
+        errs.append(float(np.abs(got[i] - e64[i]).max()) / rms)
+        errs32.append(float(np.abs(e32[i] - e64[i]).max()) / rms)
+        _say(f"{what}: position {p}: err {errs[-1]:.2e} (numpy fp32 {errs32[-1]:.2e})")
         _check_argmax(got[i:i + 1], e64[i:i + 1], 1e-3)
-    _say(f"{what}: worst logit err {worst:.2e} x rms")
+    _assert_logit_bar(errs, errs32, rcfg, what)
+    _say(f"{what}: worst logit err {max(errs):.2e} x rms")
 
 
-def test_persistent_c2_full_generation_vs_oracle(torch_dev):
+@pytest.mark.parametrize("kv_dtype", ["float32", "float16"])
+def test_persistent_c2_full_generation_vs_oracle(torch_dev, kv_dtype):
     """BASELINE config 2 end to end: 28 layers, vocab 151936, a 128-token
     prompt and 256 greedy tokens (KV to 384 positions). The generation runs in
     chunks (1, 7 x 32, 31 tokens) so the logits of the first generated token,
@@ -166,8 +170,8 @@ def test_persistent_c2_full_generation_vs_oracle(torch_dev):
     run must produce the same 384 ids as one launch."""
     from mod_amd.qwen3 import Qwen3Config, Qwen3Int8Decoder, random_weights
     P, NG = 128, 256
-    cfg = Qwen3Config(max_seq=P + NG)
-    rcfg = qwen3_ref.Qwen3Config(max_seq=P + NG)
+    cfg = Qwen3Config(max_seq=P + NG, kv_dtype=kv_dtype)
+    rcfg = qwen3_ref.Qwen3Config(max_seq=P + NG, kv_dtype=kv_dtype)
     _say("C2 full generation: building weights")
     w = random_weights(cfg, seed=0)
     dec = Qwen3Int8Decoder(cfg, w)
@@ -194,7 +198,7 @@ def test_persistent_c2_full_generation_vs_oracle(torch_dev):
     dec.run(P - 1 + NG, mode="persistent")
     assert np.array_equal(dec.read(P + NG), ids)
     _say("C2 full generation: oracle (batched, teacher forced)")
-    _check_against_batched_oracle(np.stack(logits), ids, pos, rcfg, w, "C2 full generation")
+    _check_against_batched_oracle(np.stack(logits), ids, pos, rcfg, w, f"C2 full generation ({kv_dtype} KV)")
 
 
 def test_persistent_rejects_other_shapes(torch_dev):

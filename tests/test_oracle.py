@@ -449,7 +449,8 @@ def test_decoder_oracle_pin_resolves_a_rope_slip(monkeypatch):
     assert err > 1e-2, err
 
 
-def test_decoder_oracle_batched_forward_equals_steps():
+@pytest.mark.parametrize("kv_dtype", ["float32", "float16"])
+def test_decoder_oracle_batched_forward_equals_steps(kv_dtype):
     """qwen3_ref.forward_all (every position at once, causal mask) computes
     what Qwen3Ref.step computes position by position: float64 logits agree to
     1e-12 of their rms at every position, GQA (4 query heads on 2 KV heads)
@@ -457,7 +458,7 @@ def test_decoder_oracle_batched_forward_equals_steps():
     import oracle.qwen3_ref as q3
     from mod_amd.qwen3 import random_weights, Qwen3Config
     kw = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=128, intermediate=512,
-              vocab=500, max_seq=64)
+              vocab=500, max_seq=64, kv_dtype=kv_dtype)
     w = random_weights(Qwen3Config(**kw), seed=9)
     cfg = q3.Qwen3Config(**kw)
     ids = np.random.default_rng(10).integers(0, cfg.vocab, 40)

@@ -49,9 +49,11 @@
 //     itself (no cross-wave rendezvous except around attention and the merge).
 //
 // Hand-off: every value a phase produces for other workgroups is stored as a
-// tagged 64-bit word {tag:32 | fp32 bits:32} with a device-scope store; a
-// consumer polls the words it needs with device-scope loads until every tag
-// equals the producing phase's tag. Tags grow monotonically over the
+// tagged 64-bit word {tag:32 | fp32 bits:32}; a consumer polls the words it
+// needs until every tag equals the producing phase's tag. Words bound for
+// other XCDs (the opart/dpart partials) use device-scope stores and loads;
+// words consumed within the producer's XCD go through that XCD's L2 (st_l2 /
+// ld_l2_* below). Tags grow monotonically over the
 // decoder's lifetime, so no buffer is ever reset and no barrier is needed. A
 // buffer is rewritten one layer later, when every workgroup of every XCD has
 // consumed it: each layer's gathers (P2, P6) need all workgroups of the XCD,

@@ -284,11 +284,17 @@ def bench_kernels(torch, timer):
         sw = torch.rand((N,), device=dev) * 0.019 + 0.001
         yh = torch.empty((M, N), dtype=torch.float16, device=dev)
         reps = 20
+        gam = torch.rand((K,), device=dev) + 0.5
         tq = timer.time_graph(timer.graph(lambda s: ops.quantize_per_token(xh, q, sa, M, K, s), reps)) / reps
+        trq = timer.time_graph(timer.graph(
+            lambda s: ops.rmsnorm_quant(xh, gam, q, sa, M, K, 1e-6, stream=s), reps)) / reps
         tg = timer.time_graph(timer.graph(lambda s: ops.gemm_w8a8(q, sa, W, sw, None, yh, M, N, K, s), reps)) / reps
         tops = 2 * M * N * K / tg / 1e12
         c3[f"K{K}_N{N}"] = {"gemm_us": tg * 1e6, "TOPS": tops, "mfma_frac": tops / INT8_PEAK_TOPS,
-                            "quant_us": tq * 1e6, "quant_GBs": (3 * M * K + 4 * M) / tq / 1e9}
+                            "quant_us": tq * 1e6, "quant_GBs": (3 * M * K + 4 * M) / tq / 1e9,
+                            "with_quant_TOPS": 2 * M * N * K / (tg + tq) / 1e12,
+                            "rmsnorm_quant_us": trq * 1e6,
+                            "rmsnorm_quant_GBs": (3 * M * K + 4 * M + 4 * K) / trq / 1e9}
     out["c3_w8a8"] = c3
 
     # C4: Qwen3-8B linears, GEMV across M (skinny) + lm_head [151936, 4096].

@@ -179,6 +179,25 @@ int tensor_linear_w8_status(Tensor* x, Tensor* w, Tensor* s_w, Tensor* bias, Ten
 void tensor_quantize_per_token(Tensor* x, Tensor* q, Tensor* s);
 int tensor_quantize_per_token_status(Tensor* x, Tensor* q, Tensor* s);
 
+/* RMSNorm -> per-token quantizer in one pass (the producer of a prefill
+ * W8A8 linear's input): y = RMSNorm(x) * weight as tensor_rms_norm
+ * (tensor_ops.c:369-383; its sum of squares in a fixed pairwise order, stated
+ * in quant.hip), then q, s = the per-token quantizer of y, without writing y.
+ * x fp32|fp16 [..,K] with K % 8 == 0 and K <= 32768; weight fp32 [K]; q int8
+ * [..,K]; s fp32 [..]. No reference counterpart fuses these: it replaces the
+ * pair tensor_rms_norm + tensor_quantize_per_token. */
+void tensor_rms_norm_quantize(Tensor* x, Tensor* weight, Tensor* q, Tensor* s, float eps);
+int tensor_rms_norm_quantize_status(Tensor* x, Tensor* weight, Tensor* q, Tensor* s, float eps);
+
+/* The same after the residual add of tensor_fused_add_rms_norm
+ * (tensor_ops_opencl.c:1471-1483, bound at backend.py:157-158): x <- x +
+ * residual (in x's dtype, in place, as the reference updates x), then the
+ * RMSNorm -> quantizer of the sum. */
+void tensor_fused_add_rms_norm_quantize(Tensor* x, Tensor* residual, Tensor* weight, Tensor* q,
+                                        Tensor* s, float eps);
+int tensor_fused_add_rms_norm_quantize_status(Tensor* x, Tensor* residual, Tensor* weight,
+                                              Tensor* q, Tensor* s, float eps);
+
 /* W8A8 linear: acc = sum_k q[m,k]*W[n,k] (int32, bit-exact vs tensor_ops.c:
  * 217-246); out[m,n] = cvt(float(acc)*s_a[m]*s_w[n] (+ bias[n])).
  * out fp32|fp16 [..,N]. Runs on int8 MFMA. */
@@ -219,6 +238,14 @@ int pio_gemv_w8(const void* x, int x_dtype, const int8_t* w, const float* s_w, c
 /* Per-token quantizer as tensor_quantize_per_token. Any K >= 1. */
 int pio_quantize_per_token(const void* x, int x_dtype, int8_t* q, float* s, int M, int K,
                            void* stream);
+
+/* RMSNorm -> quantizer as tensor_rms_norm_quantize on raw pointers. With
+ * residual != NULL, x_sum receives x + residual (x's dtype; may equal x) and
+ * the norm is taken of that sum (tensor_fused_add_rms_norm_quantize).
+ * Pointers 16-byte aligned. */
+int pio_rmsnorm_quant(const void* x, int x_dtype, const void* residual, void* x_sum,
+                      const float* gamma, float eps, int8_t* q, float* s, int M, int K,
+                      void* stream);
 
 /* W8A8 GEMM as tensor_linear_w8a8; y_dtype in {F32,F16,I32}. With y_dtype ==
  * PIO_I32 the raw int32 accumulators are written and s_a/s_w/bias are ignored.

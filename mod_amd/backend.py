@@ -164,6 +164,29 @@ class Tensor:
               "tensor_quantize_per_token")
         return q, s
 
+    def rms_norm_quantize(self, weight: "Tensor", eps: float = 1e-6) -> Tuple["Tensor", "Tensor"]:
+        """RMSNorm (reference Tensor.rms_norm, backend.py:502-506) and the
+        per-token quantizer in one pass: returns (q int8, s fp32)."""
+        q = self._new(self.shape, "int8")
+        s = self._new(list(self.shape[:-1]) or [1], "float32")
+        check(lib.tensor_rms_norm_quantize_status(self._handle, weight._handle, q._handle,
+                                                  s._handle, ctypes.c_float(eps)),
+              "tensor_rms_norm_quantize")
+        return q, s
+
+    def fused_add_rms_norm_quantize(self, residual: "Tensor", weight: "Tensor",
+                                    eps: float = 1e-6) -> Tuple["Tensor", "Tensor"]:
+        """self <- self + residual in place (as the reference's
+        fused_add_rms_norm, backend.py:515-523), then rms_norm_quantize of the
+        sum: returns (q, s)."""
+        q = self._new(self.shape, "int8")
+        s = self._new(list(self.shape[:-1]) or [1], "float32")
+        check(lib.tensor_fused_add_rms_norm_quantize_status(self._handle, residual._handle,
+                                                            weight._handle, q._handle, s._handle,
+                                                            ctypes.c_float(eps)),
+              "tensor_fused_add_rms_norm_quantize")
+        return q, s
+
     def linear_w8(self, weight: "Tensor", scale: "Tensor", bias: Optional["Tensor"] = None,
                   out_dtype: Optional[str] = None) -> "Tensor":
         n = weight.shape[0]
@@ -269,6 +292,12 @@ class W8A8Linear(W8Linear):
 
     def forward(self, x: Tensor) -> Tensor:
         q, s = x.quantize_per_token()
+        return self.forward_quantized(q, s)
+
+    def forward_quantized(self, q: Tensor, s: Tensor) -> Tensor:
+        """The linear on activations already quantized per token, e.g. by
+        Tensor.rms_norm_quantize, which folds the quantizer into the RMSNorm
+        that produces a prefill layer's qkv and gate_up inputs."""
         return q.linear_w8a8(s, self.weight, self.weight_scale, self.bias, self.out_dtype)
 
 

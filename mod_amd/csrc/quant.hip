@@ -178,6 +178,194 @@ int quantize_per_token(const void* x, int x_dtype, int8_t* q, float* s, int M, i
     return PIO_OK;
 }
 
+
+// ------------------------------------------ RMSNorm -> per-token quantizer
+// The producer of a W8A8 linear's input in a prefill layer: RMSNorm
+// (tensor_ops.c:369-383), optionally after the residual add of
+// tensor_fused_add_rms_norm (tensor_ops_opencl.c:676-691), and the per-token
+// quantizer above, in one pass over the row. Per row (K % 8 == 0):
+//   v[k]  = x[k] (+ r[k], fp32 add, stored back in x's dtype; v is the stored value)
+//   ss    = sum of v[k]^2 in one fixed order: chunk c = v[8c .. 8c+7], its
+//           partial P[c] = fmaf(v, v, P) over the chunk in k order from 0;
+//           P zero-padded to n = the next power of two >= K/8 chunks, then
+//           for h = n/2, n/4, .., 1: P[c] += P[c + h] for c < h; ss = P[0]
+//   scale = 1.0f / sqrtf(ss / K + eps)     (IEEE division and square root)
+//   y[k]  = v[k] * scale * w[k]           (two roundings, in that order)
+//   s, q  = the per-token quantizer of y
+// The reference sums the squares in OpenMP's order, which no other
+// implementation can reproduce; the pairwise order is this library's
+// definition (the host restatement follows it, so q and s are bit-exact).
+// Layout: T threads per row (64, 128 or 256; 256 / T rows per block); thread
+// t holds chunks t + T i (i < n / T), so the tree levels h >= T run inside a
+// thread, h = T/2 .. 64 through LDS and h = 32 .. 1 as a wave butterfly
+// (lane t gets P[t] + P[t ^ h], which for t < h is the tree's P[t] + P[t + h]).
+template <typename XT>
+__device__ __forceinline__ void store8(XT* p, const float (&v)[8]);
+template <>
+__device__ __forceinline__ void store8<float>(float* p, const float (&v)[8]) {
+    *(float4*)p = make_float4(v[0], v[1], v[2], v[3]);
+    *(float4*)(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+}
+template <>
+__device__ __forceinline__ void store8<_Float16>(_Float16* p, const float (&v)[8]) {
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    h8 h;
+#pragma unroll
+    for (int i = 0; i < 8; i++) h[i] = (_Float16)v[i];
+    *(h8*)p = h;
+}
+
+template <typename XT, int T, int NV, bool RES>
+__global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const XT* __restrict__ x,
+                                                            const XT* __restrict__ r,
+                                                            XT* __restrict__ xs,
+                                                            const float* __restrict__ w,
+                                                            int8_t* __restrict__ q,
+                                                            float* __restrict__ s, int M, int K,
+                                                            float eps) {
+    constexpr int RPB = 256 / T;
+    __shared__ float red[256];
+    __shared__ float bc[RPB][2];
+    const int t = threadIdx.x % T, rg = threadIdx.x / T;
+    const int row = blockIdx.x * RPB + rg;
+    const bool live = row < M;                 // every thread joins the reductions
+    const int64_t base = (int64_t)min(row, M - 1) * K;
+    const int nch = K / 8;
+    float v[NV][8];
+    float part[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int c = t + T * i;
+        part[i] = 0.f;
+        if (c < nch) {
+            load8<XT>(x + base + 8 * c, v[i]);
+            if (RES) {
+                float rv[8];
+                load8<XT>(r + base + 8 * c, rv);
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[i][e] = to_f32<XT>(from_f32<XT>(v[i][e] + rv[e]));
+                if (live) store8<XT>(xs + base + 8 * c, v[i]);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) part[i] = __builtin_fmaf(v[i][e], v[i][e], part[i]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[i][e] = 0.f;
+        }
+    }
+    // tree levels h >= T: inside the thread (chunk t + T i pairs with t + T (i + h/T))
+#pragma unroll
+    for (int hs = NV / 2; hs >= 1; hs >>= 1)
+#pragma unroll
+        for (int i = 0; i < hs; i++) part[i] += part[i + hs];
+    float ss = part[0];
+    // levels T/2 .. 64 through LDS
+    if constexpr (T > 64) {
+        float* rr = red + rg * T;
+#pragma unroll
+        for (int h = T / 2; h >= 64; h >>= 1) {
+            rr[t] = ss;
+            __syncthreads();
+            if (t < h) ss = rr[t] + rr[t + h];
+            __syncthreads();
+        }
+    }
+    // levels 32 .. 1: wave butterfly (lanes >= h of the first wave carry copies)
+#pragma unroll
+    for (int h = 32; h >= 1; h >>= 1) ss += __shfl_xor(ss, h, 64);
+    if (t == 0) bc[rg][0] = ss;
+    __syncthreads();
+    ss = bc[rg][0];
+    const float scale = 1.0f / __builtin_sqrtf(ss / (float)K + eps);
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int c = t + T * i;
+        if (c < nch) {
+            const float4 g0 = *(const float4*)(w + 8 * c), g1 = *(const float4*)(w + 8 * c + 4);
+            const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                float y = v[i][e] * scale;
+                asm volatile("" : "+v"(y));       // two roundings, no fused form
+                y = y * g[e];
+                v[i][e] = y;
+                amax = fmaxf(amax, fabsf(y));
+            }
+        }
+    }
+    amax = wave_max(amax);
+    if constexpr (T > 64) {
+        __syncthreads();
+        if ((t & 63) == 0) red[rg * T + t / 64] = amax;
+        __syncthreads();
+        amax = red[rg * T];
+#pragma unroll
+        for (int k = 1; k < T / 64; k++) amax = fmaxf(amax, red[rg * T + k]);
+    }
+    if (!live) return;
+    const float sc = amax == 0.f ? 1.f : amax / 127.0f;
+    if (t == 0) s[row] = sc;
+    int8_t* qr = q + (int64_t)row * K;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int c = t + T * i;
+        if (c < nch) {
+            uint32_t lo = 0, hi = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) lo |= (uint32_t)(uint8_t)quant1(v[i][e], sc) << (8 * e);
+#pragma unroll
+            for (int e = 0; e < 4; e++) hi |= (uint32_t)(uint8_t)quant1(v[i][4 + e], sc) << (8 * e);
+            *(uint2*)(qr + 8 * c) = make_uint2(lo, hi);
+        }
+    }
+}
+
+template <typename XT, int T, int NV>
+static void launch_rq(const XT* x, const XT* r, XT* xs, const float* w, int8_t* q, float* s,
+                      int M, int K, float eps, hipStream_t st) {
+    const dim3 grid(ceil_div(M, 256 / T)), block(256);
+    if (r) rmsnorm_quant_kernel<XT, T, NV, true><<<grid, block, 0, st>>>(x, r, xs, w, q, s, M, K, eps);
+    else rmsnorm_quant_kernel<XT, T, NV, false><<<grid, block, 0, st>>>(x, r, xs, w, q, s, M, K, eps);
+}
+
+template <typename XT>
+static void launch_rq_any(const XT* x, const XT* r, XT* xs, const float* w, int8_t* q, float* s,
+                          int M, int K, float eps, hipStream_t st) {
+    int n = 1;
+    while (n < K / 8) n <<= 1;          // chunks, padded to a power of two
+    if (n <= 64) launch_rq<XT, 64, 1>(x, r, xs, w, q, s, M, K, eps, st);
+    else if (n == 128) launch_rq<XT, 128, 1>(x, r, xs, w, q, s, M, K, eps, st);
+    else if (n == 256) launch_rq<XT, 256, 1>(x, r, xs, w, q, s, M, K, eps, st);
+    else if (n == 512) launch_rq<XT, 256, 2>(x, r, xs, w, q, s, M, K, eps, st);
+    else if (n == 1024) launch_rq<XT, 256, 4>(x, r, xs, w, q, s, M, K, eps, st);
+    else if (n == 2048) launch_rq<XT, 256, 8>(x, r, xs, w, q, s, M, K, eps, st);
+    else launch_rq<XT, 256, 16>(x, r, xs, w, q, s, M, K, eps, st);
+}
+
+int rmsnorm_quant(const void* x, int x_dtype, const void* residual, void* x_sum,
+                  const float* gamma, float eps, int8_t* q, float* s, int M, int K,
+                  hipStream_t st) {
+    PIO_REQUIRE(x && gamma && q && s, "rmsnorm_quant: null pointer");
+    PIO_REQUIRE((residual == nullptr) == (x_sum == nullptr),
+                "rmsnorm_quant: residual and x_sum go together");
+    PIO_REQUIRE(M >= 0 && K >= 8 && K % 8 == 0 && K <= 32768,
+                "rmsnorm_quant: K=%d must be a multiple of 8 in [8, 32768] (M=%d)", K, M);
+    PIO_REQUIRE(x_dtype == PIO_F32 || x_dtype == PIO_F16, "rmsnorm_quant: x must be fp32 or fp16");
+    PIO_REQUIRE(aligned16(x) && aligned16(gamma) && aligned16(q) &&
+                (!residual || (aligned16(residual) && aligned16(x_sum))),
+                "rmsnorm_quant: pointers must be 16-byte aligned");
+    PIO_REQUIRE(eps >= 0.f, "rmsnorm_quant: eps must be >= 0");
+    if (M == 0) return PIO_OK;
+    if (x_dtype == PIO_F32)
+        launch_rq_any((const float*)x, (const float*)residual, (float*)x_sum, gamma, q, s, M, K, eps, st);
+    else
+        launch_rq_any((const _Float16*)x, (const _Float16*)residual, (_Float16*)x_sum, gamma, q, s, M,
+                      K, eps, st);
+    PIO_LAUNCHED();
+    return PIO_OK;
+}
+
 }  // namespace pio
 
 using namespace pio;
@@ -205,4 +393,52 @@ PIO_EXPORT int tensor_quantize_per_token_status(Tensor* x, Tensor* q, Tensor* s)
 }
 PIO_EXPORT void tensor_quantize_per_token(Tensor* x, Tensor* q, Tensor* s) {
     tensor_quantize_per_token_status(x, q, s);
+}
+
+PIO_EXPORT int pio_rmsnorm_quant(const void* x, int x_dtype, const void* residual, void* x_sum,
+                                 const float* gamma, float eps, int8_t* q, float* s, int M, int K,
+                                 void* stream) {
+    return rmsnorm_quant(x, x_dtype, residual, x_sum, gamma, eps, q, s, M, K, pick_stream(stream));
+}
+
+// Shape checks shared by the two Tensor forms; r (the residual) may be null.
+static int rmsnorm_quant_tensor(Tensor* x, Tensor* r, Tensor* weight, Tensor* q, Tensor* s,
+                                float eps) {
+    PIO_TRY(check_device_tensor(x, "rms_norm_quantize x"));
+    PIO_TRY(check_device_tensor(weight, "rms_norm_quantize weight"));
+    PIO_TRY(check_device_tensor(q, "rms_norm_quantize q"));
+    PIO_TRY(check_device_tensor(s, "rms_norm_quantize s"));
+    const int K = last_dim(x);
+    PIO_REQUIRE(K > 0, "rms_norm_quantize: empty last dim");
+    const int M = x->size / K;
+    const int dt = tensor_dtype_of(x);
+    if (r) {
+        PIO_TRY(check_device_tensor(r, "fused_add_rms_norm_quantize residual"));
+        PIO_REQUIRE(r->size == x->size && tensor_dtype_of(r) == dt,
+                    "fused_add_rms_norm_quantize: residual must match x in size and dtype");
+    }
+    PIO_REQUIRE(weight->size == K && tensor_dtype_of(weight) == PIO_F32,
+                "rms_norm_quantize: weight must be fp32 [%d]", K);
+    PIO_REQUIRE(q->size == x->size && tensor_dtype_of(q) == PIO_I8,
+                "rms_norm_quantize: q must be int8 with x's %d elements", x->size);
+    PIO_REQUIRE(s->size == M && tensor_dtype_of(s) == PIO_F32,
+                "rms_norm_quantize: s must be fp32 [%d]", M);
+    return rmsnorm_quant(x->data, dt, r ? r->data : nullptr, r ? x->data : nullptr, weight->data,
+                         eps, (int8_t*)q->data, s->data, M, K, current_stream());
+}
+
+PIO_EXPORT int tensor_rms_norm_quantize_status(Tensor* x, Tensor* weight, Tensor* q, Tensor* s,
+                                               float eps) {
+    return rmsnorm_quant_tensor(x, nullptr, weight, q, s, eps);
+}
+PIO_EXPORT void tensor_rms_norm_quantize(Tensor* x, Tensor* weight, Tensor* q, Tensor* s, float eps) {
+    tensor_rms_norm_quantize_status(x, weight, q, s, eps);
+}
+PIO_EXPORT int tensor_fused_add_rms_norm_quantize_status(Tensor* x, Tensor* residual, Tensor* weight,
+                                                         Tensor* q, Tensor* s, float eps) {
+    return rmsnorm_quant_tensor(x, residual, weight, q, s, eps);
+}
+PIO_EXPORT void tensor_fused_add_rms_norm_quantize(Tensor* x, Tensor* residual, Tensor* weight,
+                                                   Tensor* q, Tensor* s, float eps) {
+    tensor_fused_add_rms_norm_quantize_status(x, residual, weight, q, s, eps);
 }

@@ -89,6 +89,11 @@ SIGNATURES: dict[str, tuple] = {
     "tensor_moe_w8a8_status": (_i, [TP, TP, TP, TP, TP, TP, _i, _i, TP]),
     "pio_gemv_w8": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "pio_quantize_per_token": (_i, [_vp, _i, _vp, _vp, _i, _i, _vp]),
+    "pio_rmsnorm_quant": (_i, [_vp, _i, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _i, _i, _vp]),
+    "tensor_rms_norm_quantize": (None, [TP, TP, TP, TP, ctypes.c_float]),
+    "tensor_rms_norm_quantize_status": (_i, [TP, TP, TP, TP, ctypes.c_float]),
+    "tensor_fused_add_rms_norm_quantize": (None, [TP, TP, TP, TP, TP, ctypes.c_float]),
+    "tensor_fused_add_rms_norm_quantize_status": (_i, [TP, TP, TP, TP, TP, ctypes.c_float]),
     "pio_gemm_w8a8": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "pio_gemm_w8a8_static": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "pio_matmul_int8_workspace": (_sz, [_i, _i, _i, _i]),
@@ -193,6 +198,12 @@ def gemv_w8(x, w, s_w, bias, y, M: int, N: int, K: int, stream=None) -> None:
 def quantize_per_token(x, q, s, M: int, K: int, stream=None) -> None:
     check(lib.pio_quantize_per_token(_ptr(x), _dt(x), _ptr(q), _ptr(s), M, K, _stream(stream)),
           "pio_quantize_per_token")
+
+
+def rmsnorm_quant(x, gamma, q, s, M: int, K: int, eps: float = 1e-6, residual=None,
+                  x_sum=None, stream=None) -> None:
+    check(lib.pio_rmsnorm_quant(_ptr(x), _dt(x), _ptr(residual), _ptr(x_sum), _ptr(gamma), eps,
+                                _ptr(q), _ptr(s), M, K, _stream(stream)), "pio_rmsnorm_quant")
 
 
 def gemm_w8a8(q, s_a, w, s_w, bias, y, M: int, N: int, K: int, stream=None) -> None:

@@ -83,6 +83,8 @@ def lib() -> ctypes.CDLL:
                                    _vp, ctypes.c_int] + [ctypes.c_int] * 6
         L.ref_moe_group.argtypes = [_c_i32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_i32p,
                                     _c_i32p, _c_i32p]
+        L.ref_rmsnorm_quant.argtypes = [_vp, ctypes.c_int, _vp, _vp, _c_f32p, ctypes.c_float,
+                                        _c_i8p, _c_f32p, _c_f32p, ctypes.c_int, ctypes.c_int]
         L.ref_num_threads.restype = ctypes.c_int
         L.ref_exp_det.restype = ctypes.c_float
         L.ref_exp_det.argtypes = [ctypes.c_float]
@@ -194,6 +196,34 @@ def quant_per_token(x):
 
 
 # ---------------------------------------------------------------------- W8A8
+def rmsnorm_quant(x, w, eps=1e-6, residual=None):
+    """RMSNorm (optionally after a residual add) then the per-token quantizer
+    (int8_ref.c ref_rmsnorm_quant). x, residual: [M, K] fp32 or fp16 (same
+    dtype), w: [K]. Returns (q, s, y, x_sum): y the normalized fp32 values the
+    quantizer saw, x_sum = x + residual in x's dtype (None without residual)."""
+    x = np.ascontiguousarray(x)
+    m, k = x.shape
+    x_f16 = int(x.dtype == np.float16)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    q = np.empty((m, k), np.int8)
+    s = np.empty(m, np.float32)
+    y = np.empty((m, k), np.float32)
+    r = None if residual is None else np.ascontiguousarray(residual, dtype=x.dtype)
+    xs = None if residual is None else np.empty_like(x)
+    lib().ref_rmsnorm_quant(_vpp(x), x_f16, _vpp(r), _vpp(xs), _p(w, _c_f32p), eps,
+                            _p(q, _c_i8p), _p(s, _c_f32p), _p(y, _c_f32p), m, k)
+    return q, s, y, xs
+
+
+def ref_rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """Runs the reference tensor_rms_norm (fp32) itself."""
+    tx = RefTensor(x.shape, x.astype(np.float32))
+    tw = RefTensor(w.shape, w.astype(np.float32))
+    to = RefTensor(x.shape)
+    tx.L.tensor_rms_norm(tx.h, tw.h, to.h, ctypes.c_float(eps))
+    return to.f32()
+
+
 def w8a8(q, s_a, W, s_w, bias=None, out="f16"):
     """acc = q @ W.T (int32); y = float(acc)*s_a*s_w (+bias). out in f32|f16|i32."""
     q = np.ascontiguousarray(q, np.int8)

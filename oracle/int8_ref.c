@@ -180,6 +180,58 @@ void ref_quant_per_token(const void* x, int x_f16, int8_t* q, float* s, int m, i
     }
 }
 
+/* --------------------------------- RMSNorm -> per-token quantizer (f2) --- */
+/* Row i (K % 8 == 0), following tensor_rms_norm (tensor_ops.c:369-383) and the
+ * residual add of tensor_fused_add_rms_norm (tensor_ops_opencl.c:676-691):
+ *   v[k]  = x[k] (+ r[k] in fp32, rounded to x's dtype and stored to x_sum)
+ *   ss    = pairwise sum over the chunk partials P[c] = fmaf(v, v, P) over
+ *           v[8c .. 8c+7] in k order from 0, P zero-padded to a power of two n,
+ *           for h = n/2 .. 1: P[c] += P[c+h] (c < h); ss = P[0]
+ *   scale = 1.0f / sqrtf(ss / K + eps)      (tensor_ops.c:380)
+ *   y[k]  = v[k] * scale * w[k]             (tensor_ops.c:382, left to right)
+ *   q, s  = ref_quant_per_token(y)
+ * The reference's own sum order is OpenMP's; this fixed order is the one the
+ * GPU kernel uses. */
+void ref_rmsnorm_quant(const void* x, int x_f16, const void* r, void* x_sum, const float* w,
+                       float eps, int8_t* q, float* s, float* y_out, int m, int k) {
+    const int nch = k / 8;
+    int n = 1;
+    while (n < nch) n <<= 1;
+    float* P = (float*)malloc(sizeof(float) * (size_t)n);
+    float* v = (float*)malloc(sizeof(float) * (size_t)k);
+    float* y = (float*)malloc(sizeof(float) * (size_t)k);
+    if (!P || !v || !y) { free(P); free(v); free(y); return; }
+    for (int i = 0; i < m; i++) {
+        const int64_t b = (int64_t)i * k;
+        for (int p = 0; p < k; p++) {
+            float a = load_act(x, x_f16, b + p);
+            if (r) {
+                a = a + load_act(r, x_f16, b + p);
+                store_out(x_sum, x_f16, b + p, a);
+                a = load_act(x_sum, x_f16, b + p);
+            }
+            v[p] = a;
+        }
+        for (int c = 0; c < n; c++) {
+            P[c] = 0.f;
+            if (c < nch)
+                for (int e = 0; e < 8; e++) P[c] = fmaf(v[8 * c + e], v[8 * c + e], P[c]);
+        }
+        for (int h = n / 2; h >= 1; h /= 2)
+            for (int c = 0; c < h; c++) P[c] = P[c] + P[c + h];
+        const float scale = 1.0f / sqrtf(P[0] / (float)k + eps);
+        for (int p = 0; p < k; p++) {
+            const float t = v[p] * scale;
+            y[p] = t * w[p];
+        }
+        if (y_out) memcpy(y_out + b, y, sizeof(float) * (size_t)k);
+        ref_quant_per_token(y, 0, q + b, s + i, 1, k);
+    }
+    free(P);
+    free(v);
+    free(y);
+}
+
 /* -------------------------------------------------- W8A8 linear (a8) --- */
 /* acc = int32 sum (ref_matmul_nt_i32); y = float(acc) * s_a[i] * s_w[j]
  * (+ bias[j]) in that order, stored fp32 / fp16 (RNE) / raw int32. */

@@ -240,6 +240,55 @@ def test_quant_golden_ties(env):
     assert np.array_equal(host(q), g["q"]) and np.array_equal(host(s), g["s"])
 
 
+# ------------------------------------------------- RMSNorm -> quantizer (f2)
+@pytest.mark.parametrize("M,K,xdt,res", [(2048, 1024, np.float16, False), (2048, 1024, np.float16, True),
+                                         (7, 3072, np.float32, False), (5, 3072, np.float32, True),
+                                         (3, 8, np.float32, False), (9, 1000, np.float16, True),
+                                         (4, 4096, np.float32, True), (2, 8192, np.float16, False),
+                                         (3, 32768, np.float32, False), (130, 512, np.float16, False)])
+def test_rmsnorm_quant_bitexact(env, M, K, xdt, res):
+    """Fused RMSNorm (+ residual) -> per-token quantizer: q, s and the stored
+    sum bit-exact against the oracle, which fixes the order of the sum of
+    squares (every thread/LDS/butterfly tree level of the kernel's layouts:
+    64, 128 and 256 threads per row, 1..16 chunks per thread, padded chunk
+    counts such as K = 1000)."""
+    torch, ops, d = env
+    _say(f"rmsnorm_quant M={M} K={K} {np.dtype(xdt).name} residual={res}")
+    rng = np.random.default_rng(M * 7 + K)
+    x = (rng.standard_normal((M, K), dtype=np.float32) * rng.uniform(0.1, 10, (M, 1)).astype(np.float32)).astype(xdt)
+    x[0] = 0
+    r = rng.standard_normal((M, K), dtype=np.float32).astype(xdt) if res else None
+    if res:
+        r[0] = 0
+    w = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    eps = 1e-6
+    xd = dev(torch, x, d)
+    q = torch.empty((M, K), dtype=torch.int8, device=d)
+    s = torch.empty((M,), dtype=torch.float32, device=d)
+    rd = dev(torch, r, d) if res else None
+    ops.rmsnorm_quant(xd, dev(torch, w, d), q, s, M, K, eps, residual=rd, x_sum=xd if res else None,
+                      stream=stream(torch))
+    sync(torch)
+    qr, sr, _, xs = oracle.rmsnorm_quant(x, w, eps, residual=r)
+    assert np.array_equal(host(s).view(np.uint32), sr.view(np.uint32))
+    assert np.array_equal(host(q), qr)
+    if res:
+        assert np.array_equal(host(xd).view(np.uint8), xs.view(np.uint8))
+    assert np.all(host(q)[0] == 0) and host(s)[0] == 1.0
+
+
+def test_rmsnorm_quant_rejects(env):
+    torch, ops, d = env
+    x = torch.zeros((2, 12), dtype=torch.float32, device=d)
+    w = torch.ones((12,), dtype=torch.float32, device=d)
+    q = torch.empty((2, 12), dtype=torch.int8, device=d)
+    s = torch.empty((2,), dtype=torch.float32, device=d)
+    with pytest.raises(ops.RocmError, match="multiple of 8"):
+        ops.rmsnorm_quant(x, w, q, s, 2, 12)
+    with pytest.raises(ops.RocmError, match="go together"):
+        ops.rmsnorm_quant(x, w, q, s, 2, 8, residual=x)
+
+
 # -------------------------------------------------------------------- GEMM
 @pytest.mark.parametrize("M,N,K", [(2048, 3072, 1024), (2048, 1024, 3072), (2048, 2048, 1024),
                                    (1, 64, 16), (130, 200, 80), (257, 129, 1040), (64, 4096, 4096)])

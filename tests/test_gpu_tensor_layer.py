@@ -5,6 +5,8 @@ create_tensor_typed, against the oracle:
 * tensor_dequantize, per-tensor (tensor_ops_cuda.cu:923-929: out = q * scale[0])
   and per-row scales;
 * tensor_quantize_per_token, fp32 and fp16 inputs, bit-exact;
+* tensor_rms_norm_quantize / tensor_fused_add_rms_norm_quantize (the fused
+  RMSNorm -> quantizer producer), bit-exact, feeding W8A8Linear;
 * tensor_linear_w8a8, int32 / fp32 / fp16 outputs with and without bias, on the
   one-pass, split-K and skinny paths;
 * tensor_moe_w8a8 (the routed expert layer);
@@ -79,6 +81,36 @@ def test_tensor_quantize_per_token_bit_exact(T, M, K, dt):
     qr, sr = oracle.quant_per_token(x)
     assert np.array_equal(q.numpy(), qr)
     assert np.array_equal(s.numpy().view(np.uint32), sr.view(np.uint32))
+
+
+# ------------------------------------------- RMSNorm -> quantizer producer
+@pytest.mark.parametrize("M,K,dt", [(2048, 1024, np.float16), (3, 3072, np.float32)])
+def test_tensor_rms_norm_quantize_feeds_w8a8(T, M, K, dt):
+    """tensor_rms_norm_quantize and tensor_fused_add_rms_norm_quantize through
+    Tensor handles (bit-exact q, s, and the in-place sum), then the W8A8Linear
+    on the fused producer's output equals the linear on the oracle's q, s."""
+    _say(f"tensor_rms_norm_quantize M={M} K={K} {np.dtype(dt).name}")
+    rng = np.random.default_rng(M + K)
+    x = (rng.standard_normal((M, K), dtype=np.float32) * 3).astype(dt)
+    r = rng.standard_normal((M, K), dtype=np.float32).astype(dt)
+    g = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    tx, tg = _t(T, x), _t(T, g)
+    q, s = tx.rms_norm_quantize(tg, 1e-6)
+    qr, sr, _, _ = oracle.rmsnorm_quant(x, g, 1e-6)
+    assert np.array_equal(q.numpy(), qr)
+    assert np.array_equal(s.numpy().view(np.uint32), sr.view(np.uint32))
+    q2, s2 = tx.fused_add_rms_norm_quantize(_t(T, r), tg, 1e-6)
+    qr2, sr2, _, xs = oracle.rmsnorm_quant(x, g, 1e-6, residual=r)
+    assert np.array_equal(tx.numpy().view(np.uint8), xs.view(np.uint8))   # x updated in place
+    assert np.array_equal(q2.numpy(), qr2)
+    assert np.array_equal(s2.numpy().view(np.uint32), sr2.view(np.uint32))
+    N = 256
+    lin = T.W8A8Linear(K, N, bias=False, out_dtype="float16")
+    W = rng.integers(-127, 127, size=(N, K), dtype=np.int8)
+    sw = rng.uniform(0.001, 0.02, size=N).astype(np.float32)
+    lin.load_quantized(W, sw)
+    got = lin.forward_quantized(q, s).numpy()
+    assert np.array_equal(got.view(np.uint16), oracle.w8a8(qr, sr, W, sw, None, out="f16").view(np.uint16))
 
 
 # ----------------------------------------------------------------- W8A8 GEMM

@@ -204,6 +204,62 @@ def test_quant_invariants():
 
 
 # -------------------------------------------------------------------- W8A8
+@needs_ref
+@pytest.mark.parametrize("K", [8, 1000, 1024, 4096])
+def test_rmsnorm_quant_integer_rows_bitwise_vs_reference(K):
+    """Rows of small integers have sums of squares that are exact in fp32 in
+    any order, so the oracle's normalized y must equal the compiled reference
+    tensor_rms_norm bit for bit (any slip in eps, the mean, the sqrt/division
+    or the scale-then-weight order shows), and q, s must be the per-token
+    quantizer of the reference's own output."""
+    rng = np.random.default_rng(K)
+    M = 6
+    x = rng.integers(-16, 17, (M, K)).astype(np.float32)
+    x[1] = 0.0                                    # zero row
+    x[2, :] = 3.0                                 # constant row
+    w = rng.uniform(0.5, 2.0, K).astype(np.float32)
+    for eps in (1e-6, 1e-5, 0.25):
+        q, s, y, _ = oracle.rmsnorm_quant(x, w, eps)
+        y_ref = oracle.ref_rms_norm(x, w, eps)
+        assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32)), eps
+        q_ref, s_ref = oracle.quant_per_token(y_ref)
+        assert np.array_equal(q, q_ref) and np.array_equal(s, s_ref)
+    assert np.all(q[1] == 0) and s[1] == 1.0
+
+
+def test_rmsnorm_quant_random_rows_vs_float64():
+    """Random fp32/fp16 rows: y within 4 ulp of the float64 RMSNorm, and every
+    q within half a step (plus y's rounding) of y64 / s."""
+    rng = np.random.default_rng(7)
+    for dt in (np.float32, np.float16):
+        for K in (64, 1024, 3072):
+            x = (rng.standard_normal((5, K)) * rng.uniform(0.1, 30.0, (5, 1))).astype(dt)
+            w = rng.uniform(0.2, 3.0, K).astype(np.float32)
+            q, s, y, _ = oracle.rmsnorm_quant(x, w, 1e-6)
+            x64 = x.astype(np.float64)
+            y64 = x64 / np.sqrt(np.mean(x64 * x64, axis=1, keepdims=True) + 1e-6) * w
+            ulp = np.spacing(np.abs(y64).astype(np.float32)).astype(np.float64)
+            assert np.all(np.abs(y - y64) <= 4 * ulp + 1e-30)
+            s64 = np.abs(y64).max(axis=1) / 127.0
+            assert np.allclose(s, s64, rtol=1e-6)
+            assert np.all(np.abs(q - y64 / s[:, None]) <= 0.5 + 1e-4)
+            assert np.abs(q).max() == 127
+
+
+def test_rmsnorm_quant_fused_add():
+    """With a residual the sum is stored in x's dtype (round to nearest even
+    for fp16) and the result is that of the plain form on the stored sum."""
+    rng = np.random.default_rng(8)
+    for dt in (np.float32, np.float16):
+        x = rng.standard_normal((4, 512)).astype(dt)
+        r = rng.standard_normal((4, 512)).astype(dt)
+        w = rng.uniform(0.5, 1.5, 512).astype(np.float32)
+        q, s, y, xs = oracle.rmsnorm_quant(x, w, 1e-6, residual=r)
+        assert np.array_equal(xs, (x.astype(np.float32) + r.astype(np.float32)).astype(dt))
+        q2, s2, y2, _ = oracle.rmsnorm_quant(xs, w, 1e-6)
+        assert np.array_equal(q, q2) and np.array_equal(s, s2) and np.array_equal(y, y2)
+
+
 def test_w8a8_int_core_and_epilogue():
     rng = np.random.default_rng(10)
     m, n, k = 9, 21, 160

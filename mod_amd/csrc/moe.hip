@@ -8,23 +8,21 @@
 //              max seeded with -1e9, exp(x - max), multiply by 1/sum); top-k by
 //              tensor_topk's rule (tensor_ops.c:719-738: strict '>', so equal
 //              probabilities keep the lower expert id first); weights = the top-k
-//              probabilities, optionally renormalized to sum 1.
+//              probabilities, optionally renormalized to sum 1. The same launch
+//              quantizes x per token (the rows are shared by all k slots).
 //  2. group:   (token, slot) pairs are sorted by expert, tokens ascending inside
-//              an expert (a counting sort over a token x expert bitmap in LDS), so
-//              every expert's rows are one contiguous run of an index list.
-//  3. quant:   x is quantized per token once (the rows are shared by all 8 slots).
-//  4. gate_up: grouped W8A8 GEMM, one block per (expert, 128-column tile); the
+//              an expert (one block per expert: its offset is the count of pairs
+//              routed below it, its tokens ranked by ballots), so every expert's
+//              rows are one contiguous run of an index list.
+//  3. gate_up: grouped W8A8 GEMM, one block per (expert, 128-column tile); the
 //              block walks its expert's row tiles, so each weight tile is read
 //              from HBM once. fp32 output.
-//  5. swiglu:  h = silu(g) * u (tensor_ops.c:588-604 formula) and per-row requant.
-//  6. down:    grouped W8A8 GEMM over the contiguous h rows, fp32 output.
-//  7. combine: out[t] = sum_{k=0..top_k-1} w[t,k] * down[pos(t,k)], in k order.
+//  4. swiglu:  h = silu(g) * u (tensor_ops.c:588-604 formula) and per-row requant.
+//  5. down:    grouped W8A8 GEMM over the contiguous h rows, fp32 output.
+//  6. combine: out[t] = sum_{k=0..top_k-1} w[t,k] * down[pos(t,k)], in k order.
 #include "gemm_core.hpp"
 
 namespace pio {
-
-int quantize_per_token(const void* x, int x_dtype, int8_t* q, float* s, int M, int K,
-                       hipStream_t st);
 
 // Minimum over the 64 lanes (in every lane), on DPP lane moves and readlane.
 template <int CTRL>
@@ -44,17 +42,11 @@ __device__ __forceinline__ int wmin_i(int x) {
 // One wave per token, 4 tokens per block; the token's E probabilities live in LDS.
 constexpr int ROUTE_MAX_E = 1024;
 
-__global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict__ logits,
-                                                        float* __restrict__ topk_w,
-                                                        int32_t* __restrict__ topk_id, int T,
-                                                        int E, int top_k, int renorm) {
-    __shared__ float sp[4][ROUTE_MAX_E];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int t = blockIdx.x * 4 + w;
-    if (t >= T) return;
-    const float* lr = logits + (int64_t)t * E;
-    float* p = sp[w];
-
+// Routing of one token by one wave: p (LDS, E floats) receives the
+// probabilities; lanes < top_k write the token's weights and ids.
+__device__ __forceinline__ void route_token(const float* __restrict__ lr, float* p, int lane, int E,
+                                            int top_k, int renorm, float* __restrict__ w_out,
+                                            int32_t* __restrict__ id_out) {
     float mx = -1e9f;
     for (int e = lane; e < E; e += 64) {
         p[e] = lr[e];
@@ -93,111 +85,124 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
         if (lane == (mi & 63)) p[mi] = -INFINITY;
     }
     if (lane < top_k) {
-        topk_w[(int64_t)t * top_k + lane] = renorm ? myw / wsum : myw;
-        topk_id[(int64_t)t * top_k + lane] = myid;
+        w_out[lane] = renorm ? myw / wsum : myw;
+        id_out[lane] = myid;
     }
 }
 
-// ------------------------------------------------------------------ group ---
-// Single block of 1024 threads (16 waves); wave w takes the 64-token slices
-// sl = w, w + 16, ... with lane j on token sl*64 + j:
-//  1. top-k ids staged in LDS (8 per token);
-//  2. each lane builds its token's expert bitmap one 32-expert word at a time
-//     in registers, and one wave ballot per expert gives that expert's 64-bit
-//     token mask of the slice (item (e, slice)) and its count;
-//  3. the counts are scanned in item order (experts in order, slices in order
-//     within an expert), all waves on contiguous chunks, then the chunk totals;
-//  4. each lane places its token's k pairs: row = item start + the number of
-//     the item's tokens below it (popcount of the mask under the lane).
-// The layout equals a serial walk over (expert, token). Limits:
-// T * top_k <= GROUP_MAX_PAIRS (T <= 1024 at top_k 8), E * ceil(T/64) <=
-// GROUP_MAX_ITEMS, top_k <= 8.
-constexpr int GROUP_MAX_PAIRS = 8192;     // staged topk ids (16 KB)
-constexpr int GROUP_MAX_ITEMS = 4096;     // (expert, 64-token slice) items
+__global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict__ logits,
+                                                        float* __restrict__ topk_w,
+                                                        int32_t* __restrict__ topk_id, int T,
+                                                        int E, int top_k, int renorm) {
+    __shared__ float sp[4][ROUTE_MAX_E];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int t = blockIdx.x * 4 + w;
+    if (t >= T) return;
+    route_token(logits + (int64_t)t * E, sp[w], lane, E, top_k, renorm, topk_w + (int64_t)t * top_k,
+                topk_id + (int64_t)t * top_k);
+}
 
-__global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t* __restrict__ topk_id,
-                                                         int T, int E, int top_k,
-                                                         int32_t* __restrict__ offsets,
-                                                         int32_t* __restrict__ row_token,
-                                                         int32_t* __restrict__ pos_of_pair) {
-    __shared__ __attribute__((aligned(16))) int16_t ids[GROUP_MAX_PAIRS];
-    __shared__ unsigned long long masks[GROUP_MAX_ITEMS];
-    __shared__ int32_t start[GROUP_MAX_ITEMS];
-    __shared__ int32_t chunk[1024 / 64 + 1];
-    const int nsl = (T + 63) / 64;
-    const int items = E * nsl;   // item = e * nsl + slice
-    const int nw = blockDim.x >> 6, wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int i = threadIdx.x; i < T * 8; i += blockDim.x) {
-        const int t = i >> 3, kk = i & 7;
-        ids[i] = kk < top_k ? (int16_t)topk_id[t * top_k + kk] : (int16_t)-1;
-    }
+// The layer's first launch: a wave routes its token and quantizes the
+// token's x row per token (the quantizer of quant.hip: amax / 127, IEEE
+// division, round-half-even); the row is loaded once into registers, lane l
+// holding the 8-element chunks l, l + 64, ... (H % 8 == 0, H <= 512 ROUTE_XG).
+constexpr int ROUTE_XG = 8;
+template <typename XT>
+__global__ __launch_bounds__(256) void moe_route_quant_kernel(const float* __restrict__ logits,
+                                                              const XT* __restrict__ x, int H,
+                                                              float* __restrict__ topk_w,
+                                                              int32_t* __restrict__ topk_id,
+                                                              int8_t* __restrict__ qx,
+                                                              float* __restrict__ sx, int T,
+                                                              int E, int top_k, int renorm) {
+    __shared__ float sp[4][ROUTE_MAX_E];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int t = blockIdx.x * 4 + w;
+    if (t >= T) return;
+    // issue the x loads first: their latency overlaps the routing
+    const XT* xr = x + (int64_t)t * H;
+    const int nch = H / 8;
+    float v[ROUTE_XG][8];
+#pragma unroll
+    for (int g = 0; g < ROUTE_XG; g++)
+        if (lane + 64 * g < nch) load8<XT>(xr + 8 * (lane + 64 * g), v[g]);
+    route_token(logits + (int64_t)t * E, sp[w], lane, E, top_k, renorm, topk_w + (int64_t)t * top_k,
+                topk_id + (int64_t)t * top_k);
+    float amax = 0.f;
+#pragma unroll
+    for (int g = 0; g < ROUTE_XG; g++)
+        if (lane + 64 * g < nch)
+#pragma unroll
+            for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[g][i]));
+    amax = wave_max(amax);
+    const float sc = amax == 0.f ? 1.f : amax / 127.0f;
+    if (lane == 0) sx[t] = sc;
+    int8_t* qr = qx + (int64_t)t * H;
+#pragma unroll
+    for (int g = 0; g < ROUTE_XG; g++)
+        if (lane + 64 * g < nch) {
+            uint32_t lo = 0, hi = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) lo |= (uint32_t)(uint8_t)quant1(v[g][i], sc) << (8 * i);
+#pragma unroll
+            for (int i = 0; i < 4; i++) hi |= (uint32_t)(uint8_t)quant1(v[g][4 + i], sc) << (8 * i);
+            *(uint2*)(qr + 8 * (lane + 64 * g)) = make_uint2(lo, hi);
+        }
+}
+
+// ------------------------------------------------------------------ group ---
+// One 512-thread block per expert e, all blocks independent:
+//  1. offsets[e] = the number of (token, slot) pairs routed to experts < e
+//     (a count over all T * top_k ids);
+//  2. the tokens that chose e, in ascending order, take the rows
+//     offsets[e], offsets[e] + 1, ...: 512 tokens per round, a ballot per
+//     wave and a prefix over the 8 waves give each its rank.
+// The layout equals a serial walk over (expert, token). A token's top-k ids
+// are distinct, so at most one of its slots names e.
+__global__ __launch_bounds__(512) void moe_group_kernel(const int32_t* __restrict__ topk_id, int T,
+                                                        int E, int top_k,
+                                                        int32_t* __restrict__ offsets,
+                                                        int32_t* __restrict__ row_token,
+                                                        int32_t* __restrict__ pos_of_pair) {
+    __shared__ int wcount[8];
+    const int e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int P = T * top_k;
+    int c = 0;
+    for (int i = tid; i < P; i += 512) c += topk_id[i] < e;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, 64);
+    if (lane == 0) wcount[wv] = c;
     __syncthreads();
-    const unsigned long long below = (1ull << lane) - 1ull;   // lanes under this one
-    for (int sl = wv; sl < nsl; sl += nw) {
-        const int t = sl * 64 + lane;
-        int my[8];
+    int run = 0;
 #pragma unroll
-        for (int kk = 0; kk < 8; kk++) my[kk] = t < T ? ids[t * 8 + kk] : -1;
-        for (int e0 = 0; e0 < E; e0 += 32) {
-            uint32_t word = 0;
-#pragma unroll
-            for (int kk = 0; kk < 8; kk++)
-                if (my[kk] >= e0 && my[kk] < e0 + 32) word |= 1u << (my[kk] - e0);
-            const int ne = min(32, E - e0);
-            unsigned long long mine = 0ull;   // lane b keeps expert e0 + b's mask
-            for (int b = 0; b < ne; b++) {
-                const unsigned long long m = __ballot((word >> b) & 1u);
-                if (lane == b) mine = m;
-            }
-            if (lane < ne) {
-                masks[(e0 + lane) * nsl + sl] = mine;
-                start[(e0 + lane) * nsl + sl] = __popcll(mine);
-            }
-        }
+    for (int k = 0; k < 8; k++) run += wcount[k];
+    if (tid == 0) {
+        offsets[e] = run;
+        if (e == E - 1) offsets[E] = P;
     }
-    __syncthreads();
-    // exclusive scan of start[] in item order: every wave scans a contiguous
-    // chunk, then the chunk totals are scanned and added
-    {
-        const int per = (items + nw - 1) / nw, b0 = wv * per, b1 = min(items, b0 + per);
-        int carry = 0;
-        for (int b = b0; b < b1; b += 64) {
-            const int i = b + lane;
-            const int v = i < b1 ? start[i] : 0;
-            int x = v;
+    const unsigned long long below = (1ull << lane) - 1ull;
+    for (int t0 = 0; t0 < T; t0 += 512) {
+        const int t = t0 + tid;
+        int hit = -1;
+        if (t < T)
+            for (int kk = 0; kk < top_k; kk++)
+                if (topk_id[(int64_t)t * top_k + kk] == e) hit = kk;
+        const unsigned long long m = __ballot(hit >= 0);
+        __syncthreads();   // wcount is free again
+        if (lane == 0) wcount[wv] = __popcll(m);
+        __syncthreads();
+        int before = 0, total = 0;
 #pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const int y = __shfl_up(x, o, 64);
-                if (lane >= o) x += y;
-            }
-            if (i < b1) start[i] = carry + x - v;
-            carry += __shfl(x, 63, 64);
+        for (int k = 0; k < 8; k++) {
+            before += k < wv ? wcount[k] : 0;
+            total += wcount[k];
         }
-        if (lane == 0) chunk[wv] = carry;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            int a = 0;
-            for (int w = 0; w < nw; w++) {
-                const int c = chunk[w];
-                chunk[w] = a;
-                a += c;
-            }
-            chunk[nw] = a;
-        }
-        __syncthreads();
-        for (int i = threadIdx.x; i < items; i += blockDim.x) start[i] += chunk[i / per];
-        __syncthreads();
-        for (int e = threadIdx.x; e <= E; e += blockDim.x) offsets[e] = e < E ? start[e * nsl] : chunk[nw];
-    }
-    for (int sl = wv; sl < nsl; sl += nw) {
-        const int t = sl * 64 + lane;
-        if (t >= T) continue;
-        for (int kk = 0; kk < top_k; kk++) {
-            const int e = ids[t * 8 + kk], it = e * nsl + sl;
-            const int pos = start[it] + __popcll(masks[it] & below);
+        if (hit >= 0) {
+            const int pos = run + before + __popcll(m & below);
             row_token[pos] = t;
-            pos_of_pair[t * top_k + kk] = pos;
+            pos_of_pair[(int64_t)t * top_k + hit] = pos;
         }
+        run += total;
     }
 }
 
@@ -443,12 +448,13 @@ int moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* w_gu
     PIO_REQUIRE(H <= 128 * MOE_MAX_NK && I <= 128 * MOE_MAX_NK, "moe: H=%d and I=%d must be <= %d", H,
                 I, 128 * MOE_MAX_NK);
     PIO_REQUIRE(out_dtype == PIO_F32 || out_dtype == PIO_F16, "moe: out must be fp32 or fp16");
-    PIO_REQUIRE((int64_t)T * 8 <= GROUP_MAX_PAIRS && (int64_t)E * ((T + 63) / 64) <= GROUP_MAX_ITEMS &&
-                    top_k <= 8 && E <= 32767,
-                "moe: T=%d tokens, E=%d experts, top_k=%d exceed the grouping limits "
-                "(T*8 <= %d, E*ceil(T/64) <= %d, top_k <= 8)", T, E, top_k, GROUP_MAX_PAIRS,
-                GROUP_MAX_ITEMS);
-    PIO_REQUIRE(aligned16(w_gu) && aligned16(w_down), "moe: weights must be 16-byte aligned");
+    PIO_REQUIRE(x_dtype == PIO_F32 || x_dtype == PIO_F16, "moe: x must be fp32 or fp16");
+    PIO_REQUIRE(E >= 1 && E <= ROUTE_MAX_E && top_k >= 1 && top_k <= E && top_k <= 64,
+                "moe: E=%d experts (<= %d) and top_k=%d (<= min(E, 64))", E, ROUTE_MAX_E, top_k);
+    PIO_REQUIRE((int64_t)T * top_k <= INT32_MAX / 4, "moe: T * top_k too large");
+    PIO_REQUIRE(H <= 64 * 8 * ROUTE_XG, "moe: H=%d must be <= %d", H, 64 * 8 * ROUTE_XG);
+    PIO_REQUIRE(aligned16(w_gu) && aligned16(w_down) && aligned16(x),
+                "moe: x and the weights must be 16-byte aligned");
     if (T == 0) return PIO_OK;
     Scratch own;
     if (!ws) {
@@ -458,11 +464,16 @@ int moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* w_gu
     MoeWs w = moe_layout((char*)ws, T, H, I, E, top_k);
     const int P = T * top_k;
 
-    PIO_TRY(moe_route(logits, w.topk_w, w.topk_id, T, E, top_k, renorm, st));
-    moe_group_kernel<<<1, 1024, 0, st>>>(w.topk_id, T, E, top_k, w.offsets, w.row_token,
-                                         w.pos_of_pair);
+    if (x_dtype == PIO_F32)
+        moe_route_quant_kernel<float><<<ceil_div(T, 4), 256, 0, st>>>(
+            logits, (const float*)x, H, w.topk_w, w.topk_id, w.qx, w.sx, T, E, top_k, renorm);
+    else
+        moe_route_quant_kernel<_Float16><<<ceil_div(T, 4), 256, 0, st>>>(
+            logits, (const _Float16*)x, H, w.topk_w, w.topk_id, w.qx, w.sx, T, E, top_k, renorm);
     PIO_LAUNCHED();
-    PIO_TRY(quantize_per_token(x, x_dtype, w.qx, w.sx, T, H, st));
+    moe_group_kernel<<<E, 512, 0, st>>>(w.topk_id, T, E, top_k, w.offsets, w.row_token,
+                                        w.pos_of_pair);
+    PIO_LAUNCHED();
 
     GroupedParams g{};
     g.A = w.qx; g.a_rows = w.row_token; g.s_a = w.sx;

@@ -155,6 +155,31 @@ template <> __device__ __forceinline__ _Float16 from_f32<_Float16>(float v) { re
 
 inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
+template <typename XT>
+__device__ __forceinline__ void load8(const XT* p, float (&v)[8]);
+template <>
+__device__ __forceinline__ void load8<float>(const float* p, float (&v)[8]) {
+    float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+template <>
+__device__ __forceinline__ void load8<_Float16>(const _Float16* p, float (&v)[8]) {
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    h8 h = *(const h8*)p;
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = (float)h[i];
+}
+
+// Per-token quantizer step: clamp(rint(x / s), -127, 127), IEEE division,
+// round-half-even.
+__device__ __forceinline__ int8_t quant1(float x, float s) {
+    float r = __builtin_rintf(x / s);
+    r = fminf(fmaxf(r, -127.f), 127.f);
+    return (int8_t)(int)r;
+}
+
+
 // e^x by a fixed sequence of IEEE fp32 operations (Cody-Waite reduction by
 // ln2 in two parts, degree-7 Taylor polynomial in Horner form with explicit
 // fmaf, scaling by ldexp), so that the host oracle's identical C function

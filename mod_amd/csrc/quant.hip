@@ -15,28 +15,6 @@
 
 namespace pio {
 
-template <typename XT>
-__device__ __forceinline__ void load8(const XT* p, float (&v)[8]);
-template <>
-__device__ __forceinline__ void load8<float>(const float* p, float (&v)[8]) {
-    float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-}
-template <>
-__device__ __forceinline__ void load8<_Float16>(const _Float16* p, float (&v)[8]) {
-    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-    h8 h = *(const h8*)p;
-#pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = (float)h[i];
-}
-
-__device__ __forceinline__ int8_t quant1(float x, float s) {
-    float r = __builtin_rintf(x / s);
-    r = fminf(fmaxf(r, -127.f), 127.f);
-    return (int8_t)(int)r;
-}
-
 // VEC: K % 8 == 0 and 16-byte aligned rows -> 8 elements per lane per step.
 template <typename XT, bool VEC>
 __global__ __launch_bounds__(256) void quant_per_token_kernel(const XT* __restrict__ x,

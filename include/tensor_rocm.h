@@ -140,6 +140,24 @@ void begin_capture(void);
 void end_capture(void);
 void replay_graph(void);
 
+/* New, for layer offloading (HybridScheduler, hybrid_scheduler.py:10-177,
+ * whose CUDAStream use at :22-23 and :49-72 notes that events are needed for
+ * its prefetch): a host tensor in pinned memory (device_id -1; freed by
+ * free_tensor), an asynchronous copy between any two tensors of equal bytes
+ * and dtype on a stream (NULL: the current one; a DMA that overlaps other
+ * streams' kernels when the host side is pinned), and events to order one
+ * stream after another. event_query returns 1 when the event has completed, 0
+ * when not, < 0 on error. */
+Tensor* create_tensor_pinned(int* shape, int ndim, int dtype);
+int tensor_is_pinned(Tensor* t);
+int tensor_copy_async(Tensor* dst, Tensor* src, void* stream);
+void* create_event(void);
+void destroy_event(void* event);
+int record_event(void* event, void* stream);
+int stream_wait_event(void* stream, void* event);
+int event_synchronize(void* event);
+int event_query(void* event);
+
 /* New: error channel (the reference has none; its CUDA path exit()s,
  * tensor_ops_cuda.cu:10-18). Message of the last failed call on this thread,
  * "" if none; tensor_clear_error() resets it. */

@@ -41,12 +41,13 @@ def _device_id(device: str) -> int:
 class Tensor:
     """A library-owned tensor. ``data`` may be a list or a numpy array."""
 
-    __slots__ = ("device", "dtype", "_handle", "__weakref__")
+    __slots__ = ("device", "dtype", "_handle", "_src", "__weakref__")
 
     def __init__(self, shape: Sequence[int], data=None, device: str = "rocm:0",
                  dtype: str = "float32", _handle=None):
         self.device = device
         self.dtype = dtype
+        self._src = None
         if _handle is not None:
             self._handle = _handle
         else:
@@ -114,6 +115,35 @@ class Tensor:
         if name not in _CODE:
             raise ValueError(f"unsupported dtype {arr.dtype}")
         return cls(arr.shape, arr, device=device, dtype=name)
+
+    @classmethod
+    def pinned(cls, shape: Sequence[int], dtype: str = "float32") -> "Tensor":
+        """A host tensor ("cpu") in pinned memory: copies to and from the GPU
+        run as DMA on a stream, overlapping kernels."""
+        c_shape = (ctypes.c_int * len(shape))(*[int(x) for x in shape])
+        h = lib.create_tensor_pinned(c_shape, len(shape), _CODE[dtype])
+        if not h:
+            raise RocmError(f"create_tensor_pinned failed: {ops.last_error()}")
+        return cls(shape, device="cpu", dtype=dtype, _handle=h)
+
+    def to(self, device: str, non_blocking: bool = False, stream=None) -> "Tensor":
+        """Reference Tensor.to (backend.py:302-315): a copy on `device`
+        ("cpu" or "rocm:N"). The copy runs on `stream` (a HIPStream or raw
+        handle; default the current stream). A host destination is pinned.
+        With non_blocking the call returns at once and the result keeps the
+        source alive; the caller orders later work after the copy (an event,
+        or synchronizing the stream)."""
+        if device == self.device:
+            return self
+        out = Tensor.pinned(self.shape, self.dtype) if device == "cpu" else \
+            Tensor(self.shape, device=device, dtype=self.dtype)
+        sh = _stream_handle(stream)
+        check(lib.tensor_copy_async(out._handle, self._handle, sh), "tensor_copy_async")
+        if non_blocking:
+            out._src = self
+        else:
+            lib.stream_synchronize(sh)
+        return out
 
     # ----------------------------------------------------------------- ops
     def _new(self, shape, dtype=None) -> "Tensor":
@@ -207,6 +237,13 @@ class Tensor:
         return out
 
 
+def _stream_handle(stream):
+    """Raw handle of a HIPStream (or a raw handle / None: the current stream)."""
+    if stream is None:
+        return None
+    return getattr(stream, "_handle", stream)
+
+
 def _raise_if_error(what: str) -> None:
     msg = ops.last_error()
     if msg:
@@ -237,6 +274,30 @@ class Module:
                 yield p
         for m in self._modules.values():
             yield from m.parameters()
+
+    def named_parameters(self, prefix: str = ""):
+        for n, p in self._parameters.items():
+            if p is not None:
+                yield prefix + n, p
+        for n, m in self._modules.items():
+            yield from m.named_parameters(prefix + n + ".")
+
+    def _set_parameter(self, name: str, value) -> None:
+        """Replaces a parameter (dotted names reach submodules), keeping the
+        attribute of the same name in step, as the reference's Module.to does."""
+        if "." in name:
+            head, rest = name.split(".", 1)
+            self._modules[head]._set_parameter(rest, value)
+            return
+        self._parameters[name] = value
+        if hasattr(self, name):
+            setattr(self, name, value)
+
+    def to(self, device: str, non_blocking: bool = False, stream=None):
+        """Reference Module.to (backend.py:665-674): every parameter moved."""
+        for name, p in list(self.named_parameters()):
+            self._set_parameter(name, p.to(device, non_blocking=non_blocking, stream=stream))
+        return self
 
     def state_dict(self, prefix: str = "", destination=None):
         destination = {} if destination is None else destination
@@ -345,6 +406,86 @@ def free_pinned(ptr) -> None:
 
 def synchronize() -> None:
     lib.stream_synchronize(None)
+
+
+class HIPStream:
+    """Mirror of the reference CUDAStream (backend.py:165-189): an in-order
+    stream of the library; ``with stream:`` makes it the current stream for
+    every op (and restores the previous one on exit)."""
+
+    def __init__(self):
+        self._handle = lib.create_stream()
+        if not self._handle:
+            raise RocmError(f"create_stream failed: {ops.last_error()}")
+        self._prev = None
+
+    def __del__(self):
+        h = getattr(self, "_handle", None)
+        if h:
+            try:
+                lib.destroy_stream(h)
+            except Exception:
+                pass
+            self._handle = None
+
+    def synchronize(self):
+        lib.stream_synchronize(self._handle)
+
+    def __enter__(self):
+        self._prev = lib.get_current_stream()
+        lib.set_current_stream(self._handle)
+        return self
+
+    def __exit__(self, exc_type, exc_val, exc_tb):
+        lib.set_current_stream(self._prev)
+        self._prev = None
+
+    def record_event(self) -> "HIPEvent":
+        ev = HIPEvent()
+        ev.record(self)
+        return ev
+
+    def wait_event(self, ev: "HIPEvent") -> None:
+        check(lib.stream_wait_event(self._handle, ev._handle), "stream_wait_event")
+
+
+class HIPEvent:
+    """Orders one stream's later work after what another stream queued before
+    the event (no reference counterpart; hybrid_scheduler.py:51-53 notes it
+    would need one)."""
+
+    def __init__(self):
+        self._handle = lib.create_event()
+        if not self._handle:
+            raise RocmError(f"create_event failed: {ops.last_error()}")
+
+    def __del__(self):
+        h = getattr(self, "_handle", None)
+        if h:
+            try:
+                lib.destroy_event(h)
+            except Exception:
+                pass
+            self._handle = None
+
+    def record(self, stream=None) -> None:
+        check(lib.record_event(self._handle, _stream_handle(stream)), "record_event")
+
+    @classmethod
+    def on_current_stream(cls) -> "HIPEvent":
+        """An event recorded on the current stream now."""
+        ev = cls()
+        ev.record(None)
+        return ev
+
+    def synchronize(self) -> None:
+        check(lib.event_synchronize(self._handle), "event_synchronize")
+
+    def query(self) -> bool:
+        r = lib.event_query(self._handle)
+        if r < 0:
+            raise RocmError(f"event_query failed: {ops.last_error()}")
+        return r == 1
 
 
 class HIPGraph:

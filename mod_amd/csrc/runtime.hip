@@ -295,6 +295,7 @@ void release_stream(hipStream_t s) {
 struct Meta {
     int dtype;
     size_t bytes;
+    bool pinned;   // host tensor in hipHostMalloc memory (create_tensor_pinned)
 };
 static std::mutex g_meta_mu;
 static std::unordered_map<const Tensor*, Meta> g_meta;
@@ -303,6 +304,11 @@ int tensor_dtype_of(const Tensor* t) {
     std::lock_guard<std::mutex> lk(g_meta_mu);
     auto it = g_meta.find(t);
     return it == g_meta.end() ? PIO_F32 : it->second.dtype;
+}
+static bool tensor_pinned_of(const Tensor* t) {
+    std::lock_guard<std::mutex> lk(g_meta_mu);
+    auto it = g_meta.find(t);
+    return it != g_meta.end() && it->second.pinned;
 }
 static size_t tensor_bytes_of(const Tensor* t) {
     std::lock_guard<std::mutex> lk(g_meta_mu);
@@ -353,7 +359,7 @@ PIO_EXPORT const char* pio_version(void) {
     return "libtensor_ops_rocm 0.1 (gfx950, int8 quantized-linear path)";
 }
 
-static Tensor* make_tensor(const int* shape, int ndim, int device_id, int dtype) {
+static Tensor* make_tensor(const int* shape, int ndim, int device_id, int dtype, bool pinned = false) {
     if (ndim < 0 || (ndim > 0 && !shape)) {
         set_error(PIO_ERR_INVALID, "create_tensor: bad ndim %d", ndim);
         return nullptr;
@@ -404,6 +410,16 @@ static Tensor* make_tensor(const int* shape, int ndim, int device_id, int dtype)
             return nullptr;
         }
         t->data = (float*)p;
+    } else if (pinned) {
+        void* p = nullptr;
+        if (hipHostMalloc(&p, bytes ? bytes : 64, hipHostMallocDefault) != hipSuccess) {
+            (void)hipGetLastError();
+            set_error(PIO_ERR_OOM, "create_tensor_pinned: hipHostMalloc of %zu bytes failed", bytes);
+            free(t->shape);
+            free(t);
+            return nullptr;
+        }
+        t->data = (float*)p;
     } else {
         size_t hb = (bytes + 63) / 64 * 64;
         t->data = (float*)aligned_alloc(64, hb ? hb : 64);
@@ -416,7 +432,7 @@ static Tensor* make_tensor(const int* shape, int ndim, int device_id, int dtype)
     }
     {
         std::lock_guard<std::mutex> lk(g_meta_mu);
-        g_meta[t] = Meta{dtype, bytes};
+        g_meta[t] = Meta{dtype, bytes, pinned && device_id < 0};
     }
     return t;
 }
@@ -427,17 +443,26 @@ PIO_EXPORT Tensor* create_tensor(int* shape, int ndim, int device_id) {
 PIO_EXPORT Tensor* create_tensor_typed(int* shape, int ndim, int device_id, int dtype) {
     return make_tensor(shape, ndim, device_id, dtype);
 }
+PIO_EXPORT Tensor* create_tensor_pinned(int* shape, int ndim, int dtype) {
+    return make_tensor(shape, ndim, -1, dtype, true);
+}
 PIO_EXPORT int tensor_dtype(Tensor* t) { return tensor_dtype_of(t); }
 
 PIO_EXPORT void free_tensor(Tensor* t) {
     if (!t) return;
-    bool ours;
+    bool ours = false, pinned = false;
     {
         std::lock_guard<std::mutex> lk(g_meta_mu);
-        ours = g_meta.erase(t) > 0;
+        auto it = g_meta.find(t);
+        if (it != g_meta.end()) {
+            ours = true;
+            pinned = it->second.pinned;
+            g_meta.erase(it);
+        }
     }
     if (ours && t->data) {
         if (t->device_id >= 0) device_free(t->data);
+        else if (pinned) (void)hipHostFree(t->data);
         else free(t->data);
     }
     if (ours) {
@@ -637,6 +662,69 @@ PIO_EXPORT void set_current_stream(void* s) {
     g_user_stream = (hipStream_t)s;
 }
 PIO_EXPORT void* get_current_stream(void) { return (void*)current_stream(); }
+
+// Copies src's bytes into dst (same byte size; host or device on either side)
+// on `stream` (NULL: the current stream) without waiting. Host memory must stay
+// untouched until the copy is done: record an event after it, or synchronize.
+// With a pinned host tensor (create_tensor_pinned) the copy is a DMA that
+// overlaps kernels on other streams; pageable host memory makes it synchronous.
+PIO_EXPORT int tensor_copy_async(Tensor* dst, Tensor* src, void* stream) {
+    PIO_REQUIRE(dst && src, "tensor_copy_async: null tensor");
+    const size_t nb = tensor_bytes_of(src);
+    PIO_REQUIRE(tensor_bytes_of(dst) == nb, "tensor_copy_async: %zu bytes into a tensor of %zu",
+                nb, tensor_bytes_of(dst));
+    PIO_REQUIRE(tensor_dtype_of(dst) == tensor_dtype_of(src), "tensor_copy_async: dtype mismatch");
+    if (nb == 0) return PIO_OK;
+    PIO_REQUIRE(dst->data && src->data, "tensor_copy_async: null data");
+    const hipStream_t s = pick_stream(stream);
+    const bool hd = dst->device_id >= 0, hs = src->device_id >= 0;
+    const hipMemcpyKind kind = hs ? (hd ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost)
+                                  : (hd ? hipMemcpyHostToDevice : hipMemcpyHostToHost);
+    PIO_HIP(hipMemcpyAsync(dst->data, src->data, nb, kind, s));
+    return PIO_OK;
+}
+PIO_EXPORT int tensor_is_pinned(Tensor* t) { return t && tensor_pinned_of(t) ? 1 : 0; }
+
+// ----------------------------------------------------------------- events ---
+// Ordering between streams (a transfer stream and a compute stream): record
+// on one, wait on another. Events are created without timing.
+PIO_EXPORT void* create_event(void) {
+    hipEvent_t e = nullptr;
+    if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        set_error(PIO_ERR_HIP, "create_event failed");
+        return nullptr;
+    }
+    return (void*)e;
+}
+PIO_EXPORT void destroy_event(void* e) {
+    if (e) (void)hipEventDestroy((hipEvent_t)e);
+}
+PIO_EXPORT int record_event(void* e, void* stream) {
+    PIO_REQUIRE(e, "record_event: null event");
+    PIO_HIP(hipEventRecord((hipEvent_t)e, pick_stream(stream)));
+    return PIO_OK;
+}
+PIO_EXPORT int stream_wait_event(void* stream, void* e) {
+    PIO_REQUIRE(e, "stream_wait_event: null event");
+    PIO_HIP(hipStreamWaitEvent(pick_stream(stream), (hipEvent_t)e, 0));
+    return PIO_OK;
+}
+PIO_EXPORT int event_synchronize(void* e) {
+    PIO_REQUIRE(e, "event_synchronize: null event");
+    PIO_HIP(hipEventSynchronize((hipEvent_t)e));
+    return PIO_OK;
+}
+PIO_EXPORT int event_query(void* e) {
+    PIO_REQUIRE(e, "event_query: null event");
+    const hipError_t r = hipEventQuery((hipEvent_t)e);
+    if (r == hipSuccess) return 1;
+    if (r == hipErrorNotReady) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return set_error(PIO_ERR_HIP, "event_query: %s", hipGetErrorString(r));
+}
 PIO_EXPORT void device_synchronize(void) { (void)hipDeviceSynchronize(); }
 
 // ----------------------------------------------------------------- graphs ---

@@ -8,6 +8,12 @@ Raw entry points take device pointers (ints) -- from the library's own
 allocator (``mod_amd.backend.Tensor``) or from any other owner of HBM such as
 ``torch.Tensor.data_ptr()`` -- and a ``hipStream_t`` (int or None = the
 library's current stream).
+
+In a process that also uses torch on the GPU, import torch first: torch's
+wheel carries its own HIP and HSA runtimes, and the library's libamdhip64.so.7
+then resolves to the one torch loaded. Loaded before torch, the process ends up
+with two HIP runtimes, and once torch has initialised the device the library's
+runtime reports no device.
 """
 from __future__ import annotations
 
@@ -71,6 +77,15 @@ SIGNATURES: dict[str, tuple] = {
     "begin_capture": (None, []),
     "end_capture": (None, []),
     "replay_graph": (None, []),
+    "create_tensor_pinned": (TP, [ctypes.POINTER(ctypes.c_int), _i, _i]),
+    "tensor_is_pinned": (_i, [TP]),
+    "tensor_copy_async": (_i, [TP, TP, _vp]),
+    "create_event": (_vp, []),
+    "destroy_event": (None, [_vp]),
+    "record_event": (_i, [_vp, _vp]),
+    "stream_wait_event": (_i, [_vp, _vp]),
+    "event_synchronize": (_i, [_vp]),
+    "event_query": (_i, [_vp]),
     "tensor_last_error": (ctypes.c_char_p, []),
     "tensor_clear_error": (None, []),
     "tensor_matmul_int8": (None, [TP, TP, TP]),

@@ -11,6 +11,15 @@ ROOT = Path(__file__).resolve().parents[1]
 if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
+# torch first: its wheel carries its own HIP and HSA runtimes, and the
+# library's libamdhip64.so.7 then resolves to the one already loaded. Loaded
+# the other way round, a process holds two HIP runtimes and the library's
+# finds no device once torch has claimed it. (Any test may load mod_amd.)
+try:
+    import torch  # noqa: F401
+except ImportError:
+    pass
+
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a HIP GPU (MI355X) and the built ROCm library")

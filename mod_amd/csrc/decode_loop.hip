@@ -773,13 +773,31 @@ __device__ __forceinline__ AttRange att_range(int s, int w, int pos) {
     return r;
 }
 
+// Two consecutive KV-cache values (dims d, d + 1 of one row) as fp32.
+__device__ __forceinline__ void load2g(const float* src, float (&d)[2]) {
+    typedef float lp_f2 __attribute__((ext_vector_type(2)));
+    const lp_f2 a = gld((const lp_f2*)src);
+    d[0] = a[0];
+    d[1] = a[1];
+}
+__device__ __forceinline__ void load2g(const _Float16* src, float (&d)[2]) {
+    typedef _Float16 lp_h2 __attribute__((ext_vector_type(2)));
+    const lp_h2 a = gld((const lp_h2*)src);
+    d[0] = (float)a[0];
+    d[1] = (float)a[1];
+}
+
 // Partial attention (P3) of split s = j over this workgroup's positions, for
-// both query heads of KV head g. Lane layout: 8 lanes per position (16 dims
-// each), 8 positions per pass; online softmax per lane group. The current
-// position's k/v (this step's, from the tagged copy) is one extra step, done by
-// lane group 0 of the wave whose range holds it. The per-lane-group partials
-// (scaled to the wave's max) go to LDS and one pass over them combines the 32
-// lane groups of the workgroup; the split's (max, sum, o) is stored tagged.
+// both query heads of KV head g. A wave takes its positions 8 per pass. Scores
+// use 8 lanes per position (lane group jj = position slot, 16 dims per lane);
+// the value rows are read in the accumulation layout instead (lane l holds
+// dims 2l, 2l+1 of each of the pass's 8 positions, one coalesced row per
+// load), so with the pass's 8 weights broadcast from their lane groups every
+// lane accumulates its own two output dims: the softmax state (max, sum) is
+// wave-uniform and no cross-lane combine of the outputs is needed. The current
+// position's k/v (this step's, from the tagged copy) is one extra pass with
+// slot 0 only. The waves' partials go to LDS and one pass over them combines
+// the four waves; the split's (max, sum, o) is stored tagged.
 template <typename KT>
 __device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t qtag, uint32_t tag) {
     constexpr int G = LP_G;
@@ -793,18 +811,28 @@ __device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t q
     // them): issued before the q poll, so their latency hides behind it.
     const KT* kb = (const KT*)p.kc + ((int64_t)l * LP_NX + c.g) * p.max_seq * LP_D;
     const KT* vb = (const KT*)p.vc + ((int64_t)l * LP_NX + c.g) * p.max_seq * LP_D;
-    float kp[LP_NPF][16], vp[LP_NPF][16];
-#pragma unroll
-    for (int ps = 0; ps < LP_NPF; ps++) {
+    auto load_pass = [&](int ps, float (&kk)[16], float (&vv)[8][2]) {
         const int tp = r.tw0 + ps * 8 + jj;
         if (tp < r.tw1 && tp != pos) {
-            load_row16g(kb + (int64_t)tp * LP_D + part * 16, kp[ps]);
-            load_row16g(vb + (int64_t)tp * LP_D + part * 16, vp[ps]);
+            load_row16g(kb + (int64_t)tp * LP_D + part * 16, kk);
         } else {
 #pragma unroll
-            for (int i = 0; i < 16; i++) { kp[ps][i] = 0.f; vp[ps][i] = 0.f; }
+            for (int i = 0; i < 16; i++) kk[i] = 0.f;
         }
-    }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int tv = r.tw0 + ps * 8 + i;   // the same in every lane
+            if (tv < r.tw1 && tv != pos) {
+                load2g(vb + (int64_t)tv * LP_D + 2 * c.lane, vv[i]);
+            } else {
+                vv[i][0] = 0.f;
+                vv[i][1] = 0.f;
+            }
+        }
+    };
+    float kp[LP_NPF][16], vp[LP_NPF][8][2];
+#pragma unroll
+    for (int ps = 0; ps < LP_NPF; ps++) load_pass(ps, kp[ps], vp[ps]);
     {
         // q of the two query heads and the current k/v row, in one poll
         // (words lane + 64 i: q for i < 4, then k, v)
@@ -827,80 +855,80 @@ __device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t q
     float qv[G][16];
 #pragma unroll
     for (int h = 0; h < G; h++) load_row16(stg + h * LP_D + part * 16, qv[h]);
-    float m[G], lsum[G], o[G][16];
+    float m[G], lsum[G], o[G][2];
 #pragma unroll
     for (int h = 0; h < G; h++) {
         m[h] = -INFINITY;
         lsum[h] = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; i++) o[h][i] = 0.f;
+        o[h][0] = o[h][1] = 0.f;
     }
-    auto step = [&](const float (&kk)[16], const float (&vv)[16], bool valid) {
+    // One pass: slot jj's score in its lane group (-inf when invalid), the
+    // wave's running max and sum, and every lane's two output dims. The two
+    // heads are independent chains, written side by side and branch-free so
+    // that their latencies overlap.
+    auto pass = [&](const float (&kk)[16], const float (&vv)[8][2], bool valid) {
+        float sc[G], mx[G], corr[G], e[G];
 #pragma unroll
         for (int h = 0; h < G; h++) {
             float d4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int i = 0; i < 16; i++) d4[i & 3] = fmaf(qv[h][i], kk[i], d4[i & 3]);
-            float s = sum8((d4[0] + d4[1]) + (d4[2] + d4[3])) * p.att_scale;
-            s = valid ? s : -INFINITY;
-            const float mn = fmaxf(m[h], s);
-            const float corr = mn == -INFINITY ? 1.f : __expf(m[h] - mn);
-            const float e = s == -INFINITY ? 0.f : __expf(s - mn);
-            lsum[h] = fmaf(lsum[h], corr, e);
+            sc[h] = valid ? sum8((d4[0] + d4[1]) + (d4[2] + d4[3])) * p.att_scale : -INFINITY;
+        }
 #pragma unroll
-            for (int i = 0; i < 16; i++) o[h][i] = fmaf(o[h][i], corr, e * vv[i]);
-            m[h] = mn;
+        for (int h = 0; h < G; h++) mx[h] = fmaxf(m[h], wmax(sc[h]));   // wave-uniform
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            corr[h] = mx[h] == -INFINITY ? 0.f : __expf(m[h] - mx[h]);
+            e[h] = sc[h] == -INFINITY ? 0.f : __expf(sc[h] - mx[h]);
+        }
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            float o0 = o[h][0] * corr[h], o1 = o[h][1] * corr[h], es = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float ei = rlane(e[h], 8 * i);
+                o0 = fmaf(ei, vv[i][0], o0);
+                o1 = fmaf(ei, vv[i][1], o1);
+                es += ei;
+            }
+            o[h][0] = o0;
+            o[h][1] = o1;
+            lsum[h] = fmaf(lsum[h], corr[h], es);
+            m[h] = mx[h];
         }
     };
 #pragma unroll
     for (int ps = 0; ps < LP_NPF; ps++) {
+        if (ps >= passes) break;   // wave-uniform: no work for an empty pass
         const int tp = r.tw0 + ps * 8 + jj;
-        step(kp[ps], vp[ps], ps < passes && tp < r.tw1 && tp != pos);
+        pass(kp[ps], vp[ps], tp < r.tw1 && tp != pos);
     }
     for (int ps = LP_NPF; ps < passes; ps++) {
         const int tp = r.tw0 + ps * 8 + jj;
-        const bool valid = tp < r.tw1 && tp != pos;
-        float kk[16], vv[16];
-        if (valid) {
-            load_row16g(kb + (int64_t)tp * LP_D + part * 16, kk);
-            load_row16g(vb + (int64_t)tp * LP_D + part * 16, vv);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; i++) { kk[i] = 0.f; vv[i] = 0.f; }
-        }
-        step(kk, vv, valid);
+        float kk[16], vv[8][2];
+        load_pass(ps, kk, vv);
+        pass(kk, vv, tp < r.tw1 && tp != pos);
     }
     if (has_cur) {
-        // this step's k/v as the cache holds them
-        float kk[16], vv[16];
+        // this step's k/v as the cache holds them, in slot 0
+        float kk[16], vv[8][2];
         load_row16(stg + G * LP_D + part * 16, kk);
-        load_row16(stg + G * LP_D + LP_D + part * 16, vv);
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            kk[i] = kv_round(kk[i], (KT*)nullptr);
-            vv[i] = kv_round(vv[i], (KT*)nullptr);
-        }
-        step(kk, vv, jj == 0);
+        for (int i = 0; i < 16; i++) kk[i] = kv_round(kk[i], (KT*)nullptr);
+        vv[0][0] = kv_round(stg[G * LP_D + LP_D + 2 * c.lane], (KT*)nullptr);
+        vv[0][1] = kv_round(stg[G * LP_D + LP_D + 2 * c.lane + 1], (KT*)nullptr);
+#pragma unroll
+        for (int i = 1; i < 8; i++) vv[i][0] = vv[i][1] = 0.f;
+        pass(kk, vv, jj == 0);
     }
-    // Scale every lane group to the wave's max and sum the 8 lane groups in
-    // registers (lanes with equal lane & 7 hold the same 16 dims); the wave's
-    // partial po[w][h][128] and its max / sum go to LDS.
+    // the wave's partial o[h][128] (relative to its max) and its max / sum
 #pragma unroll
     for (int h = 0; h < G; h++) {
-        const float mw = wmax(m[h]);
-        const float f = m[h] == -INFINITY ? 0.f : __expf(m[h] - mw);
-        const float lw = wsum(part == 0 ? lsum[h] * f : 0.f);
-        float os[16];
-#pragma unroll
-        for (int i = 0; i < 16; i++) os[i] = sum_stride8(o[h][i] * f);
-        if (jj == 0) {
-            float* dst = c.attp + (c.w * G + h) * LP_D + part * 16;
-#pragma unroll
-            for (int i = 0; i < 16; i += 4) *(float4*)(dst + i) = make_float4(os[i], os[i + 1], os[i + 2], os[i + 3]);
-        }
+        *(float2*)(c.attp + (c.w * G + h) * LP_D + 2 * c.lane) = make_float2(o[h][0], o[h][1]);
         if (c.lane == 0) {
-            c.attm[c.w * G + h] = mw;
-            c.attm[LP_CW * G + c.w * G + h] = lw;
+            c.attm[c.w * G + h] = m[h];
+            c.attm[LP_CW * G + c.w * G + h] = lsum[h];
         }
     }
     if (!csync(p, c, 22)) return false;

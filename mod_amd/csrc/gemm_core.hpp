@@ -387,7 +387,8 @@ template <int WMT, int WNT, int D, int NK>
 __device__ __forceinline__ void mma_tile_v6(const int8_t* __restrict__ A, int64_t lda, int m_rem,
                                             const int8_t* __restrict__ B, int64_t ldb, int n_rem,
                                             int8_t* lds, v16i (&acc)[WMT][WNT],
-                                            const int32_t* __restrict__ a_rows = nullptr) {
+                                            const int32_t* __restrict__ a_rows = nullptr,
+                                            int b_jump = 0) {
     using T = TileV6<WMT, WNT, D>;
     constexpr int L = T::L, ABLK = T::BM / 8;
     static_assert(ABLK == 8 * WMT, "copies j < WMT are A blocks, the rest B blocks");
@@ -405,7 +406,9 @@ __device__ __forceinline__ void mma_tile_v6(const int8_t* __restrict__ A, int64_
             src[j] = A + (int64_t)(a_rows ? a_rows[rr] : rr) * lda + c * 16;
         } else {
             const int r = (q - ABLK) * 8 + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
-            src[j] = B + (int64_t)min(r, n_rem - 1) * ldb + c * 16;
+            // b_jump: the tile's second half of columns reads B rows b_jump further on
+            const int rb = r >= T::BN / 2 ? r + b_jump : r;
+            src[j] = B + (int64_t)min(rb, n_rem - 1) * ldb + c * 16;
         }
         dst[j] = q * 1024 + lane * 16;
     }

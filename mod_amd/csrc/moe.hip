@@ -14,10 +14,12 @@
 //              an expert (one block per expert: its offset is the count of pairs
 //              routed below it, its tokens ranked by ballots), so every expert's
 //              rows are one contiguous run of an index list.
-//  3. gate_up: grouped W8A8 GEMM, one block per (expert, 128-column tile); the
-//              block walks its expert's row tiles, so each weight tile is read
-//              from HBM once. fp32 output.
-//  4. swiglu:  h = silu(g) * u (tensor_ops.c:588-604 formula) and per-row requant.
+//  3. gate_up: grouped W8A8 GEMM, one block per (expert, 64 gate + 64 up
+//              rows); the block walks its expert's row tiles, so each weight
+//              tile is read from HBM once. Its epilogue applies SwiGLU,
+//              h = silu(g) * u (tensor_ops.c:588-604 formula), writes h (fp32)
+//              and the row's max |h| (atomic max).
+//  4. requant: h per row to int8 with that max.
 //  5. down:    grouped W8A8 GEMM over the contiguous h rows, fp32 output.
 //  6. combine: out[t] = sum_{k=0..top_k-1} w[t,k] * down[pos(t,k)], in k order.
 #include "gemm_core.hpp"
@@ -102,10 +104,11 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
                 topk_id + (int64_t)t * top_k);
 }
 
-// The layer's first launch: a wave routes its token and quantizes the
-// token's x row per token (the quantizer of quant.hip: amax / 127, IEEE
-// division, round-half-even); the row is loaded once into registers, lane l
-// holding the 8-element chunks l, l + 64, ... (H % 8 == 0, H <= 512 ROUTE_XG).
+// The layer's first launch: block b takes tokens 2b and 2b + 1; waves 0-1
+// route them, waves 2-3 quantize their x rows per token (the quantizer of
+// quant.hip: amax / 127, IEEE division, round-half-even), each row loaded once
+// into registers, lane l holding the 8-element chunks l, l + 64, ...
+// (H % 8 == 0, H <= 512 ROUTE_XG).
 constexpr int ROUTE_XG = 8;
 template <typename XT>
 __global__ __launch_bounds__(256) void moe_route_quant_kernel(const float* __restrict__ logits,
@@ -114,27 +117,35 @@ __global__ __launch_bounds__(256) void moe_route_quant_kernel(const float* __res
                                                               int32_t* __restrict__ topk_id,
                                                               int8_t* __restrict__ qx,
                                                               float* __restrict__ sx, int T,
-                                                              int E, int top_k, int renorm) {
-    __shared__ float sp[4][ROUTE_MAX_E];
+                                                              int E, int top_k, int renorm,
+                                                              unsigned* __restrict__ hmax) {
+    __shared__ float sp[2][ROUTE_MAX_E];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int t = blockIdx.x * 4 + w;
+    // the gate_up epilogue's per-row max starts from 0 (grid >= 128 T threads >= T * top_k)
+    {
+        const int i = blockIdx.x * 256 + threadIdx.x;
+        if (i < T * top_k) hmax[i] = 0u;
+    }
+    const int t = blockIdx.x * 2 + (w & 1);
     if (t >= T) return;
-    // issue the x loads first: their latency overlaps the routing
+    if (w < 2) {
+        route_token(logits + (int64_t)t * E, sp[w], lane, E, top_k, renorm,
+                    topk_w + (int64_t)t * top_k, topk_id + (int64_t)t * top_k);
+        return;
+    }
     const XT* xr = x + (int64_t)t * H;
     const int nch = H / 8;
     float v[ROUTE_XG][8];
 #pragma unroll
     for (int g = 0; g < ROUTE_XG; g++)
         if (lane + 64 * g < nch) load8<XT>(xr + 8 * (lane + 64 * g), v[g]);
-    route_token(logits + (int64_t)t * E, sp[w], lane, E, top_k, renorm, topk_w + (int64_t)t * top_k,
-                topk_id + (int64_t)t * top_k);
     float amax = 0.f;
 #pragma unroll
     for (int g = 0; g < ROUTE_XG; g++)
         if (lane + 64 * g < nch)
 #pragma unroll
             for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[g][i]));
-    amax = wave_max(amax);
+    amax = wmax(amax);
     const float sc = amax == 0.f ? 1.f : amax / 127.0f;
     if (lane == 0) sx[t] = sc;
     int8_t* qr = qx + (int64_t)t * H;
@@ -214,7 +225,8 @@ struct GroupedParams {
     const int8_t* W;          // [E][N][K]
     const float* s_w;         // [E][N]
     const int32_t* offsets;   // [E+1]
-    float* C;                 // [rows][N], row = position
+    float* C;                 // [rows][N] (row = position); with SwiGLU [rows][N / 2] of h
+    unsigned* amax;           // SwiGLU: per position, max |h| as float bits (zeroed beforehand)
     int N, K;
 };
 
@@ -223,14 +235,28 @@ struct GroupedParams {
 // loads in flight per wave, 48 KB of LDS (two blocks per CU), A rows gathered
 // through the expert's token list. The block walks its expert's row tiles, so
 // each weight tile is streamed from HBM once per 64 tokens.
+// SWIGLU (gate_up): the tile's 128 columns are gate rows c0 .. c0 + 63 and
+// the matching up rows I + c0 .. I + c0 + 63 (I = N / 2), so the epilogue has
+// both halves of h = silu(g) * u for 64 channels: it writes h (fp32, half the
+// bytes of g and u) and raises the row's max |h| with an atomic max, which is
+// exact and order-free; the requantization then needs no second look at g, u.
 constexpr int MOE_WMT = 1, MOE_WNT = 1, MOE_D = 4;
 using MoeTile = TileV6<MOE_WMT, MOE_WNT, MOE_D>;
 constexpr int MOE_THREADS = 512;
 
-template <int NK>
+// silu(g) * u with the deterministic exp (the host oracle evaluates the same
+// operations, so h and its requantized bytes are bit-identical).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    return g * (1.0f / (1.0f + exp_det(-g))) * u;
+}
+
+template <int NK, bool SWIGLU>
 __global__ __launch_bounds__(MOE_THREADS, 2) void moe_grouped_gemm_kernel(GroupedParams p) {
     extern __shared__ __attribute__((aligned(16))) int8_t lds_moe[];
-    const int e = blockIdx.y, n0 = blockIdx.x * MoeTile::BN;
+    const int e = blockIdx.y;
+    // n0: first weight row of the tile; SwiGLU tiles take 64 gate + 64 up rows
+    const int n0 = SWIGLU ? blockIdx.x * (MoeTile::BN / 2) : blockIdx.x * MoeTile::BN;
+    const int I = p.N / 2;
     const int beg = p.offsets[e], cnt = p.offsets[e + 1] - beg;
     const int8_t* W = p.W + ((int64_t)e * p.N + n0) * p.K;
     const float* sw = p.s_w + (int64_t)e * p.N;
@@ -246,12 +272,15 @@ __global__ __launch_bounds__(MOE_THREADS, 2) void moe_grouped_gemm_kernel(Groupe
             const int pos = beg + min(m0 + tid, cnt - 1);
             my_scale = p.s_a[p.a_rows ? p.a_rows[pos] : pos];
         } else if (tid < MoeTile::BM + MoeTile::BN) {
-            my_scale = sw[min(n0 + tid - MoeTile::BM, p.N - 1)];
+            const int c = tid - MoeTile::BM;
+            const int row = SWIGLU && c >= MoeTile::BN / 2 ? I + n0 + c - MoeTile::BN / 2 : n0 + c;
+            my_scale = sw[min(row, p.N - 1)];
         }
         v16i acc[MOE_WMT][MOE_WNT];
         if (p.a_rows)
             mma_tile_v6<MOE_WMT, MOE_WNT, MOE_D, NK>(p.A, p.K, cnt - m0, W, p.K, p.N - n0, lds_moe, acc,
-                                                     p.a_rows + beg + m0);
+                                                     p.a_rows + beg + m0,
+                                                     SWIGLU ? I - MoeTile::BN / 2 : 0);
         else
             mma_tile_v6<MOE_WMT, MOE_WNT, MOE_D, NK>(p.A + (int64_t)(beg + m0) * p.K, p.K, cnt - m0, W, p.K,
                                                      p.N - n0, lds_moe, acc);
@@ -259,18 +288,59 @@ __global__ __launch_bounds__(MOE_THREADS, 2) void moe_grouped_gemm_kernel(Groupe
         __syncthreads();
         if (tid < MoeTile::BM + MoeTile::BN) scl[tid] = my_scale;
         __syncthreads();
+        if constexpr (SWIGLU) {
+            // scaled tile -> LDS; then h of (row, channel), 4 channels per thread
+            constexpr int TP = MoeTile::BN + 4;
+            float* tile = scl + MoeTile::BM + MoeTile::BN;
+            static_assert((MoeTile::BM + MoeTile::BN + MoeTile::BM * TP) * 4 <= MoeTile::LDS_BYTES,
+                          "epilogue tile fits in the stages");
 #pragma unroll
-        for (int j = 0; j < MOE_WNT; j++) {
-            const int c = v6_col<MOE_WNT>(j), n = n0 + c;
-            const float swn = scl[MoeTile::BM + c];
+            for (int j = 0; j < MOE_WNT; j++) {
+                const int c = v6_col<MOE_WNT>(j);
+                const float swn = scl[MoeTile::BM + c];
 #pragma unroll
-            for (int i = 0; i < MOE_WMT; i++)
+                for (int i = 0; i < MOE_WMT; i++)
 #pragma unroll
-                for (int v = 0; v < 16; v++) {
-                    const int rl = v6_row<MOE_WMT>(i, v), r = m0 + rl;
-                    const float val = (float)acc[i][j][v] * scl[rl] * swn;
-                    if (r < cnt && n < p.N) p.C[(int64_t)(beg + r) * p.N + n] = val;
+                    for (int v = 0; v < 16; v++) {
+                        const int rl = v6_row<MOE_WMT>(i, v);
+                        tile[rl * TP + c] = (float)acc[i][j][v] * scl[rl] * swn;
+                    }
+            }
+            __syncthreads();
+            constexpr int HC = MoeTile::BN / 2;          // channels per tile
+#pragma unroll
+            for (int it = 0; it < MoeTile::BM * (HC / 4) / MOE_THREADS; it++) {
+                const int q = it * MOE_THREADS + tid, rl = q / (HC / 4), c4 = (q % (HC / 4)) * 4;
+                const float4 g = *(const float4*)(tile + rl * TP + c4);
+                const float4 u = *(const float4*)(tile + rl * TP + HC + c4);
+                const float4 h = make_float4(silu_mul(g.x, u.x), silu_mul(g.y, u.y), silu_mul(g.z, u.z),
+                                             silu_mul(g.w, u.w));
+                // max |h| over the row's 64 channels: 16 consecutive lanes
+                float mx = fmaxf(fmaxf(fabsf(h.x), fabsf(h.y)), fmaxf(fabsf(h.z), fabsf(h.w)));
+                mx = fmaxf(mx, dpp<DPP_XOR1>(mx));
+                mx = fmaxf(mx, dpp<DPP_XOR2>(mx));
+                mx = fmaxf(mx, dpp<DPP_HMIRROR>(mx));
+                mx = fmaxf(mx, dpp<DPP_MIRROR>(mx));
+                if (m0 + rl < cnt) {
+                    const int64_t pos = beg + m0 + rl;
+                    *(float4*)(p.C + pos * I + n0 + c4) = h;
+                    if ((q % (HC / 4)) == 0) atomicMax(p.amax + pos, __float_as_uint(mx));
                 }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < MOE_WNT; j++) {
+                const int c = v6_col<MOE_WNT>(j), n = n0 + c;
+                const float swn = scl[MoeTile::BM + c];
+#pragma unroll
+                for (int i = 0; i < MOE_WMT; i++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) {
+                        const int rl = v6_row<MOE_WMT>(i, v), r = m0 + rl;
+                        const float val = (float)acc[i][j][v] * scl[rl] * swn;
+                        if (r < cnt && n < p.N) p.C[(int64_t)(beg + r) * p.N + n] = val;
+                    }
+            }
         }
         __syncthreads();   // the next row tile reuses the LDS stages
     }
@@ -278,88 +348,35 @@ __global__ __launch_bounds__(MOE_THREADS, 2) void moe_grouped_gemm_kernel(Groupe
 
 // Launches the instance for K = 128 * nk (1 <= nk <= MOE_MAX_NK).
 constexpr int MOE_MAX_NK = 32;
-template <int NK>
+template <int NK, bool SWIGLU>
 static void launch_grouped(const GroupedParams& g, dim3 grid, int nk, hipStream_t st) {
     if constexpr (NK <= MOE_MAX_NK) {
-        if (nk == NK) moe_grouped_gemm_kernel<NK><<<grid, MOE_THREADS, MoeTile::LDS_BYTES, st>>>(g);
-        else launch_grouped<NK + 1>(g, grid, nk, st);
+        if (nk == NK) moe_grouped_gemm_kernel<NK, SWIGLU><<<grid, MOE_THREADS, MoeTile::LDS_BYTES, st>>>(g);
+        else launch_grouped<NK + 1, SWIGLU>(g, grid, nk, st);
     }
 }
 
-// ------------------------------------------------------ swiglu + requant ---
-// silu(g) * u with the deterministic exp (the host oracle evaluates the same
-// operations, so h and its requantized bytes are bit-identical).
-__device__ __forceinline__ float silu_mul(float g, float u) {
-    return g * (1.0f / (1.0f + exp_det(-g))) * u;
-}
-
-// One pass: a lane keeps its h values in registers (4 consecutive columns per
-// float4 group, SWIGLU_NV groups at most: I <= 64 * 4 * SWIGLU_NV), so g and u
-// are read once and silu evaluated once per element.
-constexpr int SWIGLU_NV = 8;
-
-__global__ __launch_bounds__(256) void moe_swiglu_quant_reg_kernel(const float* __restrict__ gu,
-                                                                   int8_t* __restrict__ q,
-                                                                   float* __restrict__ s, int rows,
-                                                                   int I) {
+// --------------------------------------------------------------- requant ---
+// Requantization of h per row: s = max|h| / 127 (1 when 0), q = rint(h / s)
+// clamped to +-127, the per-token quantizer's rule; max|h| comes from the
+// gate_up epilogue's atomic max. One wave per row, 4 consecutive values per
+// lane and step.
+__global__ __launch_bounds__(256) void moe_requant_kernel(const float* __restrict__ h,
+                                                          const unsigned* __restrict__ amax,
+                                                          int8_t* __restrict__ q,
+                                                          float* __restrict__ s, int rows, int I) {
     const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= rows) return;
-    const float4* g4 = (const float4*)(gu + (int64_t)r * 2 * I);
-    const float4* u4 = (const float4*)(gu + (int64_t)r * 2 * I + I);
-    const int nv = I / 4;
-    float h[SWIGLU_NV][4];
-    float amax = 0.f;
-#pragma unroll
-    for (int j = 0; j < SWIGLU_NV; j++) {
-        const int c = lane + 64 * j;
-        if (c < nv) {
-            const float4 g = g4[c], u = u4[c];
-            h[j][0] = silu_mul(g.x, u.x);
-            h[j][1] = silu_mul(g.y, u.y);
-            h[j][2] = silu_mul(g.z, u.z);
-            h[j][3] = silu_mul(g.w, u.w);
-#pragma unroll
-            for (int e = 0; e < 4; e++) amax = fmaxf(amax, fabsf(h[j][e]));
-        }
-    }
-    amax = wave_max(amax);
-    const float sc = amax == 0.f ? 1.f : amax / 127.0f;
+    const float am = __uint_as_float(amax[r]);
+    const float sc = am == 0.f ? 1.f : am / 127.0f;
     if (lane == 0) s[r] = sc;
+    const float4* h4 = (const float4*)(h + (int64_t)r * I);
     uint32_t* qr = (uint32_t*)(q + (int64_t)r * I);
-#pragma unroll
-    for (int j = 0; j < SWIGLU_NV; j++) {
-        const int c = lane + 64 * j;
-        if (c < nv) {
-            uint32_t packed = 0;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                float v = __builtin_rintf(h[j][e] / sc);
-                v = fminf(fmaxf(v, -127.f), 127.f);
-                packed |= (uint32_t)(uint8_t)(int8_t)(int)v << (8 * e);
-            }
-            qr[c] = packed;
-        }
-    }
-}
-
-__global__ __launch_bounds__(256) void moe_swiglu_quant_kernel(const float* __restrict__ gu,
-                                                               int8_t* __restrict__ q,
-                                                               float* __restrict__ s, int rows,
-                                                               int I) {
-    const int lane = threadIdx.x & 63;
-    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (r >= rows) return;
-    const float* g = gu + (int64_t)r * 2 * I;
-    float amax = 0.f;
-    for (int i = lane; i < I; i += 64) amax = fmaxf(amax, fabsf(silu_mul(g[i], g[I + i])));
-    amax = wave_max(amax);
-    const float sc = amax == 0.f ? 1.f : amax / 127.0f;
-    if (lane == 0) s[r] = sc;
-    for (int i = lane; i < I; i += 64) {
-        float v = __builtin_rintf(silu_mul(g[i], g[I + i]) / sc);
-        v = fminf(fmaxf(v, -127.f), 127.f);
-        q[(int64_t)r * I + i] = (int8_t)(int)v;
+    for (int c = lane; c < I / 4; c += 64) {
+        const float4 v = h4[c];
+        qr[c] = (uint32_t)(uint8_t)quant1(v.x, sc) | (uint32_t)(uint8_t)quant1(v.y, sc) << 8 |
+                (uint32_t)(uint8_t)quant1(v.z, sc) << 16 | (uint32_t)(uint8_t)quant1(v.w, sc) << 24;
     }
 }
 
@@ -398,7 +415,8 @@ struct MoeWs {
     int32_t* pos_of_pair;
     int8_t* qx;
     float* sx;
-    float* gu;
+    float* h;            // [P][I] SwiGLU output (fp32)
+    unsigned* amax;      // [P] max |h| per row, float bits
     int8_t* qh;
     float* sh;
     float* d;
@@ -419,7 +437,8 @@ static MoeWs moe_layout(char* base, int T, int H, int I, int E, int k) {
     w.pos_of_pair = (int32_t*)take(P * 4);
     w.qx = (int8_t*)take((size_t)T * H);
     w.sx = (float*)take((size_t)T * 4);
-    w.gu = (float*)take(P * 2 * I * 4);
+    w.h = (float*)take(P * I * 4);
+    w.amax = (unsigned*)take(P * 4);
     w.qh = (int8_t*)take(P * I);
     w.sh = (float*)take(P * 4);
     w.d = (float*)take(P * H * 4);
@@ -465,11 +484,11 @@ int moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* w_gu
     const int P = T * top_k;
 
     if (x_dtype == PIO_F32)
-        moe_route_quant_kernel<float><<<ceil_div(T, 4), 256, 0, st>>>(
-            logits, (const float*)x, H, w.topk_w, w.topk_id, w.qx, w.sx, T, E, top_k, renorm);
+        moe_route_quant_kernel<float><<<ceil_div(T, 2), 256, 0, st>>>(
+            logits, (const float*)x, H, w.topk_w, w.topk_id, w.qx, w.sx, T, E, top_k, renorm, w.amax);
     else
-        moe_route_quant_kernel<_Float16><<<ceil_div(T, 4), 256, 0, st>>>(
-            logits, (const _Float16*)x, H, w.topk_w, w.topk_id, w.qx, w.sx, T, E, top_k, renorm);
+        moe_route_quant_kernel<_Float16><<<ceil_div(T, 2), 256, 0, st>>>(
+            logits, (const _Float16*)x, H, w.topk_w, w.topk_id, w.qx, w.sx, T, E, top_k, renorm, w.amax);
     PIO_LAUNCHED();
     moe_group_kernel<<<E, 512, 0, st>>>(w.topk_id, T, E, top_k, w.offsets, w.row_token,
                                         w.pos_of_pair);
@@ -477,22 +496,19 @@ int moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* w_gu
 
     GroupedParams g{};
     g.A = w.qx; g.a_rows = w.row_token; g.s_a = w.sx;
-    g.W = w_gu; g.s_w = s_gu; g.offsets = w.offsets; g.C = w.gu;
+    g.W = w_gu; g.s_w = s_gu; g.offsets = w.offsets; g.C = w.h; g.amax = w.amax;
     g.N = 2 * I; g.K = H;
-    launch_grouped<1>(g, dim3(ceil_div(2 * I, MoeTile::BN), E), H / 128, st);
+    launch_grouped<1, true>(g, dim3(I / (MoeTile::BN / 2), E), H / 128, st);
     PIO_LAUNCHED();
 
-    if (I <= 64 * 4 * SWIGLU_NV)
-        moe_swiglu_quant_reg_kernel<<<ceil_div(P, 4), 256, 0, st>>>(w.gu, w.qh, w.sh, P, I);
-    else
-        moe_swiglu_quant_kernel<<<ceil_div(P, 4), 256, 0, st>>>(w.gu, w.qh, w.sh, P, I);
+    moe_requant_kernel<<<ceil_div(P, 4), 256, 0, st>>>(w.h, w.amax, w.qh, w.sh, P, I);
     PIO_LAUNCHED();
 
     GroupedParams d{};
     d.A = w.qh; d.a_rows = nullptr; d.s_a = w.sh;
     d.W = w_down; d.s_w = s_down; d.offsets = w.offsets; d.C = w.d;
     d.N = H; d.K = I;
-    launch_grouped<1>(d, dim3(ceil_div(H, MoeTile::BN), E), I / 128, st);
+    launch_grouped<1, false>(d, dim3(ceil_div(H, MoeTile::BN), E), I / 128, st);
     PIO_LAUNCHED();
 
     dim3 cg(ceil_div(H, 1024), T);

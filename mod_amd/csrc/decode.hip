@@ -88,12 +88,17 @@ __device__ __forceinline__ float dot16i8(const float (&x)[16], v4i_t w, float ac
 }
 
 // Two elements (i, i + half) of a KV cache row starting at element `row`.
+// fp16 rows are paired: slot 2i holds dim i and slot 2i + 1 dim i + half, so
+// the pair is one dword store (2-byte stores slowed the later loads of the
+// lines they touched ~4x); fp32 rows are in dimension order.
 __device__ __forceinline__ void kv_store(void* base, int64_t row, int i, int half, float a, float b,
                                          int kv16) {
     if (kv16) {
-        _Float16* d = (_Float16*)base + row;
-        d[i] = (_Float16)a;
-        d[i + half] = (_Float16)b;
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        h2 v;
+        v[0] = (_Float16)a;
+        v[1] = (_Float16)b;
+        *(h2*)((_Float16*)base + row + 2 * i) = v;
     } else {
         float* d = (float*)base + row;
         d[i] = a;
@@ -357,6 +362,9 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(
     const KT* kb = kc + ((int64_t)kvh * max_seq + t0) * D;
     const KT* vb = vc + ((int64_t)kvh * max_seq + t0) * D;
     const float* qg = q + (int64_t)kvh * G * D;
+    // fp16 rows are paired (kv_store): storage slot s holds dim s / 2 + 64 (s & 1)
+    constexpr bool PAIR = sizeof(KT) == 2;
+    auto dim_of = [](int slot) { return PAIR ? (slot >> 1) + 64 * (slot & 1) : slot; };
 
     {
         const int part = tid & 7, sub = tid >> 3;
@@ -364,10 +372,9 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(
 #pragma unroll
         for (int h = 0; h < ATT_MAX_G; h++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
+            for (int i = 0; i < 16; i++) {
                 if (h >= G) continue;
-                const float4 a = *(const float4*)(qg + h * D + part * 16 + 4 * i);
-                qv[h][4 * i] = a.x; qv[h][4 * i + 1] = a.y; qv[h][4 * i + 2] = a.z; qv[h][4 * i + 3] = a.w;
+                qv[h][i] = qg[h * D + dim_of(part * 16 + i)];   // q in the rows' slot order
             }
         for (int tb = 0; tb < n; tb += 64) {
             float kv[2][16];
@@ -451,7 +458,7 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(
         const int h = tid / D, d = tid % D;
         float o = 0.f;
 #pragma unroll
-        for (int i = 0; i < 8; i++) o += po[(i * G + h) * D + d];
+        for (int i = 0; i < 8; i++) o += po[(i * G + h) * D + (PAIR ? (d < 64 ? 2 * d : 2 * (d - 64) + 1) : d)];
         att_o[(int64_t)s * nq * D + (int64_t)(kvh * G + h) * D + d] = o;
     }
     if (tid < G) {

@@ -499,30 +499,40 @@ __device__ __forceinline__ void load_row16(const float* src, float (&d)[16]) {
         d[4 * i] = a.x; d[4 * i + 1] = a.y; d[4 * i + 2] = a.z; d[4 * i + 3] = a.w;
     }
 }
-// The same from global memory (the KV cache), through the global address space.
 typedef float lp_f4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ void load_row16g(const float* src, float (&d)[16]) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const lp_f4 a = gld((const lp_f4*)(src + 4 * i));
-        d[4 * i] = a[0]; d[4 * i + 1] = a[1]; d[4 * i + 2] = a[2]; d[4 * i + 3] = a[3];
-    }
+// A KV cache element. Its readers are the attention workgroups of KV head g
+// in later tokens, which run on the same XCD as the writer (XCD g owns head
+// g in every launch), so the store goes to that XCD's L2 (sc0), like the
+// hand-off words; a row is never read before it is written within a launch
+// (rows < pos come from the cache, the current one from the tagged copy), so
+// no reader's L1 can hold it stale, and a kernel boundary writes the L2 back
+// for the next launch or the graph path. A device-scope 2-byte store here
+// (fp16 KV) went to the memory side and held the wave's following stores, the
+// tagged q/k/v words, back by ~2.4 us per layer.
+// kv_put2(row, i, a, b) stores elements i and i + 64 of a cache row: fp32
+// rows are in dimension order; fp16 rows are paired (slot 2i holds dim i,
+// slot 2i + 1 dim i + 64), so the two halves go out as one dword -- 2-byte
+// stores measured ~4x slower loads of the lines they touched afterwards.
+__device__ __forceinline__ void kv_put2(float* row, int i, float a, float b) {
+    asm volatile("global_store_dword %0, %1, off sc0" ::"v"(row + i), "v"(a) : "memory");
+    asm volatile("global_store_dword %0, %1, off sc0" ::"v"(row + i + 64), "v"(b) : "memory");
 }
-typedef _Float16 lp_h8 __attribute__((ext_vector_type(8)));
-__device__ __forceinline__ void load_row16g(const _Float16* src, float (&d)[16]) {
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const lp_h8 a = gld((const lp_h8*)(src + 8 * i));
-#pragma unroll
-        for (int k = 0; k < 8; k++) d[8 * i + k] = (float)a[k];
-    }
+__device__ __forceinline__ void kv_put2(_Float16* row, int i, float a, float b) {
+    const unsigned w = (unsigned)__builtin_bit_cast(unsigned short, (_Float16)a) |
+                       (unsigned)__builtin_bit_cast(unsigned short, (_Float16)b) << 16;
+    asm volatile("global_store_dword %0, %1, off sc0" ::"v"(row + 2 * i), "v"(w) : "memory");
 }
-// A KV cache element, stored with device scope (read by other workgroups'
-// attention in later tokens of the same launch).
-__device__ __forceinline__ void kv_put(float* p, float v) { dev_store(p, v); }
-__device__ __forceinline__ void kv_put(_Float16* p, float v) {
-    __hip_atomic_store((unsigned short*)p, __builtin_bit_cast(unsigned short, (_Float16)v),
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Storage slots 16 part .. 16 part + 15 of a row as dims: the q (or current
+// k) values to pair with them, from a dimension-ordered vector.
+__device__ __forceinline__ void slots16(const float* src, int part, float (&d)[16], float*) {
+    load_row16(src + part * 16, d);
+}
+__device__ __forceinline__ void slots16(const float* src, int part, float (&d)[16], _Float16*) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        d[2 * j] = src[part * 8 + j];
+        d[2 * j + 1] = src[64 + part * 8 + j];
+    }
 }
 // The value the cache holds for v.
 __device__ __forceinline__ float kv_round(float v, float*) { return v; }
@@ -642,15 +652,13 @@ __device__ bool phase_qkv(const LoopParams& p, Cx& c, int l, int pos, int line0,
                 st_l2(dst + (u >> 6) * LP_D + i + 64, o1, tag);
             } else {
                 KT* kr = (KT*)p.kc + (((int64_t)l * LP_NX + c.g) * p.max_seq + pos) * LP_D;
-                kv_put(kr + i, o0);
-                kv_put(kr + i + 64, o1);
+                kv_put2(kr, i, o0, o1);
                 st_l2(dst + 256 + i, o0, tag);
                 st_l2(dst + 256 + i + 64, o1, tag);
             }
         } else {
             KT* vr = (KT*)p.vc + (((int64_t)l * LP_NX + c.g) * p.max_seq + pos) * LP_D;
-            kv_put(vr + i, v0);
-            kv_put(vr + i + 64, v1);
+            kv_put2(vr, i, v0, v1);
             st_l2(dst + 384 + i, v0, tag);
             st_l2(dst + 384 + i + 64, v1, tag);
         }
@@ -773,25 +781,66 @@ __device__ __forceinline__ AttRange att_range(int s, int w, int pos) {
     return r;
 }
 
-// Two consecutive KV-cache values (dims d, d + 1 of one row) as fp32.
-__device__ __forceinline__ void load2g(const float* src, float (&d)[2]) {
-    typedef float lp_f2 __attribute__((ext_vector_type(2)));
-    const lp_f2 a = gld((const lp_f2*)src);
-    d[0] = a[0];
-    d[1] = a[1];
+// A pass's cache data as loaded (raw bits; fp16 is widened only after the q
+// poll, so no conversion sits right behind a load and makes the wave wait for
+// it): a lane's 16 key slots and its 2 value slots of each of 8 positions.
+template <typename KT>
+struct KvRaw {
+    static constexpr int KQ = 16 * (int)sizeof(KT) / 16;   // 16-byte key pieces
+    static constexpr int VW = (int)sizeof(KT) / 2;         // dwords per value pair
+    lp_v4i k[KQ];
+    uint32_t v[8][VW];
+};
+template <typename KT>
+__device__ __forceinline__ void kv_load_k(const KT* src, KvRaw<KT>& r) {
+#pragma unroll
+    for (int q = 0; q < KvRaw<KT>::KQ; q++) r.k[q] = gld((const lp_v4i*)src + q);
 }
-__device__ __forceinline__ void load2g(const _Float16* src, float (&d)[2]) {
-    typedef _Float16 lp_h2 __attribute__((ext_vector_type(2)));
-    const lp_h2 a = gld((const lp_h2*)src);
-    d[0] = (float)a[0];
-    d[1] = (float)a[1];
+template <typename KT>
+__device__ __forceinline__ void kv_zero_k(KvRaw<KT>& r) {
+#pragma unroll
+    for (int q = 0; q < KvRaw<KT>::KQ; q++) r.k[q] = lp_v4i{0, 0, 0, 0};
+}
+template <typename KT>
+__device__ __forceinline__ void kv_load_v(const KT* src, KvRaw<KT>& r, int i) {
+#pragma unroll
+    for (int w = 0; w < KvRaw<KT>::VW; w++) r.v[i][w] = gld((const uint32_t*)src + w);
+}
+__device__ __forceinline__ void kv_widen(const KvRaw<float>& r, float (&kk)[16], float (&vv)[8][2]) {
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) kk[4 * q + e] = __int_as_float(r.k[q][e]);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        vv[i][0] = __uint_as_float(r.v[i][0]);
+        vv[i][1] = __uint_as_float(r.v[i][1]);
+    }
+}
+__device__ __forceinline__ float h2f(uint32_t bits) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)bits);
+}
+__device__ __forceinline__ void kv_widen(const KvRaw<_Float16>& r, float (&kk)[16], float (&vv)[8][2]) {
+#pragma unroll
+    for (int q = 0; q < 2; q++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const uint32_t w = (uint32_t)r.k[q][e];
+            kk[8 * q + 2 * e] = h2f(w & 0xFFFFu);
+            kk[8 * q + 2 * e + 1] = h2f(w >> 16);
+        }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        vv[i][0] = h2f(r.v[i][0] & 0xFFFFu);
+        vv[i][1] = h2f(r.v[i][0] >> 16);
+    }
 }
 
 // Partial attention (P3) of split s = j over this workgroup's positions, for
 // both query heads of KV head g. A wave takes its positions 8 per pass. Scores
 // use 8 lanes per position (lane group jj = position slot, 16 dims per lane);
 // the value rows are read in the accumulation layout instead (lane l holds
-// dims 2l, 2l+1 of each of the pass's 8 positions, one coalesced row per
+// row slots 2l, 2l+1 of each of the pass's 8 positions, one coalesced row per
 // load), so with the pass's 8 weights broadcast from their lane groups every
 // lane accumulates its own two output dims: the softmax state (max, sum) is
 // wave-uniform and no cross-lane combine of the outputs is needed. The current
@@ -801,6 +850,8 @@ __device__ __forceinline__ void load2g(const _Float16* src, float (&d)[2]) {
 template <typename KT>
 __device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t qtag, uint32_t tag) {
     constexpr int G = LP_G;
+    // fp16 rows are paired (kv_put2): lane l's two value slots are dims l, l + 64
+    constexpr bool VPAIR = sizeof(KT) == 2;
     const AttRange r = att_range(c.j, c.w, pos);
     if (r.n <= 0) return true;
     const int jj = c.lane >> 3, part = c.lane & 7;
@@ -811,28 +862,24 @@ __device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t q
     // them): issued before the q poll, so their latency hides behind it.
     const KT* kb = (const KT*)p.kc + ((int64_t)l * LP_NX + c.g) * p.max_seq * LP_D;
     const KT* vb = (const KT*)p.vc + ((int64_t)l * LP_NX + c.g) * p.max_seq * LP_D;
-    auto load_pass = [&](int ps, float (&kk)[16], float (&vv)[8][2]) {
+    auto load_pass = [&](int ps, KvRaw<KT>& raw) {
         const int tp = r.tw0 + ps * 8 + jj;
-        if (tp < r.tw1 && tp != pos) {
-            load_row16g(kb + (int64_t)tp * LP_D + part * 16, kk);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; i++) kk[i] = 0.f;
-        }
+        if (tp < r.tw1 && tp != pos) kv_load_k(kb + (int64_t)tp * LP_D + part * 16, raw);
+        else kv_zero_k(raw);
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const int tv = r.tw0 + ps * 8 + i;   // the same in every lane
             if (tv < r.tw1 && tv != pos) {
-                load2g(vb + (int64_t)tv * LP_D + 2 * c.lane, vv[i]);
+                kv_load_v(vb + (int64_t)tv * LP_D + 2 * c.lane, raw, i);
             } else {
-                vv[i][0] = 0.f;
-                vv[i][1] = 0.f;
+#pragma unroll
+                for (int w = 0; w < KvRaw<KT>::VW; w++) raw.v[i][w] = 0u;
             }
         }
     };
-    float kp[LP_NPF][16], vp[LP_NPF][8][2];
+    KvRaw<KT> pre[LP_NPF];
 #pragma unroll
-    for (int ps = 0; ps < LP_NPF; ps++) load_pass(ps, kp[ps], vp[ps]);
+    for (int ps = 0; ps < LP_NPF; ps++) load_pass(ps, pre[ps]);
     {
         // q of the two query heads and the current k/v row, in one poll
         // (words lane + 64 i: q for i < 4, then k, v)
@@ -854,7 +901,7 @@ __device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t q
     cbar();
     float qv[G][16];
 #pragma unroll
-    for (int h = 0; h < G; h++) load_row16(stg + h * LP_D + part * 16, qv[h]);
+    for (int h = 0; h < G; h++) slots16(stg + h * LP_D, part, qv[h], (KT*)nullptr);
     float m[G], lsum[G], o[G][2];
 #pragma unroll
     for (int h = 0; h < G; h++) {
@@ -902,22 +949,27 @@ __device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t q
     for (int ps = 0; ps < LP_NPF; ps++) {
         if (ps >= passes) break;   // wave-uniform: no work for an empty pass
         const int tp = r.tw0 + ps * 8 + jj;
-        pass(kp[ps], vp[ps], tp < r.tw1 && tp != pos);
+        float kk[16], vv[8][2];
+        kv_widen(pre[ps], kk, vv);
+        pass(kk, vv, tp < r.tw1 && tp != pos);
     }
     for (int ps = LP_NPF; ps < passes; ps++) {
         const int tp = r.tw0 + ps * 8 + jj;
+        KvRaw<KT> raw;
+        load_pass(ps, raw);
         float kk[16], vv[8][2];
-        load_pass(ps, kk, vv);
+        kv_widen(raw, kk, vv);
         pass(kk, vv, tp < r.tw1 && tp != pos);
     }
     if (has_cur) {
         // this step's k/v as the cache holds them, in slot 0
         float kk[16], vv[8][2];
-        load_row16(stg + G * LP_D + part * 16, kk);
+        slots16(stg + G * LP_D, part, kk, (KT*)nullptr);
 #pragma unroll
         for (int i = 0; i < 16; i++) kk[i] = kv_round(kk[i], (KT*)nullptr);
-        vv[0][0] = kv_round(stg[G * LP_D + LP_D + 2 * c.lane], (KT*)nullptr);
-        vv[0][1] = kv_round(stg[G * LP_D + LP_D + 2 * c.lane + 1], (KT*)nullptr);
+        const int d0 = VPAIR ? c.lane : 2 * c.lane, d1 = VPAIR ? c.lane + 64 : 2 * c.lane + 1;
+        vv[0][0] = kv_round(stg[G * LP_D + LP_D + d0], (KT*)nullptr);
+        vv[0][1] = kv_round(stg[G * LP_D + LP_D + d1], (KT*)nullptr);
 #pragma unroll
         for (int i = 1; i < 8; i++) vv[i][0] = vv[i][1] = 0.f;
         pass(kk, vv, jj == 0);
@@ -925,7 +977,13 @@ __device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t q
     // the wave's partial o[h][128] (relative to its max) and its max / sum
 #pragma unroll
     for (int h = 0; h < G; h++) {
-        *(float2*)(c.attp + (c.w * G + h) * LP_D + 2 * c.lane) = make_float2(o[h][0], o[h][1]);
+        float* ap = c.attp + (c.w * G + h) * LP_D;
+        if (VPAIR) {
+            ap[c.lane] = o[h][0];
+            ap[c.lane + 64] = o[h][1];
+        } else {
+            *(float2*)(ap + 2 * c.lane) = make_float2(o[h][0], o[h][1]);
+        }
         if (c.lane == 0) {
             c.attm[c.w * G + h] = m[h];
             c.attm[LP_CW * G + c.w * G + h] = lsum[h];

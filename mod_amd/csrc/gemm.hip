@@ -405,9 +405,174 @@ __global__ __launch_bounds__(64 * WV) void skinny_w8a8_kernel(GemmParams p) {
     }
 }
 
+// ------------------------------------------------------ streamed skinny ---
+// W8A8 for 16 < M <= 64 (prefill tails, small batches). The one-pass skinny
+// kernel above keeps a workgroup's whole activation slice in LDS, which at 64
+// rows holds only 2 KB of K and forces K slices plus a reduce. Here the
+// activations stream with the weights instead: per K block of 256, every wave
+// loads its 16 weight rows into registers (as above) and its share of the 64
+// activation rows x 256 B into an LDS ring stage with direct-to-LDS copies,
+// both SS_D blocks ahead, and one barrier per block makes the stage visible to
+// the workgroup. The ring has SS_D + 1 stages: the stage a block's copies
+// overwrite was last read one block earlier, which every wave has finished
+// when it passes the current block's barrier. LDS rows are 256 B with the
+// 16-byte chunks XOR-swizzled by row (chunk c of row r at c ^ (r & 15)), so
+// the MFMA operand reads (16 rows, one chunk) are conflict-free; the copies
+// pick their global chunk to land that way.
+constexpr int SS_D = 3;                      // K blocks in flight (3-6 measured alike; 3 leaves LDS for 2 workgroups)
+constexpr int SS_S = SS_D + 1;               // activation ring stages
+constexpr int SS_STAGE = 64 * SK_KB;         // 64 rows x 256 B
+constexpr size_t SS_LDS = (size_t)SS_S * SS_STAGE;
+
+template <int WV, int NB, int OUT>
+__global__ __launch_bounds__(64 * WV) void skinny_stream_kernel(GemmParams p) {
+    typedef __attribute__((address_space(3))) void lds_t;
+    static_assert(16 % WV == 0, "16 activation copies per block, shared evenly");
+    constexpr int D = NB < SS_D ? NB : SS_D;
+    constexpr int CPW = 16 / WV;                 // 1 KB copies per wave per block
+    constexpr int L = 4 + CPW;                   // vector-memory ops per wave per block
+    extern __shared__ __attribute__((aligned(16))) int8_t ss_lds[];
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int r = lane & 15, q = lane >> 4;
+    const int n0 = blockIdx.x * (16 * WV) + w * 16;
+    const int64_t k0 = (int64_t)blockIdx.y * p.K;          // p.K is the K of one slice
+
+    // copy j of this wave moves activation rows 4u .. 4u + 3 (u = w + WV j):
+    // lane l lands its 16 B at stage offset 1024 u + 16 l, i.e. row 4u + l / 16,
+    // chunk position l % 16, holding the row's chunk (l % 16) ^ (row % 16)
+    const int8_t* asrc[CPW];
+    int adst[CPW];
+#pragma unroll
+    for (int j = 0; j < CPW; j++) {
+        const int u = w + WV * j, row = 4 * u + (lane >> 4), c = (lane & 15) ^ (row & 15);
+        asrc[j] = p.A + (int64_t)min(row, p.M - 1) * p.lda + k0 + c * 16;
+        adst[j] = u * 1024;
+    }
+    const int8_t* wp = p.B + (int64_t)min(n0 + r, p.N - 1) * p.ldb + k0 + 16 * q;
+    v4i wr[D][4];
+    auto issue = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            wr[b % D][i] = __builtin_nontemporal_load((sk_gv4i*)(wp + b * SK_KB + 64 * i));
+        int8_t* st = ss_lds + (b % SS_S) * SS_STAGE;
+#pragma unroll
+        for (int j = 0; j < CPW; j++)
+            __builtin_amdgcn_global_load_lds((const void*)(asrc[j] + b * SK_KB), (lds_t*)(st + adst[j]), 16, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+#pragma unroll
+    for (int b = 0; b < D; b++) issue(b);
+
+    v4i acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) acc[t] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        // block b landed (this wave's loads and copies), then every wave's copies
+        if (NB - 1 - b >= D - 1) stage_barrier<(D - 1) * L>();
+        else stage_barrier_steps<L, (D > 1 ? D - 1 : 0)>(NB - 1 - b);
+        const int8_t* st = ss_lds + (b % SS_S) * SS_STAGE;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int row = 16 * t + r;
+                const v4i a = *(const v4i*)(st + row * SK_KB + (((4 * i + q) ^ r) << 4));
+                acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, wr[b % D][i], acc[t], 0, 0, 0);
+            }
+        }
+        if (b + D < NB) issue(b + D);
+    }
+
+    // 16x16 accumulator: lane holds rows 4*q + v (v < 4) of M tile t, column r.
+    const int n = n0 + r;
+    if (n >= p.N) return;
+    const float sw = OUT == OUT_I32 ? 0.f : p.s_w[n];
+    const float bn = (OUT != OUT_I32 && p.bias) ? p.bias[n] : 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int m = t * 16 + 4 * q + v;
+            if (m >= p.M) continue;
+            const int64_t o = (int64_t)blockIdx.y * p.c_batch + (int64_t)m * p.ldc + n;
+            if constexpr (OUT == OUT_I32) {
+                ((int32_t*)p.C)[o] = acc[t][v];
+            } else {
+                const float val = scaled_value<OUT>(acc[t][v], p.s_a[m], sw, bn, p.bias != nullptr);
+                if constexpr (OUT == OUT_F32) ((float*)p.C)[o] = val;
+                else ((_Float16*)p.C)[o] = (_Float16)val;
+            }
+        }
+    }
+}
+
 struct SkinnyPlan {
     int wv = 0, nb = 0, splits = 1;
+    bool stream = false;   // the streamed kernel (16 < M <= 64)
 };
+
+// Streamed plan for 16 < M <= 64: the bytes a CU moves (each unit: 16*WV
+// weight rows and the 64 activation rows, NB blocks of 256 B) at ~100 GB/s
+// per CU, units spread over the 256 CUs (two workgroups fit a CU's LDS), plus
+// the split path's int32 partials and reduce launch.
+static SkinnyPlan plan_skinny_stream(const GemmParams& p) {
+    SkinnyPlan best;
+    if (p.M <= 16 || p.M > 64 || p.K % 1024 || !aligned16(p.A) || !aligned16(p.B) || p.lda % 16 ||
+        p.ldb % 16)
+        return best;
+    const int kb = p.K / SK_KB;
+    double best_t = 0;
+    for (int wv : {8, 4, 2}) {
+        for (int nb : {16, 12, 8, 6, 4}) {
+            if (kb % nb) continue;
+            const int sp = kb / nb;
+            if (sp > 16) continue;
+            const int64_t units = (int64_t)ceil_div(p.N, 16 * wv) * sp;
+            const double per_cu = (double)((units + 255) / 256) * nb * SK_KB * (16.0 * wv + 64.0);
+            double t = per_cu / 100.0e9;
+            if (sp > 1) t += (double)sp * p.M * p.N * 8.0 / 4.0e12 + 2.0e-6;
+            if (best.wv == 0 || t < best_t * 0.98) {
+                best_t = t;
+                best.wv = wv; best.nb = nb; best.splits = sp; best.stream = true;
+            }
+        }
+    }
+    return best;
+}
+
+template <int WV, int NB, int OUT>
+static int launch_stream_out(const GemmParams& p, int splits, hipStream_t st) {
+    PIO_TRY(allow_lds(skinny_stream_kernel<WV, NB, OUT>, SS_LDS));
+    skinny_stream_kernel<WV, NB, OUT><<<dim3(ceil_div(p.N, 16 * WV), splits), 64 * WV, SS_LDS, st>>>(p);
+    PIO_LAUNCHED();
+    return PIO_OK;
+}
+template <int WV, int NB>
+static int launch_stream_nb(const GemmParams& p, int out_mode, int splits, hipStream_t st) {
+    switch (out_mode) {
+    case OUT_I32: return launch_stream_out<WV, NB, OUT_I32>(p, splits, st);
+    case OUT_F32: return launch_stream_out<WV, NB, OUT_F32>(p, splits, st);
+    case OUT_F16: return launch_stream_out<WV, NB, OUT_F16>(p, splits, st);
+    default: return set_error(PIO_ERR_INVALID, "gemm: bad output mode");
+    }
+}
+template <int WV>
+static int launch_stream_wv(const GemmParams& p, int out_mode, const SkinnyPlan& sp, hipStream_t st) {
+    switch (sp.nb) {
+    case 16: return launch_stream_nb<WV, 16>(p, out_mode, sp.splits, st);
+    case 12: return launch_stream_nb<WV, 12>(p, out_mode, sp.splits, st);
+    case 8: return launch_stream_nb<WV, 8>(p, out_mode, sp.splits, st);
+    case 6: return launch_stream_nb<WV, 6>(p, out_mode, sp.splits, st);
+    case 4: return launch_stream_nb<WV, 4>(p, out_mode, sp.splits, st);
+    default: return set_error(PIO_ERR_INVALID, "gemm: streamed plan with %d blocks", sp.nb);
+    }
+}
+static int launch_stream_one(const GemmParams& p, int out_mode, const SkinnyPlan& sp, hipStream_t st) {
+    if (sp.wv == 8) return launch_stream_wv<8>(p, out_mode, sp, st);
+    if (sp.wv == 4) return launch_stream_wv<4>(p, out_mode, sp, st);
+    return launch_stream_wv<2>(p, out_mode, sp, st);
+}
 
 // Plan for the skinny kernel, or wv == 0 when it does not apply (M > 64, K not
 // a multiple of 1024, or unaligned operands). Cost model: the weights stream
@@ -471,6 +636,7 @@ static int launch_skinny_mt(const GemmParams& p, int out_mode, const SkinnyPlan&
 }
 
 static int launch_skinny_one(const GemmParams& p, int out_mode, const SkinnyPlan& sp, hipStream_t st) {
+    if (sp.stream) return launch_stream_one(p, out_mode, sp, st);
     if (sp.wv == 4)
         return p.M <= 16 ? launch_skinny_mt<4, 1>(p, out_mode, sp, st) : launch_skinny_mt<4, 4>(p, out_mode, sp, st);
     return p.M <= 16 ? launch_skinny_mt<3, 1>(p, out_mode, sp, st) : launch_skinny_mt<3, 4>(p, out_mode, sp, st);
@@ -640,7 +806,8 @@ static int gemm_w8a8_ws(const int8_t* q, const float* s_a, const int8_t* w, cons
     ws.ext = ws_ext;
     ws.cap = ws_cap;
     ws.ext_name = ws_name;
-    const SkinnyPlan kp = plan_skinny(p);
+    SkinnyPlan kp = plan_skinny_stream(p);
+    if (!kp.wv) kp = plan_skinny(p);
     if (kp.wv) return launch_skinny(p, mode, kp, ws, st);
     const SplitPlan sp = plan_split(p, 256);
     if (sp.splits > 1) return launch_splitk(p, mode, sp, ws, st);

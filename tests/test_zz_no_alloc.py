@@ -68,12 +68,13 @@ def test_static_entry_matches_allocating_entry(torch_dev):
 
 
 def test_static_entry_refuses_shapes_beyond_its_scratch(torch_dev):
-    """M = 64, K = 12288 plans at least 6 K slices; with N = 12288 that is at
-    least 6 x 64 x 12288 x 4 B = 18.9 MB of partials, above the 16 MiB array."""
+    """M = 64, K = 65536 plans 16 K slices (256 blocks of 256 B each, the most
+    a slice count may be); with N = 6144 that is 16 x 64 x 6144 x 4 B =
+    24 MiB of partials, above the 16 MiB array."""
     import torch
     from mod_amd import ops
     d = torch_dev
-    M, N, K = 64, 12288, 12288
+    M, N, K = 64, 6144, 65536
     q = torch.zeros((M, K), dtype=torch.int8, device=d)
     w = torch.zeros((N, K), dtype=torch.int8, device=d)
     s = torch.ones((max(M, N),), dtype=torch.float32, device=d)

@@ -148,18 +148,6 @@ __global__ __launch_bounds__(256, 1) void gemm_v2_kernel(GemmParams p, int tiles
     }
 }
 
-// Raises a kernel's dynamic-LDS limit once (tiles above 64 KB of LDS).
-template <typename F>
-static int allow_lds(F* kernel, size_t bytes) {
-    static bool done = false;   // one flag per kernel instantiation
-    if (!done && bytes > 65536) {
-        PIO_HIP(hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    (int)bytes));
-        done = true;
-    }
-    return PIO_OK;
-}
-
 template <int WMT, int WNT, int ENG, int S>
 constexpr size_t engine_lds() {
     if constexpr (ENG == 2) return TileV2<WMT, WNT>::LDS_BYTES;
@@ -170,7 +158,7 @@ constexpr size_t engine_lds() {
 template <int WMT, int WNT, int OUT, int ENG, int S>
 static int launch_v2_out(const GemmParams& p, dim3 grid, int tn, hipStream_t st) {
     constexpr size_t lds = engine_lds<WMT, WNT, ENG, S>();
-    PIO_TRY(allow_lds(gemm_v2_kernel<WMT, WNT, OUT, ENG, S>, lds));
+    PIO_TRY(allow_lds<gemm_v2_kernel<WMT, WNT, OUT, ENG, S>>(lds));
     gemm_v2_kernel<WMT, WNT, OUT, ENG, S><<<grid, 256, lds, st>>>(p, tn);
     PIO_LAUNCHED();
     return PIO_OK;
@@ -543,7 +531,7 @@ static SkinnyPlan plan_skinny_stream(const GemmParams& p) {
 
 template <int WV, int NB, int OUT>
 static int launch_stream_out(const GemmParams& p, int splits, hipStream_t st) {
-    PIO_TRY(allow_lds(skinny_stream_kernel<WV, NB, OUT>, SS_LDS));
+    PIO_TRY(allow_lds<skinny_stream_kernel<WV, NB, OUT>>(SS_LDS));
     skinny_stream_kernel<WV, NB, OUT><<<dim3(ceil_div(p.N, 16 * WV), splits), 64 * WV, SS_LDS, st>>>(p);
     PIO_LAUNCHED();
     return PIO_OK;
@@ -608,7 +596,7 @@ static SkinnyPlan plan_skinny(const GemmParams& p) {
 template <int WV, int MT, int NB, int OUT>
 static int launch_skinny_out(const GemmParams& p, int splits, hipStream_t st) {
     constexpr size_t lds = sk_lds_bytes<MT, NB>();
-    PIO_TRY(allow_lds(skinny_w8a8_kernel<WV, MT, NB, OUT>, lds));
+    PIO_TRY(allow_lds<skinny_w8a8_kernel<WV, MT, NB, OUT>>(lds));
     skinny_w8a8_kernel<WV, MT, NB, OUT><<<dim3(ceil_div(p.N, 16 * WV), splits), 64 * WV, lds, st>>>(p);
     PIO_LAUNCHED();
     return PIO_OK;

@@ -304,12 +304,7 @@ template <int R, int MT, typename XT, typename YT>
 static int launch_stream_r(const XT* x, const int8_t* w, const float* s_w, const float* bias, YT* y,
                            int N, int K, hipStream_t st) {
     const size_t lds = (size_t)MT * ((K + 1023) / 1024) * 4096;
-    static bool attr = false;   // one flag per instantiation
-    if (!attr) {
-        PIO_HIP(hipFuncSetAttribute((const void*)gemv_w8_stream_kernel<R, MT, XT, YT>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, GEMV_XLDS));
-        attr = true;
-    }
+    PIO_TRY(allow_lds<gemv_w8_stream_kernel<R, MT, XT, YT>>(lds));
     const int blocks = (int)std::min<int64_t>(ceil_div(N, R), device_cus());
     gemv_w8_stream_kernel<R, MT, XT, YT><<<blocks, 64 * GEMV_WAVES, lds, st>>>(x, w, s_w, bias, y, N, K, N);
     return PIO_OK;
@@ -488,6 +483,177 @@ __global__ __launch_bounds__(64 * WV) void gemv_w8_mfma_kernel(GemvMfma p) {
     }
 }
 
+// Streamed MFMA GEMV for 16 < M <= 64: the one-pass kernel above keeps the
+// workgroup's fp16 x slice in LDS, which at 64 rows holds only 1 KB of K and
+// forces K slices of 1024 plus a reduce. Here x streams with the weights (as
+// the streamed W8A8 kernel in gemm.hip), on v_mfma_f32_32x32x16_f16, which
+// does 1.7x the work per cycle of the 16x16x32 form and reads half the x
+// bytes from LDS per weight byte. Each wave owns 32 weight rows. Per K block
+// of 256 it loads them into registers GS_DW blocks ahead, 64 contiguous bytes
+// of 16 rows per load (4 lanes per row; the 32x32 operand layout would give
+// each row only 2 lanes, 32 bytes per load, which streams at half the rate),
+// and one v_permlane16_swap per dword pair moves them into the operand
+// layout: lane l then holds bytes 64 s + 32 (l / 32) + 0..31 of row l % 32 for
+// the block's 4 segments s. x streams GS_DX blocks ahead into an LDS ring
+// stage (direct-to-LDS copies, 32 MT rows x 512 B); one barrier per block.
+// (The wait for a block counts vector-memory operations in issue order, so
+// the weights' effective lead is GS_DX too; running x as far ahead as the
+// weights, in a deeper ring, measured slower.) The weights use ordinary
+// loads: each load covers half of a 128-byte line per row, and nontemporal
+// loads lose the other half before the next load asks for it (7% slower).
+// LDS rows are 512 B with the 16-byte chunks XOR-swizzled by row (chunk c of
+// row r at c ^ (r & 15)), so the operand reads (16 rows per quarter wave) are
+// conflict-free; the copies pick their global chunk to land that way.
+constexpr int GS_DW = 4;                     // weight blocks in flight per wave
+constexpr int GS_DX = 2;                     // x blocks in flight per workgroup
+constexpr int GS_TILE = 32 * GM_KB * 2;      // one 32-row x tile of a K block (16 KB)
+template <int MT>
+constexpr size_t gs_lds_bytes() { return (size_t)(GS_DX + 1) * MT * GS_TILE; }   // 48 or 96 KB
+
+// Vector-memory operations a wave has issued after x block b (in the order
+// the kernel issues them: per step j the weights of block j + DW, then the x
+// copies of block j + DX), counted up to the wait at the top of step b.
+template <int NB, int DW, int DX, int WOPS, int XOPS>
+__device__ constexpr int gs_after_x(int b) {
+    int n = 0;
+    for (int j = b - DX + 1; j <= b - 1; j++) n += WOPS * (j + DW < NB) + XOPS * (j + DX < NB);
+    return n;
+}
+
+// stage_barrier<n>() for a wave-uniform n in [0, MAXN] (constant-folded when
+// n is known at compile time, as in fully unrolled loops).
+template <int MAXN>
+__device__ __forceinline__ void stage_barrier_n(int n) {
+    if constexpr (MAXN > 0) {
+        if (n >= MAXN) stage_barrier<MAXN>();
+        else stage_barrier_n<MAXN - 1>(n);
+    } else {
+        stage_barrier<0>();
+    }
+}
+
+typedef float gm_v16f __attribute__((ext_vector_type(16)));
+
+template <int WV, int MT, int NB, typename YT, bool SPLIT>
+__global__ __launch_bounds__(64 * WV) void gemv_w8_mfma_stream_kernel(GemvMfma p) {
+    typedef __attribute__((address_space(3))) void lds_t;
+    static_assert((16 * MT) % WV == 0, "16 MT x copies per block, shared evenly");
+    constexpr int DW = NB < GS_DW ? NB : GS_DW;
+    constexpr int DX = NB < GS_DX ? NB : GS_DX;
+    constexpr int S = GS_DX + 1;
+    constexpr int STAGE = MT * GS_TILE;
+    constexpr int CPW = 16 * MT / WV;
+    constexpr int WOPS = 8;
+    constexpr int MAXW = (DX - 1) * (WOPS + CPW);   // the steady-state wait count
+    static_assert(DW >= DX, "weights run at least as far ahead as x");
+    static_assert(MAXW < 64, "vmcnt range");
+    extern __shared__ __attribute__((aligned(16))) int8_t gs_lds[];
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int col = lane & 31, h = lane >> 5;
+    const int n0 = blockIdx.x * (32 * WV) + w * 32;
+    const int64_t k0 = (int64_t)blockIdx.y * p.K;
+
+    // copy j moves x rows 2u, 2u + 1 (u = w + WV j): lane l lands 16 B at stage
+    // offset 1024 u + 16 l = row 2u + l / 32, chunk position l % 32, which holds
+    // the row's chunk (l % 32) ^ (row % 16)
+    const int8_t* xsrc[CPW];
+    int xdst[CPW];
+#pragma unroll
+    for (int j = 0; j < CPW; j++) {
+        const int u = w + WV * j, row = 2 * u + h, c = col ^ (row & 15);
+        xsrc[j] = (const int8_t*)(p.x + (int64_t)min(row, p.M - 1) * p.ldx + k0) + c * 16;
+        xdst[j] = u * 1024;
+    }
+    // load 2s + g of a block: rows n0 + 16 g + (l % 16), bytes 64 s + 16 (l / 16)
+    const int8_t* wp[2];
+#pragma unroll
+    for (int g = 0; g < 2; g++)
+        wp[g] = p.w + (int64_t)min(n0 + 16 * g + (lane & 15), p.N - 1) * p.ldx + k0 + 16 * (lane >> 4);
+    v4i wr[DW][8];
+    auto issue_w = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) wr[b % DW][i] = *(gm_gv4i*)(wp[i & 1] + b * GM_KB + 64 * (i >> 1));
+    };
+    auto issue_x = [&](int b) {
+        int8_t* st = gs_lds + (b % S) * STAGE;
+#pragma unroll
+        for (int j = 0; j < CPW; j++)
+            __builtin_amdgcn_global_load_lds((const void*)(xsrc[j] + b * GM_KB * 2), (lds_t*)(st + xdst[j]), 16, 0, 0);
+    };
+    // steps -DW .. -1: the weights of blocks 0 .. DW-1, the x of blocks 0 .. DX-1
+#pragma unroll
+    for (int v = 0; v < DW; v++) {
+        issue_w(v);
+        if (v >= DW - DX) issue_x(v - (DW - DX));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    gm_v16f acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[t][e] = 0.f;
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        // x block b (and the older weights of block b) landed, then every wave's copies
+        stage_barrier_n<MAXW>(gs_after_x<NB, DW, DX, WOPS, CPW>(b));
+        // the widening is register work the scheduler would hoist above the barrier
+        __builtin_amdgcn_sched_barrier(0);
+        const int8_t* st = gs_lds + (b % S) * STAGE;
+#pragma unroll
+        for (int sg = 0; sg < 4; sg++) {
+            // rows 0-15 (load 2s) and 16-31 (load 2s + 1), 16-lane groups swapped:
+            // u[0] = chunk 2h, u[1] = chunk 2h + 1 of row col's 64-byte segment
+            v4i u[2];
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                const auto sw2 = __builtin_amdgcn_permlane16_swap((unsigned)wr[b % DW][2 * sg][d],
+                                                                  (unsigned)wr[b % DW][2 * sg + 1][d], false, false);
+                u[0][d] = (int)sw2[0];
+                u[1][d] = (int)sw2[1];
+            }
+            gm_v8h wv[4];
+            gm_widen16(u[0], wv[0], wv[1]);
+            gm_widen16(u[1], wv[2], wv[3]);
+            const int c = 8 * sg + 4 * h;   // 16-byte chunk of elements 64 s + 32 h
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const int8_t* row = st + (32 * t + col) * (GM_KB * 2);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const gm_v8h a = *(const gm_v8h*)(row + (((c + e) ^ (col & 15)) << 4));
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, wv[e], acc[t], 0, 0, 0);
+                }
+            }
+        }
+        if (b + DW < NB) issue_w(b + DW);
+        if (b + DX < NB) issue_x(b + DX);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // 32x32 accumulator: element e of lane l is x row 8 (e / 4) + 4 (l / 32) + e % 4
+    // of tile t, weight row n0 + l % 32.
+    const int n = n0 + col;
+    if (n >= p.N) return;
+    const float sw = SPLIT ? 0.f : p.s_w[n];
+    const float bn = (!SPLIT && p.bias) ? p.bias[n] : 0.f;
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int m = 32 * t + 8 * (e >> 2) + 4 * h + (e & 3);
+            if (m >= p.M) continue;
+            if constexpr (SPLIT) {
+                ((float*)p.y)[((int64_t)blockIdx.y * p.M + m) * p.N + n] = acc[t][e];
+            } else {
+                float val = acc[t][e] * sw;
+                if (p.bias) val += bn;
+                ((YT*)p.y)[(int64_t)m * p.N + n] = from_f32<YT>(val);
+            }
+        }
+    }
+}
+
 // y[m,n] = (sum over slices in order of ws[z][m][n]) * s_w[n] (+ bias[n]).
 template <typename YT>
 __global__ __launch_bounds__(256) void gemv_split_reduce_kernel(const float* __restrict__ ws, int splits, int M,
@@ -505,7 +671,37 @@ __global__ __launch_bounds__(256) void gemv_split_reduce_kernel(const float* __r
 
 struct GemvMfmaPlan {
     int wv = 0, nb = 0, splits = 1;
+    bool stream = false;   // gemv_w8_mfma_stream_kernel
 };
+
+// Plan for the streamed kernel (16 < M <= 64), or wv == 0. A workgroup (one
+// per CU: its LDS ring is 48 or 96 KB) moves its weights (32 WV rows) and x
+// rows (32 or 64, fp16) at ~25 GB/s together, as measured over wv, nb and
+// both C4 shapes; the cost is the busiest CU's bytes at that rate, plus for K
+// slices the partials' write + read and the reduce launch.
+static GemvMfmaPlan plan_gemv_stream(int M, int N, int K) {
+    GemvMfmaPlan best;
+    if (M <= 16 || M > 64 || K % 1024) return best;
+    const int kb = K / GM_KB;
+    double best_t = 0;
+    for (int wv : {8, 4, 2}) {
+        if (wv == 8 && M > 32) continue;
+        for (int nb : {16, 12, 8, 6, 4}) {
+            if (kb % nb) continue;
+            const int sp = kb / nb;
+            if (sp > 16) continue;
+            const int64_t units = (int64_t)ceil_div(N, 32 * wv) * sp;
+            const double per_cu = (double)((units + 255) / 256) * nb * GM_KB * (32.0 * wv + (M > 32 ? 128.0 : 64.0));
+            double t = per_cu / 25.0e9;
+            if (sp > 1) t += (double)sp * M * N * 8.0 / 4.0e12 + 2.0e-6;
+            if (best.wv == 0 || t < best_t * 0.98) {
+                best_t = t;
+                best.wv = wv; best.nb = nb; best.splits = sp; best.stream = true;
+            }
+        }
+    }
+    return best;
+}
 
 // Same cost model as the skinny W8A8 plan; the fp16 x slice must fit the LDS
 // (16 rows x 8 KB, or 64 rows x 2 KB).
@@ -537,24 +733,47 @@ static int launch_gemv_mfma_nb(const GemvMfma& p, int splits, hipStream_t st) {
     constexpr size_t lds = gm_lds_bytes<MT, NB>();
     const dim3 grid(ceil_div(p.N, 16 * WV), splits);
     if (splits > 1) {
-        static bool done = false;
-        if (!done && lds > 65536) {
-            PIO_HIP(hipFuncSetAttribute((const void*)gemv_w8_mfma_kernel<WV, MT, NB, YT, true>,
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-            done = true;
-        }
+        PIO_TRY(allow_lds<gemv_w8_mfma_kernel<WV, MT, NB, YT, true>>(lds));
         gemv_w8_mfma_kernel<WV, MT, NB, YT, true><<<grid, 64 * WV, lds, st>>>(p);
     } else {
-        static bool done = false;
-        if (!done && lds > 65536) {
-            PIO_HIP(hipFuncSetAttribute((const void*)gemv_w8_mfma_kernel<WV, MT, NB, YT, false>,
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-            done = true;
-        }
+        PIO_TRY(allow_lds<gemv_w8_mfma_kernel<WV, MT, NB, YT, false>>(lds));
         gemv_w8_mfma_kernel<WV, MT, NB, YT, false><<<grid, 64 * WV, lds, st>>>(p);
     }
     PIO_LAUNCHED();
     return PIO_OK;
+}
+
+template <int WV, int MT, int NB, typename YT>
+static int launch_gemv_stream_nb(const GemvMfma& p, int splits, hipStream_t st) {
+    constexpr size_t lds = gs_lds_bytes<MT>();
+    const dim3 grid(ceil_div(p.N, 32 * WV), splits);
+    if (splits > 1) {
+        PIO_TRY(allow_lds<gemv_w8_mfma_stream_kernel<WV, MT, NB, YT, true>>(lds));
+        gemv_w8_mfma_stream_kernel<WV, MT, NB, YT, true><<<grid, 64 * WV, lds, st>>>(p);
+    } else {
+        PIO_TRY(allow_lds<gemv_w8_mfma_stream_kernel<WV, MT, NB, YT, false>>(lds));
+        gemv_w8_mfma_stream_kernel<WV, MT, NB, YT, false><<<grid, 64 * WV, lds, st>>>(p);
+    }
+    PIO_LAUNCHED();
+    return PIO_OK;
+}
+template <int WV, int MT, typename YT>
+static int launch_gemv_stream_mt(const GemvMfma& p, const GemvMfmaPlan& pl, hipStream_t st) {
+    switch (pl.nb) {
+    case 16: return launch_gemv_stream_nb<WV, MT, 16, YT>(p, pl.splits, st);
+    case 12: return launch_gemv_stream_nb<WV, MT, 12, YT>(p, pl.splits, st);
+    case 8: return launch_gemv_stream_nb<WV, MT, 8, YT>(p, pl.splits, st);
+    case 6: return launch_gemv_stream_nb<WV, MT, 6, YT>(p, pl.splits, st);
+    case 4: return launch_gemv_stream_nb<WV, MT, 4, YT>(p, pl.splits, st);
+    default: return set_error(PIO_ERR_INVALID, "gemv: streamed plan with %d blocks", pl.nb);
+    }
+}
+template <int WV, typename YT>
+static int launch_gemv_stream_wv(const GemvMfma& p, const GemvMfmaPlan& pl, hipStream_t st) {
+    if (p.M <= 32) return launch_gemv_stream_mt<WV, 1, YT>(p, pl, st);
+    // two x tiles and 8 waves would leave too few registers per wave
+    if constexpr (WV == 8) return set_error(PIO_ERR_INVALID, "gemv: streamed plan with 8 waves for %d rows", p.M);
+    else return launch_gemv_stream_mt<WV, 2, YT>(p, pl, st);
 }
 
 template <int WV, typename YT>
@@ -580,7 +799,13 @@ static int launch_gemv_mfma(const _Float16* x, const int8_t* w, const float* s_w
         PIO_TRY(ws.get((size_t)pl.splits * M * N * sizeof(float), st));
         p.y = ws.ptr;
     }
-    const int rc = pl.wv == 4 ? launch_gemv_mfma_wv<4, YT>(p, pl, st) : launch_gemv_mfma_wv<3, YT>(p, pl, st);
+    int rc;
+    if (pl.stream)
+        rc = pl.wv == 8   ? launch_gemv_stream_wv<8, YT>(p, pl, st)
+             : pl.wv == 4 ? launch_gemv_stream_wv<4, YT>(p, pl, st)
+                          : launch_gemv_stream_wv<2, YT>(p, pl, st);
+    else
+        rc = pl.wv == 4 ? launch_gemv_mfma_wv<4, YT>(p, pl, st) : launch_gemv_mfma_wv<3, YT>(p, pl, st);
     if (rc != PIO_OK) return rc;
     if (pl.splits > 1) {
         const int64_t MN = (int64_t)M * N;
@@ -601,7 +826,8 @@ template <typename XT, typename YT>
 static int dispatch(const XT* x, const int8_t* w, const float* s_w, const float* bias, YT* y,
                     int M, int N, int K, hipStream_t st) {
     if constexpr (std::is_same<XT, _Float16>::value) {
-        const GemvMfmaPlan pl = plan_gemv_mfma(M, N, K);
+        GemvMfmaPlan pl = plan_gemv_stream(M, N, K);
+        if (!pl.wv) pl = plan_gemv_mfma(M, N, K);
         if (pl.wv) return launch_gemv_mfma(x, w, s_w, bias, y, M, N, K, pl, st);
     }
     if ((size_t)N * K >= GEMV_STREAM_MIN_BYTES && stream_pick(1, N, K)) {

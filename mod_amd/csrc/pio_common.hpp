@@ -8,6 +8,8 @@
 #include <stddef.h>
 #include <stdarg.h>
 
+#include <atomic>
+
 #include "tensor_rocm.h"
 
 #define PIO_EXPORT extern "C" __attribute__((visibility("default")))
@@ -34,14 +36,30 @@ void clear_error();
     } while (0)
 
 // Propagates a non-OK status.
-#define PIO_TRY(expr)                                                                      \
+#define PIO_TRY(...)                                                                       \
     do {                                                                                   \
-        int _s = (expr);                                                                   \
+        int _s = (__VA_ARGS__);                                                            \
         if (_s != PIO_OK) return _s;                                                       \
     } while (0)
 
 // Checks the launch status of the kernel just issued.
 #define PIO_LAUNCHED() PIO_HIP(hipGetLastError())
+
+// Raises KERNEL's dynamic-LDS limit to the whole 160 KB once per device, when
+// a launch asks for more than the 64 KB default. One flag word per kernel (the
+// template argument is the kernel itself, not its type), one bit per device.
+template <auto KERNEL>
+inline int allow_lds(size_t bytes) {
+    static std::atomic<uint64_t> done{0};
+    if (bytes <= 65536) return PIO_OK;
+    int dev = 0;
+    PIO_HIP(hipGetDevice(&dev));
+    const uint64_t bit = 1ull << (dev & 63);
+    if (done.load(std::memory_order_acquire) & bit) return PIO_OK;
+    PIO_HIP(hipFuncSetAttribute((const void*)KERNEL, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+    done.fetch_or(bit, std::memory_order_release);
+    return PIO_OK;
+}
 
 // ---- streams -------------------------------------------------------------
 // The stream raw entry points run on when given NULL: the one set by

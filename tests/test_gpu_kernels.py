@@ -101,10 +101,14 @@ def test_gemv_shapes(env, M, N, K, xdt, ydt, bias):
     (64, 12288, 4096, np.float16, True),
     (64, 130, 1024, np.float32, True),
     (33, 2048, 12288, np.float16, False),
+    (48, 5000, 6144, np.float32, True),    # streamed x, ragged N
+    (20, 4096, 1024, np.float16, False),   # streamed x, 4 blocks, 20 live rows of 64
+    (64, 1000, 16384, np.float32, False),  # streamed x, 16-block K slices
 ])
 def test_gemv_mfma_fp16(env, M, N, K, ydt, bias):
     """fp16 activations with 2 <= M <= 64 and K % 1024 == 0 take the MFMA GEMV
-    (int8 weights widened exactly to fp16, fp32 accumulation). Every product
+    (int8 weights widened exactly to fp16, fp32 accumulation; above 16 rows x
+    streams through LDS with the weights). Every product
     is exact, so the fp32 output is held to rel 1e-3 against the oracle (the
     fp16-input bar is 1e-2); fp16 output to 1e-2. Two calls in a row."""
     torch, ops, d = env

@@ -406,7 +406,9 @@ __global__ __launch_bounds__(64 * WV) void skinny_w8a8_kernel(GemmParams p) {
 // when it passes the current block's barrier. LDS rows are 256 B with the
 // 16-byte chunks XOR-swizzled by row (chunk c of row r at c ^ (r & 15)), so
 // the MFMA operand reads (16 rows, one chunk) are conflict-free; the copies
-// pick their global chunk to land that way.
+// pick their global chunk to land that way. The weights use ordinary loads:
+// each covers half of a 128-byte line per row, and nontemporal loads lose
+// the other half before the next load asks for it (10% slower at M = 32-64).
 constexpr int SS_D = 3;                      // K blocks in flight (3-6 measured alike; 3 leaves LDS for 2 workgroups)
 constexpr int SS_S = SS_D + 1;               // activation ring stages
 constexpr int SS_STAGE = 64 * SK_KB;         // 64 rows x 256 B
@@ -441,7 +443,7 @@ __global__ __launch_bounds__(64 * WV) void skinny_stream_kernel(GemmParams p) {
     auto issue = [&](int b) {
 #pragma unroll
         for (int i = 0; i < 4; i++)
-            wr[b % D][i] = __builtin_nontemporal_load((sk_gv4i*)(wp + b * SK_KB + 64 * i));
+            wr[b % D][i] = *(sk_gv4i*)(wp + b * SK_KB + 64 * i);
         int8_t* st = ss_lds + (b % SS_S) * SS_STAGE;
 #pragma unroll
         for (int j = 0; j < CPW; j++)

@@ -430,7 +430,7 @@ __global__ __launch_bounds__(64 * WV) void gemv_w8_mfma_kernel(GemvMfma p) {
     v4i wr[D][4];
     auto load_w = [&](int b, v4i (&dst)[4]) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) dst[i] = __builtin_nontemporal_load((gm_gv4i*)(wp + b * GM_KB + 64 * i));
+        for (int i = 0; i < 4; i++) dst[i] = *(gm_gv4i*)(wp + b * GM_KB + 64 * i);   // ordinary loads: see the streamed kernel below
     };
 #pragma unroll
     for (int b = 0; b < D; b++) load_w(b, wr[b]);

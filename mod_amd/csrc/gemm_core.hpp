@@ -376,15 +376,18 @@ __device__ __forceinline__ int v6_col(int j) {
 }
 
 // Computes the block tile's int32 accumulators for K = 128 * NK exactly. A
-// rows past m_rem and B rows past n_rem re-read the last valid row (their
-// outputs are discarded by the caller); with a_rows, tile row r of A is
-// A[a_rows[r]]. B (the weights) is read with nontemporal loads. The K loop is
+// is read through a buffer resource of a_limit bytes from A: rows past m_rem
+// get an offset beyond it, so their loads return zeros without touching
+// memory (an expert's row tile is often half empty); B rows past n_rem re-read
+// the last valid row. Their outputs are discarded by the caller. With a_rows,
+// tile row r of A is A[a_rows[r]]. B (the weights) is read with nontemporal
+// loads. The K loop is
 // unrolled completely: with no loop-carried load results (a loop head makes
 // the compiler wait for every load in flight) its vmcnt tracking waits
 // exactly for the set being written and keeps the later steps' loads in
 // flight.
 template <int WMT, int WNT, int D, int NK>
-__device__ __forceinline__ void mma_tile_v6(const int8_t* __restrict__ A, int64_t lda, int m_rem,
+__device__ __forceinline__ void mma_tile_v6(const int8_t* __restrict__ A, int64_t lda, int m_rem, uint32_t a_limit,
                                             const int8_t* __restrict__ B, int64_t ldb, int n_rem,
                                             int8_t* lds, v16i (&acc)[WMT][WNT],
                                             const int32_t* __restrict__ a_rows = nullptr,
@@ -396,14 +399,16 @@ __device__ __forceinline__ void mma_tile_v6(const int8_t* __restrict__ A, int64_
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
     const int8_t* src[L];
+    uint32_t aoff[WMT];
     int dst[L];
+    const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, (int)a_limit, 0x00020000);
 #pragma unroll
     for (int j = 0; j < L; j++) {
         const int q = j * 8 + wave;   // block of 8 rows: A blocks first, then B blocks
         if (j < WMT) {
             const int r = q * 8 + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
-            const int rr = min(r, m_rem - 1);
-            src[j] = A + (int64_t)(a_rows ? a_rows[rr] : rr) * lda + c * 16;
+            aoff[j] = r < m_rem ? (uint32_t)((int64_t)(a_rows ? a_rows[r] : r) * lda + c * 16) : 0x80000000u;
+            src[j] = nullptr;
         } else {
             const int r = (q - ABLK) * 8 + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
             // b_jump: the tile's second half of columns reads B rows b_jump further on
@@ -415,8 +420,10 @@ __device__ __forceinline__ void mma_tile_v6(const int8_t* __restrict__ A, int64_
     auto issue = [&](int step, v4i (&set)[L]) {
 #pragma unroll
         for (int j = 0; j < L; j++) {
-            const int8_t* g = src[j] + step * T::BK;
-            set[j] = j < WMT ? *(const v4i*)g : __builtin_nontemporal_load((const v4i*)g);
+            if (j < WMT)
+                set[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(arsrc, (int)(aoff[j < WMT ? j : 0] + step * T::BK), 0, 0));
+            else
+                set[j] = __builtin_nontemporal_load((const v4i*)(src[j] + step * T::BK));
         }
         __builtin_amdgcn_sched_barrier(0);   // keep the loads where they are issued
     };

@@ -227,6 +227,7 @@ struct GroupedParams {
     const int32_t* offsets;   // [E+1]
     float* C;                 // [rows][N] (row = position); with SwiGLU [rows][N / 2] of h
     unsigned* amax;           // SwiGLU: per position, max |h| as float bits (zeroed beforehand)
+    int64_t a_bytes;          // extent of A (< 2^31: rows past a tile's count read as zeros)
     int N, K;
 };
 
@@ -278,11 +279,12 @@ __global__ __launch_bounds__(MOE_THREADS, 2) void moe_grouped_gemm_kernel(Groupe
         }
         v16i acc[MOE_WMT][MOE_WNT];
         if (p.a_rows)
-            mma_tile_v6<MOE_WMT, MOE_WNT, MOE_D, NK>(p.A, p.K, cnt - m0, W, p.K, p.N - n0, lds_moe, acc,
-                                                     p.a_rows + beg + m0,
+            mma_tile_v6<MOE_WMT, MOE_WNT, MOE_D, NK>(p.A, p.K, cnt - m0, (uint32_t)p.a_bytes, W, p.K, p.N - n0,
+                                                     lds_moe, acc, p.a_rows + beg + m0,
                                                      SWIGLU ? I - MoeTile::BN / 2 : 0);
         else
-            mma_tile_v6<MOE_WMT, MOE_WNT, MOE_D, NK>(p.A + (int64_t)(beg + m0) * p.K, p.K, cnt - m0, W, p.K,
+            mma_tile_v6<MOE_WMT, MOE_WNT, MOE_D, NK>(p.A + (int64_t)(beg + m0) * p.K, p.K, cnt - m0,
+                                                     (uint32_t)(p.a_bytes - (int64_t)(beg + m0) * p.K), W, p.K,
                                                      p.N - n0, lds_moe, acc);
         float* scl = (float*)lds_moe;   // the stages are free once every wave is past this barrier
         __syncthreads();
@@ -471,6 +473,8 @@ int moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* w_gu
     PIO_REQUIRE(E >= 1 && E <= ROUTE_MAX_E && top_k >= 1 && top_k <= E && top_k <= 64,
                 "moe: E=%d experts (<= %d) and top_k=%d (<= min(E, 64))", E, ROUTE_MAX_E, top_k);
     PIO_REQUIRE((int64_t)T * top_k <= INT32_MAX / 4, "moe: T * top_k too large");
+    PIO_REQUIRE((int64_t)T * H < (1ll << 31) && (int64_t)T * top_k * I < (1ll << 31),
+                "moe: the quantized activations (T*H, T*top_k*I bytes) must stay below 2 GiB");
     PIO_REQUIRE(H <= 64 * 8 * ROUTE_XG, "moe: H=%d must be <= %d", H, 64 * 8 * ROUTE_XG);
     PIO_REQUIRE(aligned16(w_gu) && aligned16(w_down) && aligned16(x),
                 "moe: x and the weights must be 16-byte aligned");
@@ -497,7 +501,7 @@ int moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* w_gu
     GroupedParams g{};
     g.A = w.qx; g.a_rows = w.row_token; g.s_a = w.sx;
     g.W = w_gu; g.s_w = s_gu; g.offsets = w.offsets; g.C = w.h; g.amax = w.amax;
-    g.N = 2 * I; g.K = H;
+    g.N = 2 * I; g.K = H; g.a_bytes = (int64_t)T * H;
     launch_grouped<1, true>(g, dim3(I / (MoeTile::BN / 2), E), H / 128, st);
     PIO_LAUNCHED();
 
@@ -507,7 +511,7 @@ int moe_w8a8(const void* x, int x_dtype, const float* logits, const int8_t* w_gu
     GroupedParams d{};
     d.A = w.qh; d.a_rows = nullptr; d.s_a = w.sh;
     d.W = w_down; d.s_w = s_down; d.offsets = w.offsets; d.C = w.d;
-    d.N = H; d.K = I;
+    d.N = H; d.K = I; d.a_bytes = (int64_t)P * I;
     launch_grouped<1, false>(d, dim3(ceil_div(H, MoeTile::BN), E), I / 128, st);
     PIO_LAUNCHED();
 

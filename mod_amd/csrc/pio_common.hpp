@@ -45,19 +45,22 @@ void clear_error();
 // Checks the launch status of the kernel just issued.
 #define PIO_LAUNCHED() PIO_HIP(hipGetLastError())
 
-// Raises KERNEL's dynamic-LDS limit to the whole 160 KB once per device, when
-// a launch asks for more than the 64 KB default. One flag word per kernel (the
-// template argument is the kernel itself, not its type), one bit per device.
+// Raises KERNEL's dynamic-LDS limit above the 64 KB default to what a launch
+// asks for, per device and only when it grows (one entry per kernel: the
+// template argument is the kernel itself, not its type). The limit is the
+// dynamic bytes, so a kernel with static LDS cannot ask for the whole 160 KB.
 template <auto KERNEL>
 inline int allow_lds(size_t bytes) {
-    static std::atomic<uint64_t> done{0};
+    static std::atomic<uint32_t> set_to[64];
     if (bytes <= 65536) return PIO_OK;
     int dev = 0;
     PIO_HIP(hipGetDevice(&dev));
-    const uint64_t bit = 1ull << (dev & 63);
-    if (done.load(std::memory_order_acquire) & bit) return PIO_OK;
-    PIO_HIP(hipFuncSetAttribute((const void*)KERNEL, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-    done.fetch_or(bit, std::memory_order_release);
+    std::atomic<uint32_t>& cur = set_to[dev & 63];
+    if (cur.load(std::memory_order_acquire) >= bytes) return PIO_OK;
+    PIO_HIP(hipFuncSetAttribute((const void*)KERNEL, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes));
+    uint32_t seen = cur.load(std::memory_order_relaxed);
+    while (seen < bytes && !cur.compare_exchange_weak(seen, (uint32_t)bytes, std::memory_order_release)) {
+    }
     return PIO_OK;
 }
 

@@ -50,9 +50,18 @@ __device__ __forceinline__ void route_token(const float* __restrict__ lr, float*
                                             int top_k, int renorm, float* __restrict__ w_out,
                                             int32_t* __restrict__ id_out) {
     float mx = -1e9f;
-    for (int e = lane; e < E; e += 64) {
-        p[e] = lr[e];
-        mx = fmaxf(mx, p[e]);
+    for (int e0 = 0; e0 < E; e0 += 256) {
+        float lv[4];   // four loads in flight (clamped index, not a guarded load each)
+#pragma unroll
+        for (int u = 0; u < 4; u++) lv[u] = lr[min(e0 + lane + 64 * u, E - 1)];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int e = e0 + lane + 64 * u;
+            if (e < E) {
+                p[e] = lv[u];
+                mx = fmaxf(mx, lv[u]);
+            }
+        }
     }
     mx = wave_max(mx);
     float sum = 0.f;
@@ -135,10 +144,13 @@ __global__ __launch_bounds__(256) void moe_route_quant_kernel(const float* __res
     }
     const XT* xr = x + (int64_t)t * H;
     const int nch = H / 8;
+    // every group's raw bits first (clamped chunk index), widened afterwards
+    Raw8<XT> raw[ROUTE_XG];
+#pragma unroll
+    for (int g = 0; g < ROUTE_XG; g++) raw[g] = raw8_load(xr + 8 * min(lane + 64 * g, nch - 1));
     float v[ROUTE_XG][8];
 #pragma unroll
-    for (int g = 0; g < ROUTE_XG; g++)
-        if (lane + 64 * g < nch) load8<XT>(xr + 8 * (lane + 64 * g), v[g]);
+    for (int g = 0; g < ROUTE_XG; g++) raw8_widen(raw[g], v[g]);
     float amax = 0.f;
 #pragma unroll
     for (int g = 0; g < ROUTE_XG; g++)
@@ -178,8 +190,32 @@ __global__ __launch_bounds__(512) void moe_group_kernel(const int32_t* __restric
     __shared__ int wcount[8];
     const int e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int P = T * top_k;
+    // the first round's ids of this thread's token, loaded with the count's
+    // (every load of the block is then in flight at once)
+    // (indices are clamped, not branched around: a guarded load becomes a
+    // branch with a wait of its own, one round trip per load)
+    auto token_hit = [&](int t) {
+        int hit = -1;
+        const int tc = min(t, T - 1);
+        for (int k0 = 0; k0 < top_k; k0 += 8) {
+            int id[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) id[j] = topk_id[(int64_t)tc * top_k + min(k0 + j, top_k - 1)];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (t < T && k0 + j < top_k && id[j] == e) hit = k0 + j;
+        }
+        return hit;
+    };
+    int hit0 = token_hit(tid);
     int c = 0;
-    for (int i = tid; i < P; i += 512) c += topk_id[i] < e;
+    for (int r0 = 0; r0 < P; r0 += 8 * 512) {
+        int id[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) id[j] = topk_id[min(r0 + 8 * tid + j, P - 1)];
+#pragma unroll
+        for (int j = 0; j < 8; j++) c += (r0 + 8 * tid + j < P) & (id[j] < e);
+    }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, 64);
     if (lane == 0) wcount[wv] = c;
@@ -194,10 +230,7 @@ __global__ __launch_bounds__(512) void moe_group_kernel(const int32_t* __restric
     const unsigned long long below = (1ull << lane) - 1ull;
     for (int t0 = 0; t0 < T; t0 += 512) {
         const int t = t0 + tid;
-        int hit = -1;
-        if (t < T)
-            for (int kk = 0; kk < top_k; kk++)
-                if (topk_id[(int64_t)t * top_k + kk] == e) hit = kk;
+        const int hit = t0 == 0 ? hit0 : token_hit(t);
         const unsigned long long m = __ballot(hit >= 0);
         __syncthreads();   // wcount is free again
         if (lane == 0) wcount[wv] = __popcll(m);
@@ -371,14 +404,24 @@ __global__ __launch_bounds__(256) void moe_requant_kernel(const float* __restric
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= rows) return;
     const float am = __uint_as_float(amax[r]);
-    const float sc = am == 0.f ? 1.f : am / 127.0f;
-    if (lane == 0) s[r] = sc;
     const float4* h4 = (const float4*)(h + (int64_t)r * I);
     uint32_t* qr = (uint32_t*)(q + (int64_t)r * I);
-    for (int c = lane; c < I / 4; c += 64) {
-        const float4 v = h4[c];
-        qr[c] = (uint32_t)(uint8_t)quant1(v.x, sc) | (uint32_t)(uint8_t)quant1(v.y, sc) << 8 |
-                (uint32_t)(uint8_t)quant1(v.z, sc) << 16 | (uint32_t)(uint8_t)quant1(v.w, sc) << 24;
+    const int n4 = I / 4;
+    // up to 256 float4 per round, all loaded before the scale is used (the
+    // max and the row's values arrive together)
+    for (int c0 = 0; c0 < n4; c0 += 256) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = h4[min(c0 + lane + 64 * u, n4 - 1)];   // clamped, not branched
+        const float sc = am == 0.f ? 1.f : am / 127.0f;
+        if (c0 == 0 && lane == 0) s[r] = sc;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int c = c0 + lane + 64 * u;
+            if (c < n4)
+                qr[c] = (uint32_t)(uint8_t)quant1(v[u].x, sc) | (uint32_t)(uint8_t)quant1(v[u].y, sc) << 8 |
+                        (uint32_t)(uint8_t)quant1(v[u].z, sc) << 16 | (uint32_t)(uint8_t)quant1(v[u].w, sc) << 24;
+        }
     }
 }
 
@@ -395,14 +438,27 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
     const int n = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (n >= H) return;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int kk = 0; kk < top_k; kk++) {
-        const int pr = t * top_k + kk;
-        const float wk = topk_w[pr];
-        const float4 v = *(const float4*)(d + (int64_t)pos_of_pair[pr] * H + n);
-        acc[0] = __builtin_fmaf(wk, v.x, acc[0]);
-        acc[1] = __builtin_fmaf(wk, v.y, acc[1]);
-        acc[2] = __builtin_fmaf(wk, v.z, acc[2]);
-        acc[3] = __builtin_fmaf(wk, v.w, acc[3]);
+    // 8 slots per round: their positions and weights, then their rows, in flight together
+    for (int k0 = 0; k0 < top_k; k0 += 8) {
+        int pos[8];
+        float wk[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {   // clamped indices: guarded loads would wait one by one
+            const int pr = t * top_k + min(k0 + j, top_k - 1);
+            pos[j] = pos_of_pair[pr];
+            wk[j] = topk_w[pr];
+        }
+        float4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = *(const float4*)(d + (int64_t)pos[j] * H + n);
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (k0 + j < top_k) {
+                acc[0] = __builtin_fmaf(wk[j], v[j].x, acc[0]);
+                acc[1] = __builtin_fmaf(wk[j], v[j].y, acc[1]);
+                acc[2] = __builtin_fmaf(wk[j], v[j].z, acc[2]);
+                acc[3] = __builtin_fmaf(wk[j], v[j].w, acc[3]);
+            }
     }
 #pragma unroll
     for (int e = 0; e < 4; e++) out[(int64_t)t * H + n + e] = from_f32<OT>(acc[e]);

@@ -192,6 +192,37 @@ __device__ __forceinline__ void load8<_Float16>(const _Float16* p, float (&v)[8]
     for (int i = 0; i < 8; i++) v[i] = (float)h[i];
 }
 
+// The same 8 elements as raw bits, widened later: a load whose conversion
+// follows at once inside a (guarded or unrolled) branch waits for that load
+// before the next one issues; loading every group's raw bits first keeps all
+// the loads in flight together.
+template <typename XT>
+struct Raw8 {
+    uint4 u[sizeof(XT) / 2];
+};
+template <typename XT>
+__device__ __forceinline__ Raw8<XT> raw8_load(const XT* p) {
+    Raw8<XT> r;
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(XT) / 2); i++) r.u[i] = ((const uint4*)p)[i];
+    return r;
+}
+template <typename XT>
+__device__ __forceinline__ void raw8_widen(const Raw8<XT>& r, float (&v)[8]) {
+    if constexpr (sizeof(XT) == 4) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            v[i] = __uint_as_float(((const uint32_t*)&r.u[0])[i]);
+            v[4 + i] = __uint_as_float(((const uint32_t*)&r.u[1])[i]);
+        }
+    } else {
+        typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+        const h8 h = __builtin_bit_cast(h8, r.u[0]);
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = (float)h[i];
+    }
+}
+
 // Per-token quantizer step: clamp(rint(x / s), -127, 127), IEEE division,
 // round-half-even.
 __device__ __forceinline__ int8_t quant1(float x, float s) {

@@ -68,16 +68,19 @@ __global__ __launch_bounds__(256) void quant_rows_reg_kernel(const XT* __restric
     const int row = blockIdx.x * RPB + threadIdx.x / TPR;
     const bool live = row < M;   // (the block-wide reduction below needs every thread)
     const XT* xr = x + (int64_t)min(row, M - 1) * K;
+    // every group's raw bits first, at clamped offsets (a load guarded by its
+    // own branch and widened at once waits before the next one issues)
+    Raw8<XT> raw[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) raw[j] = raw8_load(xr + min((t + TPR * j) * 8, K - 8));
     float v[NV][8];
     float amax = 0.f;
 #pragma unroll
     for (int j = 0; j < NV; j++) {
-        const int k = (t + TPR * j) * 8;
-        if (k < K) {
-            load8<XT>(xr + k, v[j]);
+        raw8_widen(raw[j], v[j]);
+        if ((t + TPR * j) * 8 < K)
 #pragma unroll
             for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[j][i]));
-        }
     }
     amax = wave_max(amax);
     if constexpr (TPR == 256) {
@@ -209,6 +212,15 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const XT* __restrict
     const bool live = row < M;                 // every thread joins the reductions
     const int64_t base = (int64_t)min(row, M - 1) * K;
     const int nch = K / 8;
+    // every chunk's raw bits first, at clamped offsets (loads guarded by
+    // their own branch would wait one by one)
+    Raw8<XT> rx[NV], rr[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int cc = min(t + T * i, nch - 1);
+        rx[i] = raw8_load(x + base + 8 * cc);
+        if (RES) rr[i] = raw8_load(r + base + 8 * cc);
+    }
     float v[NV][8];
     float part[NV];
 #pragma unroll
@@ -216,10 +228,10 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const XT* __restrict
         const int c = t + T * i;
         part[i] = 0.f;
         if (c < nch) {
-            load8<XT>(x + base + 8 * c, v[i]);
+            raw8_widen(rx[i], v[i]);
             if (RES) {
                 float rv[8];
-                load8<XT>(r + base + 8 * c, rv);
+                raw8_widen(rr[i], rv);
 #pragma unroll
                 for (int e = 0; e < 8; e++) v[i][e] = to_f32<XT>(from_f32<XT>(v[i][e] + rv[e]));
                 if (live) store8<XT>(xs + base + 8 * c, v[i]);

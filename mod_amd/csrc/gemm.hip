@@ -340,9 +340,15 @@ __global__ __launch_bounds__(64 * WV) void skinny_w8a8_kernel(GemmParams p) {
     // This lane's weight row, clamped: rows past N are computed, never stored.
     const int8_t* wp = p.B + (int64_t)min(n0 + r, p.N - 1) * p.ldb + k0 + 16 * q;
     v4i wr[D][4];
+    // loads 2j and 2j + 1 read the two halves of one 128-byte line of each
+    // row: the first an ordinary load, the second (the line's last use)
+    // nontemporal; all-nontemporal loses the line's second half, all-ordinary
+    // fills the L2 with dead lines (each measured up to 13% slower)
     auto load_w = [&](int b, v4i (&dst)[4]) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) dst[i] = __builtin_nontemporal_load((sk_gv4i*)(wp + b * SK_KB + 64 * i));
+        for (int i = 0; i < 4; i++)
+            dst[i] = (i & 1) ? __builtin_nontemporal_load((sk_gv4i*)(wp + b * SK_KB + 64 * i))
+                             : *(sk_gv4i*)(wp + b * SK_KB + 64 * i);
     };
 #pragma unroll
     for (int b = 0; b < D; b++) load_w(b, wr[b]);
@@ -406,9 +412,9 @@ __global__ __launch_bounds__(64 * WV) void skinny_w8a8_kernel(GemmParams p) {
 // when it passes the current block's barrier. LDS rows are 256 B with the
 // 16-byte chunks XOR-swizzled by row (chunk c of row r at c ^ (r & 15)), so
 // the MFMA operand reads (16 rows, one chunk) are conflict-free; the copies
-// pick their global chunk to land that way. The weights use ordinary loads:
-// each covers half of a 128-byte line per row, and nontemporal loads lose
-// the other half before the next load asks for it (10% slower at M = 32-64).
+// pick their global chunk to land that way. The weights load as in the
+// one-pass kernel: each load covers half of a 128-byte line per row, the
+// first half with an ordinary load and the second (last use) nontemporal.
 constexpr int SS_D = 3;                      // K blocks in flight (3-6 measured alike; 3 leaves LDS for 2 workgroups)
 constexpr int SS_S = SS_D + 1;               // activation ring stages
 constexpr int SS_STAGE = 64 * SK_KB;         // 64 rows x 256 B
@@ -443,7 +449,8 @@ __global__ __launch_bounds__(64 * WV) void skinny_stream_kernel(GemmParams p) {
     auto issue = [&](int b) {
 #pragma unroll
         for (int i = 0; i < 4; i++)
-            wr[b % D][i] = *(sk_gv4i*)(wp + b * SK_KB + 64 * i);
+            wr[b % D][i] = (i & 1) ? __builtin_nontemporal_load((sk_gv4i*)(wp + b * SK_KB + 64 * i))
+                                   : *(sk_gv4i*)(wp + b * SK_KB + 64 * i);   // as the one-pass kernel
         int8_t* st = ss_lds + (b % SS_S) * SS_STAGE;
 #pragma unroll
         for (int j = 0; j < CPW; j++)

@@ -104,6 +104,7 @@ def test_gemv_shapes(env, M, N, K, xdt, ydt, bias):
     (48, 5000, 6144, np.float32, True),    # streamed x, ragged N
     (20, 4096, 1024, np.float16, False),   # streamed x, 4 blocks, 20 live rows of 64
     (64, 1000, 16384, np.float32, False),  # streamed x, 16-block K slices
+    (24, 3000, 8192, np.float16, True),    # streamed x, one 32-row tile, K slices, ragged N
 ])
 def test_gemv_mfma_fp16(env, M, N, K, ydt, bias):
     """fp16 activations with 2 <= M <= 64 and K % 1024 == 0 take the MFMA GEMV

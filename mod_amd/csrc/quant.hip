@@ -29,11 +29,42 @@ __global__ __launch_bounds__(256) void quant_per_token_kernel(const XT* __restri
 
     float amax = 0.f;
     if (VEC) {
-        for (int k = lane * 8; k < K; k += 512) {
-            float v[8];
-            load8<XT>(xr + k, v);
+        // U chunks of 8 per lane per batch, raw bits loaded together at
+        // clamped offsets (a load-and-convert per loop trip waits for each
+        // load in turn); a row of up to 64 U chunks stays in registers and is
+        // quantized from them, a longer one is read again in the second pass
+        constexpr int U = 8;
+        const int nch = K / 8;
+        for (int c0 = 0; c0 < nch; c0 += 64 * U) {
+            Raw8<XT> raw[U];
 #pragma unroll
-            for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
+            for (int u = 0; u < U; u++) raw[u] = raw8_load(xr + 8 * min(c0 + lane + 64 * u, nch - 1));
+            float v[U][8];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                raw8_widen(raw[u], v[u]);
+                if (c0 + lane + 64 * u < nch)
+#pragma unroll
+                    for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[u][i]));
+            }
+            if (nch <= 64 * U) {   // the whole row is in v: quantize it from there
+                amax = wave_max(amax);
+                const float sc = amax == 0.f ? 1.f : amax / 127.0f;
+                if (lane == 0) s[row] = sc;
+#pragma unroll
+                for (int u = 0; u < U; u++) {
+                    const int c = lane + 64 * u;
+                    if (c < nch) {
+                        uint32_t lo = 0, hi = 0;
+#pragma unroll
+                        for (int i = 0; i < 4; i++) lo |= (uint32_t)(uint8_t)quant1(v[u][i], sc) << (8 * i);
+#pragma unroll
+                        for (int i = 0; i < 4; i++) hi |= (uint32_t)(uint8_t)quant1(v[u][4 + i], sc) << (8 * i);
+                        *(uint2*)(qr + 8 * c) = make_uint2(lo, hi);
+                    }
+                }
+                return;
+            }
         }
     } else {
         for (int k = lane; k < K; k += 64) amax = fmaxf(amax, fabsf(to_f32<XT>(xr[k])));
@@ -42,7 +73,7 @@ __global__ __launch_bounds__(256) void quant_per_token_kernel(const XT* __restri
     const float sc = amax == 0.f ? 1.f : amax / 127.0f;
     if (lane == 0) s[row] = sc;
 
-    if (VEC) {
+    if (VEC) {   // rows longer than 64 U chunks: second pass
         for (int k = lane * 8; k < K; k += 512) {
             float v[8];
             load8<XT>(xr + k, v);

@@ -491,7 +491,7 @@ __global__ __launch_bounds__(64 * WV) void gemv_w8_mfma_kernel(GemvMfma p) {
 // bytes from LDS per weight byte. Each wave owns 32 weight rows. Per K block
 // of 256 it loads them into registers GS_DW blocks ahead, 64 contiguous bytes
 // of 16 rows per load (4 lanes per row; the 32x32 operand layout would give
-// each row only 2 lanes, 32 bytes per load, which streams at half the rate),
+// each row only 2 lanes, 32 bytes per load, which measured 15-25% slower),
 // and one v_permlane16_swap per dword pair moves them into the operand
 // layout: lane l then holds bytes 64 s + 32 (l / 32) + 0..31 of row l % 32 for
 // the block's 4 segments s. x streams GS_DX blocks ahead into an LDS ring

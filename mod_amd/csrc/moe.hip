@@ -190,10 +190,10 @@ __global__ __launch_bounds__(512) void moe_group_kernel(const int32_t* __restric
     __shared__ int wcount[8];
     const int e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int P = T * top_k;
-    // the first round's ids of this thread's token, loaded with the count's
-    // (every load of the block is then in flight at once)
-    // (indices are clamped, not branched around: a guarded load becomes a
-    // branch with a wait of its own, one round trip per load)
+    // The first round's ids of this thread's token load together with the
+    // count's, so every load of the block is in flight at once. Indices are
+    // clamped, not branched around: a guarded load becomes a branch with a
+    // wait of its own, one round trip per load.
     auto token_hit = [&](int t) {
         int hit = -1;
         const int tc = min(t, T - 1);

@@ -381,6 +381,60 @@ def test_gemm_split_k(env, M, N, K):
         assert np.array_equal(host(y32).view(np.uint32), yr32.view(np.uint32)), f"f32 call {rep}"
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_gemm_skinny_random_shapes(env, seed):
+    """Seeded random skinny shapes (M 1..64, N 1..2048, K 1024..8192 in steps
+    of 1024): every plan the skinny planners pick for them (one-pass or
+    streamed, any slice count) is int32 bit-exact and fp16 byte-equal (with
+    bias) to the oracle, on two calls in a row."""
+    torch, ops, d = env
+    rng = np.random.default_rng(7000 + seed)
+    M, N, K = int(rng.integers(1, 65)), int(rng.integers(1, 2049)), 1024 * int(rng.integers(1, 9))
+    _say(f"skinny random M={M} N={N} K={K}")
+    q = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    W = rng.integers(-127, 127, size=(N, K), dtype=np.int8)
+    sa = rng.uniform(0.001, 0.05, size=M).astype(np.float32)
+    sw = rng.uniform(0.001, 0.02, size=N).astype(np.float32)
+    b = rng.standard_normal(N, dtype=np.float32)
+    qd, Wd, sad, swd, bd = (dev(torch, a, d) for a in (q, W, sa, sw, b))
+    acc_ref = oracle.matmul_nt_i32(q, W)
+    yr16 = oracle.w8a8(q, sa, W, sw, b, out="f16")
+    for rep in range(2):
+        acc = torch.full((M, N), 7, dtype=torch.int32, device=d)
+        y16 = torch.full((M, N), float("nan"), dtype=torch.float16, device=d)
+        ops.gemm_w8a8(qd, None, Wd, None, None, acc, M, N, K)
+        ops.gemm_w8a8(qd, sad, Wd, swd, bd, y16, M, N, K)
+        sync(torch)
+        assert np.array_equal(host(acc), acc_ref), f"int32 call {rep}"
+        assert np.array_equal(host(y16).view(np.uint16), yr16.view(np.uint16)), f"f16 call {rep}"
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_gemv_mfma_random_shapes(env, seed):
+    """Seeded random fp16-x GEMV shapes (M 2..64, N 1..2048, K 1024..8192 in
+    steps of 1024), so both MFMA GEMVs, every tile count and K slicing meet
+    ragged N, with and without bias, fp32 or fp16 output: held to the oracle
+    at rel 1e-3 (fp32 out) / 1e-2 (fp16 out)."""
+    torch, ops, d = env
+    rng = np.random.default_rng(8000 + seed)
+    M, N, K = int(rng.integers(2, 65)), int(rng.integers(1, 2049)), 1024 * int(rng.integers(1, 9))
+    ydt = np.float16 if seed % 2 else np.float32
+    bias = seed % 3 != 0
+    _say(f"gemv mfma random M={M} N={N} K={K} y={ydt.__name__} bias={bias}")
+    x, W, s = _inputs(9000 + seed, M, N, K, np.float16)
+    b = rng.standard_normal(N, dtype=np.float32) if bias else None
+    ref = oracle.gemv_w8(x, W, s, b, out_dtype=ydt)
+    xd, wd, sd = dev(torch, x, d), dev(torch, W, d), dev(torch, s, d)
+    bd = None if b is None else dev(torch, b, d)
+    for rep in range(2):
+        y = torch.full((M, N), float("nan"), dtype=torch.float16 if ydt == np.float16 else torch.float32,
+                       device=d)
+        ops.gemv_w8(xd, wd, sd, bd, y, M, N, K, stream(torch))
+        sync(torch)
+        assert_rel(host(y).astype(np.float64), ref.astype(np.float64),
+                   1e-2 if ydt == np.float16 else 1e-3, f"gemv mfma random call {rep}")
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 12288, 4096), (16, 12288, 4096), (64, 12288, 4096),
                                    (1, 4096, 12288), (16, 4096, 12288), (64, 4096, 12288),
                                    (16, 3072, 1024),

@@ -1294,18 +1294,17 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
             const int lb = Gl + l * LP_LPL;
             // ---- P1 + P2: x'' (embedding row or reduced), RMSNorm, q/k/v of head g
             {
-                // The reduction polls before the phase's preloads are issued:
-                // a poll's wait covers every load issued before it, and the
-                // preloads' latency hides behind the gather instead (a layer
-                // start measured 0.6-0.8% faster this way; at P5 the same
-                // order measured slower, so P5 keeps its preloads first).
+                // A poll waits for every load issued before it, so what a
+                // phase needs from memory is loaded where it has time to land:
+                // the norm weights (L2 hits after the first workgroup of the
+                // XCD) before the reduction, the scales from LDS.
                 cbar();   // nothing may move above the previous phase
                 float gam[16], xv[16], nscale;
+                gld16(Lw.in_norm + 16 * c.lane, gam);
                 if (l > 0 && !reduce_x(p, c, p.dpart, tag_of(p, t, l - 1, PH_DP), p.xr, tag_of(p, t, l, PH_XR), 1))
                     return;
                 cbar();
                 const Pre pq = pre_qkv(c, l, rcs, rsn);
-                gld16(Lw.in_norm + 16 * c.lane, gam);
                 if (l == 0) {
                     gld16(emb + 16 * c.lane, xv);
                     float ss = 0.f;

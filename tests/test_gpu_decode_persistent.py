@@ -212,3 +212,19 @@ def test_persistent_rejects_other_shapes(torch_dev):
     with pytest.raises(RocmError):
         dec.run(2, mode="persistent")
     dec.run(2, mode="graph")   # the step path still serves it
+
+
+def test_persistent_rejects_more_layers_than_its_constants_hold(torch_dev):
+    """The persistent kernel keeps every layer's per-wave scales in LDS, sized
+    for 48 layers: a 49-layer model of the supported layer shape is refused
+    with an error that says so, and the graph path still serves it."""
+    from mod_amd import ops
+    cfg, _ = _cfgs(n_layers=49, max_seq=64)
+    from mod_amd.qwen3 import Qwen3Int8Decoder, random_weights
+    dec = Qwen3Int8Decoder(cfg, random_weights(cfg, seed=6))
+    assert not dec.persistent_supported()
+    assert "layers <= 48" in ops.last_error()
+    dec.reset(np.arange(4, dtype=np.int32))
+    with pytest.raises(ops.RocmError):
+        dec.run(2, mode="persistent")
+    dec.run(2, mode="graph")

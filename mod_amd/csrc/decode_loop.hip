@@ -420,7 +420,9 @@ __device__ void lp_fail(const LoopParams& p, int code, int where) {
 // paths sit inside the wait loops.
 __device__ __forceinline__ bool keep_waiting(const LoopParams& p, Cx& c, uint32_t it, uint32_t limit,
                                              int where) {
-    if (lds_ld_u(c.abort)) return false;
+    // the abort flag every 16 iterations: an LDS read in every iteration
+    // lengthens each poll by a round trip
+    if ((it & 15) == 15 && lds_ld_u(c.abort)) return false;
     if ((it & 63) != 63) return true;
     if (__hip_atomic_load(&p.err[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) || it > limit) {
         if (it > limit) c.fail_where = where;
@@ -465,13 +467,26 @@ __device__ __forceinline__ bool csync(const LoopParams& p, Cx& c, int where) {
     return true;
 }
 
+// Four LDS counters in one read (the stream waves' landed lines ready[], or
+// the compute waves' done[]; both 16-byte aligned): four separate atomic
+// reads each waited for the previous one, four LDS round trips per check.
+static_assert(LP_SW == 4 && LP_CW == 4, "the ready[] / done[] counters are read as one 16-byte word");
+__device__ __forceinline__ lp_v4i lds_ld_ready(const int* ready) {
+    const uint32_t a = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const int*)ready;
+    lp_v4i v;
+    asm volatile("ds_read_b128 %0, %1\n s_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+    return v;
+}
+
 // Waits until every ring line up to `last` has landed (stream wave r copies
 // lines r, r+4, ... in order and counts them in ready[r]).
 __device__ __forceinline__ bool wait_upto(const LoopParams& p, Cx& c, int last, int where) {
     for (uint32_t it = 0;; it++) {
+        const lp_v4i rd = lds_ld_ready(c.ready);
         bool ok = true;
 #pragma unroll
-        for (int r = 0; r < LP_SW; r++) ok &= last < r || lds_ld_u(&c.ready[r]) >= ((last - r) >> 2) + 1;
+        for (int r = 0; r < LP_SW; r++)
+            ok &= last < r || __builtin_amdgcn_readfirstlane(rd[r]) >= ((last - r) >> 2) + 1;
         if (ok) break;
         if (!keep_waiting(p, c, it, LP_LDS_LIMIT, where)) return false;
         __builtin_amdgcn_s_sleep(1);
@@ -1211,14 +1226,12 @@ __device__ void stream_role(const LoopParams& p, Cx& c) {
         const int nl = p.lpt;
         for (int j = ((sw - G) % LP_SW + LP_SW) % LP_SW; j < nl; j += LP_SW) {
             const int Lg = G + j;
-            if (lds_ld(c.abort)) { ok = false; break; }
+            if (((j / LP_SW) & 7) == 0 && lds_ld(c.abort)) { ok = false; break; }   // every 8th line
             // the slot of line Lg held line Lg - LP_RING: free once every
             // compute wave has moved past it
             auto room = [&]() {
-                int mn = lds_ld(&c.done[0]);
-#pragma unroll
-                for (int i = 1; i < LP_CW; i++) mn = min(mn, lds_ld(&c.done[i]));
-                return mn > Lg - LP_RING;
+                const lp_v4i dn = lds_ld_ready(c.done);   // done[] is 16-byte aligned too
+                return min(min(dn[0], dn[1]), min(dn[2], dn[3])) > Lg - LP_RING;
             };
             if (!room()) {
                 wait_vm<0>();
@@ -1398,7 +1411,9 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
 template <typename KT>
 __global__ __launch_bounds__(LP_THREADS, 1) void decode_loop_kernel(LoopParams p) {
     extern __shared__ __attribute__((aligned(16))) int8_t lp_lds[];
-    __shared__ int ready[LP_SW], done[LP_CW], sync_ctr, abort_flag, role;
+    __shared__ __attribute__((aligned(16))) int ready[LP_SW];
+    __shared__ __attribute__((aligned(16))) int done[LP_CW];
+    __shared__ int sync_ctr, abort_flag, role;
     __shared__ u64 wkeys[LP_CW];
     if (threadIdx.x < LP_SW) ready[threadIdx.x] = 0;
     if (threadIdx.x < LP_CW) done[threadIdx.x] = 0;

@@ -1195,17 +1195,22 @@ __device__ __noinline__ void phase_lm(const int8_t* lm, const float* s_lm, float
 
 // Argmax over the workgroups' keys of the lm phase tagged `tag` (first max,
 // tensor_ops.c:649-662).
+// The keys are polled four per lane with no branch between the loads, so the
+// four cross-XCD round trips overlap (a guarded load in a loop waited for each
+// load before the next one issued: 21 us per token).
+static_assert(LP_NBLK % 64 == 0, "argmax keys: whole waves");
 __device__ bool argmax_id(const LoopParams& p, Cx& c, uint32_t tag, int& id) {
-    const int n = (LP_NBLK + 63) / 64;
+    constexpr int n = LP_NBLK / 64;
     for (uint32_t it = 0;; it++) {
+        u64 k[n];
+#pragma unroll
+        for (int i = 0; i < n; i++) k[i] = ll_load(p.keys + c.lane + 64 * i);
         u64 best = 0;
         bool ok = true;
+#pragma unroll
         for (int i = 0; i < n; i++) {
-            const int j = c.lane + 64 * i;
-            if (j >= LP_NBLK) continue;
-            const u64 k = ll_load(p.keys + j);
-            ok &= (uint32_t)(k & 0x3FFF) == (tag & 0x3FFFu);
-            best = k > best ? k : best;
+            ok &= (uint32_t)(k[i] & 0x3FFF) == (tag & 0x3FFFu);
+            best = k[i] > best ? k[i] : best;
         }
         if (__all(ok)) {
             best = wave_max_u64(best);

@@ -79,6 +79,12 @@ __global__ __launch_bounds__(256) void gemv_w8_direct_kernel(const XT* __restric
     const int8_t* wrow[R];
 #pragma unroll
     for (int r = 0; r < R; r++) wrow[r] = W + (int64_t)min(n0 + r, N - 1) * K;
+    // The scale and bias of the row this lane writes (lane m * R + r writes
+    // row r), loaded with the first weights: loaded at the end, behind the
+    // per-lane store branches, each waited for the previous one.
+    const int rl = min(n0 + lane % R, N - 1);
+    const float swl = s_w[rl];
+    const float bl = bias ? bias[rl] : 0.f;
 
     for (int k = lane * 16; k < K; k += 1024) {
         v4i w[R];
@@ -104,8 +110,8 @@ __global__ __launch_bounds__(256) void gemv_w8_direct_kernel(const XT* __restric
 #pragma unroll
         for (int r = 0; r < R; r++) {
             if (lane == m * R + r && n0 + r < N) {
-                float v = acc[m][r] * s_w[n0 + r];
-                if (bias) v += bias[n0 + r];
+                float v = acc[m][r] * swl;
+                if (bias) v += bl;
                 y[(int64_t)m * ldy + n0 + r] = from_f32<YT>(v);
             }
         }
@@ -207,8 +213,16 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_w8_stream_kernel(const X
             }
         }
     };
+    // The scale and bias of the row lane m*R + r writes in group g, loaded
+    // when the group starts: loaded behind the store branch they were two
+    // dependent round trips per group.
+    auto scales = [&](int g, float& sw, float& bb) {
+        const int rr = min(g * R + lane % R, N - 1);
+        sw = s_w[rr];
+        bb = bias ? bias[rr] : 0.f;
+    };
     // lane m*R + r writes output (m, g*R + r)
-    auto finish = [&](int g) {
+    auto finish = [&](int g, float sw, float bb) {
         const int n0 = g * R;
         float mine = 0.f;
 #pragma unroll
@@ -221,8 +235,8 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_w8_stream_kernel(const X
             }
         const int em = lane / R, er = lane % R;
         if (lane < MT * R && n0 + er < N) {
-            float v = mine * s_w[n0 + er];
-            if (bias) v += bias[n0 + er];
+            float v = mine * sw;
+            if (bias) v += bb;
             y[(int64_t)em * ldy + n0 + er] = from_f32<YT>(v);
         }
     };
@@ -231,6 +245,8 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_w8_stream_kernel(const X
     // latencies overlap
     v4i w0[U][R];
     load(min(wave_id, ngroups - 1), 0, w0);
+    float sw0, bb0;
+    scales(min(wave_id, ngroups - 1), sw0, bb0);
     for (int q = tid; q < MT * nch * 256; q += 64 * GEMV_WAVES) {
         const int m = q / (nch * 256), k = (q - m * nch * 256) * 4;
         float v[4] = {0.f, 0.f, 0.f, 0.f};
@@ -251,14 +267,16 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_w8_stream_kernel(const X
         load(wave_id, st, w);
         math(st, w);
     }
-    finish(wave_id);
+    finish(wave_id, sw0, bb0);
     for (int g = wave_id + n_waves; g < ngroups; g += n_waves) {
+        float sw, bb;
+        scales(g, sw, bb);
         for (int st = 0; st < nst; st++) {
             v4i w[U][R];
             load(g, st, w);
             math(st, w);
         }
-        finish(g);
+        finish(g, sw, bb);
     }
 }
 

@@ -348,6 +348,36 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const int32_t* __res
 // tiles of 16*WV; grid y: K slices (int32 partials for splitk_reduce_kernel
 // when there is more than one).
 constexpr int SK_KB = 256;                // K per block: 4 MFMAs of 64
+
+// Epilogue operands of the skinny kernels' scaled outputs, loaded at the
+// kernel's start with clamped indices (lane: column r = lane % 16, rows
+// 16 t + 4 (lane / 16) + v): the store loop skips rows past M, and a load
+// inside it waited for the previous one, MT x 4 round trips after the K loop.
+template <int MT>
+struct SkEpi {
+    float sa[MT][4];
+    float sw, bn;
+};
+template <int MT, int OUT>
+__device__ __forceinline__ SkEpi<MT> sk_epi_load(const GemmParams& p, int n0, int lane) {
+    SkEpi<MT> e;
+    if constexpr (OUT == OUT_I32) {
+        e.sw = e.bn = 0.f;
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) e.sa[t][v] = 0.f;
+    } else {
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) e.sa[t][v] = p.s_a[min(t * 16 + 4 * (lane >> 4) + v, p.M - 1)];
+        const int n = min(n0 + (lane & 15), p.N - 1);
+        e.sw = p.s_w[n];
+        e.bn = p.bias ? p.bias[n] : 0.f;
+    }
+    return e;
+}
 constexpr int SK_D = 4;                   // weight blocks in flight per wave (8 measured no faster)
 
 typedef __attribute__((address_space(1))) const v4i sk_gv4i;
@@ -370,6 +400,8 @@ __global__ __launch_bounds__(64 * WV) void skinny_w8a8_kernel(GemmParams p) {
     const int r = lane & 15, q = lane >> 4;
     const int n0 = blockIdx.x * (16 * WV) + w * 16;
     const int64_t k0 = (int64_t)blockIdx.y * p.K;          // p.K is the K of one slice
+    // older than every copy and weight load, so the waits below cover them
+    const SkEpi<MT> epi = sk_epi_load<MT, OUT>(p, n0, lane);
 
     // Activation slice -> LDS: copy u moves row u / SEG, segment u % SEG (lane l
     // lands 16 B at LDS offset 16*l of the segment). Rows >= M re-read row M-1;
@@ -430,8 +462,6 @@ __global__ __launch_bounds__(64 * WV) void skinny_w8a8_kernel(GemmParams p) {
     // 16x16 accumulator: lane holds rows 4*q + v (v < 4) of M tile t, column r.
     const int n = n0 + r;
     if (n >= p.N) return;
-    const float sw = OUT == OUT_I32 ? 0.f : p.s_w[n];
-    const float bn = (OUT != OUT_I32 && p.bias) ? p.bias[n] : 0.f;
 #pragma unroll
     for (int t = 0; t < MT; t++) {
 #pragma unroll
@@ -442,7 +472,7 @@ __global__ __launch_bounds__(64 * WV) void skinny_w8a8_kernel(GemmParams p) {
             if constexpr (OUT == OUT_I32) {
                 ((int32_t*)p.C)[o] = acc[t][v];
             } else {
-                const float val = scaled_value<OUT>(acc[t][v], p.s_a[m], sw, bn, p.bias != nullptr);
+                const float val = scaled_value<OUT>(acc[t][v], epi.sa[t][v], epi.sw, epi.bn, p.bias != nullptr);
                 if constexpr (OUT == OUT_F32) ((float*)p.C)[o] = val;
                 else ((_Float16*)p.C)[o] = (_Float16)val;
             }
@@ -483,6 +513,8 @@ __global__ __launch_bounds__(64 * WV) void skinny_stream_kernel(GemmParams p) {
     const int r = lane & 15, q = lane >> 4;
     const int n0 = blockIdx.x * (16 * WV) + w * 16;
     const int64_t k0 = (int64_t)blockIdx.y * p.K;          // p.K is the K of one slice
+    // older than every copy and weight load, so the waits below cover them
+    const SkEpi<4> epi = sk_epi_load<4, OUT>(p, n0, lane);
 
     // copy j of this wave moves activation rows 4u .. 4u + 3 (u = w + WV j):
     // lane l lands its 16 B at stage offset 1024 u + 16 l, i.e. row 4u + l / 16,
@@ -535,8 +567,6 @@ __global__ __launch_bounds__(64 * WV) void skinny_stream_kernel(GemmParams p) {
     // 16x16 accumulator: lane holds rows 4*q + v (v < 4) of M tile t, column r.
     const int n = n0 + r;
     if (n >= p.N) return;
-    const float sw = OUT == OUT_I32 ? 0.f : p.s_w[n];
-    const float bn = (OUT != OUT_I32 && p.bias) ? p.bias[n] : 0.f;
 #pragma unroll
     for (int t = 0; t < 4; t++) {
 #pragma unroll
@@ -547,7 +577,7 @@ __global__ __launch_bounds__(64 * WV) void skinny_stream_kernel(GemmParams p) {
             if constexpr (OUT == OUT_I32) {
                 ((int32_t*)p.C)[o] = acc[t][v];
             } else {
-                const float val = scaled_value<OUT>(acc[t][v], p.s_a[m], sw, bn, p.bias != nullptr);
+                const float val = scaled_value<OUT>(acc[t][v], epi.sa[t][v], epi.sw, epi.bn, p.bias != nullptr);
                 if constexpr (OUT == OUT_F32) ((float*)p.C)[o] = val;
                 else ((_Float16*)p.C)[o] = (_Float16)val;
             }

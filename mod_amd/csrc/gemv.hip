@@ -431,6 +431,12 @@ __global__ __launch_bounds__(64 * WV) void gemv_w8_mfma_kernel(GemvMfma p) {
     const int r = lane & 15, q = lane >> 4;
     const int n0 = blockIdx.x * (16 * WV) + w * 16;
     const int64_t k0 = (int64_t)blockIdx.y * p.K;
+    // the epilogue's scale and bias, loaded first (clamped column) so that
+    // they are not a round trip after the K loop; older than every copy and
+    // weight load, so the waits below cover them
+    const int nc = min(n0 + r, p.N - 1);
+    const float sw = SPLIT ? 0.f : p.s_w[nc];
+    const float bn = (!SPLIT && p.bias) ? p.bias[nc] : 0.f;
 
     // x slice -> LDS (rows >= M re-read row M-1; their outputs are dropped)
 #pragma unroll
@@ -482,8 +488,6 @@ __global__ __launch_bounds__(64 * WV) void gemv_w8_mfma_kernel(GemvMfma p) {
     // 16x16 accumulator: lane holds rows 4*q + v of M tile t, column r.
     const int n = n0 + r;
     if (n >= p.N) return;
-    const float sw = SPLIT ? 0.f : p.s_w[n];
-    const float bn = (!SPLIT && p.bias) ? p.bias[n] : 0.f;
 #pragma unroll
     for (int t = 0; t < MT; t++) {
 #pragma unroll
@@ -570,6 +574,10 @@ __global__ __launch_bounds__(64 * WV) void gemv_w8_mfma_stream_kernel(GemvMfma p
     const int col = lane & 31, h = lane >> 5;
     const int n0 = blockIdx.x * (32 * WV) + w * 32;
     const int64_t k0 = (int64_t)blockIdx.y * p.K;
+    // the epilogue's scale and bias, loaded first (as in the one-pass kernel)
+    const int nc = min(n0 + col, p.N - 1);
+    const float sw = SPLIT ? 0.f : p.s_w[nc];
+    const float bn = (!SPLIT && p.bias) ? p.bias[nc] : 0.f;
 
     // copy j moves x rows 2u, 2u + 1 (u = w + WV j): lane l lands 16 B at stage
     // offset 1024 u + 16 l = row 2u + l / 32, chunk position l % 32, which holds
@@ -653,8 +661,6 @@ __global__ __launch_bounds__(64 * WV) void gemv_w8_mfma_stream_kernel(GemvMfma p
     // of tile t, weight row n0 + l % 32.
     const int n = n0 + col;
     if (n >= p.N) return;
-    const float sw = SPLIT ? 0.f : p.s_w[n];
-    const float bn = (!SPLIT && p.bias) ? p.bias[n] : 0.f;
 #pragma unroll
     for (int t = 0; t < MT; t++) {
 #pragma unroll

@@ -302,29 +302,50 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const int32_t* __res
     const int64_t MN = (int64_t)M * N;
     const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i0 >= MN) return;
+    // Every load at a clamped index, with no branch around it (a guarded load
+    // waits for the previous one): the epilogue operands first, then the
+    // partials four slices at a time, added in slice order.
+    float sa[4], sw[4], bb[4];
+    if constexpr (OUT != OUT_I32) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int64_t i = min(i0 + u, MN - 1);
+            const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
+            sa[u] = s_a[m];
+            sw[u] = s_w[n];
+            bb[u] = bias ? bias[n] : 0.f;
+        }
+    }
     int acc[4] = {0, 0, 0, 0};
     const bool vec = (N % 4) == 0;   // then the four elements share a row and 16 B alignment
-    for (int z = 0; z < splits; z++) {
-        const int32_t* src = ws + z * MN + i0;
-        if (vec) {
-            const int4 v = *(const int4*)src;
-            acc[0] += v.x; acc[1] += v.y; acc[2] += v.z; acc[3] += v.w;
-        } else {
+    for (int z0 = 0; z0 < splits; z0 += 4) {
+        int v[4][4];
 #pragma unroll
-            for (int u = 0; u < 4; u++)
-                if (i0 + u < MN) acc[u] += src[u];
+        for (int j = 0; j < 4; j++) {
+            const int32_t* src = ws + (int64_t)min(z0 + j, splits - 1) * MN;
+            if (vec) {
+                const int4 t = *(const int4*)(src + i0);
+                v[j][0] = t.x; v[j][1] = t.y; v[j][2] = t.z; v[j][3] = t.w;
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; u++) v[j][u] = src[min(i0 + u, MN - 1)];
+            }
         }
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (z0 + j < splits)
+#pragma unroll
+                for (int u = 0; u < 4; u++) acc[u] += v[j][u];
     }
 #pragma unroll
     for (int u = 0; u < 4; u++) {
         const int64_t i = i0 + u;
         if (i >= MN) break;
-        const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
-        if (OUT == OUT_I32) {
+        if constexpr (OUT == OUT_I32) {
             ((int32_t*)C)[i] = acc[u];
         } else {
-            const float val = scaled_value<OUT>(acc[u], s_a[m], s_w[n], bias ? bias[n] : 0.f, bias != nullptr);
-            if (OUT == OUT_F32) ((float*)C)[i] = val;
+            const float val = scaled_value<OUT>(acc[u], sa[u], sw[u], bb[u], bias != nullptr);
+            if constexpr (OUT == OUT_F32) ((float*)C)[i] = val;
             else ((_Float16*)C)[i] = (_Float16)val;
         }
     }

@@ -459,10 +459,10 @@ __device__ __forceinline__ bool csync(const LoopParams& p, Cx& c, int where) {
     cbar();
     if (c.lane == 0) __hip_atomic_fetch_add(c.csync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     const int target = LP_CW * c.nsync;
-    for (uint32_t it = 0; lds_ld_u(c.csync) < target; it++) {
+    // no sleep between the reads: the four waves arrive within a few hundred
+    // cycles, and a sleep delays the last wave's exit (+0.4% tok/s without)
+    for (uint32_t it = 0; lds_ld_u(c.csync) < target; it++)
         if (!keep_waiting(p, c, it, LP_LDS_LIMIT, where)) return false;
-        __builtin_amdgcn_s_sleep(1);
-    }
     cbar();
     return true;
 }

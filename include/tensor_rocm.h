@@ -324,7 +324,10 @@ typedef struct {
     float rms_eps, rope_theta;
     /* KV cache element type: PIO_F32 (0, the reference's) or PIO_F16 (1: k and
      * v rounded to fp16 when they are written, half the cache bytes read per
-     * token). A caller that zero-initializes the struct gets fp32. */
+     * token). A caller that zero-initializes the struct gets fp32.
+     * This field was appended to the struct: a C host built against an
+     * earlier copy of this header passes a smaller struct and must be rebuilt
+     * against this one. */
     int kv_dtype;
 } pio_qwen3_config;
 
@@ -357,7 +360,11 @@ int pio_qwen3_reset(void* dec, const int32_t* ids, int prompt_len);
  * input). The modes share the KV cache and position, so they can alternate.
  * Persistent mode builds a per-workgroup copy of the weights on first use
  * (the size of the int8 weights) and needs the config checked by
- * pio_qwen3_persistent_supported. */
+ * pio_qwen3_persistent_supported. It needs every CU at once: a launch whose
+ * workgroups do not all become resident within 20 ms (other work on the
+ * device) computes nothing, nor does any persistent launch after it; the next
+ * pio_qwen3_read, or a run in another mode, re-runs those steps in graph mode
+ * (pio_qwen3_persistent_replays counts such launches). */
 #define PIO_DECODE_EAGER 0
 #define PIO_DECODE_GRAPH 1
 #define PIO_DECODE_PERSISTENT 2
@@ -366,9 +373,15 @@ int pio_qwen3_run(void* dec, int n_steps, int mode);
  * device, else 0 (the reason is in tensor_last_error). No counterpart in the
  * reference. */
 int pio_qwen3_persistent_supported(void* dec);
-/* Waits for the stream, then copies out ids[0..n) and, if logits != NULL, the
- * last step's logits [vocab]. Reports an error if a persistent run since the
- * last read gave up on a wait (its results are then invalid). */
+/* Persistent launches of this decoder that were re-run in graph mode because
+ * the device could not hold their grid at once. No counterpart in the
+ * reference. */
+int pio_qwen3_persistent_replays(void* dec);
+/* Waits for the stream (re-running steps of persistent launches that could
+ * not start, see pio_qwen3_run), then copies out ids[0..n) and, if
+ * logits != NULL, the last step's logits [vocab]. Reports an error if a
+ * persistent run since the last read gave up on a wait (its results are then
+ * invalid). */
 int pio_qwen3_read(void* dec, int32_t* ids, int n, float* logits);
 /* Device pointer of the last step's logits ([vocab] fp32). */
 const float* pio_qwen3_logits(void* dec);

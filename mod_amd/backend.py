@@ -132,12 +132,29 @@ class Tensor:
         handle; default the current stream). A host destination is pinned.
         With non_blocking the call returns at once and the result keeps the
         source alive; the caller orders later work after the copy (an event,
-        or synchronizing the stream)."""
+        or synchronizing the stream).
+
+        On a stream other than the current one, the copy first waits for the
+        work already queued on the current stream (which may still be
+        writing this tensor), and a device destination is allocated with that
+        stream current, so the allocator's per-stream cache hands its block
+        out again only behind the copy that writes it."""
         if device == self.device:
             return self
-        out = Tensor.pinned(self.shape, self.dtype) if device == "cpu" else \
-            Tensor(self.shape, device=device, dtype=self.dtype)
         sh = _stream_handle(stream)
+        cur = lib.get_current_stream()
+        side = sh is not None and (sh or None) != (cur or None)
+        if side:
+            ev = HIPEvent()
+            ev.record(None)
+            check(lib.stream_wait_event(sh, ev._handle), "stream_wait_event")
+            lib.set_current_stream(sh)
+        try:
+            out = Tensor.pinned(self.shape, self.dtype) if device == "cpu" else \
+                Tensor(self.shape, device=device, dtype=self.dtype)
+        finally:
+            if side:
+                lib.set_current_stream(cur)
         check(lib.tensor_copy_async(out._handle, self._handle, sh), "tensor_copy_async")
         if non_blocking:
             out._src = self

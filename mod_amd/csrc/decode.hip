@@ -721,6 +721,11 @@ PIO_EXPORT int pio_qwen3_reset(void* h, const int32_t* ids, int prompt_len) {
                     i);
     // Host staging keeps the copies and the state init in stream order; no memset
     // (a graph replay must not follow a memset node).
+    // persistent launches still queued run first; their results are dropped
+    PIO_HIP(hipStreamSynchronize(d->st));
+    int from = 0;
+    (void)loop_status(d, &from);
+    clear_error();
     std::vector<int32_t> st(16, 0);
     st[0] = 0;
     st[1] = prompt_len;
@@ -732,20 +737,9 @@ PIO_EXPORT int pio_qwen3_reset(void* h, const int32_t* ids, int prompt_len) {
     return PIO_OK;
 }
 
-PIO_EXPORT int pio_qwen3_run(void* h, int n_steps, int mode) {
-    Qwen3Dec* d = (Qwen3Dec*)h;
-    PIO_REQUIRE(d, "pio_qwen3_run: null handle");
-    PIO_REQUIRE(n_steps >= 0 && d->host_pos + n_steps <= d->c.max_seq,
-                "pio_qwen3_run: %d more steps exceed max_seq %d (at %d)", n_steps, d->c.max_seq,
-                d->host_pos);
-    PIO_REQUIRE(mode >= PIO_DECODE_EAGER && mode <= PIO_DECODE_PERSISTENT,
-                "pio_qwen3_run: unknown mode %d", mode);
-    if (mode == PIO_DECODE_PERSISTENT) {
-        PIO_TRY(loop_run(d, n_steps));
-        d->host_pos += n_steps;
-        return PIO_OK;
-    }
-    const bool use_graph = mode == PIO_DECODE_GRAPH;
+// n_steps decode steps of the step kernels: one captured graph per step
+// (use_graph) or the kernels launched one by one.
+static int run_stepwise(Qwen3Dec* d, int n_steps, bool use_graph) {
     if (use_graph && !d->exec && n_steps > 0) {
         PIO_HIP(hipStreamBeginCapture(d->st, hipStreamCaptureModeRelaxed));
         int rc = enqueue_step(d);
@@ -767,6 +761,47 @@ PIO_EXPORT int pio_qwen3_run(void* h, int n_steps, int mode) {
     return PIO_OK;
 }
 
+// Drains the stream and checks the persistent launches since the last check.
+// Launches that found the grid not co-resident (other work held CUs when they
+// started) computed nothing, nor did any launch after them: their steps run
+// again here in graph mode, from the first position that did not run.
+static int settle(Qwen3Dec* d) {
+    PIO_HIP(hipStreamSynchronize(d->st));
+    int from = 0;
+    const int rc = loop_status(d, &from);
+    if (rc != LOOP_REPLAY) return rc;
+    const int n = d->host_pos - from;
+    d->host_pos = from;
+    PIO_TRY(run_stepwise(d, n, true));
+    PIO_HIP(hipStreamSynchronize(d->st));
+    return PIO_OK;
+}
+
+PIO_EXPORT int pio_qwen3_run(void* h, int n_steps, int mode) {
+    Qwen3Dec* d = (Qwen3Dec*)h;
+    PIO_REQUIRE(d, "pio_qwen3_run: null handle");
+    PIO_REQUIRE(n_steps >= 0 && d->host_pos + n_steps <= d->c.max_seq,
+                "pio_qwen3_run: %d more steps exceed max_seq %d (at %d)", n_steps, d->c.max_seq,
+                d->host_pos);
+    PIO_REQUIRE(mode >= PIO_DECODE_EAGER && mode <= PIO_DECODE_PERSISTENT,
+                "pio_qwen3_run: unknown mode %d", mode);
+    if (mode == PIO_DECODE_PERSISTENT) {
+        PIO_TRY(loop_run(d, n_steps));
+        d->host_pos += n_steps;
+        return PIO_OK;
+    }
+    // the step kernels continue from the device position: persistent launches
+    // queued before must have run (or been re-run) first
+    if (loop_pending(d)) PIO_TRY(settle(d));
+    return run_stepwise(d, n_steps, mode == PIO_DECODE_GRAPH);
+}
+
+PIO_EXPORT int pio_qwen3_persistent_replays(void* h) {
+    Qwen3Dec* d = (Qwen3Dec*)h;
+    PIO_REQUIRE(d, "pio_qwen3_persistent_replays: null handle");
+    return loop_replays(d);
+}
+
 PIO_EXPORT int pio_qwen3_persistent_supported(void* h) {
     Qwen3Dec* d = (Qwen3Dec*)h;
     PIO_REQUIRE(d, "pio_qwen3_persistent_supported: null handle");
@@ -777,6 +812,7 @@ PIO_EXPORT int pio_qwen3_read(void* h, int32_t* ids, int n, float* logits) {
     Qwen3Dec* d = (Qwen3Dec*)h;
     PIO_REQUIRE(d, "pio_qwen3_read: null handle");
     PIO_REQUIRE(n >= 0 && n <= d->c.max_seq + 1, "pio_qwen3_read: n=%d out of range", n);
+    PIO_TRY(settle(d));
     if (n > 0) {
         PIO_REQUIRE(ids, "pio_qwen3_read: null ids");
         PIO_HIP(hipMemcpyAsync(ids, d->ids, (size_t)n * 4, hipMemcpyDeviceToHost, d->st));
@@ -785,7 +821,7 @@ PIO_EXPORT int pio_qwen3_read(void* h, int32_t* ids, int n, float* logits) {
         PIO_HIP(hipMemcpyAsync(logits, d->logits, (size_t)d->c.vocab * 4, hipMemcpyDeviceToHost,
                                d->st));
     PIO_HIP(hipStreamSynchronize(d->st));
-    return loop_status(d);
+    return PIO_OK;
 }
 
 PIO_EXPORT const float* pio_qwen3_logits(void* h) { return h ? ((Qwen3Dec*)h)->logits : nullptr; }

@@ -41,8 +41,14 @@ struct Qwen3Dec {
 // n_steps tokens. loop_check() says whether the config fits its kernel.
 int loop_check(const Qwen3Dec* d);
 int loop_run(Qwen3Dec* d, int n_steps);
-// Error words of the last persistent run; call after the stream has drained.
-int loop_status(Qwen3Dec* d);
+// Error words of the persistent launches since the last call; call after the
+// stream has drained. LOOP_REPLAY: a launch found the grid not co-resident
+// (other work held CUs), so it and every launch after it computed nothing;
+// *replay_pos is the first position to run again.
+constexpr int LOOP_REPLAY = 1;
+int loop_status(Qwen3Dec* d, int* replay_pos);
+int loop_replays(const Qwen3Dec* d);
+bool loop_pending(const Qwen3Dec* d);   // persistent launches not yet checked
 void loop_destroy(Qwen3Dec* d);
 
 }  // namespace pio

@@ -112,11 +112,21 @@ constexpr int LP_L_GU = 24;                // 12 (gate, up) pairs of 1 KB rows
 constexpr int LP_L_DN = 12;                // 32 rows x 384 B (8 rows x 128 B per line)
 constexpr int LP_OFF_O = LP_L_QKV, LP_OFF_GU = LP_OFF_O + LP_L_O, LP_OFF_DN = LP_OFF_GU + LP_L_GU;
 constexpr int LP_LPL = LP_OFF_DN + LP_L_DN;   // 60
-constexpr uint32_t LP_POLL_LIMIT = 1u << 21;   // device-scope polls (~0.5-1 us each)
-constexpr uint32_t LP_LDS_LIMIT = 1u << 24;    // LDS polls
+// Every wait gives up after LP_WAIT_TICKS of the 100 MHz constant clock
+// (s_memrealtime): one time limit for every site, so a wait on an LDS counter
+// outlasts the device poll of a sibling wave that it depends on.
+constexpr uint64_t LP_WAIT_TICKS = 200000000ull;     // 2 s
+// How long a workgroup waits at launch for all LP_NBLK to be resident.
+constexpr uint64_t LP_ARRIVE_TICKS = 2000000ull;     // 20 ms
 
 enum { PH_XR = 0, PH_QKV = 1, PH_ATT = 2, PH_OP = 3, PH_XR2 = 4, PH_ACT = 5, PH_DP = 6 };
-enum { LP_ERR_TIMEOUT = 1, LP_ERR_XCD = 2 };
+enum { LP_ERR_TIMEOUT = 1, LP_ERR_XCD = 2, LP_ERR_RESIDENT = 3 };
+// Error words (LoopState::err, 64 ints): [0] code, [1] site, [2] abort flag,
+// [4] workgroups arrived, [8 + g] XCD g's next slot -- cleared before every
+// launch; [16] set once a launch found the grid not co-resident (every later
+// launch then leaves at once), [17] that launch's first position -- kept until
+// the host has re-run those steps.
+constexpr int LP_E_ARRIVED = 4, LP_E_STICKY = 16, LP_E_STICKY_POS = 17;
 
 struct LoopLayer {
     const float *in_norm, *s_qkv, *b_qkv, *s_o, *post_norm, *s_gu, *s_down;
@@ -150,7 +160,8 @@ struct LoopParams {
     int32_t* state;
     int pos0, prompt_len, n_steps;
     uint32_t epoch0;
-    int* err;                  // [0] code, [1] where, [2] abort flag, [8 + g] XCD g's next slot
+    uint64_t arrive_ticks;     // co-residency wait at launch (LP_ARRIVE_TICKS)
+    int* err;                  // error words (see LP_E_*)
 };
 
 // LDS layout (dynamic): ring | per-wave x copies | merged head output |
@@ -390,6 +401,7 @@ __device__ __forceinline__ uint32_t tag_of(const LoopParams& p, int t, int l, in
 
 struct Cx {
     int lane, w, nsync, fail_where;
+    uint64_t wt0;    // s_memrealtime at the current wait's first check
     int g, j, role;  // XCD, slot within it, role index j * 8 + g
     int uv0, nuv;    // lm_head rows of this workgroup
     int* ready;      // [LP_SW] lines landed per stream wave
@@ -417,15 +429,18 @@ __device__ void lp_fail(const LoopParams& p, int code, int where) {
 // workgroup gave up. A wave that runs out of patience only notes where (and
 // raises the workgroup's abort flag); the kernel reports it once on the way
 // out -- the kernel has to fit the instruction cache, so no calls or long
-// paths sit inside the wait loops.
-__device__ __forceinline__ bool keep_waiting(const LoopParams& p, Cx& c, uint32_t it, uint32_t limit,
-                                             int where) {
+// paths sit inside the wait loops. The clock is read every 64th iteration;
+// the first read starts the wait's LP_WAIT_TICKS.
+__device__ __forceinline__ bool keep_waiting(const LoopParams& p, Cx& c, uint32_t it, int where) {
     // the abort flag every 16 iterations: an LDS read in every iteration
     // lengthens each poll by a round trip
     if ((it & 15) == 15 && lds_ld_u(c.abort)) return false;
     if ((it & 63) != 63) return true;
-    if (__hip_atomic_load(&p.err[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) || it > limit) {
-        if (it > limit) c.fail_where = where;
+    const uint64_t now = __builtin_amdgcn_s_memrealtime();
+    if (it == 63) c.wt0 = now;
+    const bool late = now - c.wt0 > LP_WAIT_TICKS;
+    if (__hip_atomic_load(&p.err[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) || late) {
+        if (late) c.fail_where = where;
         lds_st(c.abort, 1);
         return false;
     }
@@ -449,7 +464,7 @@ __device__ __forceinline__ bool poll(const LoopParams& p, Cx& c, F addr, uint32_
             for (int i = 0; i < N; i++) out[i] = __uint_as_float((uint32_t)v[i]);
             return true;
         }
-        if (!keep_waiting(p, c, it, LP_POLL_LIMIT, where)) return false;
+        if (!keep_waiting(p, c, it, where)) return false;
     }
 }
 
@@ -462,7 +477,7 @@ __device__ __forceinline__ bool csync(const LoopParams& p, Cx& c, int where) {
     // no sleep between the reads: the four waves arrive within a few hundred
     // cycles, and a sleep delays the last wave's exit (+0.4% tok/s without)
     for (uint32_t it = 0; lds_ld_u(c.csync) < target; it++)
-        if (!keep_waiting(p, c, it, LP_LDS_LIMIT, where)) return false;
+        if (!keep_waiting(p, c, it, where)) return false;
     cbar();
     return true;
 }
@@ -488,7 +503,7 @@ __device__ __forceinline__ bool wait_upto(const LoopParams& p, Cx& c, int last, 
         for (int r = 0; r < LP_SW; r++)
             ok &= last < r || __builtin_amdgcn_readfirstlane(rd[r]) >= ((last - r) >> 2) + 1;
         if (ok) break;
-        if (!keep_waiting(p, c, it, LP_LDS_LIMIT, where)) return false;
+        if (!keep_waiting(p, c, it, where)) return false;
         __builtin_amdgcn_s_sleep(1);
     }
     cbar();
@@ -576,7 +591,7 @@ __device__ __forceinline__ bool gather_x(const LoopParams& p, Cx& c, const u64* 
             for (int i = 0; i < 16; i++) xw[c.lane + 64 * i] = __uint_as_float((uint32_t)v[i]);
             break;
         }
-        if (!keep_waiting(p, c, it, LP_POLL_LIMIT, where)) return false;
+        if (!keep_waiting(p, c, it, where)) return false;
     }
     load_row16(xw + 16 * c.lane, xv);
     float ss = 0.f;
@@ -792,7 +807,7 @@ __device__ bool phase_dpart(const LoopParams& p, Cx& c, int line0, uint32_t atag
             for (int i = 0; i < 6; i++) av[i] = __uint_as_float((uint32_t)v[i]);
             break;
         }
-        if (!keep_waiting(p, c, it, LP_POLL_LIMIT, 7)) return false;
+        if (!keep_waiting(p, c, it, 7)) return false;
     }
     float* aw = c.acts + c.w * LP_IX;
 #pragma unroll
@@ -941,7 +956,7 @@ __device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t q
                 for (int i = 0; i < 8; i++) stg[c.lane + 64 * i] = __uint_as_float((uint32_t)v[i]);
                 break;
             }
-            if (!keep_waiting(p, c, it, LP_POLL_LIMIT, 20)) return false;
+            if (!keep_waiting(p, c, it, 20)) return false;
         }
     }
     cbar();
@@ -1083,7 +1098,7 @@ __device__ bool merge_heads(const LoopParams& p, Cx& c, int pos, uint32_t ptag) 
             oo[s] = __uint_as_float((uint32_t)ov[s]);
         }
         if (__all(ok)) break;
-        if (!keep_waiting(p, c, it, LP_POLL_LIMIT, 30)) return false;
+        if (!keep_waiting(p, c, it, 30)) return false;
     }
     float M = -INFINITY;
 #pragma unroll
@@ -1217,7 +1232,7 @@ __device__ bool argmax_id(const LoopParams& p, Cx& c, uint32_t tag, int& id) {
             id = (int)(0x3FFFFu - (uint32_t)((best >> 14) & 0x3FFFF));
             return true;
         }
-        if (!keep_waiting(p, c, it, LP_POLL_LIMIT, 70)) return false;
+        if (!keep_waiting(p, c, it, 70)) return false;
     }
 }
 
@@ -1244,7 +1259,7 @@ __device__ void stream_role(const LoopParams& p, Cx& c) {
                 inflight = 0;
                 lds_st_raw(&c.ready[sw], published);
                 for (uint32_t it = 0; !room(); it++) {
-                    if (!keep_waiting(p, c, it, LP_LDS_LIMIT, 80)) { ok = false; break; }
+                    if (!keep_waiting(p, c, it, 80)) { ok = false; break; }
                     __builtin_amdgcn_s_sleep(2);
                 }
                 if (!ok) break;
@@ -1425,14 +1440,42 @@ __global__ __launch_bounds__(LP_THREADS, 1) void decode_loop_kernel(LoopParams p
     if (threadIdx.x == 0) {
         sync_ctr = 0;
         abort_flag = 0;
-        // this workgroup's XCD and the next free slot in it
-        unsigned xcc;
-        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 16)" : "=s"(xcc));
-        int slot = LP_WPX;
-        if (xcc < (unsigned)LP_NX)
-            slot = __hip_atomic_fetch_add(p.err + 8 + xcc, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        role = slot < LP_WPX ? slot * LP_NX + (int)xcc : -1;
-        if (role < 0) lp_fail(p, LP_ERR_XCD, 100 + (int)xcc);
+        role = -1;
+        // An earlier launch of this decoder found the grid not co-resident:
+        // its steps have not run, so this one leaves too (the host re-runs
+        // them all in graph mode).
+        if (!__hip_atomic_load(p.err + LP_E_STICKY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+            // this workgroup's XCD and the next free slot in it
+            unsigned xcc;
+            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 16)" : "=s"(xcc));
+            int slot = LP_WPX;
+            if (xcc < (unsigned)LP_NX)
+                slot = __hip_atomic_fetch_add(p.err + 8 + xcc, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            role = slot < LP_WPX ? slot * LP_NX + (int)xcc : -1;
+            if (role < 0) lp_fail(p, LP_ERR_XCD, 100 + (int)xcc);
+            // Co-residency: every wait below assumes all LP_NBLK workgroups
+            // run at once. Other work holding CUs would leave some waiting
+            // for them, so each workgroup counts in and waits (briefly) for
+            // the rest before it writes anything; if they do not come, the
+            // launch is marked and computes nothing.
+            __hip_atomic_fetch_add(p.err + LP_E_ARRIVED, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+            while (role >= 0) {
+                const int n = __hip_atomic_load(p.err + LP_E_ARRIVED, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+                if (__hip_atomic_load(p.err + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+                    role = -1;
+                } else if (n >= LP_NBLK && p.arrive_ticks > 0) {
+                    break;
+                } else if (__builtin_amdgcn_s_memrealtime() - t0 > p.arrive_ticks) {
+                    if (atomicCAS(p.err + LP_E_STICKY, 0, 1) == 0) atomicExch(p.err + LP_E_STICKY_POS, p.pos0);
+                    lp_fail(p, LP_ERR_RESIDENT, n);
+                    role = -1;
+                } else {
+                    __builtin_amdgcn_s_sleep(2);
+                }
+            }
+        }
     }
     __syncthreads();
     if (role < 0) return;   // every wave of the workgroup leaves together
@@ -1449,6 +1492,7 @@ __global__ __launch_bounds__(LP_THREADS, 1) void decode_loop_kernel(LoopParams p
     }
     c.nsync = 0;
     c.fail_where = 0;
+    c.wt0 = 0;
     c.ready = ready;
     c.done = done;
     c.csync = &sync_ctr;
@@ -1485,6 +1529,7 @@ struct LoopState {
     int* err = nullptr;
     uint32_t epoch = 1;
     bool ran = false;
+    int replays = 0;    // launches re-run in graph mode (grid not co-resident)
 };
 
 // The kernel's dynamic LDS exceeds the 64 KB default limit.
@@ -1651,7 +1696,9 @@ int loop_run(Qwen3Dec* d, int n_steps) {
         PIO_HIP(hipMemsetAsync(s->small, 0, s->ll_bytes, d->st));
         s->epoch = 1;
     }
-    PIO_HIP(hipMemsetAsync(s->err, 0, 64, d->st));   // error words and XCD slot counters
+    // abort flag, arrival and XCD slot counters; the error code and site stay
+    // until loop_status reads them, so the first error since then is reported
+    PIO_HIP(hipMemsetAsync(s->err + 2, 0, 14 * sizeof(int), d->st));
     LoopParams p{};
     p.L = c.n_layers; p.V = c.vocab; p.max_seq = c.max_seq;
     p.eps = c.rms_eps;
@@ -1669,6 +1716,11 @@ int loop_run(Qwen3Dec* d, int n_steps) {
     p.prompt_len = d->prompt_len;
     p.n_steps = n_steps;
     p.epoch0 = s->epoch;
+    // PIO_LOOP_ARRIVE_TICKS overrides the co-residency wait (ticks of 10 ns);
+    // 0 makes every launch act as if the grid never became resident, which is
+    // how the tests reach the graph-mode re-run
+    p.arrive_ticks = LP_ARRIVE_TICKS;
+    if (const char* e = getenv("PIO_LOOP_ARRIVE_TICKS")) p.arrive_ticks = strtoull(e, nullptr, 10);
     p.err = s->err;
     PIO_TRY(loop_lds_attr());
     if (d->kv16) decode_loop_kernel<_Float16><<<dim3(LP_NBLK), dim3(LP_THREADS), LP_LDS_BYTES, d->st>>>(p);
@@ -1679,12 +1731,26 @@ int loop_run(Qwen3Dec* d, int n_steps) {
     return PIO_OK;
 }
 
-// Error words of the last persistent run (after the stream has drained).
-int loop_status(Qwen3Dec* d) {
+bool loop_pending(const Qwen3Dec* d) { return d->loop && d->loop->ran; }
+int loop_replays(const Qwen3Dec* d) { return d->loop ? d->loop->replays : 0; }
+
+// Error words of the persistent launches since the last call (after the
+// stream has drained). A launch that found the grid not co-resident, and every
+// launch after it, computed nothing: returns LOOP_REPLAY with *replay_pos = the
+// first position whose step has to be run again; the words are cleared.
+int loop_status(Qwen3Dec* d, int* replay_pos) {
     if (!d->loop || !d->loop->ran) return PIO_OK;
-    int e[2] = {0, 0};
+    int e[18] = {};
     PIO_HIP(hipMemcpy(e, d->loop->err, sizeof(e), hipMemcpyDeviceToHost));
     d->loop->ran = false;
+    const int zero[2] = {0, 0};
+    PIO_HIP(hipMemcpy(d->loop->err, zero, sizeof(zero), hipMemcpyHostToDevice));
+    if (e[LP_E_STICKY]) {
+        PIO_HIP(hipMemcpy(d->loop->err + LP_E_STICKY, zero, sizeof(zero), hipMemcpyHostToDevice));
+        d->loop->replays++;
+        *replay_pos = e[LP_E_STICKY_POS];
+        return LOOP_REPLAY;
+    }
     if (e[0] == LP_ERR_XCD)
         return set_error(PIO_ERR_HIP, "persistent decode: more than %d workgroups on XCD %d (or no "
                                       "such XCD); results of that run are invalid",

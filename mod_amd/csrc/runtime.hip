@@ -224,8 +224,10 @@ void device_free(void* p) {
     unsigned long long cid = 0;
     if (a.stream_ids.count(l.stream) && a.stream_ids[l.stream] == l.sid &&
         hipStreamGetCaptureInfo(l.stream, &cs, &cid) == hipSuccess &&
-        cs != hipStreamCaptureStatusNone) {
+        cs == hipStreamCaptureStatusActive) {
         // recorded into a graph that is still being built: keep it out of reach
+        // (a capture the runtime invalidated records nothing more, and no
+        // graph will run what it recorded)
         a.parked[cid].emplace_back(p, l);
         a.held += l.bytes;
         return;
@@ -246,7 +248,9 @@ unsigned long long capture_id(hipStream_t s) {
 
 // end_capture's hand-over: the blocks parked under capture `cid` now belong to
 // the library's graph; the ones the replaced graph held return to the cache.
-static void graph_replaced(unsigned long long cid) {
+// When the capture failed (`captured` false) no graph will ever run the
+// recorded kernels, so the blocks parked under it return to the cache too.
+static void graph_replaced(unsigned long long cid, bool captured) {
     Alloc& a = A();
     std::lock_guard<std::mutex> lk(a.mu);
     for (auto& pl : a.graph_held) {
@@ -256,7 +260,14 @@ static void graph_replaced(unsigned long long cid) {
     a.graph_held.clear();
     auto it = cid ? a.parked.find(cid) : a.parked.end();
     if (it != a.parked.end()) {
-        a.graph_held = std::move(it->second);
+        if (captured) {
+            a.graph_held = std::move(it->second);
+        } else {
+            for (auto& pl : it->second) {
+                a.held -= pl.second.bytes;
+                cache_block_locked(a, pl.first, pl.second);
+            }
+        }
         a.parked.erase(it);
     }
 }
@@ -266,7 +277,7 @@ static void graph_replaced(unsigned long long cid) {
 // tensor_empty_cache or an out-of-memory retry once freed).
 void release_stream(hipStream_t s) {
     if (!s) return;
-    (void)hipStreamSynchronize(s);
+    if (hipStreamSynchronize(s) != hipSuccess) (void)hipGetLastError();
     Alloc& a = A();
     std::lock_guard<std::mutex> lk(a.mu);
     auto it = a.stream_ids.find(s);
@@ -652,10 +663,12 @@ PIO_EXPORT void destroy_stream(void* s) {
         if (g_user_stream == (hipStream_t)s) g_user_stream = nullptr;
     }
     release_stream((hipStream_t)s);
-    (void)hipStreamDestroy((hipStream_t)s);
+    if (hipStreamDestroy((hipStream_t)s) != hipSuccess) (void)hipGetLastError();
 }
 PIO_EXPORT void stream_synchronize(void* s) {
-    (void)hipStreamSynchronize(s ? (hipStream_t)s : current_stream());
+    // a failure here (e.g. a synchronize while the stream captures) must not
+    // stay behind as the runtime's last error for the next launch check
+    if (hipStreamSynchronize(s ? (hipStream_t)s : current_stream()) != hipSuccess) (void)hipGetLastError();
 }
 PIO_EXPORT void set_current_stream(void* s) {
     std::lock_guard<std::mutex> lk(g_mu);
@@ -733,15 +746,22 @@ PIO_EXPORT void device_synchronize(void) { (void)hipDeviceSynchronize(); }
 static hipGraph_t g_graph = nullptr;
 static hipGraphExec_t g_graph_exec = nullptr;
 static hipStream_t g_capture_stream = nullptr;
+// id of the capture begin_capture started: taken at the start, since a capture
+// the runtime has invalidated may no longer report it
+static unsigned long long g_capture_cid = 0;
 
 PIO_EXPORT void begin_capture(void) {
     g_capture_stream = current_stream();
+    g_capture_cid = 0;
     if (hipStreamBeginCapture(g_capture_stream, hipStreamCaptureModeRelaxed) != hipSuccess)
         set_error(PIO_ERR_HIP, "begin_capture failed");
+    else
+        g_capture_cid = capture_id(g_capture_stream);
 }
 PIO_EXPORT void end_capture(void) {
     if (!g_capture_stream) return;
-    const unsigned long long cid = capture_id(g_capture_stream);
+    const unsigned long long cid = g_capture_cid;
+    g_capture_cid = 0;
     if (g_graph_exec) {
         (void)hipGraphExecDestroy(g_graph_exec);
         g_graph_exec = nullptr;
@@ -751,11 +771,13 @@ PIO_EXPORT void end_capture(void) {
         g_graph = nullptr;
     }
     if (hipStreamEndCapture(g_capture_stream, &g_graph) != hipSuccess) {
+        (void)hipGetLastError();
         set_error(PIO_ERR_HIP, "end_capture failed");
-        graph_replaced(0);
+        g_graph = nullptr;
+        graph_replaced(cid, false);
         return;
     }
-    graph_replaced(cid);
+    graph_replaced(cid, true);
     if (hipGraphInstantiate(&g_graph_exec, g_graph, nullptr, nullptr, 0) != hipSuccess)
         set_error(PIO_ERR_HIP, "hipGraphInstantiate failed");
 }

@@ -298,6 +298,11 @@ class Qwen3Int8Decoder:
         """Whether the "persistent" mode runs this config on this device."""
         return bool(lib.pio_qwen3_persistent_supported(self._h))
 
+    def persistent_replays(self) -> int:
+        """Persistent launches re-run in graph mode because the device could
+        not hold their whole grid at once (other work held CUs)."""
+        return int(lib.pio_qwen3_persistent_replays(self._h))
+
     def run(self, n_steps: int, use_graph: bool = True, mode: Optional[str] = None) -> None:
         check(lib.pio_qwen3_run(self._h, n_steps, _mode(use_graph, mode)), "pio_qwen3_run")
 

@@ -211,6 +211,48 @@ def test_capture_keeps_workspace_from_later_tensors(T):
     assert int(lib.tensor_pool_graph_bytes()) == held0
 
 
+def test_failed_capture_returns_its_parked_blocks(T):
+    """A capture that the runtime invalidates (here: a stream synchronize on
+    the capturing stream, which HIP rejects) ends in a failed end_capture. The
+    workspace the captured op parked under it belongs to no graph, so it
+    returns to the cache instead of staying counted as graph-held. The capture
+    runs on a stream of its own: HIP leaves a stream whose capture was
+    invalidated unusable, so that stream is destroyed afterwards."""
+    from mod_amd.ops import check, lib, last_error
+    M, N, K = 16, 4096, 12288
+    rng = np.random.default_rng(5)
+    tq = _t(T, rng.integers(-127, 128, size=(M, K), dtype=np.int8))
+    tsa = _t(T, rng.uniform(0.001, 0.05, size=M).astype(np.float32))
+    tw = _t(T, rng.integers(-127, 128, size=(N, K), dtype=np.int8))
+    tsw = _t(T, rng.uniform(0.001, 0.02, size=N).astype(np.float32))
+    out = T.Tensor([M, N], dtype="float32")
+    T.synchronize()
+    lib.begin_capture()
+    lib.end_capture()                        # an empty graph: nothing held
+    held0 = int(lib.tensor_pool_graph_bytes())
+    lib.tensor_clear_error()
+    side = T.HIPStream()
+    with side:
+        lib.begin_capture()
+        rc = lib.tensor_linear_w8a8_status(tq._handle, tsa._handle, tw._handle, tsw._handle,
+                                           None, out._handle)
+        lib.stream_synchronize(None)         # not allowed while capturing
+        lib.end_capture()
+        err = last_error()
+    lib.tensor_clear_error()
+    del side
+    if "end_capture failed" not in err:
+        pytest.skip("this runtime did not invalidate the capture")
+    assert rc == 0
+    assert int(lib.tensor_pool_graph_bytes()) == held0
+    # the library still works on the default stream
+    ref = oracle.w8a8(tq.numpy(), tsa.numpy(), tw.numpy(), tsw.numpy(), out="f32")
+    check(lib.tensor_linear_w8a8_status(tq._handle, tsa._handle, tw._handle, tsw._handle,
+                                        None, out._handle), "tensor_linear_w8a8 after the failed capture")
+    T.synchronize()
+    assert np.array_equal(out.numpy().view(np.uint32), ref.view(np.uint32))
+
+
 def test_torch_graph_of_several_ops_with_workspaces(torch_dev):
     """The capture pattern of bench.py: one warm call outside the capture, then
     a torch.cuda.graph holding several ops whose plans need workspaces (the

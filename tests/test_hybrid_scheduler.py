@@ -92,3 +92,31 @@ def test_hybrid_execution_matches_resident_stack(torch_dev):
         assert all(p.device == ("cpu" if i >= 3 else "rocm:0")
                    for i, L in enumerate(model.layers) for p in L.parameters())
     assert sched.stats["max_offloaded_on_device"] <= 4
+
+
+@pytest.mark.gpu
+def test_to_on_a_side_stream_is_ordered_after_the_current_stream(torch_dev):
+    """Tensor.to(..., stream=s) with s not the current stream: the copy waits
+    for the work queued on the current stream that writes the source (here a
+    chain of 64 MB fills, the last one with the expected value), to a pinned
+    host tensor both blocking and non-blocking, and from there back to the
+    device on the side stream."""
+    from mod_amd.backend import HIPStream, Tensor
+    n = 16 << 20
+    x = Tensor((n,), device="rocm:0", dtype="float32")
+    s = HIPStream()
+    for rep in range(3):
+        for v in range(1, 9):
+            x.fill(float(v + 10 * rep))          # queued on the current stream
+        h = x.to("cpu", stream=s)
+        assert np.all(h.numpy() == float(8 + 10 * rep))
+        for v in range(1, 5):
+            x.fill(float(v + 100 * rep))
+        z = x.to("cpu", non_blocking=True, stream=s)
+        s.synchronize()
+        assert np.all(z.numpy() == float(4 + 100 * rep))
+        # back to the device on the side stream: the destination block is
+        # allocated for that stream
+        d = z.to("rocm:0", non_blocking=True, stream=s)
+        s.synchronize()
+        assert np.all(d.numpy() == float(4 + 100 * rep))

@@ -175,7 +175,8 @@ constexpr size_t LP_LDS_ATT = (size_t)LP_CW * LP_G * LP_D * 4 + 2 * LP_CW * LP_G
 constexpr size_t LP_STG = LP_G * LP_D + 256;   // floats per wave: q heads + current k,v
 constexpr size_t LP_LDS_STG = (size_t)LP_CW * LP_STG * 4;
 constexpr size_t LP_LDS_CST = (size_t)LP_LMAX * LP_CW * LP_NCST * 4;
-constexpr size_t LP_LDS_BYTES = LP_LDS_RING + LP_LDS_XW + LP_LDS_OS + LP_LDS_ACT + LP_LDS_ATT + LP_LDS_STG + LP_LDS_CST;
+constexpr size_t LP_LDS_XS = (size_t)2 * LP_H * 4;   // the shared input vectors x'', x'
+constexpr size_t LP_LDS_BYTES = LP_LDS_RING + LP_LDS_XW + LP_LDS_OS + LP_LDS_ACT + LP_LDS_ATT + LP_LDS_STG + LP_LDS_CST + LP_LDS_XS;
 
 // ------------------------------------------------------------------ helpers
 __device__ __forceinline__ u64 ll_load(const u64* p) {
@@ -219,6 +220,20 @@ __device__ __forceinline__ void ld_l2_16s(const u64* a, const u64* b, u64 (&v)[1
                    "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]),
                    "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15])
                  : [a] "v"(a), [b] "v"(b)
+                 : "memory");
+}
+// 2 tagged words 64 words apart
+__device__ __forceinline__ void ld_l2_2s(const u64* p, u64 (&v)[2]) {
+    asm volatile(LP_LD(0, 0) LP_LD(1, 512) "s_waitcnt vmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1])
+                 : [a] "v"(p)
+                 : "memory");
+}
+// 4 tagged words 64 words apart
+__device__ __forceinline__ void ld_l2_4s(const u64* p, u64 (&v)[4]) {
+    asm volatile(LP_LD(0, 0) LP_LD(1, 512) LP_LD(2, 1024) LP_LD(3, 1536) "s_waitcnt vmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+                 : [a] "v"(p)
                  : "memory");
 }
 // 8 tagged words 64 words apart
@@ -411,11 +426,12 @@ struct Cx {
     int8_t* ring;
     float* xw;       // [LP_CW][H] each wave's copy of the current input vector
     float* os;       // [256] merged attention output of KV head g
-    float* acts;     // [LP_CW][384] each wave's copy of XCD g's act slice
+    float* acts;     // [384] the workgroup's copy of XCD g's act slice
     float* attp;     // [LP_CW][LP_G][128] attention partials
     float* attm;     // [2][LP_CW][LP_G] wave max, wave sum
     float* stg;      // [LP_CW][LP_STG]
     float* cst;      // [LP_LMAX][LP_CW][LP_NCST] per-layer constants of each compute wave
+    float* xs;       // [2][H] the workgroup's copies of x'' (0) and x' (1)
     u64* wkeys;      // [LP_CW]
 };
 
@@ -573,27 +589,32 @@ __device__ __forceinline__ void slots16(const float* src, int part, float (&d)[1
 __device__ __forceinline__ float kv_round(float v, float*) { return v; }
 __device__ __forceinline__ float kv_round(float v, _Float16*) { return (float)(_Float16)v; }
 
-// The full input vector (H values), polled by this wave into the lane layout
-// of a 1 KB weight line (lane l holds x[16 l .. 16 l + 15]) and copied to the
-// wave's own LDS vector; returns the RMSNorm scale of g * x (g = gamma).
+// The full input vector (H values) into the workgroup's LDS copy xs: each of
+// the four compute waves polls one quarter (words 256 w + lane + 64 i, i < 4:
+// coalesced), so the XCD's L2 serves each word once per workgroup rather than
+// once per wave, and a poll is 4 loads per lane instead of 16; after the
+// waves meet, each reads the vector in the lane layout of a 1 KB weight line
+// (lane l holds x[16 l .. 16 l + 15]). Returns the RMSNorm scale of g * x
+// (g = gamma). xs is one of two buffers that alternate between the two
+// gathers of a layer: the other still holds the previous vector, the base of
+// the reduction that precedes the next gather, and the rendezvous here
+// orders every wave's reads of a buffer before the writes that reuse it.
 __device__ __forceinline__ bool gather_x(const LoopParams& p, Cx& c, const u64* src, uint32_t tag,
                                          const float (&gam)[16], float (&xv)[16], float& nscale,
-                                         int where) {
-    // coalesced poll (word lane + 64 i), transposed through the wave's LDS copy
-    // into the line layout (lane l: x[16 l .. 16 l + 15])
-    const u64* base = src + c.g * LP_H + c.lane;
-    float* xw = c.xw + c.w * LP_H;
+                                         float* xs, int where) {
+    const u64* base = src + c.g * LP_H + 256 * c.w + c.lane;
     for (uint32_t it = 0;; it++) {
-        u64 v[16];
-        ld_l2_16s(base, base + 512, v);
+        u64 v[4];
+        ld_l2_4s(base, v);
         if (__all(tags_ok(v, tag))) {
 #pragma unroll
-            for (int i = 0; i < 16; i++) xw[c.lane + 64 * i] = __uint_as_float((uint32_t)v[i]);
+            for (int i = 0; i < 4; i++) xs[256 * c.w + c.lane + 64 * i] = __uint_as_float((uint32_t)v[i]);
             break;
         }
         if (!keep_waiting(p, c, it, where)) return false;
     }
-    load_row16(xw + 16 * c.lane, xv);
+    if (!csync(p, c, where + 200)) return false;
+    load_row16(xs + 16 * c.lane, xv);
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; i += 4)
@@ -606,16 +627,16 @@ __device__ __forceinline__ bool gather_x(const LoopParams& p, Cx& c, const u64* 
 
 // Cross-XCD reduction (P1 / P5): x_new[e] = base[e] + sum over the 8 XCDs'
 // partials part[h][e], for this wave's 8 elements e = 32 j + 8 w + (lane >> 3)
-// (lane & 7 = h); the 8-lane sum has one fixed order. base is the wave's own
+// (lane & 7 = h); the 8-lane sum has one fixed order. xb is the workgroup's
 // copy of the previous input vector. Stored tagged for the XCD's gather.
 __device__ __forceinline__ bool reduce_x(const LoopParams& p, Cx& c, const u64* part, uint32_t ptag,
-                                         u64* out, uint32_t otag, int where) {
+                                         u64* out, uint32_t otag, const float* xb, int where) {
     const int e = 32 * c.j + 8 * c.w + (c.lane >> 3);
     const u64* src = part + (c.lane & 7) * LP_H + e;
     float v[1];
     if (!poll<1>(p, c, [&](int) { return src; }, ptag, v, where)) return false;
     const float s = sum8(v[0]);
-    if ((c.lane & 7) == 0) st_l2(out + c.g * LP_H + e, c.xw[c.w * LP_H + e] + s, otag);
+    if ((c.lane & 7) == 0) st_l2(out + c.g * LP_H + e, xb[e] + s, otag);
     return true;
 }
 
@@ -797,21 +818,24 @@ __device__ bool phase_opart(const LoopParams& p, Cx& c, int line0, uint32_t tag,
 // lane: 16 channels 128 cc + 16 (lane & 7).
 __device__ bool phase_dpart(const LoopParams& p, Cx& c, int line0, uint32_t atag, uint32_t tag,
                             float sd) {
-    float av[6];
-    const u64* src = p.act + c.g * LP_IX + c.lane;
-    for (uint32_t it = 0;; it++) {
-        u64 v[6];
-        ld_l2_6s(src, v);
-        if (__all(tags_ok(v, atag))) {
-#pragma unroll
-            for (int i = 0; i < 6; i++) av[i] = __uint_as_float((uint32_t)v[i]);
-            break;
+    // XCD g's 384 act values into the workgroup's LDS copy: waves 0-2 poll
+    // 128 words each (2 per lane, coalesced), then the four waves meet
+    static_assert(LP_IX == 3 * 128, "three waves poll the act slice");
+    float* aw = c.acts;
+    if (c.w < 3) {
+        const u64* src = p.act + c.g * LP_IX + 128 * c.w + c.lane;
+        for (uint32_t it = 0;; it++) {
+            u64 v[2];
+            ld_l2_2s(src, v);
+            if (__all(tags_ok(v, atag))) {
+                aw[128 * c.w + c.lane] = __uint_as_float((uint32_t)v[0]);
+                aw[128 * c.w + c.lane + 64] = __uint_as_float((uint32_t)v[1]);
+                break;
+            }
+            if (!keep_waiting(p, c, it, 7)) return false;
         }
-        if (!keep_waiting(p, c, it, 7)) return false;
     }
-    float* aw = c.acts + c.w * LP_IX;
-#pragma unroll
-    for (int i = 0; i < 6; i++) aw[c.lane + 64 * i] = av[i];
+    if (!csync(p, c, 207)) return false;
     if (!wait_upto(p, c, line0 + 3 * c.w + 2, 50)) return false;
     float s[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1334,14 +1358,16 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
                 cbar();   // nothing may move above the previous phase
                 float gam[16], xv[16], nscale;
                 gld16(Lw.in_norm + 16 * c.lane, gam);
-                if (l > 0 && !reduce_x(p, c, p.dpart, tag_of(p, t, l - 1, PH_DP), p.xr, tag_of(p, t, l, PH_XR), 1))
+                if (l > 0 && !reduce_x(p, c, p.dpart, tag_of(p, t, l - 1, PH_DP), p.xr, tag_of(p, t, l, PH_XR),
+                                       c.xs + LP_H, 1))
                     return;
                 cbar();
                 const Pre pq = pre_qkv(c, l, rcs, rsn);
                 if (l == 0) {
                     gld16(emb + 16 * c.lane, xv);
                     float ss = 0.f;
-                    float* xw = c.xw + c.w * LP_H + 16 * c.lane;
+                    // every wave writes the same row: x'' of layer 0
+                    float* xw = c.xs + 16 * c.lane;
 #pragma unroll
                     for (int i = 0; i < 16; i += 4) {
                         *(float4*)(xw + i) = make_float4(xv[i], xv[i + 1], xv[i + 2], xv[i + 3]);
@@ -1352,7 +1378,7 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
                     for (int i = 0; i < 16; i++) xv[i] *= gam[i];
                     nscale = rsqrtf(wsum(ss) * (1.0f / (float)LP_H) + p.eps);
                 } else {
-                    if (!gather_x(p, c, p.xr, tag_of(p, t, l, PH_XR), gam, xv, nscale, 2)) return;
+                    if (!gather_x(p, c, p.xr, tag_of(p, t, l, PH_XR), gam, xv, nscale, c.xs, 2)) return;
                 }
                 if (!phase_qkv<KT>(p, c, l, pos, lb, tag_of(p, t, l, PH_QKV), xv, nscale, pq)) return;
                 set_done(c, lb + LP_OFF_O);
@@ -1374,9 +1400,9 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
                 const Pre pg = pre_gu(c, l);
                 float gam[16], xv[16], nscale;
                 gld16(Lw.post_norm + 16 * c.lane, gam);
-                if (!reduce_x(p, c, p.opart, tag_of(p, t, l, PH_OP), p.xr2, tag_of(p, t, l, PH_XR2), 3))
+                if (!reduce_x(p, c, p.opart, tag_of(p, t, l, PH_OP), p.xr2, tag_of(p, t, l, PH_XR2), c.xs, 3))
                     return;
-                if (!gather_x(p, c, p.xr2, tag_of(p, t, l, PH_XR2), gam, xv, nscale, 4)) return;
+                if (!gather_x(p, c, p.xr2, tag_of(p, t, l, PH_XR2), gam, xv, nscale, c.xs + LP_H, 4)) return;
                 if (!phase_gu(p, c, lb + LP_OFF_GU, tag_of(p, t, l, PH_ACT), xv, nscale, pg)) return;
                 set_done(c, lb + LP_OFF_DN);
             }
@@ -1391,9 +1417,10 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
         if (lm) {
             float gam[16], xv[16], nscale;
             gld16(p.final_norm + 16 * c.lane, gam);
-            if (!reduce_x(p, c, p.dpart, tag_of(p, t, p.L - 1, PH_DP), p.xr, tag_of(p, t, p.L, PH_XR), 9))
+            if (!reduce_x(p, c, p.dpart, tag_of(p, t, p.L - 1, PH_DP), p.xr, tag_of(p, t, p.L, PH_XR),
+                          c.xs + LP_H, 9))
                 return;
-            if (!gather_x(p, c, p.xr, tag_of(p, t, p.L, PH_XR), gam, xv, nscale, 11)) return;
+            if (!gather_x(p, c, p.xr, tag_of(p, t, p.L, PH_XR), gam, xv, nscale, c.xs, 11)) return;
             // the lm phase reads gamma * x from the wave's LDS copy
             float* xw = c.xw + c.w * LP_H + 16 * c.lane;
 #pragma unroll
@@ -1505,6 +1532,7 @@ __global__ __launch_bounds__(LP_THREADS, 1) void decode_loop_kernel(LoopParams p
     c.attm = c.attp + LP_CW * LP_G * LP_D;
     c.stg = (float*)(lp_lds + LP_LDS_RING + LP_LDS_XW + LP_LDS_OS + LP_LDS_ACT + LP_LDS_ATT);
     c.cst = (float*)(lp_lds + LP_LDS_RING + LP_LDS_XW + LP_LDS_OS + LP_LDS_ACT + LP_LDS_ATT + LP_LDS_STG);
+    c.xs = (float*)(lp_lds + LP_LDS_RING + LP_LDS_XW + LP_LDS_OS + LP_LDS_ACT + LP_LDS_ATT + LP_LDS_STG + LP_LDS_CST);
     c.wkeys = wkeys;
     if (c.w >= LP_CW) {
         stream_role(p, c);

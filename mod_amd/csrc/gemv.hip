@@ -10,8 +10,9 @@
 // byte select), accumulate in fp32 FMA, and apply the per-channel scale once
 // per output after the cross-lane reduction. fp16 activations with
 // 2 <= M <= 64 and K % 1024 == 0 go to the MFMA kernel (gemv_w8_mfma_kernel,
-// below), where the FMA kernels would be VALU-bound. Requires K % 16 == 0 and
-// 16 B aligned x and W rows.
+// below), where the FMA kernels would be VALU-bound; any other batch of more
+// than 4 rows to the MFMA GEMM of gemm_w8f.hip, which reads W once. Requires
+// K % 16 == 0 and 16 B aligned x and W rows.
 #include "pio_common.hpp"
 #include "gemm_core.hpp"
 
@@ -840,6 +841,11 @@ static int launch_gemv_mfma(const _Float16* x, const int8_t* w, const float* s_w
     return PIO_OK;
 }
 
+// The W8 linear on the matrix cores (gemm_w8f.hip), for more than 4 rows.
+int gemm_w8f(const void* x, int x_dtype, int64_t ldx, const int8_t* w, const float* s_w, const float* bias,
+             void* y, int y_dtype, int64_t ldy, int M, int N, int K, bool resid, hipStream_t st);
+constexpr int GEMV_MAX_FMA_ROWS = 4;
+
 // Below this weight size a launch is bounded by its start-up (one HBM round
 // trip), not by streaming: the direct kernel's one-wave-per-row-group grid
 // reaches its first weight bytes sooner than the stream kernel, which first
@@ -854,6 +860,11 @@ static int dispatch(const XT* x, const int8_t* w, const float* s_w, const float*
         if (!pl.wv) pl = plan_gemv_mfma(M, N, K);
         if (pl.wv) return launch_gemv_mfma(x, w, s_w, bias, y, M, N, K, pl, st);
     }
+    // More rows than one FMA launch serves: the MFMA GEMM reads W once, where
+    // the FMA kernels would re-stream it every few rows.
+    if (M > GEMV_MAX_FMA_ROWS)
+        return gemm_w8f(x, std::is_same<XT, float>::value ? PIO_F32 : PIO_F16, K, w, s_w, bias, y,
+                        std::is_same<YT, float>::value ? PIO_F32 : PIO_F16, N, M, N, K, false, st);
     if ((size_t)N * K >= GEMV_STREAM_MIN_BYTES && stream_pick(1, N, K)) {
         // x rows in launches of up to 4 (as many as the LDS takes); each launch re-streams W
         for (int m0 = 0; m0 < M;) {

@@ -128,13 +128,76 @@ def test_gemv_mfma_fp16(env, M, N, K, ydt, bias):
                    1e-2 if ydt == np.float16 else 1e-3, f"gemv mfma call {rep}")
 
 
+@pytest.mark.parametrize("M,N,K,xdt,ydt,bias", [
+    (128, 4096, 1024, np.float32, np.float32, True),     # C2 prefill qkv (128-token prompt)
+    (128, 1024, 2048, np.float32, np.float32, False),    # prefill o_proj: K in 2 slices
+    (128, 1024, 3072, np.float32, np.float32, False),    # prefill down: K in 4 slices
+    (128, 6144, 1024, np.float32, np.float32, False),    # prefill gate_up
+    (2048, 3072, 1024, np.float32, np.float32, False),   # C1's linear over 2048 rows
+    (2048, 3072, 1024, np.float16, np.float16, True),
+    (65, 1000, 1040, np.float32, np.float16, True),      # ragged M and N, K % 64 != 0
+    (5, 4000, 1040, np.float32, np.float32, True),       # just past the FMA kernels' 4 rows
+    (100, 130, 80, np.float16, np.float32, True),        # fp16 x, K % 1024 != 0, one partial step
+    (300, 2048, 4096, np.float16, np.float32, False),    # fp16 x past the MFMA GEMVs' 64 rows
+])
+def test_gemv_many_rows_mfma_gemm(env, M, N, K, xdt, ydt, bias):
+    """More than 4 rows (other than fp16 x at 2..64 rows with K % 1024 == 0)
+    go to the W8 MFMA GEMM, which reads every weight once per launch: fp32 x
+    as three exact bf16 parts, fp16 x as is, int8 weights exact, so only the
+    fp32 accumulation rounds -- held to the fp32 bar (rel 1e-3) against the
+    float64 oracle, fp16 outputs to 1e-2. Two calls in a row into a NaN-filled
+    output (every element written)."""
+    torch, ops, d = env
+    _say(f"w8 mfma gemm M={M} N={N} K={K} x {np.dtype(xdt).name} y {np.dtype(ydt).name}")
+    x, W, s = _inputs(M * 3 + N + K, M, N, K, xdt)
+    b = np.random.default_rng(4).standard_normal(N, dtype=np.float32) if bias else None
+    ref = oracle.gemv_w8(x, W, s, b, out_dtype=ydt)
+    xd, wd, sd = dev(torch, x, d), dev(torch, W, d), dev(torch, s, d)
+    bd = None if b is None else dev(torch, b, d)
+    for rep in range(2):
+        y = torch.full((M, N), float("nan"), dtype=torch.float16 if ydt == np.float16 else torch.float32,
+                       device=d)
+        ops.gemv_w8(xd, wd, sd, bd, y, M, N, K, stream(torch))
+        sync(torch)
+        got = host(y).astype(np.float64)
+        assert np.isfinite(got).all(), "an output was never written"
+        assert_rel(got, ref.astype(np.float64), 1e-2 if ydt == np.float16 else 1e-3, f"w8 mfma gemm call {rep}")
+
+
+def test_gemv_many_rows_exact_parts(env):
+    """The fp32-x MFMA GEMM splits x into bf16 parts exactly: with x values
+    that need all 24 significand bits and weight rows +-e_j, every output is
+    the selected x value times its (power-of-two) scale, bit for bit: any
+    partial sum of the parts' products is then exact, so a part dropped,
+    shifted or rounded would show; and scaling the scales by 4 scales y
+    exactly."""
+    torch, ops, d = env
+    M, N, K = 96, 256, 1024
+    rng = np.random.default_rng(77)
+    x = (rng.standard_normal((M, K)) * np.exp2(rng.integers(-20, 20, (M, K)))).astype(np.float32)
+    x.view(np.uint32)[:] |= 0x00000001            # the last significand bit set
+    sel = rng.integers(0, K, N)
+    W = np.zeros((N, K), np.int8)
+    W[np.arange(N), sel] = rng.choice([-1, 1], N).astype(np.int8)
+    s = np.exp2(rng.integers(-8, 0, N)).astype(np.float32)   # powers of two: exact products
+    y = torch.empty((M, N), dtype=torch.float32, device=d)
+    ops.gemv_w8(dev(torch, x, d), dev(torch, W, d), dev(torch, s, d), None, y, M, N, K, stream(torch))
+    sync(torch)
+    want = (x[:, sel].astype(np.float64) * W[np.arange(N), sel].astype(np.float64) * s).astype(np.float32)
+    assert np.array_equal(host(y), want)
+    y2 = torch.empty((M, N), dtype=torch.float32, device=d)
+    ops.gemv_w8(dev(torch, x, d), dev(torch, W, d), dev(torch, s * 4, d), None, y2, M, N, K, stream(torch))
+    sync(torch)
+    assert np.array_equal(host(y2), host(y) * 4)
+
+
 @pytest.mark.parametrize("M,N,K,xdt", [
     (1, 151936, 1024, np.float16),   # lm_head-sized N: many row groups per wave
     (5, 20000, 4096, np.float16),    # fp16 x at 2 <= M <= 64: the MFMA GEMV
     (1, 50001, 3072, np.float32),    # 4-row groups, ragged last group
-    (5, 20000, 4096, np.float32),    # stream kernel: a 4-x-row launch, then 1 row
+    (5, 20000, 4096, np.float32),    # more than 4 fp32 rows: the MFMA GEMM
     (2, 4096, 12288, np.float32),    # stream kernel: one 2-x-row launch
-    (9, 12288, 4096, np.float32),    # stream kernel: 4 + 4 + 1 x rows
+    (9, 12288, 4096, np.float32),    # the MFMA GEMM, 9 live rows of a 64-row tile
 ])
 def test_gemv_many_row_groups(env, M, N, K, xdt):
     """Large N: every persistent wave walks many row groups; every output must

@@ -4,8 +4,10 @@
 Headline (BASELINE.json metric, config 2): greedy int8 decode tok/s of a
 Qwen3-0.6B-shaped decoder (28 layers, hidden 1024, 16/8 heads, head_dim 128,
 SwiGLU 3072, vocab 151936, int8 lm_head), batch 1. A "step" is one whole
-config-2 generation: reset to a 128-token random prompt, run the prompt
-positions, then 256 greedy tokens. `--steps K` times K generations after
+config-2 generation: reset to a 128-token random prompt, run the prompt's
+first 127 positions as one batch (pio_qwen3_prefill: every int8 linear once
+over all 127 rows on the W8 MFMA GEMM), then 256 greedy tokens (the first of
+them consumes the last prompt position). `--steps K` times K generations after
 `--warmup W` untimed ones, bracketed by device synchronization; HIP events on
 the decoder's stream split each generation into prefill and decode, and
 `value` = generated tokens / decode time (so every step decodes at the
@@ -60,6 +62,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA, TOP/s
+BF16_PEAK_TFLOPS = 2500.0       # MI355X dense bf16 / fp16 MFMA, TFLOP/s
 METRIC = "int8 GEMV % HBM peak; W8A8 GEMM % int8 MFMA peak; Qwen3-0.6B decode tok/s"
 
 
@@ -108,8 +111,9 @@ GEN_LEN = 256        # ... then 256 greedy tokens
 
 def bench_decode(torch, args):
     """BASELINE config 2, as stated: every step is one whole generation --
-    reset to a 128-token prompt, the prompt positions, then 256 greedy tokens
-    -- so each timed step decodes at mean context 255.5 whatever --steps is.
+    reset to a 128-token prompt, the prompt's first 127 positions as one batch
+    (prefill), then 256 greedy tokens -- so each timed step decodes at mean
+    context 255.5 whatever --steps is.
     HIP events on the decoder's stream split each generation into prefill and
     decode; `value` is generated tokens / decode time."""
     import numpy as np
@@ -131,7 +135,7 @@ def bench_decode(torch, args):
         dec.reset(prompt)                 # host-synchronous upload of the prompt
         e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
         e[0].record(st)
-        dec.run(P - 1, mode=mode)
+        dec.prefill(P - 1)
         e[1].record(st)
         dec.run(NG, mode=mode)
         e[2].record(st)
@@ -272,6 +276,26 @@ def bench_kernels(torch, timer):
     out["c1_gemv"] = {"us": t * 1e6, "GBs": b / t / 1e9, "hbm_frac": b / t / 1e9 / HBM_PEAK_GBS,
                       "bytes": b}
     del Ws, ss
+
+    # The C1 linear over many fp32 rows (the prefill and large-M W8 path,
+    # pio_gemv_w8 above 4 rows): the W8 MFMA GEMM, fp32 x as three exact bf16
+    # parts. Algorithmic work 2MNK; the matrix cores run 3x that in bf16.
+    many = {}
+    for M in (128, 2048):
+        N, K = 3072, 1024
+        W = torch.randint(-127, 127, (N, K), dtype=torch.int8, device=dev)
+        sw = torch.rand((N,), device=dev) * 0.019 + 0.001
+        xm = torch.randn((M, K), device=dev)
+        ym = torch.empty((M, N), device=dev)
+        reps = 10
+        t = timer.time_graph(timer.graph(lambda s: ops.gemv_w8(xm, W, sw, None, ym, M, N, K, s), reps)) / reps
+        fl = 2.0 * M * N * K
+        many[f"M{M}_N{N}_K{K}_f32"] = {
+            "us": t * 1e6, "TFLOPs": fl / t / 1e12, "bf16_mfma_TFLOPs": 3 * fl / t / 1e12,
+            "bf16_mfma_frac": 3 * fl / t / 1e12 / BF16_PEAK_TFLOPS,
+            "weight_reads_GBs": (N * K + 4 * N) / t / 1e9}
+        del W, xm, ym
+    out["w8_linear_many_rows"] = many
 
     # C3: per-token quant + W8A8 GEMM, M=2048, fp16 in/out.
     c3 = {}
@@ -470,6 +494,17 @@ def cpu_kernel_baselines():
                       "int8_matmul_us": t_i8 * 1e6,
                       "sample": f"full C1: tensor_linear fp32 [1,1024]x[3072,1024]^T median of {n1}; "
                                 f"int8 leg tensor_matmul_int8 [1,1024]x[1024,3072] + epilogue, median of {n2}"}
+    # The same linear over many rows: tensor_linear parallelizes over rows
+    # (tensor_ops.c:306), so here the host's OpenMP threads all work.
+    Ms = 64
+    txm, tym = RT((Ms, K), rng.standard_normal((Ms, K), dtype=np.float32)), RT((Ms, N))
+    t_m, n3 = _median_time(lambda: L.tensor_linear(txm.h, tw.h, None, tym.h))
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    out["w8_linear_many_rows"] = {
+        f"M{M}_N{N}_K{K}_f32": {"us": t_m * M / Ms * 1e6, "kind": "reference", "cores": min(Ms, threads),
+                                "sample": f"tensor_linear fp32 [{Ms},1024]x[3072,1024]^T (median of {n3}), "
+                                          f"scaled x{M / Ms:g}"}
+        for M in (128, 2048)}
     del tw
 
     # C3: M=2048 rows; an 8-row sample of the int8 matmul (time is linear in M).
@@ -838,7 +873,7 @@ def main():
             for key, leg in legs.items():
                 if key not in kern:
                     continue
-                if key in ("c3_w8a8", "c4_skinny"):
+                if key in ("c3_w8a8", "c4_skinny", "w8_linear_many_rows"):
                     for sub, v in leg.items():
                         for tgt in (sub, f"gemv_{sub}", f"w8a8_{sub}"):
                             if tgt in kern[key]:

@@ -369,6 +369,15 @@ int pio_qwen3_reset(void* dec, const int32_t* ids, int prompt_len);
 #define PIO_DECODE_GRAPH 1
 #define PIO_DECODE_PERSISTENT 2
 int pio_qwen3_run(void* dec, int n_steps, int mode);
+/* Batched prompt: runs the next n_steps positions, all of them prompt
+ * positions (position + n_steps <= prompt_len), in one pass per layer -- each
+ * int8 linear once over all n_steps rows on the matrix cores, causal
+ * attention, RoPE and KV-cache rows for every position -- as the reference
+ * forwards the whole prompt at its first step (architecture.py:204-213);
+ * the step modes then continue from the cache and position it leaves. With
+ * logits != 0 the last position's logits (and, at the prompt's end, the next
+ * id) are produced as its step would produce them. */
+int pio_qwen3_prefill(void* dec, int n_steps, int logits);
 /* 1 if the persistent mode supports this decoder's config on the current
  * device, else 0 (the reason is in tensor_last_error). No counterpart in the
  * reference. */

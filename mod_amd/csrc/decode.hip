@@ -561,11 +561,21 @@ static int enqueue_step(Qwen3Dec* d) {
         g.x = d->act; g.W = L.w_down; g.s_w = L.s_down; g.N = H; g.K = I; g.y = d->x;
         PIO_TRY((launch_dec_gemv<EPI_RESID, 1>(g, ceil_div(g.N, 4), st)));
     }
-    DecGemv g = base;
+    return enqueue_lm(d);
+}
+
+// The step's tail: logits = W8_lm_head(rmsnorm(x) * w_final), the argmax, and
+// finish (ids[pos + 1] unless still inside the prompt, pos += 1).
+int enqueue_lm(Qwen3Dec* d) {
+    const pio_qwen3_config& c = d->c;
+    DecGemv g{};
+    g.eps = c.rms_eps;
+    g.state = d->state;
+    g.max_seq = c.max_seq;
     g.x = d->x; g.norm_w = d->final_norm; g.W = d->lm_head; g.s_w = d->s_lm; g.N = c.vocab;
-    g.K = H; g.y = d->logits; g.part_keys = d->part_keys;
-    PIO_TRY((launch_dec_gemv<EPI_LOGITS, 4>(g, d->lm_blocks, st)));
-    dec_finish_kernel<<<1, 1024, 0, st>>>(d->state, d->part_keys, d->lm_blocks, d->ids, c.max_seq);
+    g.K = c.hidden; g.y = d->logits; g.part_keys = d->part_keys;
+    PIO_TRY((launch_dec_gemv<EPI_LOGITS, 4>(g, d->lm_blocks, d->st)));
+    dec_finish_kernel<<<1, 1024, 0, d->st>>>(d->state, d->part_keys, d->lm_blocks, d->ids, c.max_seq);
     PIO_LAUNCHED();
     return PIO_OK;
 }
@@ -794,6 +804,17 @@ PIO_EXPORT int pio_qwen3_run(void* h, int n_steps, int mode) {
     // queued before must have run (or been re-run) first
     if (loop_pending(d)) PIO_TRY(settle(d));
     return run_stepwise(d, n_steps, mode == PIO_DECODE_GRAPH);
+}
+
+PIO_EXPORT int pio_qwen3_prefill(void* h, int n_steps, int logits) {
+    Qwen3Dec* d = (Qwen3Dec*)h;
+    PIO_REQUIRE(d, "pio_qwen3_prefill: null handle");
+    PIO_REQUIRE(n_steps >= 1 && d->host_pos + n_steps <= d->c.max_seq,
+                "pio_qwen3_prefill: %d more positions exceed max_seq %d (at %d)", n_steps, d->c.max_seq,
+                d->host_pos);
+    // the batch continues from the device position and cache
+    if (loop_pending(d)) PIO_TRY(settle(d));
+    return prefill(d, n_steps, logits != 0);
 }
 
 PIO_EXPORT int pio_qwen3_persistent_replays(void* h) {

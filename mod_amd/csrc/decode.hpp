@@ -51,4 +51,13 @@ int loop_replays(const Qwen3Dec* d);
 bool loop_pending(const Qwen3Dec* d);   // persistent launches not yet checked
 void loop_destroy(Qwen3Dec* d);
 
+// The step kernels' tail (decode.hip): lm_head on the decoder's x with the
+// final RMSNorm, argmax, then ids[pos + 1] (past the prompt) and pos += 1.
+int enqueue_lm(Qwen3Dec* d);
+
+// Batched prompt (prefill.hip): the next M positions (all prompt positions) in
+// one pass per layer; with `logits`, the last one's logits and argmax as its
+// step would produce them. Advances the position by M.
+int prefill(Qwen3Dec* d, int M, bool logits);
+
 }  // namespace pio

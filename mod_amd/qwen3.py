@@ -298,6 +298,12 @@ class Qwen3Int8Decoder:
         """Whether the "persistent" mode runs this config on this device."""
         return bool(lib.pio_qwen3_persistent_supported(self._h))
 
+    def prefill(self, n_steps: int, logits: bool = False) -> None:
+        """The next n_steps prompt positions in one batched pass (the int8
+        linears over all rows at once on the matrix cores); with logits, the
+        last position's logits and next id as its step would give them."""
+        check(lib.pio_qwen3_prefill(self._h, n_steps, int(logits)), "pio_qwen3_prefill")
+
     def persistent_replays(self) -> int:
         """Persistent launches re-run in graph mode because the device could
         not hold their whole grid at once (other work held CUs)."""

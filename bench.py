@@ -253,6 +253,81 @@ def bench_decode_gemv(torch, timer, cfg, dec):
     }
 
 
+TL_SLOTS = ["layer start", "P1 cross-XCD reduction", "P2 gather", "q/k/v stored", "attention stored",
+            "merged", "o_proj partial stored", "P5 cross-XCD reduction", "P6 gather", "act stored",
+            "down partial stored"]
+
+
+def decode_timeline(torch):
+    """Per-phase timeline of the persistent decode at config 2: a generation
+    (batched prompt, then 256 tokens in one traced launch) whose steps 124 and
+    125 (context ~252, the generation's mean) are stamped at every phase
+    boundary by every workgroup. Durations are medians over workgroups and
+    layers 1 .. L-2 of step 124; a phase's time runs from the previous
+    boundary, so it includes waiting for its input."""
+    import numpy as np
+    from mod_amd.qwen3 import Qwen3Config, Qwen3Int8Decoder, random_weights
+    P, NG, T0 = PROMPT_LEN, GEN_LEN, 124
+    cfg = Qwen3Config(max_seq=P + NG)
+    w = random_weights(cfg, seed=0)
+    dec = Qwen3Int8Decoder(cfg, w)
+    if not dec.persistent_supported():
+        return {"error": "persistent decode unsupported here"}
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab, size=P).astype(np.int32)
+    for traced in (False, True):
+        dec.reset(prompt)
+        dec.prefill(P - 1)
+        if traced:
+            dec.trace_next(T0)
+        dec.run(NG, mode="persistent")
+    ids = dec.read(P + NG)
+    A = dec.phase_trace()[0]                   # step T0: [256][L + 1][16], ns
+    L = cfg.n_layers
+    mid = A[:, 1:L - 1, :]
+    att = (np.arange(256) // 8) < 8            # roles j * 8 + g with j < 8 run attention
+    out = {"step": T0, "context": P - 1 + T0 + 1, "first_ids": ids[P:P + 4].tolist(), "phases_us": {}}
+
+    def med(a):
+        a = a[np.isfinite(a)]
+        return round(float(np.median(a)) / 1e3, 3) if a.size else None
+
+    prev = 0
+    for k in range(1, 11):
+        src = 3 if k == 5 else prev        # "merged" counts from the q/k/v store on every workgroup
+        rows = att if k == 4 else slice(None)
+        out["phases_us"][f"{TL_SLOTS[src]} -> {TL_SLOTS[k]}"] = med(mid[rows, :, k] - mid[rows, :, src])
+        prev = k if k != 4 else 3
+    out["phases_us"]["attention wgs: q/k/v stored -> merged"] = med(mid[att, :, 5] - mid[att, :, 3])
+    out["subphases_us"] = {
+        "P2 gather -> q/k/v weight lines landed": med(mid[:, :, 11] - mid[:, :, 2]),
+        "weight lines landed -> q/k/v stored": med(mid[:, :, 3] - mid[:, :, 11]),
+        "attention wgs: q/k/v stored -> q arrived": med(mid[att, :, 12] - mid[att, :, 3]),
+        "attention wgs: q arrived -> computed": med(mid[att, :, 13] - mid[att, :, 12]),
+        "attention wgs: computed -> stored (waves combined)": med(mid[att, :, 4] - mid[att, :, 13]),
+        "attention wgs: stored -> merge inputs arrived": med(mid[att, :, 14] - mid[att, :, 4]),
+        "other wgs: q/k/v stored -> merge inputs arrived": med(mid[~att, :, 14] - mid[~att, :, 3]),
+        "merge inputs arrived -> merged": med(mid[:, :, 5] - mid[:, :, 14]),
+    }
+    starts = np.nanmedian(A[:, :L, 0], axis=0)
+    out["layer_period_us"] = round(float(np.median(np.diff(starts[1:L - 1]))) / 1e3, 3)
+    lm = A[:, L, :]
+    out["lm_us"] = {"start -> reduced": med(lm[:, 1] - lm[:, 0]), "reduced -> gathered": med(lm[:, 2] - lm[:, 1]),
+                    "gathered -> lm_head rows done": med(lm[:, 3] - lm[:, 2]),
+                    "rows done -> key stored": med(lm[:, 4] - lm[:, 3])}
+    B = dec.phase_trace()[1]
+    out["token_period_us"] = round(float(np.nanmedian(B[:, 0, 0]) - np.nanmedian(A[:, 0, 0])) / 1e3, 3)
+    out["layers_us"] = round(float(starts[L - 1] - starts[0]) / (L - 1) / 1e3, 3)
+    # skew: spread of each boundary over the 256 workgroups (median over layers)
+    out["boundary_spread_us"] = {TL_SLOTS[k]: med(np.nanmax(mid[:, :, k], axis=0) - np.nanmin(mid[:, :, k], axis=0))
+                                 for k in range(11) if k != 4}
+    for k, v in list(out["phases_us"].items()) + list(out["subphases_us"].items()):
+        log(f"[timeline] {k:55s} {v} us")
+    log(f"[timeline] layer period {out['layer_period_us']} us, token period {out['token_period_us']} us, "
+        f"lm {out['lm_us']}")
+    dec.close()
+    return out
+
+
 # ----------------------------------------------------------------- kernels
 def bench_kernels(torch, timer):
     from mod_amd import ops
@@ -777,6 +852,10 @@ def main():
                     help="only run 10 plain (ungraphed) W8 GEMV launches per shape (fp32 x and y, "
                          "or fp16 with ':f16'), each on its own weight copy, then exit -- the "
                          "command the GEMV traffic counter passes profile")
+    ap.add_argument("--decode-timeline", action="store_true",
+                    help="only run the config-2 generation with one traced persistent launch and print "
+                         "the per-phase timeline of two mid-generation tokens (the kernel's traced "
+                         "build stamps every phase boundary of every workgroup)")
     ap.add_argument("--weights", action="store_true",
                     help="only time checkpoint loading (config-2 decoder weights, int8 and BF16 "
                          "safetensors from the page cache into HBM) and print its own JSON line")
@@ -826,6 +905,9 @@ def main():
                 ops.gemv_w8(x, Ws[i % 2], sw, None, y, M, N, K)
             torch.cuda.synchronize()
             print(f"done {spec}", flush=True)
+        return 0
+    if args.decode_timeline:
+        print(json.dumps(decode_timeline(torch)))
         return 0
     if args.weights:
         r = bench_weights(torch)

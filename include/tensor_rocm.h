@@ -382,6 +382,22 @@ int pio_qwen3_prefill(void* dec, int n_steps, int logits);
  * device, else 0 (the reason is in tensor_last_error). No counterpart in the
  * reference. */
 int pio_qwen3_persistent_supported(void* dec);
+/* Phase timeline of the persistent decode (measurement; no counterpart in the
+ * reference). pio_qwen3_trace_next makes the next persistent launch of this
+ * decoder run the kernel's traced build, which stamps the 100 MHz constant
+ * clock at every phase boundary of that launch's steps first_step and
+ * first_step + 1 (wave 0 of each workgroup); pio_qwen3_trace_read waits for
+ * the stream and copies the stamps out: uint64 [2][256 workgroups]
+ * [n_layers + 1][16] (pio_qwen3_trace_bytes bytes; 0 = not reached). Slots
+ * per layer: 0 start, 1 cross-XCD reduction, 2 gather, 3 q/k/v stored,
+ * 4 attention stored, 5 merged, 6 o_proj partial, 7 reduction, 8 gather,
+ * 9 act stored, 10 down partial, 11 q/k/v weight lines landed, 12 the
+ * attention's q arrived, 13 attention computed, 14 merge inputs arrived;
+ * layer n_layers: 0 start, 1 reduction, 2 gather, 3 lm_head rows, 4 argmax
+ * key stored. */
+int pio_qwen3_trace_next(void* dec, int first_step);
+size_t pio_qwen3_trace_bytes(void* dec);
+int pio_qwen3_trace_read(void* dec, void* out, size_t bytes);
 /* Persistent launches of this decoder that were re-run in graph mode because
  * the device could not hold their grid at once. No counterpart in the
  * reference. */

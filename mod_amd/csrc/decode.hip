@@ -817,6 +817,20 @@ PIO_EXPORT int pio_qwen3_prefill(void* h, int n_steps, int logits) {
     return prefill(d, n_steps, logits != 0);
 }
 
+PIO_EXPORT int pio_qwen3_trace_next(void* h, int first_step) {
+    Qwen3Dec* d = (Qwen3Dec*)h;
+    PIO_REQUIRE(d && first_step >= 0, "pio_qwen3_trace_next: null handle or negative step");
+    return loop_trace_next(d, first_step);
+}
+
+PIO_EXPORT size_t pio_qwen3_trace_bytes(void* h) { return h ? loop_trace_bytes((Qwen3Dec*)h) : 0; }
+
+PIO_EXPORT int pio_qwen3_trace_read(void* h, void* out, size_t bytes) {
+    Qwen3Dec* d = (Qwen3Dec*)h;
+    PIO_REQUIRE(d && out, "pio_qwen3_trace_read: null argument");
+    return loop_trace_read(d, out, bytes);
+}
+
 PIO_EXPORT int pio_qwen3_persistent_replays(void* h) {
     Qwen3Dec* d = (Qwen3Dec*)h;
     PIO_REQUIRE(d, "pio_qwen3_persistent_replays: null handle");

@@ -49,6 +49,11 @@ constexpr int LOOP_REPLAY = 1;
 int loop_status(Qwen3Dec* d, int* replay_pos);
 int loop_replays(const Qwen3Dec* d);
 bool loop_pending(const Qwen3Dec* d);   // persistent launches not yet checked
+// Phase timeline: the next persistent launch runs the traced kernel and stamps
+// steps first_step, first_step + 1 of it (u64 [2][256][n_layers + 1][12]).
+size_t loop_trace_bytes(const Qwen3Dec* d);
+int loop_trace_next(Qwen3Dec* d, int first_step);
+int loop_trace_read(Qwen3Dec* d, void* out, size_t bytes);
 void loop_destroy(Qwen3Dec* d);
 
 // The step kernels' tail (decode.hip): lm_head on the decoder's x with the

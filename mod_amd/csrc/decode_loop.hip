@@ -101,7 +101,7 @@ constexpr int LP_NPMAX = 8;                // attention passes (8 positions each
 constexpr int LP_MAX_SEQ = LP_S * LP_CW * 8 * LP_NPMAX;   // 2048
 constexpr int LP_PART = 2 + LP_D;          // (max, sum, o[128]) per split and head
 static_assert(LP_S == 8, "the merge loads the partials of 8 splits in one batch");
-constexpr int LP_LM_B = 6;                 // lm_head rows per wave and batch (double-buffered)
+constexpr int LP_LM_B = 6;                 // lm_head rows per wave and batch (three batches in flight)
 constexpr int LP_LMAX = 48;                // layers whose per-wave constants LDS holds
 constexpr int LP_NCST = 32;                // constants per layer and compute wave (30 used)
 constexpr int LP_PH = 7;                   // tagged phases per layer
@@ -162,7 +162,22 @@ struct LoopParams {
     uint32_t epoch0;
     uint64_t arrive_ticks;     // co-residency wait at launch (LP_ARRIVE_TICKS)
     int* err;                  // error words (see LP_E_*)
+    u64* trace;                // traced launches: phase stamps (see lp_stamp)
+    int tr_t0;                 // the first traced step of the launch
 };
+
+// Phase timeline of a traced launch (the kernel's TR instantiation): wave 0 of
+// every workgroup stamps the 100 MHz constant clock at each phase boundary of
+// LP_TR_TOK consecutive steps, trace[step][role][layer][slot]; layer L holds
+// the last layer's reduction, the gather, the lm_head rows and the key store.
+// Slots: 0 layer start, 1 P1 reduced, 2 P2 gathered, 3 q/k/v stored,
+// 4 attention stored (its workgroups only), 5 merged, 6 o_proj partial stored,
+// 7 P5 reduced, 8 P6 gathered, 9 act stored, 10 down partial stored; inside
+// phases: 11 q/k/v weight lines landed, 12 attention's q arrived, 13 attention
+// computed (before its workgroup combines the waves), 14 merge inputs
+// arrived; in layer L: 0 start, 1 reduced, 2 gathered, 3 lm rows done, 4 key
+// stored.
+constexpr int LP_TR_TOK = 2, LP_TR_K = 16;
 
 // LDS layout (dynamic): ring | per-wave x copies | merged head output |
 // per-wave act copies | attention partials | attention staging | per-layer
@@ -242,14 +257,6 @@ __device__ __forceinline__ void ld_l2_8s(const u64* p, u64 (&v)[8]) {
                  LP_LD(5, 2560) LP_LD(6, 3072) LP_LD(7, 3584) "s_waitcnt vmcnt(0)"
                  : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
                    "=&v"(v[6]), "=&v"(v[7])
-                 : [a] "v"(p)
-                 : "memory");
-}
-// 6 tagged words 64 words apart
-__device__ __forceinline__ void ld_l2_6s(const u64* p, u64 (&v)[6]) {
-    asm volatile(LP_LD(0, 0) LP_LD(1, 512) LP_LD(2, 1024) LP_LD(3, 1536) LP_LD(4, 2048)
-                 LP_LD(5, 2560) "s_waitcnt vmcnt(0)"
-                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5])
                  : [a] "v"(p)
                  : "memory");
 }
@@ -418,6 +425,7 @@ struct Cx {
     int lane, w, nsync, fail_where;
     uint64_t wt0;    // s_memrealtime at the current wait's first check
     int g, j, role;  // XCD, slot within it, role index j * 8 + g
+    int tt, tl;      // current step and layer (for the traced build's stamps)
     int uv0, nuv;    // lm_head rows of this workgroup
     int* ready;      // [LP_SW] lines landed per stream wave
     int* done;       // [LP_CW] first line each compute wave may still need
@@ -434,6 +442,21 @@ struct Cx {
     float* xs;       // [2][H] the workgroup's copies of x'' (0) and x' (1)
     u64* wkeys;      // [LP_CW]
 };
+
+template <bool TR>
+__device__ __forceinline__ void lp_stamp(const LoopParams& p, const Cx& c, int t, int l, int k) {
+    if constexpr (TR) {
+        const int tt = t - p.tr_t0;
+        if (c.w == 0 && c.lane == 0 && tt >= 0 && tt < LP_TR_TOK)
+            p.trace[(((int64_t)tt * LP_NBLK + c.role) * (p.L + 1) + l) * LP_TR_K + k] = wall_clock64();
+    }
+}
+
+// A stamp inside a phase, at the step and layer compute_role is in.
+template <bool TR>
+__device__ __forceinline__ void lp_stamp_in(const LoopParams& p, const Cx& c, int k) {
+    lp_stamp<TR>(p, c, c.tt, c.tl, k);
+}
 
 // Records a timed-out wait (site `where`) and tells every workgroup to stop.
 __device__ void lp_fail(const LoopParams& p, int code, int where) {
@@ -703,10 +726,11 @@ __device__ __forceinline__ Pre pre_qkv(const Cx& c, int l, float rcs, float rsn)
 
 // qkv (P2): this wave's 2 units, from ring lines line0 + 2 (w + 4 m) + r.
 // KT = the KV cache element type.
-template <typename KT>
+template <typename KT, bool TR>
 __device__ bool phase_qkv(const LoopParams& p, Cx& c, int l, int pos, int line0, uint32_t tag,
                           const float (&xv)[16], float nscale, const Pre& pre) {
     if (!wait_upto(p, c, line0 + 2 * (c.w + LP_CW) + 1, 10)) return false;
+    lp_stamp_in<TR>(p, c, 11);
     lp_v4i wv[2][2];
 #pragma unroll
     for (int m = 0; m < 2; m++)
@@ -932,7 +956,7 @@ __device__ __forceinline__ void kv_widen(const KvRaw<_Float16>& r, float (&kk)[1
 // position's k/v (this step's, from the tagged copy) is one extra pass with
 // slot 0 only. The waves' partials go to LDS and one pass over them combines
 // the four waves; the split's (max, sum, o) is stored tagged.
-template <typename KT>
+template <typename KT, bool TR>
 __device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t qtag, uint32_t tag) {
     constexpr int G = LP_G;
     // fp16 rows are paired (kv_put2): lane l's two value slots are dims l, l + 64
@@ -983,6 +1007,7 @@ __device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t q
             if (!keep_waiting(p, c, it, 20)) return false;
         }
     }
+    lp_stamp_in<TR>(p, c, 12);
     cbar();
     float qv[G][16];
 #pragma unroll
@@ -1074,6 +1099,7 @@ __device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t q
             c.attm[LP_CW * G + c.w * G + h] = lsum[h];
         }
     }
+    lp_stamp_in<TR>(p, c, 13);
     if (!csync(p, c, 22)) return false;
     // combine: one (head, dim) per thread of the four waves; partial layout
     // att[g][h][split][max, sum, o[128]]
@@ -1103,6 +1129,7 @@ __device__ bool phase_att(const LoopParams& p, Cx& c, int l, int pos, uint32_t q
 // Merge (start of P4) of the active splits of KV head g's query heads into the
 // head output o_g [2][128] in LDS: wave w merges head w >> 1, dims
 // 64 (w & 1) + lane, in split order; then the four waves meet.
+template <bool TR>
 __device__ bool merge_heads(const LoopParams& p, Cx& c, int pos, uint32_t ptag) {
     const int hh = c.w >> 1, d = 64 * (c.w & 1) + c.lane;
     const int Lc = pos + 1, cs = (Lc + LP_S - 1) / LP_S, sact = (Lc + cs - 1) / cs;
@@ -1124,6 +1151,7 @@ __device__ bool merge_heads(const LoopParams& p, Cx& c, int pos, uint32_t ptag) 
         if (__all(ok)) break;
         if (!keep_waiting(p, c, it, 30)) return false;
     }
+    lp_stamp_in<TR>(p, c, 14);
     float M = -INFINITY;
 #pragma unroll
     for (int s = 0; s < LP_S; s++)
@@ -1187,8 +1215,8 @@ __device__ __forceinline__ void lm_batch(int k0, int nk, int sbase, float sv, fl
 
 // lm_head: the one phase that is pure streaming (155 MB at the Qwen3-0.6B
 // shape) and waits on no other workgroup, so the compute waves read its rows
-// straight from HBM into registers, LP_LM_B rows per batch, double-buffered
-// (the next batch's loads are in flight while the current one is reduced).
+// straight from HBM into registers, LP_LM_B rows per batch, three batches in
+// flight (the next two batches' loads are in flight while one is reduced).
 // This wave's rows: uv0 + w + 4k. Out of line, so that its registers are its
 // own; x comes from the staged LDS copy. Writes the wave's argmax key.
 template <int C>
@@ -1209,24 +1237,33 @@ __device__ __noinline__ void phase_lm(const int8_t* lm, const float* s_lm, float
     int besti = 0;
     int sbase = 0;
     float sv = w + LP_CW * lane < nuv ? *(glb_f32*)(s_lm + row0 + LP_CW * lane) : 0.f;
-    lp_v4i wa[LP_LM_B][C], wb[LP_LM_B][C];
+    // three batches in flight: 18 KB per wave, 72 KB per CU (with two, the
+    // CU's 48 KB in flight covered too little of the HBM latency under load)
+    constexpr int B = LP_LM_B;
+    lp_v4i wa[B][C], wb[B][C], wc[B][C];
     if (nk > 0) lm_load<C>(lm, H, uv0, nuv, w, lane, 0, wa);
-    for (int k0 = 0; k0 < nk; k0 += 2 * LP_LM_B) {
-        if (k0 - sbase > 64 - 2 * LP_LM_B) {
+    if (nk > B) lm_load<C>(lm, H, uv0, nuv, w, lane, B, wb);
+    for (int k0 = 0; k0 < nk; k0 += 3 * B) {
+        if (k0 - sbase > 64 - 3 * B) {
             sbase = k0;
             const int ub = w + LP_CW * (k0 + lane);
             sv = ub < nuv ? *(glb_f32*)(s_lm + uv0 + ub) : 0.f;
         }
         // sched_barrier: keep each batch's conversions next to its FMAs (the
-        // scheduler would otherwise convert the in-flight batch too, and spill)
-        if (k0 + LP_LM_B < nk) lm_load<C>(lm, H, uv0, nuv, w, lane, k0 + LP_LM_B, wb);
+        // scheduler would otherwise convert the batches in flight too, and spill)
+        if (k0 + 2 * B < nk) lm_load<C>(lm, H, uv0, nuv, w, lane, k0 + 2 * B, wc);
         __builtin_amdgcn_sched_barrier(0);
         lm_batch<C>(k0, nk, sbase, sv, nscale, logits, row0, lane, xr, xoff, wa, bestv, besti);
         __builtin_amdgcn_sched_barrier(0);
-        if (k0 + LP_LM_B >= nk) break;
-        if (k0 + 2 * LP_LM_B < nk) lm_load<C>(lm, H, uv0, nuv, w, lane, k0 + 2 * LP_LM_B, wa);
+        if (k0 + B >= nk) break;
+        if (k0 + 3 * B < nk) lm_load<C>(lm, H, uv0, nuv, w, lane, k0 + 3 * B, wa);
         __builtin_amdgcn_sched_barrier(0);
-        lm_batch<C>(k0 + LP_LM_B, nk, sbase, sv, nscale, logits, row0, lane, xr, xoff, wb, bestv, besti);
+        lm_batch<C>(k0 + B, nk, sbase, sv, nscale, logits, row0, lane, xr, xoff, wb, bestv, besti);
+        __builtin_amdgcn_sched_barrier(0);
+        if (k0 + 2 * B >= nk) break;
+        if (k0 + 4 * B < nk) lm_load<C>(lm, H, uv0, nuv, w, lane, k0 + 4 * B, wb);
+        __builtin_amdgcn_sched_barrier(0);
+        lm_batch<C>(k0 + 2 * B, nk, sbase, sv, nscale, logits, row0, lane, xr, xoff, wc, bestv, besti);
         __builtin_amdgcn_sched_barrier(0);
     }
     if (lane == 0) *wkey = nk > 0 ? lp_key(bestv, besti, tag) : 0;
@@ -1315,7 +1352,7 @@ __device__ __forceinline__ void gld16(const float* src, float (&d)[16]) {
     }
 }
 
-template <typename KT>
+template <typename KT, bool TR>
 __device__ void compute_role(const LoopParams& p, Cx& c) {
     __builtin_amdgcn_s_setprio(2);
     load_constants(p, c);
@@ -1347,6 +1384,8 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
             // hoisting every per-lane address of the loop body out of the loop
             // (they would stay live across all phases and spill).
             asm volatile("" : "+v"(c.lane));
+            c.tt = t;
+            c.tl = l;
             const LoopLayer& Lw = p.layers[l];
             const int lb = Gl + l * LP_LPL;
             // ---- P1 + P2: x'' (embedding row or reduced), RMSNorm, q/k/v of head g
@@ -1356,11 +1395,13 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
                 // the norm weights (L2 hits after the first workgroup of the
                 // XCD) before the reduction, the scales from LDS.
                 cbar();   // nothing may move above the previous phase
+                lp_stamp<TR>(p, c, t, l, 0);
                 float gam[16], xv[16], nscale;
                 gld16(Lw.in_norm + 16 * c.lane, gam);
                 if (l > 0 && !reduce_x(p, c, p.dpart, tag_of(p, t, l - 1, PH_DP), p.xr, tag_of(p, t, l, PH_XR),
                                        c.xs + LP_H, 1))
                     return;
+                lp_stamp<TR>(p, c, t, l, 1);
                 cbar();
                 const Pre pq = pre_qkv(c, l, rcs, rsn);
                 if (l == 0) {
@@ -1380,18 +1421,23 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
                 } else {
                     if (!gather_x(p, c, p.xr, tag_of(p, t, l, PH_XR), gam, xv, nscale, c.xs, 2)) return;
                 }
-                if (!phase_qkv<KT>(p, c, l, pos, lb, tag_of(p, t, l, PH_QKV), xv, nscale, pq)) return;
+                lp_stamp<TR>(p, c, t, l, 2);
+                if (!phase_qkv<KT, TR>(p, c, l, pos, lb, tag_of(p, t, l, PH_QKV), xv, nscale, pq)) return;
+                lp_stamp<TR>(p, c, t, l, 3);
                 set_done(c, lb + LP_OFF_O);
             }
             // ---- P3: attention partials of head g's splits
-            if (att_blk && !phase_att<KT>(p, c, l, pos, tag_of(p, t, l, PH_QKV), tag_of(p, t, l, PH_ATT)))
+            if (att_blk && !phase_att<KT, TR>(p, c, l, pos, tag_of(p, t, l, PH_QKV), tag_of(p, t, l, PH_ATT)))
                 return;
+            if (att_blk) lp_stamp<TR>(p, c, t, l, 4);
             // ---- P4: merge, o_proj partial over head g's columns
             {
                 const float* lk = layer_cst(c, l) + 14 + (c.lane >> 4);
                 const float so[2] = {lk[0], lk[4]};
-                if (!merge_heads(p, c, pos, tag_of(p, t, l, PH_ATT))) return;
+                if (!merge_heads<TR>(p, c, pos, tag_of(p, t, l, PH_ATT))) return;
+                lp_stamp<TR>(p, c, t, l, 5);
                 if (!phase_opart(p, c, lb + LP_OFF_O, tag_of(p, t, l, PH_OP), so)) return;
+                lp_stamp<TR>(p, c, t, l, 6);
                 set_done(c, lb + LP_OFF_GU);
             }
             // ---- P5 + P6: x' (reduced), RMSNorm, gate_up + SwiGLU for XCD g's channels
@@ -1402,8 +1448,11 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
                 gld16(Lw.post_norm + 16 * c.lane, gam);
                 if (!reduce_x(p, c, p.opart, tag_of(p, t, l, PH_OP), p.xr2, tag_of(p, t, l, PH_XR2), c.xs, 3))
                     return;
+                lp_stamp<TR>(p, c, t, l, 7);
                 if (!gather_x(p, c, p.xr2, tag_of(p, t, l, PH_XR2), gam, xv, nscale, c.xs + LP_H, 4)) return;
+                lp_stamp<TR>(p, c, t, l, 8);
                 if (!phase_gu(p, c, lb + LP_OFF_GU, tag_of(p, t, l, PH_ACT), xv, nscale, pg)) return;
+                lp_stamp<TR>(p, c, t, l, 9);
                 set_done(c, lb + LP_OFF_DN);
             }
             // ---- P7: down partial over XCD g's channels
@@ -1411,16 +1460,20 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
                 const float sd = layer_cst(c, l)[22 + (c.lane >> 3)];
                 if (!phase_dpart(p, c, lb + LP_OFF_DN, tag_of(p, t, l, PH_ACT), tag_of(p, t, l, PH_DP), sd))
                     return;
+                lp_stamp<TR>(p, c, t, l, 10);
                 set_done(c, lb + LP_LPL);
             }
         }
         if (lm) {
+            lp_stamp<TR>(p, c, t, p.L, 0);
             float gam[16], xv[16], nscale;
             gld16(p.final_norm + 16 * c.lane, gam);
             if (!reduce_x(p, c, p.dpart, tag_of(p, t, p.L - 1, PH_DP), p.xr, tag_of(p, t, p.L, PH_XR),
                           c.xs + LP_H, 9))
                 return;
+            lp_stamp<TR>(p, c, t, p.L, 1);
             if (!gather_x(p, c, p.xr, tag_of(p, t, p.L, PH_XR), gam, xv, nscale, c.xs, 11)) return;
+            lp_stamp<TR>(p, c, t, p.L, 2);
             // the lm phase reads gamma * x from the wave's LDS copy
             float* xw = c.xw + c.w * LP_H + 16 * c.lane;
 #pragma unroll
@@ -1430,6 +1483,7 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
             phase_lm<1>(p.lm_head, p.s_lm, t == p.n_steps - 1 ? p.logits : nullptr, LP_H, c.uv0, c.nuv,
                         c.w, c.lane, (const lds_f32*)(c.xw + c.w * LP_H), nscale, tl,
                         (lds_u64*)(c.wkeys + c.w));
+            lp_stamp<TR>(p, c, t, p.L, 3);
             if (!csync(p, c, 61)) return;
             if (c.w == 0 && c.lane == 0) {
                 u64 b = c.wkeys[0];
@@ -1437,6 +1491,7 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
                 b = (b & ~(u64)0x3FFF) | (u64)(tl & 0x3FFFu);
                 __hip_atomic_store(p.keys + c.role, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
+            lp_stamp<TR>(p, c, t, p.L, 4);
         }
         Gl += p.lpt;
     }
@@ -1455,7 +1510,7 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
     }
 }
 
-template <typename KT>
+template <typename KT, bool TR>
 __global__ __launch_bounds__(LP_THREADS, 1) void decode_loop_kernel(LoopParams p) {
     extern __shared__ __attribute__((aligned(16))) int8_t lp_lds[];
     __shared__ __attribute__((aligned(16))) int ready[LP_SW];
@@ -1520,6 +1575,7 @@ __global__ __launch_bounds__(LP_THREADS, 1) void decode_loop_kernel(LoopParams p
     c.nsync = 0;
     c.fail_where = 0;
     c.wt0 = 0;
+    c.tt = c.tl = 0;
     c.ready = ready;
     c.done = done;
     c.csync = &sync_ctr;
@@ -1537,7 +1593,7 @@ __global__ __launch_bounds__(LP_THREADS, 1) void decode_loop_kernel(LoopParams p
     if (c.w >= LP_CW) {
         stream_role(p, c);
     } else {
-        compute_role<KT>(p, c);
+        compute_role<KT, TR>(p, c);
         // a compute wave that leaves early must not hold the ring
         cbar();
         if (c.lane == 0) lds_st(&done[c.w], 0x7fffffff);
@@ -1558,14 +1614,16 @@ struct LoopState {
     uint32_t epoch = 1;
     bool ran = false;
     int replays = 0;    // launches re-run in graph mode (grid not co-resident)
+    int trace_t0 = -1;  // the next launch is traced from this step (-1: not traced)
+    u64* trace = nullptr;
 };
 
 // The kernel's dynamic LDS exceeds the 64 KB default limit.
 static int loop_lds_attr() {
-    PIO_HIP(hipFuncSetAttribute((const void*)decode_loop_kernel<float>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)LP_LDS_BYTES));
-    PIO_HIP(hipFuncSetAttribute((const void*)decode_loop_kernel<_Float16>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)LP_LDS_BYTES));
+    const void* k[] = {(const void*)decode_loop_kernel<float, false>, (const void*)decode_loop_kernel<_Float16, false>,
+                       (const void*)decode_loop_kernel<float, true>, (const void*)decode_loop_kernel<_Float16, true>};
+    for (const void* f : k)
+        PIO_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LP_LDS_BYTES));
     return PIO_OK;
 }
 
@@ -1576,10 +1634,10 @@ int loop_check(const Qwen3Dec* d) {
     PIO_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
     PIO_TRY(loop_lds_attr());
     if (d->kv16)
-        PIO_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_loop_kernel<_Float16>,
+        PIO_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_loop_kernel<_Float16, false>,
                                                              LP_THREADS, LP_LDS_BYTES));
     else
-        PIO_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_loop_kernel<float>,
+        PIO_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_loop_kernel<float, false>,
                                                              LP_THREADS, LP_LDS_BYTES));
     const bool ok = c.head_dim == LP_D && c.hidden == LP_H && c.n_heads * LP_D == LP_KO &&
                     c.n_kv_heads == LP_NX && c.intermediate == LP_I && cus == LP_NBLK &&
@@ -1702,6 +1760,7 @@ void loop_destroy(Qwen3Dec* d) {
     if (!d || !d->loop) return;
     if (d->loop->stream) device_free(d->loop->stream);
     if (d->loop->small) device_free(d->loop->small);
+    if (d->loop->trace) device_free(d->loop->trace);
     delete d->loop;
     d->loop = nullptr;
 }
@@ -1751,8 +1810,21 @@ int loop_run(Qwen3Dec* d, int n_steps) {
     if (const char* e = getenv("PIO_LOOP_ARRIVE_TICKS")) p.arrive_ticks = strtoull(e, nullptr, 10);
     p.err = s->err;
     PIO_TRY(loop_lds_attr());
-    if (d->kv16) decode_loop_kernel<_Float16><<<dim3(LP_NBLK), dim3(LP_THREADS), LP_LDS_BYTES, d->st>>>(p);
-    else decode_loop_kernel<float><<<dim3(LP_NBLK), dim3(LP_THREADS), LP_LDS_BYTES, d->st>>>(p);
+    const dim3 grid(LP_NBLK), block(LP_THREADS);
+    if (s->trace_t0 >= 0) {
+        // one traced launch: the phase stamps of steps trace_t0 .. + LP_TR_TOK
+        const size_t tb = loop_trace_bytes(d);
+        if (!s->trace) PIO_TRY(device_alloc((void**)&s->trace, tb, d->st));
+        PIO_HIP(hipMemsetAsync(s->trace, 0, tb, d->st));
+        p.trace = s->trace;
+        p.tr_t0 = s->trace_t0;
+        s->trace_t0 = -1;
+        if (d->kv16) decode_loop_kernel<_Float16, true><<<grid, block, LP_LDS_BYTES, d->st>>>(p);
+        else decode_loop_kernel<float, true><<<grid, block, LP_LDS_BYTES, d->st>>>(p);
+    } else {
+        if (d->kv16) decode_loop_kernel<_Float16, false><<<grid, block, LP_LDS_BYTES, d->st>>>(p);
+        else decode_loop_kernel<float, false><<<grid, block, LP_LDS_BYTES, d->st>>>(p);
+    }
     PIO_LAUNCHED();
     s->epoch += (uint32_t)n_steps * per_tok;
     s->ran = true;
@@ -1760,6 +1832,30 @@ int loop_run(Qwen3Dec* d, int n_steps) {
 }
 
 bool loop_pending(const Qwen3Dec* d) { return d->loop && d->loop->ran; }
+
+size_t loop_trace_bytes(const Qwen3Dec* d) {
+    return (size_t)LP_TR_TOK * LP_NBLK * (d->c.n_layers + 1) * LP_TR_K * sizeof(u64);
+}
+int loop_trace_next(Qwen3Dec* d, int first_step) {
+    PIO_TRY(loop_check(d));
+    if (!d->loop) {
+        const int rc = loop_build(d);
+        if (rc != PIO_OK) {
+            loop_destroy(d);
+            return rc;
+        }
+    }
+    d->loop->trace_t0 = first_step;
+    return PIO_OK;
+}
+int loop_trace_read(Qwen3Dec* d, void* out, size_t bytes) {
+    PIO_REQUIRE(d->loop && d->loop->trace, "pio_qwen3_trace_read: no traced launch has run");
+    PIO_REQUIRE(bytes == loop_trace_bytes(d), "pio_qwen3_trace_read: %zu bytes, the trace has %zu", bytes,
+                loop_trace_bytes(d));
+    PIO_HIP(hipStreamSynchronize(d->st));
+    PIO_HIP(hipMemcpy(out, d->loop->trace, bytes, hipMemcpyDeviceToHost));
+    return PIO_OK;
+}
 int loop_replays(const Qwen3Dec* d) { return d->loop ? d->loop->replays : 0; }
 
 // Error words of the persistent launches since the last call (after the

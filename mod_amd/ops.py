@@ -124,6 +124,9 @@ SIGNATURES: dict[str, tuple] = {
     "pio_qwen3_persistent_supported": (_i, [_vp]),
     "pio_qwen3_persistent_replays": (_i, [_vp]),
     "pio_qwen3_prefill": (_i, [_vp, _i, _i]),
+    "pio_qwen3_trace_next": (_i, [_vp, _i]),
+    "pio_qwen3_trace_bytes": (_sz, [_vp]),
+    "pio_qwen3_trace_read": (_i, [_vp, _vp, _sz]),
     "pio_qwen3_read": (_i, [_vp, _vp, _i, _vp]),
     "pio_qwen3_logits": (_vp, [_vp]),
     "open_safetensors": (_vp, [ctypes.c_char_p]),

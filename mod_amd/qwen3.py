@@ -304,6 +304,23 @@ class Qwen3Int8Decoder:
         last position's logits and next id as its step would give them."""
         check(lib.pio_qwen3_prefill(self._h, n_steps, int(logits)), "pio_qwen3_prefill")
 
+    def trace_next(self, first_step: int) -> None:
+        """The next persistent run is traced: phase stamps of its steps
+        first_step and first_step + 1 (see phase_trace)."""
+        check(lib.pio_qwen3_trace_next(self._h, first_step), "pio_qwen3_trace_next")
+
+    def phase_trace(self) -> np.ndarray:
+        """Stamps of the last traced run, in ns relative to the earliest
+        one: float64 [2 steps][256 workgroups][n_layers + 1][16 slots], NaN
+        where a slot was not reached (the slot meanings are in tensor_rocm.h)."""
+        nb = int(lib.pio_qwen3_trace_bytes(self._h))
+        raw = np.zeros(nb // 8, np.uint64)
+        check(lib.pio_qwen3_trace_read(self._h, raw.ctypes.data, nb), "pio_qwen3_trace_read")
+        raw = raw.reshape(2, 256, self.cfg.n_layers + 1, -1)
+        t = raw.astype(np.float64)
+        t[raw == 0] = np.nan
+        return (t - np.nanmin(t)) * 10.0   # 100 MHz ticks -> ns
+
     def persistent_replays(self) -> int:
         """Persistent launches re-run in graph mode because the device could
         not hold their whole grid at once (other work held CUs)."""

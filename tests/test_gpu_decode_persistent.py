@@ -266,3 +266,32 @@ def test_persistent_launch_without_the_whole_grid_reruns_in_graph_mode(torch_dev
     got2 = dec.read(len(prompt) + n_new)
     assert dec.persistent_replays() == 2
     assert np.mean(got2 == want) >= 0.9
+
+
+def test_persistent_traced_launch_stamps_every_phase(torch_dev):
+    """The traced build (pio_qwen3_trace_next) computes the same tokens as the
+    product kernel and stamps every phase boundary of the two traced steps on
+    every workgroup, in order."""
+    cfg, _ = _cfgs()
+    dec, _ = _decoder(cfg, seed=71)
+    prompt = np.random.default_rng(72).integers(0, cfg.vocab, size=5).astype(np.int32)
+    # traced steps at positions 64, 65: every attention split has positions
+    want = dec.generate(prompt, 80, mode="persistent")
+    dec.reset(prompt)
+    dec.run(len(prompt) - 1, mode="persistent")
+    dec.trace_next(60)
+    dec.run(80, mode="persistent")
+    assert np.array_equal(dec.read(len(prompt) + 80), want)
+    t = dec.phase_trace()                          # [2][256][L + 1][16] ns
+    L = cfg.n_layers
+    att = (np.arange(256) // 8) < 8
+    main = [0, 1, 2, 3, 5, 6, 7, 8, 9, 10]
+    for s in range(2):
+        blk = t[s, :, :L, :]
+        assert np.isfinite(blk[:, 1:, main]).all()                 # layer 0 has no P1 reduction
+        assert np.isfinite(blk[att][:, :, [4, 12, 13]]).all()
+        assert np.isnan(blk[~att][:, :, 4]).all()
+        order = blk[:, 1:, main]
+        assert (np.diff(order, axis=-1) >= 0).all()
+        assert np.isfinite(t[s, :, L, :5]).all()
+    assert np.nanmin(t[1]) > np.nanmax(t[0, :, :L, :11])

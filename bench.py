@@ -253,6 +253,43 @@ def bench_decode_gemv(torch, timer, cfg, dec):
     }
 
 
+def gemm_supply(torch):
+    """What bounds the C3 GEMM's K loop: the GEMM itself (fp16 out, graph of
+    10 launches over 8 rotating operand sets) beside the probe that issues only
+    its operand copies -- same 128 x 192 tiles, same XCD rectangles, two K steps
+    in flight, one barrier per step -- with K steps of 128 B per row (the
+    GEMM's), 256 B and 512 B. Per-CU supply = 320 rows x K bytes per block /
+    the launch time (one block per CU)."""
+    from mod_amd import ops
+    timer = Timer(torch)
+    out = {}
+    for (M, N, K) in [(2048, 3072, 1024), (2048, 3072, 3072)]:
+        sets = 8
+        A = torch.randint(-127, 127, (sets, M, K), dtype=torch.int8, device="cuda")
+        B = torch.randint(-127, 127, (sets, N, K), dtype=torch.int8, device="cuda")
+        sa = torch.rand((M,), device="cuda") * 0.01
+        sw = torch.rand((N,), device="cuda") * 0.01
+        y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+
+        def g(s):
+            for i in range(sets):
+                ops.gemm_w8a8(A[i], sa, B[i], sw, None, y, M, N, K, s)
+        tg = timer.time_graph(timer.graph(g, 1), replays=5) / sets
+        row = {"gemm_us": round(tg * 1e6, 2), "gemm_TOPS": round(2 * M * N * K / tg / 1e12, 1)}
+        for step in (128, 256, 512):
+            def f(s, step=step):
+                for i in range(sets):
+                    ops.check(ops.lib.pio_probe_gemm_supply(ops._ptr(A[i]), ops._ptr(B[i]), M, N, K, 128, 192,
+                                                            step, 1, s), "pio_probe_gemm_supply")
+            t = timer.time_graph(timer.graph(f, 1), replays=5) / sets
+            row[f"copies_step{step}_us"] = round(t * 1e6, 2)
+            row[f"copies_step{step}_GBs_per_CU"] = round(320 * K / t / 1e9, 1)
+        out[f"M{M}_N{N}_K{K}"] = row
+        log(f"[gemm-supply] {M}x{N}x{K}: {row}")
+        del A, B
+    return out
+
+
 TL_SLOTS = ["layer start", "P1 cross-XCD reduction", "P2 gather", "q/k/v stored", "attention stored",
             "merged", "o_proj partial stored", "P5 cross-XCD reduction", "P6 gather", "act stored",
             "down partial stored"]
@@ -856,6 +893,10 @@ def main():
                     help="only run the config-2 generation with one traced persistent launch and print "
                          "the per-phase timeline of two mid-generation tokens (the kernel's traced "
                          "build stamps every phase boundary of every workgroup)")
+    ap.add_argument("--gemm-supply", action="store_true",
+                    help="only time the C3 W8A8 GEMM beside its operand-supply probe (the K loop's "
+                         "copies alone, in K steps of 128, 256 and 512 bytes per row) and print the "
+                         "per-CU rates")
     ap.add_argument("--weights", action="store_true",
                     help="only time checkpoint loading (config-2 decoder weights, int8 and BF16 "
                          "safetensors from the page cache into HBM) and print its own JSON line")
@@ -908,6 +949,9 @@ def main():
         return 0
     if args.decode_timeline:
         print(json.dumps(decode_timeline(torch)))
+        return 0
+    if args.gemm_supply:
+        print(json.dumps(gemm_supply(torch)))
         return 0
     if args.weights:
         r = bench_weights(torch)

@@ -398,6 +398,13 @@ int pio_qwen3_persistent_supported(void* dec);
 int pio_qwen3_trace_next(void* dec, int first_step);
 size_t pio_qwen3_trace_bytes(void* dec);
 int pio_qwen3_trace_read(void* dec, void* out, size_t bytes);
+/* Measurement only (no counterpart in the reference): `reps` back-to-back
+ * launches of the dense W8A8 GEMM's K loop with its copies only (no MFMA, no
+ * output) for an M x N x K problem in 128 x 192 tiles (BM + BN = 320) mapped to
+ * the XCDs as the GEMM maps them, in K steps of `step` = 128 (the GEMM's), 256
+ * or 512 bytes per row. bench.py --gemm-supply times it. */
+int pio_probe_gemm_supply(const int8_t* A, const int8_t* B, int M, int N, int K, int BM, int BN, int step,
+                          int reps, void* stream);
 /* Persistent launches of this decoder that were re-run in graph mode because
  * the device could not hold their grid at once. No counterpart in the
  * reference. */

@@ -20,9 +20,11 @@
 // stage; rows are 128 B (64 two-byte elements) with the 16-byte chunks
 // XOR-swizzled by row pair (chunk c of row r at c ^ ((r >> 1) & 7)), so the
 // MFMA operand reads (16 consecutive rows per quarter wave, one chunk) are
-// conflict-free. Two stages, one barrier per step. A wave owns one 32 x 32
-// tile. When the tiles cannot fill the CUs, K is split and a reduce launch
-// sums the fp32 partials in slice order.
+// conflict-free. Two stages, one barrier per step. Tiles of 128 x 128 (each
+// wave 2 x 2 MFMA tiles of 32 x 32, so each fragment read feeds two MFMAs)
+// when they still give every CU a tile, else 64 x 64 (one MFMA tile per wave);
+// when even those cannot fill the CUs, K is split and a reduce launch sums the
+// fp32 partials in slice order.
 #include "pio_common.hpp"
 
 #include <type_traits>
@@ -37,7 +39,7 @@ typedef float wf_f4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) const wf_v4i wf_gv4i;
 typedef __attribute__((address_space(1))) const wf_f4 wf_gf4;
 
-constexpr int WF_BM = 64, WF_BN = 64, WF_BK = 64;
+constexpr int WF_BK = 64;
 constexpr int WF_ROW = WF_BK * 2;   // LDS bytes per tile row
 
 enum { WF_STORE = 0, WF_RESID = 1, WF_PARTIAL = 2 };
@@ -93,12 +95,15 @@ template <typename XT> struct WfXRegs;
 template <> struct WfXRegs<float> { wf_f4 v[4]; };      // 16 fp32
 template <> struct WfXRegs<_Float16> { wf_v4i v[2]; };  // 16 fp16
 
-template <int NL, typename XT, typename YT, int EPI>
+// Block tile BM x BN = 64 TM x 64 TN: 2 x 2 waves, each owning TM x TN MFMA
+// tiles of 32 x 32 (a fragment read from LDS then feeds TN or TM MFMAs).
+template <int NL, typename XT, typename YT, int EPI, int TM, int TN>
 __global__ __launch_bounds__(256) void gemm_w8f_kernel(W8fParams p) {
     static_assert((NL == 3) == std::is_same<XT, float>::value, "three bf16 parts for fp32 x, one for fp16");
     extern __shared__ __attribute__((aligned(16))) int8_t wf_lds[];
-    constexpr int XB = WF_BM * WF_ROW;                 // one part's x tile
-    constexpr int STAGE = NL * XB + WF_BN * WF_ROW;
+    constexpr int BM = 64 * TM, BN = 64 * TN;
+    constexpr int XB = BM * WF_ROW;                    // one part's x tile
+    constexpr int STAGE = NL * XB + BN * WF_ROW;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     // block b runs on XCD b % 8: each XCD takes a contiguous run of tiles,
@@ -107,80 +112,103 @@ __global__ __launch_bounds__(256) void gemm_w8f_kernel(W8fParams p) {
     const int t = (b & 7) * p.per_xcd + (b >> 3);
     if (t >= p.m_tiles * p.n_tiles) return;
     const int nt = t / p.m_tiles, mt = t - nt * p.m_tiles;
-    const int m0 = mt * WF_BM, n0 = nt * WF_BN;
+    const int m0 = mt * BM, n0 = nt * BN;
     const int64_t kb = (int64_t)blockIdx.y * p.ks;
     const int klen = (int)min((int64_t)p.ks, (int64_t)p.K - kb);
     const int nk = (klen + WF_BK - 1) / WF_BK;
 
-    // the epilogue's scale and bias first (clamped: loaded with no branch)
+    // the epilogue's scales and biases first (clamped: loaded with no branch)
     const int col = lane & 31, h = lane >> 5;
-    const int n = n0 + 32 * wn + col;
-    const int nc = min(n, p.N - 1);
-    const float sw = EPI == WF_PARTIAL ? 0.f : p.s_w[nc];
-    const float bn = (EPI != WF_PARTIAL && p.bias) ? p.bias[nc] : 0.f;
+    float sw[TN], bn[TN];
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int nc = min(n0 + 32 * TN * wn + 32 * j + col, p.N - 1);
+        sw[j] = EPI == WF_PARTIAL ? 0.f : p.s_w[nc];
+        bn[j] = (EPI != WF_PARTIAL && p.bias) ? p.bias[nc] : 0.f;
+    }
 
-    // loads: thread -> row r of the tile, elements 16 q .. 16 q + 15 of the step
+    // loads: thread -> rows r + 64 i of the tile, elements 16 q .. 16 q + 15 of the step
     const int r = tid >> 2, q = tid & 3;
-    const XT* xsrc = (const XT*)p.x + (int64_t)min(m0 + r, p.M - 1) * p.ldx + kb + 16 * q;
-    const int8_t* wsrc = p.w + (int64_t)min(n0 + r, p.N - 1) * p.ldw + kb + 16 * q;
-    WfXRegs<XT> xr;
-    wf_v4i wr;
+    const XT* xsrc[TM];
+    const int8_t* wsrc[TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++) xsrc[i] = (const XT*)p.x + (int64_t)min(m0 + r + 64 * i, p.M - 1) * p.ldx + kb + 16 * q;
+#pragma unroll
+    for (int j = 0; j < TN; j++) wsrc[j] = p.w + (int64_t)min(n0 + r + 64 * j, p.N - 1) * p.ldw + kb + 16 * q;
+    WfXRegs<XT> xr[TM];
+    wf_v4i wr[TN];
     auto gload = [&](int kk) {
         // K % 16 == 0: a thread's 16 elements are all inside or all past the end
         const bool in = kk + 16 * q < klen;
         const int off = in ? kk : 0;
-        if constexpr (std::is_same<XT, float>::value) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) xr.v[i] = *(wf_gf4*)(xsrc + off + 4 * i);
-            if (!in)
+        for (int i = 0; i < TM; i++) {
+            if constexpr (std::is_same<XT, float>::value) {
 #pragma unroll
-                for (int i = 0; i < 4; i++) xr.v[i] = wf_f4{0.f, 0.f, 0.f, 0.f};
-        } else {
+                for (int u = 0; u < 4; u++) xr[i].v[u] = *(wf_gf4*)(xsrc[i] + off + 4 * u);
+                if (!in)
 #pragma unroll
-            for (int i = 0; i < 2; i++) xr.v[i] = *(wf_gv4i*)(xsrc + off + 8 * i);
-            if (!in)
+                    for (int u = 0; u < 4; u++) xr[i].v[u] = wf_f4{0.f, 0.f, 0.f, 0.f};
+            } else {
 #pragma unroll
-                for (int i = 0; i < 2; i++) xr.v[i] = wf_v4i{0, 0, 0, 0};
+                for (int u = 0; u < 2; u++) xr[i].v[u] = *(wf_gv4i*)(xsrc[i] + off + 8 * u);
+                if (!in)
+#pragma unroll
+                    for (int u = 0; u < 2; u++) xr[i].v[u] = wf_v4i{0, 0, 0, 0};
+            }
         }
-        wr = *(wf_gv4i*)(wsrc + off);
-        if (!in) wr = wf_v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            wr[j] = *(wf_gv4i*)(wsrc[j] + off);
+            if (!in) wr[j] = wf_v4i{0, 0, 0, 0};
+        }
     };
     auto sstore = [&](int buf) {
         int8_t* st = wf_lds + buf * STAGE;
-        const int c0 = wf_swz(r, 2 * q), c1 = wf_swz(r, 2 * q + 1);
-        if constexpr (NL == 3) {
-            uint32_t pt[3][8];
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                uint32_t h0, m0_, l0, h1, m1, l1;
-                wf_split3(xr.v[j >> 1][2 * (j & 1)], h0, m0_, l0);
-                wf_split3(xr.v[j >> 1][2 * (j & 1) + 1], h1, m1, l1);
-                pt[0][j] = h0 | (h1 << 16);
-                pt[1][j] = m0_ | (m1 << 16);
-                pt[2][j] = l0 | (l1 << 16);
-            }
+        for (int i = 0; i < TM; i++) {
+            const int c0 = wf_swz(r + 64 * i, 2 * q), c1 = wf_swz(r + 64 * i, 2 * q + 1);
+            if constexpr (NL == 3) {
+                uint32_t pt[3][8];
 #pragma unroll
-            for (int L = 0; L < 3; L++) {
-                *(wf_v4i*)(st + L * XB + c0) = wf_v4i{(int)pt[L][0], (int)pt[L][1], (int)pt[L][2], (int)pt[L][3]};
-                *(wf_v4i*)(st + L * XB + c1) = wf_v4i{(int)pt[L][4], (int)pt[L][5], (int)pt[L][6], (int)pt[L][7]};
+                for (int u = 0; u < 8; u++) {
+                    uint32_t h0, m0_, l0, h1, m1, l1;
+                    wf_split3(xr[i].v[u >> 1][2 * (u & 1)], h0, m0_, l0);
+                    wf_split3(xr[i].v[u >> 1][2 * (u & 1) + 1], h1, m1, l1);
+                    pt[0][u] = h0 | (h1 << 16);
+                    pt[1][u] = m0_ | (m1 << 16);
+                    pt[2][u] = l0 | (l1 << 16);
+                }
+#pragma unroll
+                for (int L = 0; L < 3; L++) {
+                    *(wf_v4i*)(st + L * XB + c0) = wf_v4i{(int)pt[L][0], (int)pt[L][1], (int)pt[L][2], (int)pt[L][3]};
+                    *(wf_v4i*)(st + L * XB + c1) = wf_v4i{(int)pt[L][4], (int)pt[L][5], (int)pt[L][6], (int)pt[L][7]};
+                }
+            } else {
+                *(wf_v4i*)(st + c0) = xr[i].v[0];
+                *(wf_v4i*)(st + c1) = xr[i].v[1];
             }
-        } else {
-            *(wf_v4i*)(st + c0) = xr.v[0];
-            *(wf_v4i*)(st + c1) = xr.v[1];
         }
-        uint32_t o[8];
-        wf_widen<NL>(wr, o);
-        *(wf_v4i*)(st + NL * XB + c0) = wf_v4i{(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
-        *(wf_v4i*)(st + NL * XB + c1) = wf_v4i{(int)o[4], (int)o[5], (int)o[6], (int)o[7]};
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int c0 = wf_swz(r + 64 * j, 2 * q), c1 = wf_swz(r + 64 * j, 2 * q + 1);
+            uint32_t o[8];
+            wf_widen<NL>(wr[j], o);
+            *(wf_v4i*)(st + NL * XB + c0) = wf_v4i{(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
+            *(wf_v4i*)(st + NL * XB + c1) = wf_v4i{(int)o[4], (int)o[5], (int)o[6], (int)o[7]};
+        }
     };
 
-    wf_v16f acc;
+    wf_v16f acc[TM][TN];
 #pragma unroll
-    for (int e = 0; e < 16; e++) acc[e] = 0.f;
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
     gload(0);
     sstore(0);
     __syncthreads();
-    const int ar = 32 * wm + col, br = 32 * wn + col;
     for (int kt = 0; kt < nk; kt++) {
         const int cur = kt & 1;
         if (kt + 1 < nk) gload((kt + 1) * WF_BK);
@@ -188,19 +216,30 @@ __global__ __launch_bounds__(256) void gemm_w8f_kernel(W8fParams p) {
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             const int c = 2 * ks + h;   // elements 16 ks + 8 h .. + 8 of the step
-            const wf_v4i bw = *(const wf_v4i*)(st + NL * XB + wf_swz(br, c));
+            wf_v4i bw[TN];
+#pragma unroll
+            for (int j = 0; j < TN; j++) bw[j] = *(const wf_v4i*)(st + NL * XB + wf_swz(32 * TN * wn + 32 * j + col, c));
             if constexpr (NL == 3) {
                 // the low part first: the small products meet the smaller sums
 #pragma unroll
-                for (int L = 2; L >= 0; L--) {
-                    const wf_v4i a = *(const wf_v4i*)(st + L * XB + wf_swz(ar, c));
-                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(wf_bf8, a),
-                                                                  __builtin_bit_cast(wf_bf8, bw), acc, 0, 0, 0);
-                }
+                for (int L = 2; L >= 0; L--)
+#pragma unroll
+                    for (int i = 0; i < TM; i++) {
+                        const wf_v4i a = *(const wf_v4i*)(st + L * XB + wf_swz(32 * TM * wm + 32 * i + col, c));
+#pragma unroll
+                        for (int j = 0; j < TN; j++)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                                __builtin_bit_cast(wf_bf8, a), __builtin_bit_cast(wf_bf8, bw[j]), acc[i][j], 0, 0, 0);
+                    }
             } else {
-                const wf_v4i a = *(const wf_v4i*)(st + wf_swz(ar, c));
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(wf_h8, a),
-                                                             __builtin_bit_cast(wf_h8, bw), acc, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < TM; i++) {
+                    const wf_v4i a = *(const wf_v4i*)(st + wf_swz(32 * TM * wm + 32 * i + col, c));
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                            __builtin_bit_cast(wf_h8, a), __builtin_bit_cast(wf_h8, bw[j]), acc[i][j], 0, 0, 0);
+                }
             }
         }
         if (kt + 1 < nk) sstore(cur ^ 1);
@@ -208,21 +247,27 @@ __global__ __launch_bounds__(256) void gemm_w8f_kernel(W8fParams p) {
     }
 
     // accumulator: element e of lane l is row 8 (e / 4) + 4 (l / 32) + e % 4 of
-    // the wave's tile, column l % 32
-    if (n >= p.N) return;
+    // MFMA tile (i, j), column l % 32
 #pragma unroll
-    for (int e = 0; e < 16; e++) {
-        const int m = m0 + 32 * wm + 8 * (e >> 2) + 4 * h + (e & 3);
-        if (m >= p.M) continue;
-        if constexpr (EPI == WF_PARTIAL) {
-            ((float*)p.y)[((int64_t)blockIdx.y * p.M + m) * p.N + n] = acc[e];
-        } else {
-            float v = acc[e] * sw;
-            if (p.bias) v += bn;
-            YT* yp = (YT*)p.y + (int64_t)m * p.ldy + n;
-            if constexpr (EPI == WF_RESID) v += to_f32<YT>(*yp);
-            *yp = from_f32<YT>(v);
-        }
+    for (int j = 0; j < TN; j++) {
+        const int n = n0 + 32 * TN * wn + 32 * j + col;
+        if (n >= p.N) continue;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int m = m0 + 32 * TM * wm + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+                if (m >= p.M) continue;
+                if constexpr (EPI == WF_PARTIAL) {
+                    ((float*)p.y)[((int64_t)blockIdx.y * p.M + m) * p.N + n] = acc[i][j][e];
+                } else {
+                    float v = acc[i][j][e] * sw[j];
+                    if (p.bias) v += bn[j];
+                    YT* yp = (YT*)p.y + (int64_t)m * p.ldy + n;
+                    if constexpr (EPI == WF_RESID) v += to_f32<YT>(*yp);
+                    *yp = from_f32<YT>(v);
+                }
+            }
     }
 }
 
@@ -245,11 +290,45 @@ __global__ __launch_bounds__(256) void gemm_w8f_reduce_kernel(const float* __res
     *yp = from_f32<YT>(v);
 }
 
-template <int NL, typename XT, typename YT, int EPI>
+template <int NL, typename XT, typename YT, int EPI, int TM, int TN>
 static int launch_w8f(const W8fParams& p, int splits, hipStream_t st) {
-    constexpr size_t lds = 2 * (size_t)(NL * WF_BM + WF_BN) * WF_ROW;
-    PIO_TRY(allow_lds<gemm_w8f_kernel<NL, XT, YT, EPI>>(lds));
-    gemm_w8f_kernel<NL, XT, YT, EPI><<<dim3(8 * p.per_xcd, splits), 256, lds, st>>>(p);
+    constexpr size_t lds = 2 * (size_t)(NL * 64 * TM + 64 * TN) * WF_ROW;
+    PIO_TRY((allow_lds<gemm_w8f_kernel<NL, XT, YT, EPI, TM, TN>>(lds)));
+    gemm_w8f_kernel<NL, XT, YT, EPI, TM, TN><<<dim3(8 * p.per_xcd, splits), 256, lds, st>>>(p);
+    PIO_LAUNCHED();
+    return PIO_OK;
+}
+
+template <int NL, typename XT, typename YT, int TM, int TN>
+static int run_tiles(W8fParams p, bool resid, const float* s_w, const float* bias, YT* y, int64_t ldy,
+                     hipStream_t st) {
+    const int M = p.M, N = p.N, K = p.K;
+    p.m_tiles = ceil_div(M, 64 * TM);
+    p.n_tiles = ceil_div(N, 64 * TN);
+    const int tiles = p.m_tiles * p.n_tiles;
+    p.per_xcd = ceil_div(tiles, 8);
+    // K slices when the tiles leave most CUs idle and each slice keeps >= 8 steps
+    int splits = 1;
+    const int steps = ceil_div(K, WF_BK);
+    while (tiles * splits * 2 <= 256 && steps / (splits * 2) >= 8) splits *= 2;
+    p.ks = ceil_div(steps, splits) * WF_BK;
+    splits = ceil_div(K, p.ks);
+    if (splits == 1) {
+        p.ks = K;
+        return resid ? launch_w8f<NL, XT, YT, WF_RESID, TM, TN>(p, 1, st)
+                     : launch_w8f<NL, XT, YT, WF_STORE, TM, TN>(p, 1, st);
+    }
+    Scratch ws;
+    PIO_TRY(ws.get((size_t)splits * M * N * sizeof(float), st));
+    p.y = ws.ptr;
+    PIO_TRY((launch_w8f<NL, XT, YT, WF_PARTIAL, TM, TN>(p, splits, st)));
+    const int64_t MN = (int64_t)M * N;
+    if (resid)
+        gemm_w8f_reduce_kernel<YT, true><<<(unsigned)ceil_div(MN, 256), 256, 0, st>>>((const float*)ws.ptr, splits, M,
+                                                                                     N, s_w, bias, y, ldy);
+    else
+        gemm_w8f_reduce_kernel<YT, false><<<(unsigned)ceil_div(MN, 256), 256, 0, st>>>((const float*)ws.ptr, splits,
+                                                                                      M, N, s_w, bias, y, ldy);
     PIO_LAUNCHED();
     return PIO_OK;
 }
@@ -262,33 +341,11 @@ static int run_w8f(const XT* x, int64_t ldx, const int8_t* w, const float* s_w, 
     p.x = x; p.w = w; p.s_w = s_w; p.bias = bias; p.y = y;
     p.M = M; p.N = N; p.K = K;
     p.ldx = ldx; p.ldw = K; p.ldy = ldy;
-    p.m_tiles = ceil_div(M, WF_BM);
-    p.n_tiles = ceil_div(N, WF_BN);
-    const int tiles = p.m_tiles * p.n_tiles;
-    p.per_xcd = ceil_div(tiles, 8);
-    // K slices when the tiles leave most CUs idle and each slice keeps >= 8 steps
-    int splits = 1;
-    const int steps = ceil_div(K, WF_BK);
-    while (tiles * splits * 2 <= 256 && steps / (splits * 2) >= 8) splits *= 2;
-    p.ks = ceil_div(steps, splits) * WF_BK;
-    splits = ceil_div(K, p.ks);
-    if (splits == 1) {
-        p.ks = K;
-        return resid ? launch_w8f<NL, XT, YT, WF_RESID>(p, 1, st) : launch_w8f<NL, XT, YT, WF_STORE>(p, 1, st);
-    }
-    Scratch ws;
-    PIO_TRY(ws.get((size_t)splits * M * N * sizeof(float), st));
-    p.y = ws.ptr;
-    PIO_TRY((launch_w8f<NL, XT, YT, WF_PARTIAL>(p, splits, st)));
-    const int64_t MN = (int64_t)M * N;
-    if (resid)
-        gemm_w8f_reduce_kernel<YT, true><<<(unsigned)ceil_div(MN, 256), 256, 0, st>>>((const float*)ws.ptr, splits, M,
-                                                                                     N, s_w, bias, y, ldy);
-    else
-        gemm_w8f_reduce_kernel<YT, false><<<(unsigned)ceil_div(MN, 256), 256, 0, st>>>((const float*)ws.ptr, splits,
-                                                                                      M, N, s_w, bias, y, ldy);
-    PIO_LAUNCHED();
-    return PIO_OK;
+    // 128 x 128 tiles (every fragment read feeds two MFMAs) when they still
+    // give every CU a tile; 64 x 64 tiles (with K slices if needed) otherwise
+    if ((int64_t)ceil_div(M, 128) * ceil_div(N, 128) >= 256)
+        return run_tiles<NL, XT, YT, 2, 2>(p, resid, s_w, bias, y, ldy, st);
+    return run_tiles<NL, XT, YT, 1, 1>(p, resid, s_w, bias, y, ldy, st);
 }
 
 // Row strides: ldx elements of x, ldy elements of y (W rows are K bytes).

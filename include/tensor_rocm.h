@@ -484,6 +484,77 @@ int pio_safetensors_to_device_f32(void* ctx, const char* name, float* dst, int64
 void tensor_load_safetensors(void* ctx, const char* name, Tensor* out);
 int tensor_load_safetensors_status(void* ctx, const char* name, Tensor* out);
 
+/* ---------------------------------------------------------------------------
+ * Drop-in: companion ops of the reference model layers on rocm:N, fp32 device
+ * tensors (bound by hasattr at backend.py:60-111, 157; called by
+ * qwen3_0_6b/architecture.py:16-135 through backend.py:385-600, 740-790).
+ * Each follows the reference CPU loop cited; the void forms drop the status,
+ * as the reference's do, and leave the message for tensor_last_error.
+ * ------------------------------------------------------------------------- */
+
+/* tensor.h:46; backend.py:63, 502; tensor_ops.c:369-383: per row of the last dimension,
+ * out = x * (1 / sqrt(sum(x^2) / cols + eps)) * weight. */
+void tensor_rms_norm(Tensor* input, Tensor* weight, Tensor* out, float eps);
+int tensor_rms_norm_status(Tensor* input, Tensor* weight, Tensor* out, float eps);
+/* backend.py:157, 515; tensor_ops_cuda.cu:914-921: x <- x + residual (in
+ * place), out = rms_norm(x). */
+void tensor_fused_add_rms_norm(Tensor* x, Tensor* residual, Tensor* weight, Tensor* out, float eps);
+int tensor_fused_add_rms_norm_status(Tensor* x, Tensor* residual, Tensor* weight, Tensor* out,
+                                     float eps);
+/* tensor.h:47; backend.py:64, 508; tensor_ops.c:384-413: q [.., S, Hq, D], k [.., S, Hk, D],
+ * cos / sin [>= S, D/2] (row s for position s): rotate-half RoPE. k keeps its
+ * own head count (the reference walks k with q's). */
+void tensor_rope(Tensor* q, Tensor* k, Tensor* cos, Tensor* sin, Tensor* out_q, Tensor* out_k);
+int tensor_rope_status(Tensor* q, Tensor* k, Tensor* cos, Tensor* sin, Tensor* out_q,
+                       Tensor* out_k);
+/* tensor.h:44; backend.py:61, 490; tensor_ops.c:336-342: x * (1 / (1 + exp(-x))). */
+void tensor_silu(Tensor* input, Tensor* out);
+int tensor_silu_status(Tensor* input, Tensor* out);
+/* backend.py:103, 385; tensor_ops.c:579-587: silu(gate) * up. */
+void tensor_swiglu(Tensor* gate, Tensor* up, Tensor* out);
+int tensor_swiglu_status(Tensor* gate, Tensor* up, Tensor* out);
+/* backend.py:105, 395; tensor_ops.c:588-604: rows of [gate | up] (2h columns) ->
+ * silu(gate) * up (h columns). */
+void tensor_fused_gate_up_swiglu(Tensor* gate_up, Tensor* out);
+int tensor_fused_gate_up_swiglu_status(Tensor* gate_up, Tensor* out);
+/* tensor.h:43; backend.py:60, 484; tensor_ops.c:351-367: per row, max from -1e9, exp(x - max),
+ * times 1 / sum. */
+void tensor_softmax(Tensor* input, Tensor* out);
+int tensor_softmax_status(Tensor* input, Tensor* out);
+/* tensor.h:55; backend.py:70, 552; tensor_ops.c:649-661: per row the first index of the largest
+ * value above -1e9 (0 when none), as a float. */
+void tensor_argmax(Tensor* input, Tensor* out);
+int tensor_argmax_status(Tensor* input, Tensor* out);
+/* tensor.h:56; backend.py:71, 559; tensor_ops.c:663-671: out[i] = weight[(int)indices[i]]
+ * ([vocab, dim] weight); indices outside [0, vocab) read row 0. */
+void tensor_embed(Tensor* weight, Tensor* indices, Tensor* out);
+int tensor_embed_status(Tensor* weight, Tensor* indices, Tensor* out);
+/* backend.py:109, 771; tensor_ops.c:536-578: q [B, S, H, D], k / v [B, T, Hk, D]
+ * (Hk divides H; query head h reads kv head h / (H / Hk)), out [B, S, H, D]:
+ * softmax(q.k * scale) over all T keys (no mask, as the reference), the
+ * weights normalised before the sum over v. T comes from k (the reference
+ * loop takes q's sequence length for the keys; equal when S == T);
+ * T <= 32768. */
+void tensor_scaled_dot_product_attention(Tensor* q, Tensor* k, Tensor* v, Tensor* out,
+                                         float scale);
+int tensor_scaled_dot_product_attention_status(Tensor* q, Tensor* k, Tensor* v, Tensor* out,
+                                               float scale);
+/* tensor.h:50; backend.py:74, 566; tensor_ops.c:605-637: out's elements from the input at
+ * start_indices + out's coordinates (offsets outside the input are
+ * skipped); slice_shapes is unused, as in the reference. Rank <= 8. */
+void tensor_slice(Tensor* input, Tensor* out, int* start_indices, int* slice_shapes);
+int tensor_slice_status(Tensor* input, Tensor* out, int* start_indices, int* slice_shapes);
+/* backend.py:78, 594; tensor_ops.c:504-535: src written into dst at
+ * start_indices (the KV-cache update, architecture.py:95-96). */
+void tensor_set_slice(Tensor* dst, Tensor* src, int* start_indices);
+int tensor_set_slice_status(Tensor* dst, Tensor* src, int* start_indices);
+/* backend.py:111; tensor_ops.c:672: out <- input's elements in order. */
+void tensor_reshape(Tensor* input, Tensor* out);
+int tensor_reshape_status(Tensor* input, Tensor* out);
+/* tensor.h:57; backend.py:72, 740; tensor_ops.c:702-718: the inputs in order along `axis`. */
+void tensor_cat(Tensor** inputs, int count, int axis, Tensor* out);
+int tensor_cat_status(Tensor** inputs, int count, int axis, Tensor* out);
+
 /* Library version string and the gfx target it was built for. */
 const char* pio_version(void);
 

@@ -10,11 +10,21 @@ that contract on top of libtensor_ops_rocm.so, so model code written against
 * ``W8A8Linear`` -- per-token int8 activations x int8 weights on MFMA;
 * ``MoEW8A8``    -- routed int8 expert layer (replaces Qwen3Coder30BMoE).
 
+The layer ops around the linears (rms_norm, fused_add_rms_norm, rope,
+swiglu / fused_swiglu, softmax, argmax, embed, slice / set_slice / reshape,
+``cat``, ``scaled_dot_product_attention``, ``RMSNorm``, ``Embedding``) run on
+the device too (model_ops.hip), so a reference-style decoder layer with a KV
+cache runs on ``rocm:N`` end to end.
+
 Differences from the reference, on purpose:
 * tensors free through the library that created them (the reference frees
   every tensor through ``_lib_cpu``, backend.py:266-272);
 * failed C calls raise ``RocmError`` instead of being ignored;
-* tensors carry a dtype (float32 / float16 / int8 / int32).
+* tensors carry a dtype (float32 / float16 / int8 / int32);
+* ``reshape`` copies the data into the new tensor (the reference returns a
+  fresh tensor of the new shape, backend.py:416-421); ``slice`` zero-fills
+  what falls outside the source;
+* attention takes grouped-query k / v directly (no repeat_kv copy needed).
 """
 from __future__ import annotations
 
@@ -254,6 +264,97 @@ class Tensor:
         return out
 
 
+    # ------------------------- companion ops of the model layers (model_ops.hip)
+    def rms_norm(self, weight: "Tensor", eps: float = 1e-6) -> "Tensor":
+        """backend.py:502-506 (tensor_ops.c:369-383)."""
+        out = self._new(self.shape)
+        check(lib.tensor_rms_norm_status(self._handle, weight._handle, out._handle, ctypes.c_float(eps)),
+              "tensor_rms_norm")
+        return out
+
+    def fused_add_rms_norm(self, residual: "Tensor", weight: "Tensor", eps: float) -> "Tensor":
+        """backend.py:515-523: self <- self + residual (in place); returns the
+        RMSNorm of the sum."""
+        out = self._new(self.shape)
+        check(lib.tensor_fused_add_rms_norm_status(self._handle, residual._handle, weight._handle,
+                                                   out._handle, ctypes.c_float(eps)),
+              "tensor_fused_add_rms_norm")
+        return out
+
+    def rope(self, k: "Tensor", cos: "Tensor", sin: "Tensor") -> Tuple["Tensor", "Tensor"]:
+        """backend.py:508-513 (tensor_ops.c:384-413); k may have fewer heads."""
+        out_q, out_k = self._new(self.shape), k._new(k.shape)
+        check(lib.tensor_rope_status(self._handle, k._handle, cos._handle, sin._handle, out_q._handle,
+                                     out_k._handle), "tensor_rope")
+        return out_q, out_k
+
+    def silu(self) -> "Tensor":
+        """backend.py:490-495 (tensor_ops.c:336-342)."""
+        out = self._new(self.shape)
+        check(lib.tensor_silu_status(self._handle, out._handle), "tensor_silu")
+        return out
+
+    def swiglu(self, up_proj_out: "Tensor") -> "Tensor":
+        """backend.py:385-393 (tensor_ops.c:579-587): silu(self) * up."""
+        out = self._new(self.shape)
+        check(lib.tensor_swiglu_status(self._handle, up_proj_out._handle, out._handle), "tensor_swiglu")
+        return out
+
+    def fused_swiglu(self) -> "Tensor":
+        """backend.py:395-401 (tensor_ops.c:588-604): rows [gate | up]."""
+        out = self._new(list(self.shape[:-1]) + [self.shape[-1] // 2])
+        check(lib.tensor_fused_gate_up_swiglu_status(self._handle, out._handle),
+              "tensor_fused_gate_up_swiglu")
+        return out
+
+    def softmax(self, dim: int = -1) -> "Tensor":
+        """backend.py:484-488 (tensor_ops.c:351-367), over the last dimension."""
+        out = self._new(self.shape)
+        check(lib.tensor_softmax_status(self._handle, out._handle), "tensor_softmax")
+        return out
+
+    def argmax(self, dim: int = -1) -> "Tensor":
+        """backend.py:552-557 (tensor_ops.c:649-661): indices as floats."""
+        out = self._new(list(self.shape[:-1]) or [1], "float32")
+        check(lib.tensor_argmax_status(self._handle, out._handle), "tensor_argmax")
+        return out
+
+    def embed(self, indices: "Tensor") -> "Tensor":
+        """backend.py:559-564 (tensor_ops.c:663-671): self is [vocab, dim]."""
+        out = self._new(list(indices.shape) + [self.shape[1]])
+        check(lib.tensor_embed_status(self._handle, indices._handle, out._handle), "tensor_embed")
+        return out
+
+    def slice(self, start_indices: Sequence[int], slice_shapes: Sequence[int]) -> "Tensor":
+        """backend.py:566-592 (tensor_ops.c:605-637) with host start indices.
+        Elements whose source falls outside self are 0 (the reference leaves
+        them as the fresh tensor holds them)."""
+        if len(start_indices) != self.ndim or len(slice_shapes) != self.ndim:
+            raise ValueError("slice: start and shape need one entry per dimension")
+        out = self._new(slice_shapes)
+        out.fill(0.0)
+        c_start = (ctypes.c_int * self.ndim)(*[int(v) for v in start_indices])
+        c_shape = (ctypes.c_int * self.ndim)(*[int(v) for v in slice_shapes])
+        check(lib.tensor_slice_status(self._handle, out._handle, c_start, c_shape), "tensor_slice")
+        return out
+
+    def set_slice(self, src: "Tensor", start_indices: Sequence[int]) -> None:
+        """backend.py:594-611 (tensor_ops.c:504-535): src into self at start."""
+        if len(start_indices) != self.ndim:
+            raise ValueError("set_slice: start needs one entry per dimension")
+        c_start = (ctypes.c_int * self.ndim)(*[int(v) for v in start_indices])
+        check(lib.tensor_set_slice_status(self._handle, src._handle, c_start), "tensor_set_slice")
+
+    def reshape(self, new_shape: Sequence[int]) -> "Tensor":
+        """backend.py:416-421, with the data: the reference returns a fresh
+        tensor of the new shape without copying into it; this one copies
+        (tensor_reshape, tensor_ops.c:672)."""
+        if int(np.prod(new_shape)) != self.size:
+            raise ValueError("Reshape size mismatch")
+        out = self._new(new_shape)
+        check(lib.tensor_reshape_status(self._handle, out._handle), "tensor_reshape")
+        return out
+
 def _stream_handle(stream):
     """Raw handle of a HIPStream (or a raw handle / None: the current stream)."""
     if stream is None:
@@ -401,6 +502,56 @@ class MoEW8A8(Module):
                                          self.s_down._handle, self.top_k,
                                          int(self.renormalize), out._handle), "tensor_moe_w8a8")
         return out
+
+
+# ------------------------------------- model-layer functions and modules
+def cat(tensors: List[Tensor], axis: int = 0) -> Tensor:
+    """backend.py:740-754 (tensor_ops.c:702-718)."""
+    if not tensors:
+        return None
+    shape = list(tensors[0].shape)
+    shape[axis] = sum(t.shape[axis] for t in tensors)
+    out = tensors[0]._new(shape)
+    arr = (ctypes.POINTER(CTensor) * len(tensors))(*[t._handle for t in tensors])
+    check(lib.tensor_cat_status(arr, len(tensors), axis, out._handle), "tensor_cat")
+    return out
+
+
+def scaled_dot_product_attention(q: Tensor, k: Tensor, v: Tensor, scale: Optional[float] = None) -> Tensor:
+    """backend.py:771-790 (tensor_ops.c:536-578): q [B, S, H, D], k / v
+    [B, T, Hk, D] (Hk dividing H: no repeat_kv copy needed), no mask."""
+    if scale is None:
+        scale = 1.0 / (q.shape[-1] ** 0.5)
+    out = q._new(q.shape)
+    check(lib.tensor_scaled_dot_product_attention_status(q._handle, k._handle, v._handle, out._handle,
+                                                         ctypes.c_float(scale)),
+          "tensor_scaled_dot_product_attention")
+    return out
+
+
+class RMSNorm(Module):
+    """backend.py:726-731."""
+
+    def __init__(self, normalized_shape: int, eps: float = 1e-6, device: str = "rocm:0"):
+        super().__init__()
+        self.eps = eps
+        self.weight = Tensor([normalized_shape], device=device)
+        self.register_parameter("weight", self.weight)
+
+    def forward(self, input: Tensor) -> Tensor:
+        return input.rms_norm(self.weight, self.eps)
+
+
+class Embedding(Module):
+    """backend.py:719-724."""
+
+    def __init__(self, num_embeddings: int, embedding_dim: int, device: str = "rocm:0"):
+        super().__init__()
+        self.weight = Tensor([num_embeddings, embedding_dim], device=device)
+        self.register_parameter("weight", self.weight)
+
+    def forward(self, input: Tensor) -> Tensor:
+        return self.weight.embed(input)
 
 
 # ------------------------------------------------- allocator and streams

@@ -77,6 +77,35 @@ SIGNATURES: dict[str, tuple] = {
     "begin_capture": (None, []),
     "end_capture": (None, []),
     "replay_graph": (None, []),
+    # companion ops of the reference model layers (model_ops.hip)
+    "tensor_rms_norm": (None, [TP, TP, TP, ctypes.c_float]),
+    "tensor_rms_norm_status": (_i, [TP, TP, TP, ctypes.c_float]),
+    "tensor_fused_add_rms_norm": (None, [TP, TP, TP, TP, ctypes.c_float]),
+    "tensor_fused_add_rms_norm_status": (_i, [TP, TP, TP, TP, ctypes.c_float]),
+    "tensor_rope": (None, [TP, TP, TP, TP, TP, TP]),
+    "tensor_rope_status": (_i, [TP, TP, TP, TP, TP, TP]),
+    "tensor_silu": (None, [TP, TP]),
+    "tensor_silu_status": (_i, [TP, TP]),
+    "tensor_swiglu": (None, [TP, TP, TP]),
+    "tensor_swiglu_status": (_i, [TP, TP, TP]),
+    "tensor_fused_gate_up_swiglu": (None, [TP, TP]),
+    "tensor_fused_gate_up_swiglu_status": (_i, [TP, TP]),
+    "tensor_softmax": (None, [TP, TP]),
+    "tensor_softmax_status": (_i, [TP, TP]),
+    "tensor_argmax": (None, [TP, TP]),
+    "tensor_argmax_status": (_i, [TP, TP]),
+    "tensor_embed": (None, [TP, TP, TP]),
+    "tensor_embed_status": (_i, [TP, TP, TP]),
+    "tensor_scaled_dot_product_attention": (None, [TP, TP, TP, TP, ctypes.c_float]),
+    "tensor_scaled_dot_product_attention_status": (_i, [TP, TP, TP, TP, ctypes.c_float]),
+    "tensor_slice": (None, [TP, TP, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]),
+    "tensor_slice_status": (_i, [TP, TP, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]),
+    "tensor_set_slice": (None, [TP, TP, ctypes.POINTER(ctypes.c_int)]),
+    "tensor_set_slice_status": (_i, [TP, TP, ctypes.POINTER(ctypes.c_int)]),
+    "tensor_reshape": (None, [TP, TP]),
+    "tensor_reshape_status": (_i, [TP, TP]),
+    "tensor_cat": (None, [ctypes.POINTER(TP), _i, _i, TP]),
+    "tensor_cat_status": (_i, [ctypes.POINTER(TP), _i, _i, TP]),
     "create_tensor_pinned": (TP, [ctypes.POINTER(ctypes.c_int), _i, _i]),
     "tensor_is_pinned": (_i, [TP]),
     "tensor_copy_async": (_i, [TP, TP, _vp]),

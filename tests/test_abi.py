@@ -108,6 +108,26 @@ def test_tensor_layer_rejects_host_tensors_and_nulls():
     try:
         assert ops.lib.tensor_quantize_per_token_status(t, t, t) == ops.ERR_INVALID
         assert "host" in ops.last_error()
+        # the model-layer companion ops too, each before any device work
+        eps = ctypes.c_float(1e-6)
+        start = (ctypes.c_int * 2)(0, 0)
+        for name, args in [("tensor_rms_norm_status", (t, t, t, eps)),
+                           ("tensor_fused_add_rms_norm_status", (t, t, t, t, eps)),
+                           ("tensor_rope_status", (t, t, t, t, t, t)),
+                           ("tensor_silu_status", (t, t)), ("tensor_swiglu_status", (t, t, t)),
+                           ("tensor_fused_gate_up_swiglu_status", (t, t)),
+                           ("tensor_softmax_status", (t, t)), ("tensor_argmax_status", (t, t)),
+                           ("tensor_embed_status", (t, t, t)),
+                           ("tensor_scaled_dot_product_attention_status", (t, t, t, t, eps)),
+                           ("tensor_slice_status", (t, t, start, start)),
+                           ("tensor_set_slice_status", (t, t, start)),
+                           ("tensor_reshape_status", (t, t))]:
+            assert getattr(ops.lib, name)(*args) == ops.ERR_INVALID, name
+            assert "host" in ops.last_error(), name
+        assert ops.lib.tensor_rope_status(None, t, t, t, t, t) == ops.ERR_INVALID
+        assert "null" in ops.last_error()
+        arr = (ctypes.POINTER(ops.CTensor) * 1)(t)
+        assert ops.lib.tensor_cat_status(arr, 1, 0, t) == ops.ERR_INVALID
     finally:
         ops.lib.free_tensor(t)
 

@@ -359,10 +359,12 @@ class Qwen3Int8Decoder:
 
 def _main(argv=None) -> int:
     """Runs the config-2 decode workload once and exits: random-init weights
-    (seed 0), a random 128-token prompt (seed 1), then `--steps` generated
-    tokens in the fastest supported mode -- the same launches as bench.py's
-    timed decode (a warmup run, the prompt steps, the generated steps), as a
-    plain driver for profilers (rocprofv3 counter passes)."""
+    (seed 0), a random 128-token prompt (seed 1) as one batch, then `--steps`
+    generated tokens in the fastest supported mode -- the same launches as
+    bench.py's timed decode (a warmup generation of `--warmup` tokens, then the
+    batched prompt and the generated steps), as a plain driver for profilers
+    (rocprofv3 counter passes). In persistent mode the second decode launch
+    is the one that runs the `--steps` tokens."""
     import argparse
     ap = argparse.ArgumentParser(prog="python -m mod_amd.qwen3")
     ap.add_argument("--steps", type=int, default=256)
@@ -375,9 +377,10 @@ def _main(argv=None) -> int:
     mode = args.mode or ("persistent" if dec.persistent_supported() else "graph")
     prompt = np.random.default_rng(1).integers(0, cfg.vocab, size=P).astype(np.int32)
     dec.reset(prompt)
-    dec.run(P - 1 + min(args.warmup, cfg.max_seq - P + 1), mode=mode)
+    dec.prefill(P - 1)
+    dec.run(min(max(args.warmup, 1), cfg.max_seq - P + 1), mode=mode)
     dec.reset(prompt)
-    dec.run(P - 1, mode=mode)
+    dec.prefill(P - 1)
     dec.run(args.steps, mode=mode)
     ids = dec.read(P + args.steps)
     print(f"decoded {args.steps} tokens ({mode}); first generated ids {ids[P:P + 4].tolist()}", flush=True)

@@ -357,6 +357,32 @@ def decode_timeline(torch):
     # skew: spread of each boundary over the 256 workgroups (median over layers)
     out["boundary_spread_us"] = {TL_SLOTS[k]: med(np.nanmax(mid[:, :, k], axis=0) - np.nanmin(mid[:, :, k], axis=0))
                                  for k in range(11) if k != 4}
+    # hand-offs: each consumer's stamp after the LAST producer it waits for
+    # (the XCD's, or every workgroup's across XCDs), percentiles over
+    # workgroups and layers: the wait that no producer skew explains
+    g = np.arange(256) % 8
+    hops = [("down partial stored (layer start) -> P1 reduced, across XCDs", 0, 1, True, None),
+            ("o_proj partial stored -> P5 reduced, across XCDs", 6, 7, True, None),
+            ("P1 reduced -> P2 gathered, in the XCD", 1, 2, False, None),
+            ("P5 reduced -> P6 gathered, in the XCD", 7, 8, False, None),
+            ("act stored -> down partial stored, in the XCD", 9, 10, False, None),
+            ("q/k/v stored -> attention's q arrived, in the XCD", 3, 12, False, att),
+            ("attention stored -> merge inputs arrived, in the XCD", 4, 14, False, None)]
+    out["hop_after_last_producer_us"] = {}
+    for name, src, dst, cross, rows in hops:
+        d = []
+        for x in range(8):
+            prod = mid[att & (g == x)] if src == 4 else (mid if cross else mid[g == x])
+            last = np.nanmax(prod[:, :, src], axis=0)
+            cons = mid[(g == x) & (rows if rows is not None else True)][:, :, dst]
+            d.append(cons - last[None, :])
+        d = np.concatenate(d).ravel()
+        d = d[np.isfinite(d)]
+        q = np.percentile(d, [0, 10, 50, 90, 100]) / 1e3
+        out["hop_after_last_producer_us"][name] = {k: round(float(v), 2) for k, v in
+                                                     zip(("min", "p10", "p50", "p90", "max"), q)}
+    for k, v in out["hop_after_last_producer_us"].items():
+        log(f"[timeline] hop {k:55s} {v}")
     for k, v in list(out["phases_us"].items()) + list(out["subphases_us"].items()):
         log(f"[timeline] {k:55s} {v} us")
     log(f"[timeline] layer period {out['layer_period_us']} us, token period {out['token_period_us']} us, "

@@ -23,8 +23,8 @@
 // conflict-free. Two stages, one barrier per step. Tiles of 128 x 128 (each
 // wave 2 x 2 MFMA tiles of 32 x 32, so each fragment read feeds two MFMAs)
 // when they still give every CU a tile, else 64 x 64 (one MFMA tile per wave);
-// when even those cannot fill the CUs, K is split and a reduce launch sums the
-// fp32 partials in slice order.
+// when those leave CUs without two blocks, K is split and a reduce launch sums
+// the fp32 partials in slice order.
 #include "pio_common.hpp"
 
 #include <type_traits>
@@ -307,10 +307,12 @@ static int run_tiles(W8fParams p, bool resid, const float* s_w, const float* bia
     p.n_tiles = ceil_div(N, 64 * TN);
     const int tiles = p.m_tiles * p.n_tiles;
     p.per_xcd = ceil_div(tiles, 8);
-    // K slices when the tiles leave most CUs idle and each slice keeps >= 8 steps
+    // K slices while the blocks stay within two per CU and each slice keeps
+    // >= 4 steps (the prefill's M = 127 linears: 2.64 -> 2.35 ms per prompt
+    // against at most one block per CU and 8 steps)
     int splits = 1;
     const int steps = ceil_div(K, WF_BK);
-    while (tiles * splits * 2 <= 256 && steps / (splits * 2) >= 8) splits *= 2;
+    while (tiles * splits * 2 <= 512 && steps / (splits * 2) >= 4) splits *= 2;
     p.ks = ceil_div(steps, splits) * WF_BK;
     splits = ceil_div(K, p.ks);
     if (splits == 1) {

@@ -145,6 +145,17 @@ __global__ __launch_bounds__(256) void pf_attn_kernel(const float* __restrict__ 
     const int part8 = tid & 7, sub = tid >> 3;   // 32 positions x 8 slices of 16 slots
     for (int t0 = 0; t0 < L; t0 += P) {
         const int np = min(P, L - t0);
+        // the pass's values of this thread's two output dims, loaded with the
+        // keys (positions clamped, used only below np): all in flight at once,
+        // their latency behind the scores (one load round trip per pass; a
+        // load per position in the value loop was one round trip each)
+        float v_lo[P / 2], v_hi[P / 2];
+#pragma unroll
+        for (int jj = 0; jj < P / 2; jj++) {
+            const KT* vr = vb + (int64_t)(t0 + min(ph + 2 * jj, np - 1)) * D;
+            v_lo[jj] = PAIR ? (float)vr[2 * d] : (float)vr[d];
+            v_hi[jj] = PAIR ? (float)vr[2 * d + 1] : (float)vr[d + 64];
+        }
         {
             const int t = t0 + sub;
             float kv[16];
@@ -191,17 +202,17 @@ __global__ __launch_bounds__(256) void pf_attn_kernel(const float* __restrict__ 
                 o1[k] *= corr_s[h];
             }
         }
-        for (int j = ph; j < np; j += 2) {
-            const KT* vr = vb + (int64_t)(t0 + j) * D;
-            const float v0 = PAIR ? (float)vr[2 * d] : (float)vr[d];
-            const float v1 = PAIR ? (float)vr[2 * d + 1] : (float)vr[d + 64];
+#pragma unroll
+        for (int jj = 0; jj < P / 2; jj++) {
+            const int j = ph + 2 * jj;
+            if (j >= np) continue;
 #pragma unroll
             for (int k = 0; k < 2; k++) {
                 const int h = hh + 2 * k;
                 if (h >= G) continue;
                 const float e = sc[h][j];
-                o0[k] = fmaf(e, v0, o0[k]);
-                o1[k] = fmaf(e, v1, o1[k]);
+                o0[k] = fmaf(e, v_lo[jj], o0[k]);
+                o1[k] = fmaf(e, v_hi[jj], o1[k]);
             }
         }
         __syncthreads();

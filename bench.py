@@ -46,6 +46,9 @@ Other modes (each prints its own line and exits):
                         the MFMA counter passes profile).
   --gemv-launches S..   10 plain W8 GEMV launches per MxKxN[:f16] shape (the
                         command the HBM traffic counter passes profile).
+  --decode-timeline, --gemm-supply, --gemm-timeline: the decode's per-phase
+                        timeline, the C3 GEMM's operand-supply probe and its
+                        per-block timeline (the profiles' commands).
   --decode-only, --calibrate-copy: see --help.
 """
 from __future__ import annotations
@@ -287,6 +290,54 @@ def gemm_supply(torch):
         out[f"M{M}_N{N}_K{K}"] = row
         log(f"[gemm-supply] {M}x{N}x{K}: {row}")
         del A, B
+    return out
+
+
+def gemm_timeline(torch):
+    """Per-block timeline of the C3 GEMM (fp16 out) through its traced build
+    (pio_probe_gemm_timeline): every block stamps its start, the end of its K
+    loop, its stores issued and its stores complete. Times are relative to the
+    first block's start; five eager launches on warm operands, medians."""
+    import numpy as np
+    from mod_amd import ops
+    out = {}
+    for (K, N) in [(1024, 3072), (3072, 1024), (1024, 2048)]:
+        M = 2048
+        A = torch.randint(-127, 127, (M, K), dtype=torch.int8, device="cuda")
+        B = torch.randint(-127, 127, (N, K), dtype=torch.int8, device="cuda")
+        sa = torch.rand((M,), device="cuda") * 0.01
+        sw = torch.rand((N,), device="cuda") * 0.01
+        y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        words = 4 * 2048
+        tr = torch.zeros((words,), dtype=torch.int64, device="cuda")
+        s = torch.cuda.current_stream().cuda_stream
+        rows = []
+        for rep in range(6):
+            n = ops.lib.pio_probe_gemm_timeline(ops._ptr(A), ops._ptr(sa), ops._ptr(B), ops._ptr(sw), ops._ptr(y),
+                                                M, N, K, ops._ptr(tr), words, s)
+            torch.cuda.synchronize()
+            ops.check(n if n < 0 else 0, "pio_probe_gemm_timeline")
+            t = tr[:4 * n].view(n, 4).cpu().numpy().astype(np.float64)
+            t = t[t[:, 0] > 0]
+            t0 = t[:, 0].min()
+            if rep == 0:
+                continue   # first touch of the operands
+            rows.append({"blocks": int(t.shape[0]),
+                         "first_to_last_start_us": (t[:, 0].max() - t0) / 100,
+                         "k_loop_us_median": float(np.median(t[:, 1] - t[:, 0])) / 100,
+                         "k_loop_us_max": float((t[:, 1] - t[:, 0]).max()) / 100,
+                         "stores_issue_us_median": float(np.median(t[:, 2] - t[:, 1])) / 100,
+                         "stores_drain_us_median": float(np.median(t[:, 3] - t[:, 2])) / 100,
+                         "block_life_us_median": float(np.median(t[:, 3] - t[:, 0])) / 100,
+                         "first_start_to_last_end_us": (t[:, 3].max() - t0) / 100})
+        med = {k: round(float(np.median([r[k] for r in rows])), 2) for k in rows[0]}
+        med["steps"] = K // 128
+        med["per_launch"] = [{k: round(float(v), 2) for k, v in r.items()} for r in rows]
+        out[f"M{M}_N{N}_K{K}"] = med
+        log(f"[gemm-timeline] {M}x{N}x{K}: {dict((k, v) for k, v in med.items() if k != 'per_launch')}")
+        for r in med["per_launch"]:
+            log(f"[gemm-timeline]     {r}")
+        del A, B, y
     return out
 
 
@@ -923,6 +974,9 @@ def main():
                     help="only time the C3 W8A8 GEMM beside its operand-supply probe (the K loop's "
                          "copies alone, in K steps of 128, 256 and 512 bytes per row) and print the "
                          "per-CU rates")
+    ap.add_argument("--gemm-timeline", action="store_true",
+                    help="only run the C3 W8A8 GEMM through its traced build and print the per-block "
+                         "timeline (start, K loop, stores issued, stores complete)")
     ap.add_argument("--weights", action="store_true",
                     help="only time checkpoint loading (config-2 decoder weights, int8 and BF16 "
                          "safetensors from the page cache into HBM) and print its own JSON line")
@@ -978,6 +1032,9 @@ def main():
         return 0
     if args.gemm_supply:
         print(json.dumps(gemm_supply(torch)))
+        return 0
+    if args.gemm_timeline:
+        print(json.dumps(gemm_timeline(torch)))
         return 0
     if args.weights:
         r = bench_weights(torch)

@@ -405,6 +405,16 @@ int pio_qwen3_trace_read(void* dec, void* out, size_t bytes);
  * or 512 bytes per row. bench.py --gemm-supply times it. */
 int pio_probe_gemm_supply(const int8_t* A, const int8_t* B, int M, int N, int K, int BM, int BN, int step,
                           int reps, void* stream);
+/* Measurement, no reference counterpart: the per-block timeline of the dense
+ * W8A8 GEMM with f16 output (the C3 path), through the kernel's traced build
+ * and the tile choice pio_gemm_w8a8 makes for the shape (which must run the
+ * dense direct-to-LDS engine: K % 128 == 0, not a skinny or split-K shape).
+ * trace gets 4 stamps per block of the 100 MHz constant clock (start, K loop
+ * done, stores issued, stores complete); returns how many 4-word entries to
+ * read (entries of blocks the chosen grid lacks stay 0), or a negative
+ * status. */
+int pio_probe_gemm_timeline(const int8_t* q, const float* s_a, const int8_t* w, const float* s_w, void* y, int M,
+                            int N, int K, unsigned long long* trace, int trace_words, void* stream);
 /* Persistent launches of this decoder that were re-run in graph mode because
  * the device could not hold their grid at once. No counterpart in the
  * reference. */

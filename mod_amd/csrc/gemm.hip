@@ -9,6 +9,7 @@
 #include "gemm_core.hpp"
 
 #include <stdlib.h>
+#include <algorithm>
 #include <mutex>
 
 namespace pio {
@@ -27,6 +28,7 @@ struct GemmParams {
     int64_t ldc, c_batch;
     int M, N, K;
     int xr, xc;   // XCD rectangles: tile rows split xr ways, tile columns xc ways (xr*xc == 8), or 0
+    unsigned long long* trace;   // traced launches only (pio_probe_gemm_timeline): 4 stamps per block
 };
 
 // Scaled output value of one int32 accumulator. Each product and the bias add
@@ -62,11 +64,16 @@ constexpr size_t engine_lds() {
 // ENG 2: register-staged v2 engine (any K % 16 == 0); 4: direct-to-LDS v4
 // engine, square tiles, half-step ring (K % 128 == 0); 5: direct-to-LDS v5
 // engine, S-stage ring on the v4 schedule (K % 128 == 0).
-template <int WMT, int WNT, int OUT, int ENG, int S>
+// TR: the traced build (pio_probe_gemm_timeline): thread 0 of every block
+// stamps the 100 MHz constant clock at its start, after the K loop, after the
+// epilogue's stores are issued and once they have completed.
+template <int WMT, int WNT, int OUT, int ENG, int S, bool TR = false>
 __global__ __launch_bounds__(256, 1) void gemm_v2_kernel(GemmParams p, int tiles_n) {
     using T = TileV2<WMT, WNT>;
     extern __shared__ __attribute__((aligned(16))) int8_t lds_v2[];
     const int b = blockIdx.x;
+    unsigned long long ts[2] = {0, 0};
+    if constexpr (TR) ts[0] = wall_clock64();
     int tr, tc;
     if (p.xr) {
         const int x = b % 8, k = b / 8;
@@ -108,6 +115,7 @@ __global__ __launch_bounds__(256, 1) void gemm_v2_kernel(GemmParams p, int tiles
     if constexpr (ENG == 2) mma_tile_v2<WMT, WNT>(A, p.lda, p.M - m0, B, p.ldb, p.N - n0, p.K, lds_v2, acc);
     else if constexpr (ENG == 5) mma_tile_v5<WMT, WNT, S>(A, p.lda, p.M - m0, B, p.ldb, p.N - n0, p.K, lds_v2, acc);
     else mma_tile_v4<WMT>(A, p.lda, p.M - m0, B, p.ldb, p.N - n0, p.K, lds_v2, acc);
+    if constexpr (TR) ts[1] = wall_clock64();
     if (SCALED && LATE) load_scales();
     char* C = (char*)p.C + z * p.c_batch * (OUT == OUT_F16 ? 2 : 4);
     const bool has_bias = SCALED && p.bias;
@@ -139,6 +147,22 @@ __global__ __launch_bounds__(256, 1) void gemm_v2_kernel(GemmParams p, int tiles
     // end-of-kernel writeback (C3's (2048, 3072) f16 output: 15.3 -> 14.2 us
     // with the staging, 13.1 us with the hint; 2-byte stores of half-lines
     // with the hint were slower than without).
+    // traced build: the stamps after the stores are issued, and once every
+    // thread's have completed
+    auto finish = [&]() {
+        if constexpr (TR) {
+            const unsigned long long t2 = wall_clock64();
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                unsigned long long* tr = p.trace + (int64_t)(blockIdx.z * gridDim.x + b) * 4;
+                tr[0] = ts[0];
+                tr[1] = ts[1];
+                tr[2] = t2;
+                tr[3] = wall_clock64();
+            }
+        }
+    };
     constexpr int ES = OUT == OUT_F16 ? 2 : 4;
     constexpr int SROW = T::BN * ES + 32;
     constexpr int CPR = T::BN * ES / 16;   // 16-byte pieces per tile row
@@ -175,6 +199,7 @@ __global__ __launch_bounds__(256, 1) void gemm_v2_kernel(GemmParams p, int tiles
                 __builtin_nontemporal_store(*(const v4i*)(lds_v2 + r * SROW + ch * 16),
                                             (v4i*)(Ct + (int64_t)r * p.ldc * ES + ch * 16));
             }
+            finish();
             return;
         }
     }
@@ -204,11 +229,22 @@ __global__ __launch_bounds__(256, 1) void gemm_v2_kernel(GemmParams p, int tiles
                 }
         }
     }
+    finish();
 }
 
 template <int WMT, int WNT, int OUT, int ENG, int S>
 static int launch_v2_out(const GemmParams& p, dim3 grid, int tn, hipStream_t st) {
     constexpr size_t lds = engine_lds<WMT, WNT, ENG, S>();
+    if constexpr (OUT == OUT_F16 && ENG == 5) {
+        // the traced build exists for the f16-out direct-to-LDS engine (C3)
+        if (p.trace) {
+            PIO_TRY((allow_lds<gemm_v2_kernel<WMT, WNT, OUT, ENG, S, true>>(lds)));
+            gemm_v2_kernel<WMT, WNT, OUT, ENG, S, true><<<grid, 256, lds, st>>>(p, tn);
+            PIO_LAUNCHED();
+            return PIO_OK;
+        }
+    }
+    PIO_REQUIRE(!p.trace, "gemm: the traced build covers the f16-out direct-to-LDS engine only");
     PIO_TRY(allow_lds<gemm_v2_kernel<WMT, WNT, OUT, ENG, S>>(lds));
     gemm_v2_kernel<WMT, WNT, OUT, ENG, S><<<grid, 256, lds, st>>>(p, tn);
     PIO_LAUNCHED();
@@ -978,6 +1014,40 @@ PIO_EXPORT int pio_gemm_w8a8(const int8_t* q, const float* s_a, const int8_t* w,
                              const float* bias, void* y, int y_dtype, int M, int N, int K,
                              void* stream) {
     return gemm_w8a8(q, s_a, w, s_w, bias, y, y_dtype, M, N, K, pick_stream(stream));
+}
+
+// Per-block timeline of the dense W8A8 GEMM (f16 out, the direct-to-LDS
+// engine: the C3 path): the same tile choice and launch as pio_gemm_w8a8 for
+// a shape that runs dense, through the kernel's traced build. trace receives
+// 4 stamps per block (100 MHz constant clock: start, K loop done, stores
+// issued, stores complete), in block order. Returns how many 4-word entries
+// to read -- the block count of the largest tile grid the launch can pick;
+// entries of blocks the chosen grid does not have stay 0 -- or a negative
+// status.
+PIO_EXPORT int pio_probe_gemm_timeline(const int8_t* q, const float* s_a, const int8_t* w, const float* s_w,
+                                       void* y, int M, int N, int K, unsigned long long* trace, int trace_words,
+                                       void* stream) {
+    PIO_REQUIRE(q && s_a && w && s_w && y && trace, "pio_probe_gemm_timeline: null pointer");
+    PIO_REQUIRE(M > 0 && N > 0 && K > 0 && K % 128 == 0 && aligned16(q) && aligned16(w),
+                "pio_probe_gemm_timeline: shape or alignment outside the direct-to-LDS engine");
+    GemmParams p{};
+    p.A = q; p.lda = K;
+    p.B = w; p.ldb = K;
+    p.s_a = s_a; p.s_w = s_w;
+    p.C = y; p.ldc = N;
+    p.M = M; p.N = N; p.K = K;
+    PIO_REQUIRE(!plan_skinny_stream(p).wv && !plan_skinny(p).wv && plan_split(p, 256).splits <= 1,
+                "pio_probe_gemm_timeline: this shape does not run on the dense kernel");
+    int64_t blocks = 0;
+    for (int wnt : {4, 3, 2, 1}) blocks = std::max<int64_t>(blocks, (int64_t)ceil_div(M, 128) * ceil_div(N, 64 * wnt));
+    blocks = std::max<int64_t>(blocks, (int64_t)ceil_div(M, 256) * ceil_div(N, 256));
+    PIO_REQUIRE(trace_words >= 4 * blocks, "pio_probe_gemm_timeline: trace holds %d words, need %lld", trace_words,
+                (long long)(4 * blocks));
+    p.trace = trace;
+    const hipStream_t st = pick_stream(stream);
+    PIO_HIP(hipMemsetAsync(trace, 0, (size_t)trace_words * 8, st));
+    PIO_TRY(launch_dense(p, OUT_F16, 1, st));
+    return (int)blocks;
 }
 
 // pio_gemm_w8a8 without any allocation: the K-slice partials live in the

@@ -154,6 +154,7 @@ SIGNATURES: dict[str, tuple] = {
     "pio_qwen3_persistent_replays": (_i, [_vp]),
     "pio_qwen3_prefill": (_i, [_vp, _i, _i]),
     "pio_probe_gemm_supply": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp]),
+    "pio_probe_gemm_timeline": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _vp]),
     "pio_qwen3_trace_next": (_i, [_vp, _i]),
     "pio_qwen3_trace_bytes": (_sz, [_vp]),
     "pio_qwen3_trace_read": (_i, [_vp, _vp, _sz]),

@@ -299,9 +299,19 @@ static int launch_w8f(const W8fParams& p, int splits, hipStream_t st) {
     return PIO_OK;
 }
 
+// W8fSplit: a caller that finishes the K-slice sums itself (the prefill's
+// fused epilogues). When the plan splits K, the slices' unscaled fp32 partials
+// part[z][m][n] (z < splits) are left in `ws` and no reduce runs; otherwise
+// y is written as usual and splits = 0.
+struct W8fSplit {
+    Scratch* ws;
+    const float* part;
+    int splits;
+};
+
 template <int NL, typename XT, typename YT, int TM, int TN>
 static int run_tiles(W8fParams p, bool resid, const float* s_w, const float* bias, YT* y, int64_t ldy,
-                     hipStream_t st) {
+                     hipStream_t st, W8fSplit* out) {
     const int M = p.M, N = p.N, K = p.K;
     p.m_tiles = ceil_div(M, 64 * TM);
     p.n_tiles = ceil_div(N, 64 * TN);
@@ -315,15 +325,25 @@ static int run_tiles(W8fParams p, bool resid, const float* s_w, const float* bia
     while (tiles * splits * 2 <= 512 && steps / (splits * 2) >= 4) splits *= 2;
     p.ks = ceil_div(steps, splits) * WF_BK;
     splits = ceil_div(K, p.ks);
+    if (out) {
+        out->part = nullptr;
+        out->splits = 0;
+    }
     if (splits == 1) {
         p.ks = K;
         return resid ? launch_w8f<NL, XT, YT, WF_RESID, TM, TN>(p, 1, st)
                      : launch_w8f<NL, XT, YT, WF_STORE, TM, TN>(p, 1, st);
     }
-    Scratch ws;
+    Scratch own;
+    Scratch& ws = out ? *out->ws : own;
     PIO_TRY(ws.get((size_t)splits * M * N * sizeof(float), st));
     p.y = ws.ptr;
     PIO_TRY((launch_w8f<NL, XT, YT, WF_PARTIAL, TM, TN>(p, splits, st)));
+    if (out) {
+        out->part = (const float*)ws.ptr;
+        out->splits = splits;
+        return PIO_OK;
+    }
     const int64_t MN = (int64_t)M * N;
     if (resid)
         gemm_w8f_reduce_kernel<YT, true><<<(unsigned)ceil_div(MN, 256), 256, 0, st>>>((const float*)ws.ptr, splits, M,
@@ -337,7 +357,7 @@ static int run_tiles(W8fParams p, bool resid, const float* s_w, const float* bia
 
 template <typename XT, typename YT>
 static int run_w8f(const XT* x, int64_t ldx, const int8_t* w, const float* s_w, const float* bias, YT* y,
-                   int64_t ldy, int M, int N, int K, bool resid, hipStream_t st) {
+                   int64_t ldy, int M, int N, int K, bool resid, hipStream_t st, W8fSplit* out) {
     constexpr int NL = std::is_same<XT, float>::value ? 3 : 1;
     W8fParams p{};
     p.x = x; p.w = w; p.s_w = s_w; p.bias = bias; p.y = y;
@@ -346,14 +366,12 @@ static int run_w8f(const XT* x, int64_t ldx, const int8_t* w, const float* s_w, 
     // 128 x 128 tiles (every fragment read feeds two MFMAs) when they still
     // give every CU a tile; 64 x 64 tiles (with K slices if needed) otherwise
     if ((int64_t)ceil_div(M, 128) * ceil_div(N, 128) >= 256)
-        return run_tiles<NL, XT, YT, 2, 2>(p, resid, s_w, bias, y, ldy, st);
-    return run_tiles<NL, XT, YT, 1, 1>(p, resid, s_w, bias, y, ldy, st);
+        return run_tiles<NL, XT, YT, 2, 2>(p, resid, s_w, bias, y, ldy, st, out);
+    return run_tiles<NL, XT, YT, 1, 1>(p, resid, s_w, bias, y, ldy, st, out);
 }
 
-// Row strides: ldx elements of x, ldy elements of y (W rows are K bytes).
-// resid: y += the linear's output (y fp32 or fp16, read before it is written).
-int gemm_w8f(const void* x, int x_dtype, int64_t ldx, const int8_t* w, const float* s_w, const float* bias,
-             void* y, int y_dtype, int64_t ldy, int M, int N, int K, bool resid, hipStream_t st) {
+static int check_w8f(const void* x, int x_dtype, int64_t ldx, const int8_t* w, const float* s_w, const void* y,
+                     int y_dtype, int M, int N, int K) {
     PIO_REQUIRE(x && w && s_w && y, "gemm_w8f: null pointer");
     PIO_REQUIRE(M >= 0 && N >= 0 && K >= 0, "gemm_w8f: negative shape");
     PIO_REQUIRE(K % 16 == 0 && ldx % 8 == 0, "gemm_w8f: K=%d and the x row stride must be multiples of 16 and 8",
@@ -361,15 +379,40 @@ int gemm_w8f(const void* x, int x_dtype, int64_t ldx, const int8_t* w, const flo
     PIO_REQUIRE(aligned16(x) && aligned16(w), "gemm_w8f: x and W must be 16-byte aligned");
     PIO_REQUIRE(x_dtype == PIO_F32 || x_dtype == PIO_F16, "gemm_w8f: x must be fp32 or fp16");
     PIO_REQUIRE(y_dtype == PIO_F32 || y_dtype == PIO_F16, "gemm_w8f: y must be fp32 or fp16");
+    return PIO_OK;
+}
+
+// Row strides: ldx elements of x, ldy elements of y (W rows are K bytes).
+// resid: y += the linear's output (y fp32 or fp16, read before it is written).
+int gemm_w8f(const void* x, int x_dtype, int64_t ldx, const int8_t* w, const float* s_w, const float* bias,
+             void* y, int y_dtype, int64_t ldy, int M, int N, int K, bool resid, hipStream_t st) {
+    PIO_TRY(check_w8f(x, x_dtype, ldx, w, s_w, y, y_dtype, M, N, K));
     if (M == 0 || N == 0) return PIO_OK;
     if (x_dtype == PIO_F32) {
         if (y_dtype == PIO_F32)
-            return run_w8f((const float*)x, ldx, w, s_w, bias, (float*)y, ldy, M, N, K, resid, st);
-        return run_w8f((const float*)x, ldx, w, s_w, bias, (_Float16*)y, ldy, M, N, K, resid, st);
+            return run_w8f((const float*)x, ldx, w, s_w, bias, (float*)y, ldy, M, N, K, resid, st, nullptr);
+        return run_w8f((const float*)x, ldx, w, s_w, bias, (_Float16*)y, ldy, M, N, K, resid, st, nullptr);
     }
     if (y_dtype == PIO_F32)
-        return run_w8f((const _Float16*)x, ldx, w, s_w, bias, (float*)y, ldy, M, N, K, resid, st);
-    return run_w8f((const _Float16*)x, ldx, w, s_w, bias, (_Float16*)y, ldy, M, N, K, resid, st);
+        return run_w8f((const _Float16*)x, ldx, w, s_w, bias, (float*)y, ldy, M, N, K, resid, st, nullptr);
+    return run_w8f((const _Float16*)x, ldx, w, s_w, bias, (_Float16*)y, ldy, M, N, K, resid, st, nullptr);
+}
+
+// fp32 x and y. When the plan splits K, only the slices' unscaled partials
+// are produced (*part, *splits, in `ws`; y untouched) for the caller to finish;
+// otherwise y is written (scaled, + bias, + y when resid) and *splits = 0.
+int gemm_w8f_split(const float* x, int64_t ldx, const int8_t* w, const float* s_w, const float* bias, float* y,
+                   int64_t ldy, int M, int N, int K, bool resid, Scratch& ws, const float** part, int* splits,
+                   hipStream_t st) {
+    PIO_TRY(check_w8f(x, PIO_F32, ldx, w, s_w, y, PIO_F32, M, N, K));
+    W8fSplit out{&ws, nullptr, 0};
+    *part = nullptr;
+    *splits = 0;
+    if (M == 0 || N == 0) return PIO_OK;
+    PIO_TRY(run_w8f(x, ldx, w, s_w, bias, y, ldy, M, N, K, resid, st, &out));
+    *part = out.part;
+    *splits = out.splits;
+    return PIO_OK;
 }
 
 }  // namespace pio

@@ -27,6 +27,9 @@ namespace pio {
 
 int gemm_w8f(const void* x, int x_dtype, int64_t ldx, const int8_t* w, const float* s_w, const float* bias,
              void* y, int y_dtype, int64_t ldy, int M, int N, int K, bool resid, hipStream_t st);
+int gemm_w8f_split(const float* x, int64_t ldx, const int8_t* w, const float* s_w, const float* bias, float* y,
+                   int64_t ldy, int M, int N, int K, bool resid, Scratch& ws, const float** part, int* splits,
+                   hipStream_t st);
 
 // x[m] = embed[ids[pos0 + m]] (an out-of-range id reads row 0, as the step).
 __global__ __launch_bounds__(256) void pf_embed_kernel(const float* __restrict__ embed, const int32_t* __restrict__ ids,
@@ -65,18 +68,15 @@ __global__ __launch_bounds__(256) void pf_rmsnorm_kernel(const float* __restrict
 // Rotate-half RoPE at each row's position on the q and k heads of qkv (row m,
 // position pos0 + m; q rotated in place), then k and v into the cache rows of
 // that position, fp32 or fp16 in the step kernels' layout (fp16 rows paired:
-// slot 2i holds dim i, slot 2i + 1 dim i + 64). Block (m, head), 64 threads:
-// thread i takes dims (i, i + 64).
+// slot 2i holds dim i, slot 2i + 1 dim i + 64). Thread i of (m, head) takes
+// dims (i, i + 64) with values a, b.
 template <typename KT>
-__global__ __launch_bounds__(64) void pf_rope_kv_kernel(float* __restrict__ qkv, int ldq, int pos0, int nq, int nkv,
-                                                        const float* __restrict__ cos_t,
-                                                        const float* __restrict__ sin_t, KT* __restrict__ kc,
-                                                        KT* __restrict__ vc, int max_seq) {
+__device__ __forceinline__ void pf_rope_kv_put(float* __restrict__ qkv, int ldq, int pos0, int nq, int nkv,
+                                               const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                                               KT* __restrict__ kc, KT* __restrict__ vc, int max_seq, int m, int head,
+                                               int i, float a, float b) {
     constexpr int D = 128, HALF = 64;
-    const int m = blockIdx.x, head = blockIdx.y, i = threadIdx.x;
     const int pos = pos0 + m;
-    float* row = qkv + (int64_t)m * ldq + head * D;
-    float a = row[i], b = row[i + HALF];
     if (head < nq + nkv) {
         const float c = cos_t[(int64_t)pos * HALF + i], s = sin_t[(int64_t)pos * HALF + i];
         const float a2 = a * c - b * s, b2 = a * s + b * c;
@@ -84,6 +84,7 @@ __global__ __launch_bounds__(64) void pf_rope_kv_kernel(float* __restrict__ qkv,
         b = b2;
     }
     if (head < nq) {
+        float* row = qkv + (int64_t)m * ldq + head * D;
         row[i] = a;
         row[i + HALF] = b;
         return;
@@ -100,6 +101,100 @@ __global__ __launch_bounds__(64) void pf_rope_kv_kernel(float* __restrict__ qkv,
     } else {
         dst[i] = a;
         dst[i + HALF] = b;
+    }
+}
+
+// Block (m, head), 64 threads: RoPE and KV rows from the stored q/k/v.
+template <typename KT>
+__global__ __launch_bounds__(64) void pf_rope_kv_kernel(float* __restrict__ qkv, int ldq, int pos0, int nq, int nkv,
+                                                        const float* __restrict__ cos_t,
+                                                        const float* __restrict__ sin_t, KT* __restrict__ kc,
+                                                        KT* __restrict__ vc, int max_seq) {
+    const int m = blockIdx.x, head = blockIdx.y, i = threadIdx.x;
+    const float* row = qkv + (int64_t)m * ldq + head * 128;
+    pf_rope_kv_put<KT>(qkv, ldq, pos0, nq, nkv, cos_t, sin_t, kc, vc, max_seq, m, head, i, row[i], row[i + 64]);
+}
+
+// The q/k/v linear's K slices finished here instead of by the GEMM's reduce:
+// y = (sum over slices in order) * s + bias, exactly as that reduce forms it,
+// then RoPE and the KV rows as pf_rope_kv_kernel (one launch instead of two).
+template <typename KT>
+__global__ __launch_bounds__(64) void pf_qkv_finish_kernel(const float* __restrict__ part, int splits, int N,
+                                                           const float* __restrict__ s_w,
+                                                           const float* __restrict__ bias, float* __restrict__ qkv,
+                                                           int ldq, int pos0, int nq, int nkv,
+                                                           const float* __restrict__ cos_t,
+                                                           const float* __restrict__ sin_t, KT* __restrict__ kc,
+                                                           KT* __restrict__ vc, int max_seq, int M) {
+    const int m = blockIdx.x, head = blockIdx.y, i = threadIdx.x;
+    const int c0 = head * 128 + i, c1 = c0 + 64;
+    const int64_t MN = (int64_t)M * N, r = (int64_t)m * N;
+    float a = 0.f, b = 0.f;
+    for (int z = 0; z < splits; z++) {
+        a += part[z * MN + r + c0];
+        b += part[z * MN + r + c1];
+    }
+    a = a * s_w[c0];
+    b = b * s_w[c1];
+    if (bias) {
+        a += bias[c0];
+        b += bias[c1];
+    }
+    pf_rope_kv_put<KT>(qkv, ldq, pos0, nq, nkv, cos_t, sin_t, kc, vc, max_seq, m, head, i, a, b);
+}
+
+// The gate_up linear's K slices finished with SwiGLU: act[m][i] = silu(g) * u
+// for g, u formed as the GEMM's reduce forms them (no bias), the arithmetic of
+// pf_swiglu_kernel.
+__global__ __launch_bounds__(256) void pf_gu_finish_kernel(const float* __restrict__ part, int splits, int M, int I,
+                                                           const float* __restrict__ s_w, float* __restrict__ act) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= (int64_t)M * I) return;
+    const int64_t m = e / I, i = e - m * I, MN = (int64_t)M * 2 * I, r = m * 2 * I;
+    float g = 0.f, u = 0.f;
+    for (int z = 0; z < splits; z++) {
+        g += part[z * MN + r + i];
+        u += part[z * MN + r + I + i];
+    }
+    g = g * s_w[i];
+    u = u * s_w[I + i];
+    act[e] = g / (1.0f + expf(-g)) * u;
+}
+
+// A residual linear's K slices finished into x (x += slices * s, as the
+// GEMM's reduce forms it), then -- when w is given -- the RMSNorm of the new
+// row into h with pf_rmsnorm_kernel's arithmetic. One block per row; H % 4 == 0.
+__global__ __launch_bounds__(256) void pf_resid_norm_kernel(const float* __restrict__ part, int splits, int M, int H,
+                                                            const float* __restrict__ s_w, float* __restrict__ x,
+                                                            const float* __restrict__ w, float* __restrict__ h,
+                                                            float eps) {
+    __shared__ float red[4];
+    const int m = blockIdx.x, tid = threadIdx.x;
+    const int64_t MN = (int64_t)M * H;
+    float* xr = x + (int64_t)m * H;
+    float ss = 0.f;
+    for (int i = tid * 4; i < H; i += 1024) {
+        float v[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            float acc = 0.f;
+            for (int z = 0; z < splits; z++) acc += part[z * MN + (int64_t)m * H + i + k];
+            v[k] = acc * s_w[i + k] + xr[i + k];
+        }
+        const float4 a = make_float4(v[0], v[1], v[2], v[3]);
+        *(float4*)(xr + i) = a;
+        ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+    }
+    if (!w) return;
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    const float r = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + eps);
+    float* hr = h + (int64_t)m * H;
+    for (int i = tid * 4; i < H; i += 1024) {
+        const float4 a = *(const float4*)(xr + i);
+        const float4 g = *(const float4*)(w + i);
+        *(float4*)(hr + i) = make_float4(a.x * r * g.x, a.y * r * g.y, a.z * r * g.z, a.w * r * g.w);
     }
 }
 
@@ -275,37 +370,86 @@ int prefill(Qwen3Dec* d, int M, bool logits) {
     pf_embed_kernel<<<M, 256, 0, st>>>(d->embed, d->ids, pos0, x, H, c.vocab);
     PIO_LAUNCHED();
     const float scale = 1.0f / sqrtf((float)D);
+    // When a linear's plan splits K, its slices are finished by the next step's
+    // own kernel (RoPE + KV rows, SwiGLU, residual + the next RMSNorm) instead
+    // of by the GEMM's reduce launch; h_ready: h already holds this layer's
+    // input RMSNorm (the previous layer's down finish wrote it).
+    bool h_ready = false;
     for (int l = 0; l < c.n_layers; l++) {
         const pio_qwen3_layer& L = d->layers[l];
         const int64_t lkv = (int64_t)l * nkv * c.max_seq * D;   // elements
-        pf_rmsnorm_kernel<<<M, 256, 0, st>>>(x, L.in_norm, h, H, c.rms_eps);
-        PIO_LAUNCHED();
-        PIO_TRY(gemm_w8f(h, PIO_F32, H, L.w_qkv, L.s_qkv, L.b_qkv, qkv, PIO_F32, nqkv, M, nqkv, H, false, st));
-        if (d->kv16) {
-            _Float16* kc = (_Float16*)d->kc + lkv;
-            _Float16* vc = (_Float16*)d->vc + lkv;
-            pf_rope_kv_kernel<_Float16><<<dim3(M, nq + 2 * nkv), 64, 0, st>>>(qkv, nqkv, pos0, nq, nkv, d->cos_t,
-                                                                                d->sin_t, kc, vc, c.max_seq);
+        if (!h_ready) {
+            pf_rmsnorm_kernel<<<M, 256, 0, st>>>(x, L.in_norm, h, H, c.rms_eps);
             PIO_LAUNCHED();
-            pf_attn_kernel<_Float16><<<dim3(M, nkv), 256, 0, st>>>(qkv, nqkv, pos0, nq, nkv, kc, vc, c.max_seq,
-                                                                     scale, o, nq * D);
-        } else {
-            float* kc = (float*)d->kc + lkv;
-            float* vc = (float*)d->vc + lkv;
-            pf_rope_kv_kernel<float><<<dim3(M, nq + 2 * nkv), 64, 0, st>>>(qkv, nqkv, pos0, nq, nkv, d->cos_t,
-                                                                             d->sin_t, kc, vc, c.max_seq);
-            PIO_LAUNCHED();
-            pf_attn_kernel<float><<<dim3(M, nkv), 256, 0, st>>>(qkv, nqkv, pos0, nq, nkv, kc, vc, c.max_seq, scale,
-                                                                  o, nq * D);
         }
-        PIO_LAUNCHED();
-        PIO_TRY(gemm_w8f(o, PIO_F32, nq * D, L.w_o, L.s_o, nullptr, x, PIO_F32, H, M, H, nq * D, true, st));
-        pf_rmsnorm_kernel<<<M, 256, 0, st>>>(x, L.post_norm, h, H, c.rms_eps);
-        PIO_LAUNCHED();
-        PIO_TRY(gemm_w8f(h, PIO_F32, H, L.w_gu, L.s_gu, nullptr, gu, PIO_F32, 2 * I, M, 2 * I, H, false, st));
-        pf_swiglu_kernel<<<ceil_div((int64_t)M * I, 256), 256, 0, st>>>(gu, act, M, I);
-        PIO_LAUNCHED();
-        PIO_TRY(gemm_w8f(act, PIO_F32, I, L.w_down, L.s_down, nullptr, x, PIO_F32, H, M, H, I, true, st));
+        {
+            Scratch pw;
+            const float* part;
+            int sp;
+            PIO_TRY(gemm_w8f_split(h, H, L.w_qkv, L.s_qkv, L.b_qkv, qkv, nqkv, M, nqkv, H, false, pw, &part, &sp, st));
+            const dim3 g(M, nq + 2 * nkv);
+            if (d->kv16) {
+                _Float16* kc = (_Float16*)d->kc + lkv;
+                _Float16* vc = (_Float16*)d->vc + lkv;
+                if (sp)
+                    pf_qkv_finish_kernel<_Float16><<<g, 64, 0, st>>>(part, sp, nqkv, L.s_qkv, L.b_qkv, qkv, nqkv, pos0,
+                                                                     nq, nkv, d->cos_t, d->sin_t, kc, vc, c.max_seq, M);
+                else
+                    pf_rope_kv_kernel<_Float16><<<g, 64, 0, st>>>(qkv, nqkv, pos0, nq, nkv, d->cos_t, d->sin_t, kc, vc,
+                                                                  c.max_seq);
+                PIO_LAUNCHED();
+                pf_attn_kernel<_Float16><<<dim3(M, nkv), 256, 0, st>>>(qkv, nqkv, pos0, nq, nkv, kc, vc, c.max_seq,
+                                                                         scale, o, nq * D);
+            } else {
+                float* kc = (float*)d->kc + lkv;
+                float* vc = (float*)d->vc + lkv;
+                if (sp)
+                    pf_qkv_finish_kernel<float><<<g, 64, 0, st>>>(part, sp, nqkv, L.s_qkv, L.b_qkv, qkv, nqkv, pos0, nq,
+                                                                  nkv, d->cos_t, d->sin_t, kc, vc, c.max_seq, M);
+                else
+                    pf_rope_kv_kernel<float><<<g, 64, 0, st>>>(qkv, nqkv, pos0, nq, nkv, d->cos_t, d->sin_t, kc, vc,
+                                                               c.max_seq);
+                PIO_LAUNCHED();
+                pf_attn_kernel<float><<<dim3(M, nkv), 256, 0, st>>>(qkv, nqkv, pos0, nq, nkv, kc, vc, c.max_seq,
+                                                                      scale, o, nq * D);
+            }
+            PIO_LAUNCHED();
+        }
+        {
+            Scratch pw;
+            const float* part;
+            int sp;
+            PIO_TRY(gemm_w8f_split(o, nq * D, L.w_o, L.s_o, nullptr, x, H, M, H, nq * D, true, pw, &part, &sp, st));
+            if (sp)
+                pf_resid_norm_kernel<<<M, 256, 0, st>>>(part, sp, M, H, L.s_o, x, L.post_norm, h, c.rms_eps);
+            else
+                pf_rmsnorm_kernel<<<M, 256, 0, st>>>(x, L.post_norm, h, H, c.rms_eps);
+            PIO_LAUNCHED();
+        }
+        {
+            Scratch pw;
+            const float* part;
+            int sp;
+            PIO_TRY(gemm_w8f_split(h, H, L.w_gu, L.s_gu, nullptr, gu, 2 * I, M, 2 * I, H, false, pw, &part, &sp, st));
+            if (sp)
+                pf_gu_finish_kernel<<<ceil_div((int64_t)M * I, 256), 256, 0, st>>>(part, sp, M, I, L.s_gu, act);
+            else
+                pf_swiglu_kernel<<<ceil_div((int64_t)M * I, 256), 256, 0, st>>>(gu, act, M, I);
+            PIO_LAUNCHED();
+        }
+        {
+            Scratch pw;
+            const float* part;
+            int sp;
+            PIO_TRY(gemm_w8f_split(act, I, L.w_down, L.s_down, nullptr, x, H, M, H, I, true, pw, &part, &sp, st));
+            const bool next = l + 1 < c.n_layers;
+            h_ready = sp && next;
+            if (sp) {
+                pf_resid_norm_kernel<<<M, 256, 0, st>>>(part, sp, M, H, L.s_down, x,
+                                                        next ? d->layers[l + 1].in_norm : nullptr, h, c.rms_eps);
+                PIO_LAUNCHED();
+            }
+        }
     }
     // the last row as the decoder's x; the device position: the step tail
     // (logits, argmax, next id) advances it from the last row's position

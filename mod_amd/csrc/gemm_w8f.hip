@@ -280,7 +280,8 @@ __global__ __launch_bounds__(256) void gemm_w8f_reduce_kernel(const float* __res
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x, MN = (int64_t)M * N;
     if (i >= MN) return;
     float acc = 0.f;
-    for (int z = 0; z < splits; z++) acc += part[z * MN + i];
+#pragma unroll 8
+    for (int z = 0; z < splits; z++) acc += part[z * MN + i];   // unrolled: 8 slices' loads in flight
     const int n = (int)(i % N);
     const int64_t m = i / N;
     float v = acc * s_w[n];

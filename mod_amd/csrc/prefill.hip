@@ -130,6 +130,7 @@ __global__ __launch_bounds__(64) void pf_qkv_finish_kernel(const float* __restri
     const int c0 = head * 128 + i, c1 = c0 + 64;
     const int64_t MN = (int64_t)M * N, r = (int64_t)m * N;
     float a = 0.f, b = 0.f;
+#pragma unroll 8
     for (int z = 0; z < splits; z++) {
         a += part[z * MN + r + c0];
         b += part[z * MN + r + c1];
@@ -152,6 +153,7 @@ __global__ __launch_bounds__(256) void pf_gu_finish_kernel(const float* __restri
     if (e >= (int64_t)M * I) return;
     const int64_t m = e / I, i = e - m * I, MN = (int64_t)M * 2 * I, r = m * 2 * I;
     float g = 0.f, u = 0.f;
+#pragma unroll 8
     for (int z = 0; z < splits; z++) {
         g += part[z * MN + r + i];
         u += part[z * MN + r + I + i];
@@ -174,14 +176,21 @@ __global__ __launch_bounds__(256) void pf_resid_norm_kernel(const float* __restr
     float* xr = x + (int64_t)m * H;
     float ss = 0.f;
     for (int i = tid * 4; i < H; i += 1024) {
-        float v[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            float acc = 0.f;
-            for (int z = 0; z < splits; z++) acc += part[z * MN + (int64_t)m * H + i + k];
-            v[k] = acc * s_w[i + k] + xr[i + k];
+        // the slices' 4 columns as one 16-byte load each, unrolled so that the
+        // loads of up to 8 slices are in flight together (a load per slice and
+        // column, each waited for, was most of this kernel's time)
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
+        for (int z = 0; z < splits; z++) {
+            const float4 q = *(const float4*)(part + z * MN + (int64_t)m * H + i);
+            acc.x += q.x;
+            acc.y += q.y;
+            acc.z += q.z;
+            acc.w += q.w;
         }
-        const float4 a = make_float4(v[0], v[1], v[2], v[3]);
+        const float4 xo = *(const float4*)(xr + i);
+        const float4 sw = *(const float4*)(s_w + i);
+        const float4 a = make_float4(acc.x * sw.x + xo.x, acc.y * sw.y + xo.y, acc.z * sw.z + xo.z, acc.w * sw.w + xo.w);
         *(float4*)(xr + i) = a;
         ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
     }

@@ -686,11 +686,16 @@ __global__ __launch_bounds__(256) void gemv_split_reduce_kernel(const float* __r
                                                                 const float* __restrict__ bias, YT* __restrict__ y) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x, MN = (int64_t)M * N;
     if (i >= MN) return;
-    float acc = 0.f;
-    for (int z = 0; z < splits; z++) acc += ws[z * MN + i];
+    // the scale and bias first, then the slices with their loop unrolled, so
+    // every load is in flight together instead of one round trip each
     const int n = (int)(i % N);
-    float val = acc * s_w[n];
-    if (bias) val += bias[n];
+    const float sw = s_w[n];
+    const float bn = (bias ? bias : s_w)[n];
+    float acc = 0.f;
+#pragma unroll 8
+    for (int z = 0; z < splits; z++) acc += ws[z * MN + i];
+    float val = acc * sw;
+    if (bias) val += bn;
     y[i] = from_f32<YT>(val);
 }
 

@@ -100,7 +100,9 @@ static int rms_norm_impl(Tensor* x, Tensor* res, Tensor* w, Tensor* out, float e
 // (tensor_ops.c:384-413). k keeps its own head count: the reference loop
 // walks k with q's (one pointer per q head), which for a grouped-query k
 // reads past its end; with Hk == Hq the two agree.
-__global__ __launch_bounds__(MO_THREADS) void mo_rope_kernel(const float* __restrict__ q, const float* __restrict__ k,
+// q / k may be out_q / out_k (in place): each thread reads its element pair
+// before it writes the same pair, so neither is marked __restrict__.
+__global__ __launch_bounds__(MO_THREADS) void mo_rope_kernel(const float* q, const float* k,
                                                              const float* __restrict__ cs, const float* __restrict__ sn,
                                                              float* oq, float* ok, int64_t tok, int S, int Hq, int Hk,
                                                              int half) {
@@ -133,8 +135,11 @@ __global__ __launch_bounds__(MO_THREADS) void mo_rope_kernel(const float* __rest
 // gate_up[r][h..2h) (:588-604).
 __device__ __forceinline__ float mo_silu(float x) { return x * (1.0f / (1.0f + expf(-x))); }
 
-__global__ __launch_bounds__(MO_THREADS) void mo_act_kernel(const float* __restrict__ a, const float* __restrict__ b,
-                                                            float* out, int64_t n, int hidden, int mode) {
+// silu and swiglu may run in place (out == a or b: each element is read and
+// written by one thread); the fused form may not (act_impl refuses an out that
+// overlaps gate_up: an output row lands on input rows other threads read).
+__global__ __launch_bounds__(MO_THREADS) void mo_act_kernel(const float* a, const float* b, float* out, int64_t n,
+                                                            int hidden, int mode) {
     for (int64_t i = (int64_t)blockIdx.x * MO_THREADS + threadIdx.x; i < n; i += (int64_t)gridDim.x * MO_THREADS) {
         if (mode == 0) {
             out[i] = mo_silu(a[i]);
@@ -151,7 +156,7 @@ __global__ __launch_bounds__(MO_THREADS) void mo_act_kernel(const float* __restr
 // ------------------------------------------------------------ softmax ------
 // One block per row: m = max(-1e9, row); e = exp(x - m); out = e * (1 / sum e)
 // (tensor_ops.c:351-367).
-__global__ __launch_bounds__(MO_THREADS) void mo_softmax_kernel(const float* __restrict__ x, float* y, int cols) {
+__global__ __launch_bounds__(MO_THREADS) void mo_softmax_kernel(const float* x, float* y, int cols) {   // y may be x
     __shared__ float red[4];
     const float* xr = x + (int64_t)blockIdx.x * cols;
     float* yr = y + (int64_t)blockIdx.x * cols;
@@ -274,8 +279,8 @@ struct SliceGeom {
 };
 __global__ __launch_bounds__(MO_THREADS) void mo_slice_kernel(const float* __restrict__ src, float* dst, int n,
                                                               int other_size, SliceGeom g, int gather) {
-    for (int i = blockIdx.x * MO_THREADS + threadIdx.x; i < n; i += gridDim.x * MO_THREADS) {
-        int rem = i;
+    for (int64_t i = (int64_t)blockIdx.x * MO_THREADS + threadIdx.x; i < n; i += (int64_t)gridDim.x * MO_THREADS) {
+        int rem = (int)i;
         int64_t off = 0;
         for (int d = 0; d < g.ndim; d++) {
             if (g.walk[d] == 0) continue;
@@ -372,6 +377,8 @@ static int act_impl(Tensor* a, Tensor* b, Tensor* out, int mode, const char* nm)
         hidden = last_dim(out);
         PIO_REQUIRE(hidden > 0 && out->size % hidden == 0 && a->size >= 2 * (int64_t)out->size,
                     "%s: gate_up needs 2 x %d columns per row of out", nm, hidden);
+        const float *o0 = out->data, *o1 = out->data + out->size, *a0 = a->data, *a1 = a->data + a->size;
+        PIO_REQUIRE(o1 <= a0 || a1 <= o0, "%s: out overlaps gate_up (threads would overwrite rows others read)", nm);
     } else {
         PIO_REQUIRE(a->size >= out->size, "%s: input smaller than out", nm);
     }

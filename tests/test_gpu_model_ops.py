@@ -8,6 +8,7 @@ RTOL = 2e-5 of the float64 oracle (conftest.assert_rel: relative, with a floor
 of 1e-2 x the output rms; attention on the scale of max |v|, its outputs being
 convex combinations of v rows), which covers fp32 summation order and the
 device expf / sqrtf against float64."""
+import ctypes
 import sys
 
 import numpy as np
@@ -148,6 +149,51 @@ def test_ops_reject_host_tensors_and_bad_shapes(B):
     k = _t(B, np.ones((1, 4, 2, 8), np.float32))
     with pytest.raises(RocmError, match="Hk dividing"):
         B.scaled_dot_product_attention(q, k, k)
+
+
+def test_in_place_forms_and_fused_overlap_refused(B):
+    """silu, swiglu, softmax and RoPE with the output being an input (each
+    element is read and written by one thread) equal their out-of-place
+    results bit for bit; the fused gate_up SwiGLU refuses an output that
+    overlaps gate_up, whose rows other threads still read."""
+    from mod_amd import ops
+    from mod_amd.ops import lib
+    _say("in-place forms")
+    rng = np.random.default_rng(11)
+    g = (rng.standard_normal(5000) * 4).astype(np.float32)
+    u = rng.standard_normal(5000).astype(np.float32)
+    want = _t(B, g).silu().numpy()
+    t = _t(B, g)
+    assert lib.tensor_silu_status(t._handle, t._handle) == ops.OK
+    assert np.array_equal(t.numpy(), want)
+    want = _t(B, g).swiglu(_t(B, u)).numpy()
+    t, tu = _t(B, g), _t(B, u)
+    assert lib.tensor_swiglu_status(t._handle, tu._handle, t._handle) == ops.OK
+    assert np.array_equal(t.numpy(), want)
+    x = (rng.standard_normal((6, 777)) * 3).astype(np.float32)
+    want = _t(B, x).softmax().numpy()
+    t = _t(B, x)
+    assert lib.tensor_softmax_status(t._handle, t._handle) == ops.OK
+    assert np.array_equal(t.numpy(), want)
+    q = rng.standard_normal((2, 3, 4, 64)).astype(np.float32)
+    k = rng.standard_normal((2, 3, 2, 64)).astype(np.float32)
+    ang = rng.uniform(-9, 9, (3, 32)).astype(np.float32)
+    c, sn = _t(B, np.cos(ang)), _t(B, np.sin(ang))
+    wq, wk = _t(B, q).rope(_t(B, k), c, sn)
+    tq, tk = _t(B, q), _t(B, k)
+    assert lib.tensor_rope_status(tq._handle, tk._handle, c._handle, sn._handle, tq._handle,
+                                  tk._handle) == ops.OK
+    assert np.array_equal(tq.numpy(), wq.numpy()) and np.array_equal(tk.numpy(), wk.numpy())
+    gu = _t(B, rng.standard_normal((4, 256)).astype(np.float32))
+    half = B.Tensor([4, 128])
+    # a [4, 128] tensor over gate_up's first 512 floats (the struct is the
+    # reference's plain Tensor, so a caller can build such a view)
+    g0 = gu._handle.contents
+    shp = (ctypes.c_int * 2)(4, 128)
+    view = ops.CTensor(g0.data, ctypes.cast(shp, ctypes.POINTER(ctypes.c_int)), 2, 512, g0.device_id)
+    assert lib.tensor_fused_gate_up_swiglu_status(gu._handle, ctypes.byref(view)) == ops.ERR_INVALID
+    assert "overlaps" in ops.last_error()
+    assert lib.tensor_fused_gate_up_swiglu_status(gu._handle, half._handle) == ops.OK
 
 
 def test_reference_style_decoder_layer_with_kv_cache(B):

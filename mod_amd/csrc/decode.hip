@@ -372,19 +372,19 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(
 #pragma unroll
         for (int h = 0; h < ATT_MAX_G; h++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                if (h >= G) continue;
-                qv[h][i] = qg[h * D + dim_of(part * 16 + i)];   // q in the rows' slot order
-            }
+            for (int i = 0; i < 16; i++)   // q in the rows' slot order; heads past G re-read the last
+                qv[h][i] = qg[min(h, G - 1) * D + dim_of(part * 16 + i)];
         for (int tb = 0; tb < n; tb += 64) {
+            // rows past the split's end load its last row (clamped, no branch:
+            // a guarded load waits for the previous one); their scores are not
+            // stored
             float kv[2][16];
 #pragma unroll
             for (int u = 0; u < 2; u++) {
-                const int t = tb + sub + 32 * u;
+                const int t = min(tb + sub + 32 * u, n - 1);
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (t < n) a = kv_ld4(kb + (int64_t)t * D + part * 16 + 4 * i);
+                    const float4 a = kv_ld4(kb + (int64_t)t * D + part * 16 + 4 * i);
                     kv[u][4 * i] = a.x; kv[u][4 * i + 1] = a.y; kv[u][4 * i + 2] = a.z; kv[u][4 * i + 3] = a.w;
                 }
             }
@@ -431,12 +431,9 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(
 #pragma unroll
         for (int h = 0; h < ATT_MAX_G; h++) o[h] = make_float4(0.f, 0.f, 0.f, 0.f);
         for (int tb = pg; tb < n; tb += 32) {
-            float4 vv[4];
+            float4 vv[4];   // clamped like the keys; rows past the end are skipped below
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int t = tb + 8 * u;
-                vv[u] = t < n ? kv_ld4(vb + (int64_t)t * D + 4 * dg) : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
+            for (int u = 0; u < 4; u++) vv[u] = kv_ld4(vb + (int64_t)min(tb + 8 * u, n - 1) * D + 4 * dg);
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 const int t = tb + 8 * u;

@@ -152,12 +152,41 @@ __global__ __launch_bounds__(256) void dec_gemv_kernel(DecGemv p) {
         }
     };
 
+    // A group's epilogue operands (scale, bias; for RoPE the angles at the
+    // current position) are loaded with its weights, not after its math: there
+    // they were dependent round trips at the end of every group (the position,
+    // then cos / sin). Indices are clamped so every load is issued.
+    constexpr int RP = R / 2 > 0 ? R / 2 : 1;
+    int pos = 0;
+    if constexpr (EPI == EPI_ROPE) pos = p.state[0];   // first, so the angle loads wait for it alone
+    const int tpos = EPI == EPI_ROPE ? min(pos, p.max_seq - 1) : 0;
+    auto epi_ops = [&](const int (&row)[R], float (&sw)[R], float (&bb)[R], float (&cs)[RP], float (&sn)[RP]) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            sw[r] = p.s_w[row[r]];
+            bb[r] = (p.bias ? p.bias : p.s_w)[row[r]];
+        }
+        if constexpr (EPI == EPI_ROPE) {
+#pragma unroll
+            for (int j = 0; j < RP; j++) {
+                const int i = row[2 * j] % (2 * p.half);
+                const int64_t t = (int64_t)tpos * p.half + min(i, p.half - 1);
+                cs[j] = p.cos_t[t];
+                sn[j] = p.sin_t[t];
+            }
+        }
+    };
+
     int g = blockIdx.x * 4 + wid;
     int row[R];
     bool ok[R];
     v4i_t w[KC][R];
+    float sw[R], bb[R], cs[RP], sn[RP];
     rows_of(g < groups ? g : 0, row, ok);
-    if (g < groups) load_w(row, w);
+    if (g < groups) {
+        load_w(row, w);
+        epi_ops(row, sw, bb, cs, sn);
+    }
 
     // Block prologue: xs = x * norm_w (or x, or the merged attention output),
     // and the RMSNorm scale.
@@ -213,9 +242,11 @@ __global__ __launch_bounds__(256) void dec_gemv_kernel(DecGemv p) {
         int rown[R];
         bool okn[R];
         v4i_t wn[KC][R];
+        float swn[R], bbn[R], csn[RP], snn[RP];
         if (gn < groups) {
             rows_of(gn, rown, okn);
             load_w(rown, wn);
+            epi_ops(rown, swn, bbn, csn, snn);
         }
         float acc[R];
 #pragma unroll
@@ -239,8 +270,8 @@ __global__ __launch_bounds__(256) void dec_gemv_kernel(DecGemv p) {
         float v[R];
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            v[r] = acc[r] * p.s_w[row[r]] * nscale;
-            if (p.bias) v[r] += p.bias[row[r]];
+            v[r] = acc[r] * sw[r] * nscale;
+            if (p.bias) v[r] += bb[r];
         }
 
         if (EPI == EPI_PLAIN || EPI == EPI_RESID || EPI == EPI_LOGITS) {
@@ -268,7 +299,6 @@ __global__ __launch_bounds__(256) void dec_gemv_kernel(DecGemv p) {
                 }
         }
         if (EPI == EPI_ROPE) {
-            const int pos = p.state[0];
             const int D = 2 * p.half;
 #pragma unroll
             for (int j = 0; j < R / 2; j++) {
@@ -277,9 +307,8 @@ __global__ __launch_bounds__(256) void dec_gemv_kernel(DecGemv p) {
                 const int head = n0 / D, i = n0 % D;
                 const float re = v[2 * j], im = v[2 * j + 1];
                 if (head < p.nq + p.nkv) {
-                    const float c = p.cos_t[(int64_t)pos * p.half + i];
-                    const float sn = p.sin_t[(int64_t)pos * p.half + i];
-                    const float o0 = re * c - im * sn, o1 = re * sn + im * c;
+                    const float c = cs[j], sj = sn[j];
+                    const float o0 = re * c - im * sj, o1 = re * sj + im * c;
                     if (head < p.nq) {
                         float* dst = p.q_out + (int64_t)head * D;
                         dst[i] = o0;
@@ -300,6 +329,10 @@ __global__ __launch_bounds__(256) void dec_gemv_kernel(DecGemv p) {
         for (int c = 0; c < KC; c++)
 #pragma unroll
             for (int r = 0; r < R; r++) w[c][r] = wn[c][r];
+#pragma unroll
+        for (int r = 0; r < R; r++) { sw[r] = swn[r]; bb[r] = bbn[r]; }
+#pragma unroll
+        for (int j = 0; j < RP; j++) { cs[j] = csn[j]; sn[j] = snn[j]; }
         g = gn;
     }
     if (EPI == EPI_LOGITS) {

@@ -90,6 +90,37 @@ def test_persistent_one_launch_equals_many(torch_dev):
     assert np.mean(mixed == one) >= 0.9
 
 
+@pytest.mark.parametrize("mode", ["persistent", "graph"])
+@pytest.mark.parametrize("kv_dtype", ["float32", "float16"])
+def test_decode_at_max_context(torch_dev, kv_dtype, mode):
+    """The persistent kernel's context limit (2048 positions: 8 splits x 4
+    waves x 8 positions x 8 passes): a 2040-position prompt as one batch, then
+    the positions up to 2047 one launch each, every wave's last pass and the
+    last position slot in use; the graph path on the same sequence (its
+    attention splits of 256 positions); logits against the oracle."""
+    cfg, rcfg = _cfgs(max_seq=2048, kv_dtype=kv_dtype)
+    dec, w = _decoder(cfg, seed=41)
+    ids = np.random.default_rng(42).integers(0, cfg.vocab, size=2048).astype(np.int32)
+    dec.reset(ids)
+    npre = 2040
+    _say(f"max context ({kv_dtype}, {mode}): batched prompt of {npre}")
+    dec.prefill(npre)
+    got = []
+    for _ in range(len(ids) - 1 - npre):
+        dec.run(1, mode=mode)
+        got.append(dec.read(0, with_logits=True)[1].copy())
+    _say("max context: batched oracle")
+    want = list(range(npre, len(ids) - 1))
+    e64 = qwen3_ref.forward_all(rcfg, w, ids[:-1], want, np.float64)
+    e32 = qwen3_ref.forward_all(rcfg, w, ids[:-1], want, np.float32).astype(np.float64)
+    for k, i in enumerate(want):
+        rms = float(np.sqrt(np.mean(e64[k] * e64[k])))
+        err = float(np.abs(got[k] - e64[k]).max()) / rms
+        err32 = float(np.abs(e32[k] - e64[k]).max()) / rms
+        _say(f"position {i}: err {err:.2e} (numpy fp32 {err32:.2e})")
+        assert err <= max(1e-4, 4 * err32), (i, err, err32)
+
+
 def test_persistent_long_context(torch_dev):
     """Contexts past 384 positions read part of each split's keys straight from
     the cache instead of the prefetched registers."""

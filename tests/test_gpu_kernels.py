@@ -663,6 +663,35 @@ def test_moe_layer_matches_oracle(env, T, H, I, E, k, xdt):
     assert_rel(host(out), ref, 1e-4, "moe")
 
 
+@pytest.mark.parametrize("bias_experts", [(5, 9), (0, 1, 2, 3)])
+def test_moe_skewed_routing(env, bias_experts):
+    """Routing concentrated on a few experts: most experts get no rows (their
+    GEMM blocks find an empty range and write nothing), the chosen ones get
+    every token (several 64-row tiles each); against the oracle."""
+    torch, ops, d = env
+    T, H, I, E, k = 300, 256, 128, 64, 2
+    _say(f"moe skewed routing to experts {bias_experts}")
+    rng = np.random.default_rng(77 + len(bias_experts))
+    x = rng.standard_normal((T, H), dtype=np.float32)
+    lg = rng.standard_normal((T, E), dtype=np.float32)
+    for j, e in enumerate(bias_experts):
+        lg[:, e] += 20.0 - j
+    wgu = rng.integers(-127, 127, size=(E, 2 * I, H), dtype=np.int8)
+    sgu = rng.uniform(0.001, 0.02, size=(E, 2 * I)).astype(np.float32)
+    wd = rng.integers(-127, 127, size=(E, H, I), dtype=np.int8)
+    sd = rng.uniform(0.001, 0.02, size=(E, H)).astype(np.float32)
+    out = torch.full((T, H), float("nan"), dtype=torch.float32, device=d)
+    ops.moe_w8a8(dev(torch, x, d), dev(torch, lg, d), dev(torch, wgu, d), dev(torch, sgu, d),
+                 dev(torch, wd, d), dev(torch, sd, d), out, T, H, I, E, k, False)
+    sync(torch)
+    _, ids = oracle.moe_route(lg, k, False)
+    assert set(np.unique(ids)) <= set(bias_experts)
+    ref = oracle.moe_w8a8(x, lg, wgu, sgu, wd, sd, k)
+    got = host(out)
+    assert np.isfinite(got).all()
+    assert_rel(got, ref, 1e-4, "moe skewed")
+
+
 @pytest.mark.parametrize("renorm", [False, True])
 def test_moe_c5_fp16_out_matches_oracle(env, renorm):
     """The full C5 layer (512 tokens, H 2048, I 768, 128 experts, top-8) with

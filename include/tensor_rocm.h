@@ -358,9 +358,11 @@ int pio_qwen3_reset(void* dec, const int32_t* ids, int prompt_len);
  * PIO_DECODE_PERSISTENT runs all n steps in one kernel launch (one
  * workgroup per CU; weights stream through LDS while each phase waits for its
  * input). The modes share the KV cache and position, so they can alternate.
- * Persistent mode builds a per-workgroup copy of the weights on first use
- * (the size of the int8 weights) and needs the config checked by
- * pio_qwen3_persistent_supported. It needs every CU at once: a launch whose
+ * Persistent mode builds a per-workgroup copy of the int8 layer weights on
+ * first use (their size; scales, norms, embeddings and the lm_head are read
+ * from the caller's buffers in every mode) and needs the config checked by
+ * pio_qwen3_persistent_supported. After the caller changes those int8
+ * weights in place, pio_qwen3_refresh_weights copies them again. It needs every CU at once: a launch whose
  * workgroups do not all become resident within 20 ms (other work on the
  * device) computes nothing, nor does any persistent launch after it; the next
  * pio_qwen3_read, or a run in another mode, re-runs those steps in graph mode
@@ -382,6 +384,12 @@ int pio_qwen3_prefill(void* dec, int n_steps, int logits);
  * device, else 0 (the reason is in tensor_last_error). No counterpart in the
  * reference. */
 int pio_qwen3_persistent_supported(void* dec);
+/* Copies the caller's int8 layer weights into the persistent mode's
+ * per-workgroup copy again, on the decoder's stream (after earlier work on it,
+ * before later). Call it after changing those weights in place; without a
+ * copy yet (no persistent run so far) it does nothing. No counterpart in the
+ * reference, whose layers read their weights on every call. */
+int pio_qwen3_refresh_weights(void* dec);
 /* Phase timeline of the persistent decode (measurement; no counterpart in the
  * reference). pio_qwen3_trace_next makes the next persistent launch of this
  * decoder run the kernel's traced build, which stamps the 100 MHz constant

@@ -867,6 +867,12 @@ PIO_EXPORT int pio_qwen3_persistent_replays(void* h) {
     return loop_replays(d);
 }
 
+PIO_EXPORT int pio_qwen3_refresh_weights(void* h) {
+    Qwen3Dec* d = (Qwen3Dec*)h;
+    PIO_REQUIRE(d, "pio_qwen3_refresh_weights: null handle");
+    return loop_refresh(d);
+}
+
 PIO_EXPORT int pio_qwen3_persistent_supported(void* h) {
     Qwen3Dec* d = (Qwen3Dec*)h;
     PIO_REQUIRE(d, "pio_qwen3_persistent_supported: null handle");

@@ -54,6 +54,7 @@ bool loop_pending(const Qwen3Dec* d);   // persistent launches not yet checked
 size_t loop_trace_bytes(const Qwen3Dec* d);
 int loop_trace_next(Qwen3Dec* d, int first_step);
 int loop_trace_read(Qwen3Dec* d, void* out, size_t bytes);
+int loop_refresh(Qwen3Dec* d);
 void loop_destroy(Qwen3Dec* d);
 
 // The step kernels' tail (decode.hip): lm_head on the decoder's x with the

@@ -1607,6 +1607,8 @@ struct LoopState {
     int nblk = 0;
     int lpt = 0;
     void* stream = nullptr;      // relaid weights
+    void* tab = nullptr;         // source address of every 128-byte piece of them (the caller's weights)
+    int64_t nlines = 0;
     void* small = nullptr;       // tagged buffers + layer table + error words
     size_t small_bytes = 0, ll_bytes = 0;
     LoopLayer* layers = nullptr;
@@ -1717,12 +1719,11 @@ static int loop_build(Qwen3Dec* d) {
         }
     }
     PIO_TRY(device_alloc(&s->stream, (size_t)nlines * 1024, d->st));
-    void* dtab = nullptr;
-    PIO_TRY(device_alloc(&dtab, tab.size() * sizeof(void*), d->st));
-    Scratch tab_guard;
-    tab_guard.ptr = dtab;
-    PIO_HIP(hipMemcpyAsync(dtab, tab.data(), tab.size() * sizeof(void*), hipMemcpyHostToDevice, d->st));
-    loop_gather_kernel<<<(unsigned)((nlines + 3) / 4), 256, 0, d->st>>>((const int8_t* const*)dtab,
+    // the table stays (nlines * 64 B): pio_qwen3_refresh_weights gathers again from it
+    PIO_TRY(device_alloc(&s->tab, tab.size() * sizeof(void*), d->st));
+    s->nlines = nlines;
+    PIO_HIP(hipMemcpyAsync(s->tab, tab.data(), tab.size() * sizeof(void*), hipMemcpyHostToDevice, d->st));
+    loop_gather_kernel<<<(unsigned)((nlines + 3) / 4), 256, 0, d->st>>>((const int8_t* const*)s->tab,
                                                                         (int8_t*)s->stream, nlines);
     PIO_LAUNCHED();
 
@@ -1752,14 +1753,26 @@ static int loop_build(Qwen3Dec* d) {
     PIO_HIP(hipMemsetAsync(s->small, 0, s->small_bytes, d->st));
     PIO_HIP(hipMemcpyAsync(s->layers, lt.data(), lt.size() * sizeof(LoopLayer), hipMemcpyHostToDevice,
                            d->st));
-    PIO_HIP(hipStreamSynchronize(d->st));   // the host table and the guard go out of scope
+    PIO_HIP(hipStreamSynchronize(d->st));   // the host tables go out of scope
     s->epoch = 1;
+    return PIO_OK;
+}
+
+// Copies the caller's int8 layer weights into the relaid copy again (after the
+// caller changed them in place), ordered on the decoder's stream.
+int loop_refresh(Qwen3Dec* d) {
+    LoopState* s = d->loop;
+    if (!s) return PIO_OK;   // no copy yet: the first persistent run makes it
+    loop_gather_kernel<<<(unsigned)((s->nlines + 3) / 4), 256, 0, d->st>>>((const int8_t* const*)s->tab,
+                                                                           (int8_t*)s->stream, s->nlines);
+    PIO_LAUNCHED();
     return PIO_OK;
 }
 
 void loop_destroy(Qwen3Dec* d) {
     if (!d || !d->loop) return;
     if (d->loop->stream) device_free(d->loop->stream);
+    if (d->loop->tab) device_free(d->loop->tab);
     if (d->loop->small) device_free(d->loop->small);
     if (d->loop->trace) device_free(d->loop->trace);
     delete d->loop;

@@ -151,6 +151,7 @@ SIGNATURES: dict[str, tuple] = {
     "pio_qwen3_reset": (_i, [_vp, _vp, _i]),
     "pio_qwen3_run": (_i, [_vp, _i, _i]),
     "pio_qwen3_persistent_supported": (_i, [_vp]),
+    "pio_qwen3_refresh_weights": (_i, [_vp]),
     "pio_qwen3_persistent_replays": (_i, [_vp]),
     "pio_qwen3_prefill": (_i, [_vp, _i, _i]),
     "pio_probe_gemm_supply": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp]),

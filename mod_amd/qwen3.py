@@ -321,6 +321,12 @@ class Qwen3Int8Decoder:
         t[raw == 0] = np.nan
         return (t - np.nanmin(t)) * 10.0   # 100 MHz ticks -> ns
 
+    def refresh_weights(self) -> None:
+        """The persistent mode's copy of the int8 layer weights, taken again
+        from the buffers this decoder was created with (after changing them
+        in place)."""
+        check(lib.pio_qwen3_refresh_weights(self._h), "pio_qwen3_refresh_weights")
+
     def persistent_replays(self) -> int:
         """Persistent launches re-run in graph mode because the device could
         not hold their whole grid at once (other work held CUs)."""

@@ -121,6 +121,40 @@ def test_decode_at_max_context(torch_dev, kv_dtype, mode):
         assert err <= max(1e-4, 4 * err32), (i, err, err32)
 
 
+def test_persistent_refresh_after_weights_change(torch_dev):
+    """The persistent mode decodes from its own copy of the int8 layer
+    weights: after the caller rewrites one in place, the graph path (which
+    reads the caller's buffers) sees the change and the persistent path does
+    not until pio_qwen3_refresh_weights; then the two agree again."""
+    cfg, _ = _cfgs()
+    dec, w = _decoder(cfg, seed=51)
+    ids = np.random.default_rng(52).integers(0, cfg.vocab, size=40).astype(np.int32)
+
+    def logits(mode):
+        dec.reset(ids)
+        dec.run(len(ids) - 1, mode=mode)
+        return dec.read(0, with_logits=True)[1].astype(np.float64)
+
+    def rel(a, b):
+        return float(np.abs(a - b).max() / np.sqrt(np.mean(b * b)))
+
+    _say("refresh: before the change")
+    before = logits("persistent")
+    assert rel(before, logits("graph")) < 1e-4
+    ptr = dec._layers_c[1].w_down
+    buf = next(t for t in dec._keep if t.data_ptr() == ptr)
+    new_down = np.random.default_rng(53).integers(-127, 127, size=w["layers"][1]["w_down"].shape,
+                                                  dtype=np.int8)
+    buf.load(new_down)
+    _say("refresh: after the change, before the refresh")
+    g = logits("graph")
+    assert rel(g, before) > 1e-2                      # the change matters
+    assert rel(logits("persistent"), before) < 1e-4   # the stale copy still decodes as before
+    dec.refresh_weights()
+    _say("refresh: after the refresh")
+    assert rel(logits("persistent"), g) < 1e-4
+
+
 def test_persistent_long_context(torch_dev):
     """Contexts past 384 positions read part of each split's keys straight from
     the cache instead of the prefetched registers."""

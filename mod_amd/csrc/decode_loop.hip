@@ -101,7 +101,6 @@ constexpr int LP_NPMAX = 8;                // attention passes (8 positions each
 constexpr int LP_MAX_SEQ = LP_S * LP_CW * 8 * LP_NPMAX;   // 2048
 constexpr int LP_PART = 2 + LP_D;          // (max, sum, o[128]) per split and head
 static_assert(LP_S == 8, "the merge loads the partials of 8 splits in one batch");
-constexpr int LP_LM_B = 6;                 // lm_head rows per wave and batch (three batches in flight)
 constexpr int LP_LMAX = 48;                // layers whose per-wave constants LDS holds
 constexpr int LP_NCST = 32;                // constants per layer and compute wave (30 used)
 constexpr int LP_PH = 7;                   // tagged phases per layer
@@ -184,6 +183,7 @@ constexpr int LP_TR_TOK = 2, LP_TR_K = 16;
 // constants
 constexpr size_t LP_LDS_RING = (size_t)LP_RING * 1024;
 constexpr size_t LP_LDS_XW = (size_t)LP_CW * LP_H * 4;
+static_assert(LP_LDS_XW == (LP_H / 64) * 64 * 16, "the lm phase's A operand fills the x-copy region");
 constexpr size_t LP_LDS_OS = (size_t)LP_G * LP_D * 4;
 constexpr size_t LP_LDS_ACT = (size_t)LP_CW * LP_IX * 4;
 constexpr size_t LP_LDS_ATT = (size_t)LP_CW * LP_G * LP_D * 4 + 2 * LP_CW * LP_G * 4;
@@ -432,7 +432,7 @@ struct Cx {
     int* csync;      // compute-wave rendezvous counter
     int* abort;      // workgroup abort flag
     int8_t* ring;
-    float* xw;       // [LP_CW][H] each wave's copy of the current input vector
+    float* xw;       // 16 KB: the lm phase's A operand (16 MFMAs x 64 lanes x 16 B)
     float* os;       // [256] merged attention output of KV head g
     float* acts;     // [384] the workgroup's copy of XCD g's act slice
     float* attp;     // [LP_CW][LP_G][128] attention partials
@@ -1169,104 +1169,158 @@ __device__ bool merge_heads(const LoopParams& p, Cx& c, int pos, uint32_t ptag) 
 }
 
 typedef __attribute__((address_space(3))) float lds_f32;
+typedef __attribute__((address_space(3))) const int8_t lds_i8;
 typedef __attribute__((address_space(3))) u64 lds_u64;
 typedef __attribute__((address_space(1))) const lp_v4i glb_v4i;   // global (not flat) loads
 typedef __attribute__((address_space(1))) const float glb_f32;
 
-template <int C>
-__device__ __forceinline__ void lm_load(const int8_t* lm, int H, int uv0, int nuv, int w, int lane,
-                                        int k0, lp_v4i (&wr)[LP_LM_B][C]) {
+// ----------------------------------------------------- lm_head on MFMA
+// The lm phase multiplies one vector by 151936 x 1024 int8 rows. On the VALU
+// that is a byte conversion and an fp32 FMA per weight (one compute wave per
+// SIMD: ~14 us of issue per token); here the rows go to the matrix cores
+// (v_mfma_i32_16x16x64_i8) untouched, against an exact int8 decomposition of
+// the vector. v = gamma * x (the RMSNorm scale nscale multiplies the sums) is
+// split under one power-of-two scale S = 2^(E - 6), where max |v| = m 2^E with
+// m in [0.5, 1): u = v / S (exact, |u| < 64), q1 = rint(u) and
+// q_{i+1} = rint(128 (u_i - q_i)) (every step exact), so every part is in
+// [-64, 64] and v = S (q1 + q2/128 + q3/128^2 + q4/128^3) + e with
+// |e| <= S 2^-22 (about 2^-27 max |v|, far below fp32 rounding of the sums).
+// A row's four sums c_i = sum_k W[row][k] q_i[k] are exact int32
+// (|c_i| <= 64 * 127 * 1024 < 2^23), and its value is
+// S (((c4 / 128 + c3) / 128 + c2) / 128 + c1): a few fp32 roundings in all,
+// where the FMA chain rounded once per weight.
+//
+// Operand layout (as the skinny W8A8 kernel's): lane l = r + 16 q supplies the
+// 16 bytes at K = 64 i + 16 q of MFMA i (16 per 1024-byte row); for B that is
+// lm_head row r of the group, for A part r of the vector (r < 4) or zeros.
+// The A operand lives in LDS, [16 MFMAs][64 lanes][16 B], and is read back
+// whole lines at a time; the C rows 0-3 (lanes 0-15) are the four sums of
+// row r = lane.
+
+// Writes this wave's share of the A operand (the 4-byte column 4 w of every
+// part slot, and the zero rows of MFMAs 4 w .. 4 w + 3) from gamma * x in
+// xv (lane l: elements 16 l .. 16 l + 15, the whole vector in every wave);
+// returns S. The caller's rendezvous then makes the operand whole.
+__device__ __forceinline__ float lm_split(const Cx& c, const float (&xv)[16], int8_t* A) {
+    float amax = 0.f;
 #pragma unroll
-    for (int m = 0; m < LP_LM_B; m++) {
-        const int ub = min(w + LP_CW * (k0 + m), nuv - 1);   // past the end: re-read the last row
-        const int8_t* row = lm + (int64_t)(uv0 + ub) * H + lane * 16;
+    for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(xv[i]));
+    amax = wmax(amax);
+    int E;
+    (void)frexpf(amax, &E);   // amax = 0: E = 0, every part 0
+    const float inv = ldexpf(1.f, 6 - E);
+    // this wave's elements 16 l + 4 w + t: MFMA i = l / 4, lane chunk q = l % 4,
+    // byte 4 w + t of the chunk
+    uint32_t pk[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int ch = 0; ch < C; ch++) wr[m][ch] = *(glb_v4i*)(row + ch * 1024);
+    for (int t = 0; t < 4; t++) {
+        const float x = c.w == 0 ? xv[t] : c.w == 1 ? xv[4 + t] : c.w == 2 ? xv[8 + t] : xv[12 + t];
+        float u = x * inv;
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const float q = rintf(u);
+            pk[m] |= ((uint32_t)(int)q & 0xFFu) << (8 * t);
+            u = (u - q) * 128.f;
+        }
     }
+    typedef __attribute__((address_space(3))) uint32_t lds_u32w;
+    typedef __attribute__((address_space(3))) lp_v4i lds_v4w;
+    typedef __attribute__((address_space(3))) int8_t lds_i8w;
+    lds_i8w* L = (lds_i8w*)A;
+    const int i = c.lane >> 2, q = c.lane & 3;
+#pragma unroll
+    for (int m = 0; m < 4; m++) *(lds_u32w*)(L + i * 1024 + (m + 16 * q) * 16 + 4 * c.w) = pk[m];
+    // zero rows 4..15 of MFMAs 4 w .. 4 w + 3: 192 slots of 16 bytes, 3 per lane
+#pragma unroll
+    for (int s = 0; s < 3; s++) {
+        const int slot = c.lane + 64 * s, r = slot % 48;
+        *(lds_v4w*)(L + (4 * c.w + slot / 48) * 1024 + (4 + r % 12 + 16 * (r / 12)) * 16) = lp_v4i{0, 0, 0, 0};
+    }
+    return ldexpf(1.f, E - 6);
 }
 
-// One batch of LP_LM_B rows (k0 .. k0 + LP_LM_B - 1 of this wave).
-template <int C>
-__device__ __forceinline__ void lm_batch(int k0, int nk, int sbase, float sv, float nscale,
-                                         float* logits, int row0, int lane,
-                                         const float (&xr)[C][16], float xoff,
-                                         const lp_v4i (&wr)[LP_LM_B][C], float& bestv, int& besti) {
-    float acc[LP_LM_B];
+// 16 lm_head rows (group g of this wave: rows w + 4 (16 g + r)) into the B
+// operand registers, and their scales.
+__device__ __forceinline__ void lm_load(const int8_t* lm, const float* s_lm, int uv0, int w, int nk, int lane,
+                                        int g, lp_v4i (&wr)[16], float& s) {
+    const int k = min(16 * g + (lane & 15), nk - 1);   // past the end: re-read the last row
+    const int row = uv0 + w + 4 * k;
+    const int8_t* src = lm + (int64_t)row * LP_H + 16 * (lane >> 4);
 #pragma unroll
-    for (int m = 0; m < LP_LM_B; m++) {
-        float s[4] = {xoff, 0.f, 0.f, 0.f};
+    for (int i = 0; i < 16; i++) wr[i] = *(glb_v4i*)(src + 64 * i);
+    s = *(glb_f32*)(s_lm + row);
+}
+
+// One group: 16 MFMAs on two accumulators, then lanes 0-15 hold the four sums
+// of row r = lane; its value, the lane's running maximum (rows ascend within a
+// lane, ties keep the first) and, on the last step, its logit.
+__device__ __forceinline__ void lm_group(const lds_i8* A, int g, int uv0, int w, int nk, int lane, float sn,
+                                         const lp_v4i (&wr)[16], float s, float* logits, float& bestv,
+                                         int& besti) {
+    lp_v4i c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
 #pragma unroll
-        for (int ch = 0; ch < C; ch++) lp_dot16(xr[ch], wr[m][ch], s);
-        acc[m] = (s[0] + s[1]) + (s[2] + s[3]);
+    for (int i = 0; i < 16; i += 2) {
+        const lp_v4i a0 = *(const __attribute__((address_space(3))) lp_v4i*)(A + i * 1024 + lane * 16);
+        const lp_v4i a1 = *(const __attribute__((address_space(3))) lp_v4i*)(A + (i + 1) * 1024 + lane * 16);
+        c0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, wr[i], c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, wr[i + 1], c1, 0, 0, 0);
     }
-    wsum_n<LP_LM_B>(acc);
-#pragma unroll
-    for (int m = 0; m < LP_LM_B; m++) {
-        const int row = row0 + LP_CW * (k0 + m);
-        const float v = acc[m] * rlane(sv, k0 + m - sbase) * nscale;
-        const bool in = k0 + m < nk;
-        if (in && v > bestv) {   // rows ascend: ties keep the first
-            bestv = v;
-            besti = row;
-        }
-        if (in && logits && lane == 0) logits[row] = v;
+    const lp_v4i cs = c0 + c1;   // |c| < 2^24
+    const float y = (((float)cs[3] * 0.0078125f + (float)cs[2]) * 0.0078125f + (float)cs[1]) * 0.0078125f +
+                    (float)cs[0];
+    const float v = y * sn * s;
+    const int k = 16 * g + lane;
+    const bool in = lane < 16 && k < nk;
+    const int row = uv0 + w + 4 * k;
+    if (in && v > bestv) {
+        bestv = v;
+        besti = row;
     }
+    // a global (not flat) store: a pending flat store makes the compiler's
+    // next wait drain every load in flight
+    if (in && logits) *(__attribute__((address_space(1))) float*)(logits + row) = v;
 }
 
 // lm_head: the one phase that is pure streaming (155 MB at the Qwen3-0.6B
 // shape) and waits on no other workgroup, so the compute waves read its rows
-// straight from HBM into registers, LP_LM_B rows per batch, three batches in
-// flight (the next two batches' loads are in flight while one is reduced).
-// This wave's rows: uv0 + w + 4k. Out of line, so that its registers are its
-// own; x comes from the staged LDS copy. Writes the wave's argmax key.
-template <int C>
-__device__ __noinline__ void phase_lm(const int8_t* lm, const float* s_lm, float* logits, int H,
-                                      int uv0, int nuv, int w, int lane, const lds_f32* xs,
-                                      float nscale, uint32_t tag, lds_u64* wkey) {
-    float xr[C][16];
-#pragma unroll
-    for (int ch = 0; ch < C; ch++)
-#pragma unroll
-        for (int i = 0; i < 16; i++) xr[ch][i] = xs[ch * 1024 + lane * 16 + i];
-    float xoff = 0.f;
-#pragma unroll
-    for (int ch = 0; ch < C; ch++) xoff += lp_xoff(xr[ch]);
+// straight from HBM into the B operand registers, 16 rows (16 KB) per group,
+// two groups in flight. This wave's rows: uv0 + w + 4 k. Out of line, so that
+// its registers are its own. sn = S * nscale. Writes the wave's argmax key.
+__device__ __noinline__ void phase_lm(const int8_t* lm, const float* s_lm, float* logits, int uv0, int nuv, int w,
+                                      int lane, const lds_i8* A, float sn, uint32_t tag, lds_u64* wkey) {
     const int nk = nuv > w ? (nuv - w + LP_CW - 1) / LP_CW : 0;   // rows of this wave
-    const int row0 = uv0 + w;
+    const int ng = (nk + 15) / 16;
     float bestv = -INFINITY;
-    int besti = 0;
-    int sbase = 0;
-    float sv = w + LP_CW * lane < nuv ? *(glb_f32*)(s_lm + row0 + LP_CW * lane) : 0.f;
-    // three batches in flight: 18 KB per wave, 72 KB per CU (with two, the
-    // CU's 48 KB in flight covered too little of the HBM latency under load)
-    constexpr int B = LP_LM_B;
-    lp_v4i wa[B][C], wb[B][C], wc[B][C];
-    if (nk > 0) lm_load<C>(lm, H, uv0, nuv, w, lane, 0, wa);
-    if (nk > B) lm_load<C>(lm, H, uv0, nuv, w, lane, B, wb);
-    for (int k0 = 0; k0 < nk; k0 += 3 * B) {
-        if (k0 - sbase > 64 - 3 * B) {
-            sbase = k0;
-            const int ub = w + LP_CW * (k0 + lane);
-            sv = ub < nuv ? *(glb_f32*)(s_lm + uv0 + ub) : 0.f;
+    int besti = -1;
+    lp_v4i wa[16], wb[16];
+    float sa = 0.f, sb = 0.f;
+    // Every load below is unconditional within its block, so the compiler's
+    // waits count exactly (a load behind a branch makes it wait for all).
+    if (ng > 0) {
+        lm_load(lm, s_lm, uv0, w, nk, lane, 0, wa, sa);
+        int g = 0;
+        for (; g + 2 < ng; g += 2) {
+            lm_load(lm, s_lm, uv0, w, nk, lane, g + 1, wb, sb);
+            __builtin_amdgcn_sched_barrier(0);
+            lm_group(A, g, uv0, w, nk, lane, sn, wa, sa, logits, bestv, besti);
+            __builtin_amdgcn_sched_barrier(0);
+            lm_load(lm, s_lm, uv0, w, nk, lane, g + 2, wa, sa);
+            __builtin_amdgcn_sched_barrier(0);
+            lm_group(A, g + 1, uv0, w, nk, lane, sn, wb, sb, logits, bestv, besti);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        // sched_barrier: keep each batch's conversions next to its FMAs (the
-        // scheduler would otherwise convert the batches in flight too, and spill)
-        if (k0 + 2 * B < nk) lm_load<C>(lm, H, uv0, nuv, w, lane, k0 + 2 * B, wc);
-        __builtin_amdgcn_sched_barrier(0);
-        lm_batch<C>(k0, nk, sbase, sv, nscale, logits, row0, lane, xr, xoff, wa, bestv, besti);
-        __builtin_amdgcn_sched_barrier(0);
-        if (k0 + B >= nk) break;
-        if (k0 + 3 * B < nk) lm_load<C>(lm, H, uv0, nuv, w, lane, k0 + 3 * B, wa);
-        __builtin_amdgcn_sched_barrier(0);
-        lm_batch<C>(k0 + B, nk, sbase, sv, nscale, logits, row0, lane, xr, xoff, wb, bestv, besti);
-        __builtin_amdgcn_sched_barrier(0);
-        if (k0 + 2 * B >= nk) break;
-        if (k0 + 4 * B < nk) lm_load<C>(lm, H, uv0, nuv, w, lane, k0 + 4 * B, wb);
-        __builtin_amdgcn_sched_barrier(0);
-        lm_batch<C>(k0 + 2 * B, nk, sbase, sv, nscale, logits, row0, lane, xr, xoff, wc, bestv, besti);
-        __builtin_amdgcn_sched_barrier(0);
+        if (g + 1 < ng) {
+            lm_load(lm, s_lm, uv0, w, nk, lane, g + 1, wb, sb);
+            __builtin_amdgcn_sched_barrier(0);
+            lm_group(A, g, uv0, w, nk, lane, sn, wa, sa, logits, bestv, besti);
+            __builtin_amdgcn_sched_barrier(0);
+            lm_group(A, g + 1, uv0, w, nk, lane, sn, wb, sb, logits, bestv, besti);
+        } else {
+            lm_group(A, g, uv0, w, nk, lane, sn, wa, sa, logits, bestv, besti);
+        }
     }
-    if (lane == 0) *wkey = nk > 0 ? lp_key(bestv, besti, tag) : 0;
+    const u64 key = wave_max_u64(besti >= 0 ? lp_key(bestv, besti, tag) : 0);
+    if (lane == 0) *wkey = key;
 }
 
 // Argmax over the workgroups' keys of the lm phase tagged `tag` (first max,
@@ -1475,15 +1529,14 @@ __device__ void compute_role(const LoopParams& p, Cx& c) {
             lp_stamp<TR>(p, c, t, p.L, 1);
             if (!gather_x(p, c, p.xr, tag_of(p, t, p.L, PH_XR), gam, xv, nscale, c.xs, 11)) return;
             lp_stamp<TR>(p, c, t, p.L, 2);
-            // the lm phase reads gamma * x from the wave's LDS copy
-            float* xw = c.xw + c.w * LP_H + 16 * c.lane;
-#pragma unroll
-            for (int i = 0; i < 16; i += 4) *(float4*)(xw + i) = make_float4(xv[i], xv[i + 1], xv[i + 2], xv[i + 3]);
-            cbar();
+            // gamma * x as the lm phase's int8 matrix operand (in the x-copy region
+            // of LDS), each wave writing its share; the rendezvous makes it whole
+            int8_t* A = (int8_t*)c.xw;
+            const float S = lm_split(c, xv, A);
+            if (!csync(p, c, 60)) return;
             const uint32_t tl = tag_of(p, t, p.L, 1);
-            phase_lm<1>(p.lm_head, p.s_lm, t == p.n_steps - 1 ? p.logits : nullptr, LP_H, c.uv0, c.nuv,
-                        c.w, c.lane, (const lds_f32*)(c.xw + c.w * LP_H), nscale, tl,
-                        (lds_u64*)(c.wkeys + c.w));
+            phase_lm(p.lm_head, p.s_lm, t == p.n_steps - 1 ? p.logits : nullptr, c.uv0, c.nuv, c.w, c.lane,
+                     (const lds_i8*)A, S * nscale, tl, (lds_u64*)(c.wkeys + c.w));
             lp_stamp<TR>(p, c, t, p.L, 3);
             if (!csync(p, c, 61)) return;
             if (c.w == 0 && c.lane == 0) {

@@ -185,6 +185,35 @@ def test_persistent_long_context(torch_dev):
         assert err <= max(1e-4, 4 * err32), (i, err, err32)
 
 
+def test_persistent_lm_head_small_vocab_and_ties(torch_dev):
+    """The lm phase deals the vocabulary rows over the 256 workgroups and their
+    waves in 16-row MFMA groups. With vocab 200, 56 workgroups own no row at
+    all (their key must not win): teacher-forced logits against the oracle.
+    With every lm_head row and scale equal, every logit ties: greedy decode
+    must pick id 0 (the reference argmax keeps the first maximum,
+    tensor_ops.c:649-662) across lanes, waves and workgroups, in the
+    persistent mode as in the graph mode."""
+    from mod_amd.qwen3 import Qwen3Int8Decoder, random_weights
+    cfg, rcfg = _cfgs(vocab=200)
+    dec, w = _decoder(cfg, seed=61)
+    ids = np.random.default_rng(62).integers(0, cfg.vocab, size=24).astype(np.int32)
+    _say("lm small vocab: teacher forced")
+    got = dec.teacher_forced_logits(ids, mode="persistent")
+    _check_logits(got, ids, rcfg, w, "persistent vocab 200")
+
+    cfg, _ = _cfgs(vocab=4096)
+    w = random_weights(cfg, seed=63)
+    w["lm_head"] = np.ascontiguousarray(np.broadcast_to(w["lm_head"][:1], w["lm_head"].shape))
+    w["s_lm_head"] = np.full_like(w["s_lm_head"], w["s_lm_head"][0])
+    dec = Qwen3Int8Decoder(cfg, w)
+    prompt = np.random.default_rng(64).integers(0, cfg.vocab, size=6).astype(np.int32)
+    for mode in ("persistent", "graph"):
+        _say(f"lm ties: greedy, {mode}")
+        out = dec.generate(prompt, 12, mode=mode)
+        assert np.array_equal(out[:len(prompt)], prompt)
+        assert np.all(out[len(prompt):] == 0), (mode, out)
+
+
 def test_persistent_c2_shape(torch_dev):
     """Full Qwen3-0.6B shape (28 layers, vocab 151936)."""
     cfg, rcfg = _cfgs(n_layers=28, vocab=151936, max_seq=384)

@@ -521,6 +521,15 @@ __device__ __forceinline__ bool csync(const LoopParams& p, Cx& c, int where) {
     return true;
 }
 
+// One LDS word, read without the compiler's knowledge: the stream waves' own
+// global->LDS copies in flight then need no wait before it.
+__device__ __forceinline__ int lds_ld_asm(const int* p) {
+    const uint32_t a = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const int*)p;
+    int v;
+    asm volatile("ds_read_b32 %0, %1\n s_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+    return __builtin_amdgcn_readfirstlane(v);
+}
+
 // Four LDS counters in one read (the stream waves' landed lines ready[], or
 // the compute waves' done[]; both 16-byte aligned): four separate atomic
 // reads each waited for the previous one, four LDS round trips per check.
@@ -1361,7 +1370,9 @@ __device__ void stream_role(const LoopParams& p, Cx& c) {
         const int nl = p.lpt;
         for (int j = ((sw - G) % LP_SW + LP_SW) % LP_SW; j < nl; j += LP_SW) {
             const int Lg = G + j;
-            if (((j / LP_SW) & 7) == 0 && lds_ld(c.abort)) { ok = false; break; }   // every 8th line
+            // every 8th line; an asm read, so the compiler does not first wait
+            // for every copy in flight (it cannot tell the flag from the ring)
+            if (((j / LP_SW) & 7) == 0 && lds_ld_asm(c.abort)) { ok = false; break; }
             // the slot of line Lg held line Lg - LP_RING: free once every
             // compute wave has moved past it
             auto room = [&]() {

@@ -42,8 +42,8 @@
 //
 // Workgroup = 8 waves:
 //   waves 4-7 ("stream waves") copy this workgroup's weight lines, in the order
-//     the compute waves consume them, from a per-workgroup contiguous copy of
-//     the weights (built once) into an LDS ring of 1 KB lines with
+//     the compute waves consume them, from a relaid copy of the weights
+//     (built once, line-major over the workgroups) into an LDS ring of 1 KB lines with
 //     global_load_lds_dwordx4; a line is published when its copy has landed.
 //   waves 0-3 ("compute waves") run the phases; each polls whole input vectors
 //     itself (no cross-wave rendezvous except around attention and the merge).
@@ -139,7 +139,7 @@ struct LoopParams {
     const float* s_lm;
     const int8_t* lm_head;     // [V][H] int8, read directly by the lm phase
     const LoopLayer* layers;
-    const int8_t* stream;      // [nblk][lpt][1024] weight lines in consumption order
+    const int8_t* stream;      // [lpt][nblk][1024] weight lines in consumption order
     int lpt;                   // weight lines per token (n_layers * LP_LPL)
     void* kc;                  // KV cache [L][8][max_seq][128], fp32 or fp16 (kernel's KV16)
     void* vc;
@@ -1362,7 +1362,7 @@ __device__ bool argmax_id(const LoopParams& p, Cx& c, uint32_t tag, int& id) {
 
 __device__ void stream_role(const LoopParams& p, Cx& c) {
     const int sw = c.w - LP_CW;
-    const int8_t* src = p.stream + (int64_t)c.role * p.lpt * 1024 + c.lane * 16;
+    const int8_t* src = p.stream + (int64_t)c.role * 1024 + c.lane * 16;
     typedef __attribute__((address_space(3))) void lds_t;
     int G = 0, inflight = 0, published = 0;
     bool ok = true;
@@ -1392,7 +1392,7 @@ __device__ void stream_role(const LoopParams& p, Cx& c) {
                 cbar();
             }
             // nt: the weights are read once per token; keep them out of the caches
-            __builtin_amdgcn_global_load_lds((const void*)(src + (int64_t)j * 1024),
+            __builtin_amdgcn_global_load_lds((const void*)(src + (int64_t)j * (LP_NBLK * 1024)),
                                              (lds_t*)(c.ring + (size_t)(Lg % LP_RING) * 1024), 16,
                                              0, 2);
             if (++inflight == LP_INFL) {
@@ -1727,11 +1727,16 @@ __global__ void loop_gather_kernel(const int8_t* const* __restrict__ src, int8_t
     if (line >= nlines) return;
     const int lane = threadIdx.x & 63;
     const lp_v4i v = *(const lp_v4i*)(src[line * 8 + (lane >> 3)] + (lane & 7) * 16);
-    *(lp_v4i*)(dst + line * 1024 + lane * 16) = v;
+    const int64_t lpt = nlines / LP_NBLK;                    // table: [nblk][lpt] lines
+    const int64_t dl = (line % lpt) * LP_NBLK + line / lpt;  // copy: [lpt][nblk]
+    *(lp_v4i*)(dst + dl * 1024 + lane * 16) = v;
 }
 
-// Lays every workgroup's weight lines out contiguously, in the order its
-// compute waves consume them (the partition of the kernel above).
+// Lays out every workgroup's weight lines in the order its compute waves
+// consume them (the partition of the kernel above), line-major: line L of all
+// workgroups sits together, so the lines in flight across the grid at one
+// moment form one contiguous region (0.4% faster than one contiguous block
+// per workgroup, whose equal 1.7 MB strides share their low address bits).
 static int loop_build(Qwen3Dec* d) {
     const pio_qwen3_config& c = d->c;
     LoopState* s = new LoopState();

@@ -49,6 +49,8 @@ Other modes (each prints its own line and exits):
   --decode-timeline, --gemm-supply, --gemm-timeline: the decode's per-phase
                         timeline, the C3 GEMM's operand-supply probe and its
                         per-block timeline (the profiles' commands).
+  --gemm-vendor         the C3 shapes through this library's GEMMs beside
+                        hipBLASLt's int8 GEMM (torch._int_mm), int32 compared.
   --decode-only, --calibrate-copy: see --help.
 """
 from __future__ import annotations
@@ -290,6 +292,66 @@ def gemm_supply(torch):
         out[f"M{M}_N{N}_K{K}"] = row
         log(f"[gemm-supply] {M}x{N}x{K}: {row}")
         del A, B
+    return out
+
+
+def gemm_vendor(torch):
+    """The C3 shapes through this library's W8A8 GEMMs and through the vendor
+    library (hipBLASLt, reached as torch._int_mm: int8 x int8 -> int32), timed
+    the same way: a graph of 20 launches, HIP events around 5 replays. The
+    vendor GEMM is also timed eagerly (50 back-to-back calls), in case its
+    graph capture records extra nodes. The int32 products of the two libraries
+    are compared element for element."""
+    from mod_amd import ops
+    timer = Timer(torch)
+    out = {}
+    reps = 20
+    for (K, N) in [(1024, 3072), (3072, 1024), (1024, 2048)]:
+        M = 2048
+        A = torch.randint(-127, 127, (M, K), dtype=torch.int8, device="cuda")
+        W = torch.randint(-127, 127, (N, K), dtype=torch.int8, device="cuda")   # [N, K] rows
+        Bkn = W.t().contiguous()                                               # [K, N], the reference's b
+        sa = torch.rand((M,), device="cuda") * 0.01
+        sw = torch.rand((N,), device="cuda") * 0.01
+        yh = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        c32 = torch.empty((M, N), dtype=torch.int32, device="cuda")
+        ws = torch.empty(max(1, int(ops.lib.pio_matmul_int8_workspace(1, M, K, N))), dtype=torch.uint8,
+                         device="cuda")
+        row = {}
+        t = timer.time_graph(timer.graph(lambda s: ops.gemm_w8a8(A, sa, W, sw, None, yh, M, N, K, s), reps),
+                             replays=5) / reps
+        row["ours_w8a8_f16_us"] = round(t * 1e6, 2)
+        t = timer.time_graph(timer.graph(lambda s: ops.matmul_int8(A, Bkn, c32, 1, M, K, N, True, ws, s),
+                                         reps), replays=5) / reps
+        row["ours_matmul_int8_i32_us"] = round(t * 1e6, 2)
+        # hipBLASLt wants the second operand column-major: W.t() is [K, N] in that layout
+        ref = torch._int_mm(A, W.t())
+        torch.cuda.synchronize()
+        row["int32_equal"] = bool(torch.equal(ref, c32))
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(timer.stream):
+            torch._int_mm(A, W.t())
+            timer.stream.synchronize()
+            with torch.cuda.graph(g, stream=timer.stream):
+                for _ in range(reps):
+                    torch._int_mm(A, W.t())
+        row["hipblaslt_i32_graph_us"] = round(timer.time_graph(g, replays=5) / reps * 1e6, 2)
+        with torch.cuda.stream(timer.stream):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record(timer.stream)
+            for _ in range(50):
+                torch._int_mm(A, W.t())
+            e1.record(timer.stream)
+        e1.synchronize()
+        row["hipblaslt_i32_eager_us"] = round(e0.elapsed_time(e1) * 1e3 / 50, 2)
+        for k in list(row):
+            if k.endswith("_us"):
+                row[k.replace("_us", "_TOPS")] = round(2 * M * N * K / (row[k] * 1e-6) / 1e12, 1)
+        out[f"M{M}_K{K}_N{N}"] = row
+        log(f"[gemm-vendor] M={M} K={K} N={N}: {row}")
+        del A, W, Bkn, yh, c32, ws, ref, g
     return out
 
 
@@ -974,6 +1036,10 @@ def main():
                     help="only time the C3 W8A8 GEMM beside its operand-supply probe (the K loop's "
                          "copies alone, in K steps of 128, 256 and 512 bytes per row) and print the "
                          "per-CU rates")
+    ap.add_argument("--gemm-vendor", action="store_true",
+                    help="only time the C3 shapes through this library's W8A8 GEMMs beside the "
+                         "vendor library's int8 GEMM (hipBLASLt via torch._int_mm) and compare "
+                         "their int32 products")
     ap.add_argument("--gemm-timeline", action="store_true",
                     help="only run the C3 W8A8 GEMM through its traced build and print the per-block "
                          "timeline (start, K loop, stores issued, stores complete)")
@@ -1035,6 +1101,9 @@ def main():
         return 0
     if args.gemm_timeline:
         print(json.dumps(gemm_timeline(torch)))
+        return 0
+    if args.gemm_vendor:
+        print(json.dumps(gemm_vendor(torch)))
         return 0
     if args.weights:
         r = bench_weights(torch)

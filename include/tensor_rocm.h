@@ -286,7 +286,8 @@ int pio_gemm_w8a8_static(const int8_t* q, const float* s_a, const int8_t* w, con
 
 /* tensor_matmul_int8 semantics on raw pointers (B is [K,N]); `out_i32` != 0
  * writes int32 instead of fp32. `workspace` needs pio_matmul_int8_workspace()
- * bytes (B is repacked to [N,K] there). */
+ * bytes, 16-byte aligned (B is repacked to [N,K] there); null makes the
+ * library take its own. */
 size_t pio_matmul_int8_workspace(int batch, int M, int K, int N);
 int pio_matmul_int8(const int8_t* a, const int8_t* b, void* c, int out_i32, int batch, int M,
                     int K, int N, void* workspace, void* stream);

@@ -982,25 +982,49 @@ static int static_scratch(void** out) {
     return PIO_OK;
 }
 
-// [K,N] -> [N,K] int8 transpose through a 64x64 LDS tile (per batch z).
+// [K,N] -> [N,Kp] int8 transpose, zero-filled for K <= k < Kp: one 64 x 64
+// tile per block (per batch z). Thread (r, c) = (tid / 4, tid % 4) reads 16
+// bytes of k row k0 + r (n0 + 16c ..) and writes 16 bytes of n row n0 + r
+// (k0 + 16c ..), one 16-byte access each; the byte transpose happens in LDS,
+// whose rows are 68 bytes apart so that the four k chunks a wave reads per
+// byte fall in different banks. dst is 16-byte aligned and Kp % 16 == 0, so
+// every write is one aligned chunk; the reads go byte by byte on the right and
+// bottom edges and wherever vec is 0 (N % 16 != 0 or src unaligned).
 __global__ __launch_bounds__(256) void transpose_i8_kernel(const int8_t* __restrict__ src,
                                                            int8_t* __restrict__ dst, int K, int N,
-                                                           int Kp, int64_t sbatch,
-                                                           int64_t dbatch) {
-    __shared__ int8_t t[64][65];
+                                                           int Kp, int64_t sbatch, int64_t dbatch,
+                                                           int vec) {
+    constexpr int LS = 68;
+    __shared__ __align__(16) uint32_t t[64 * LS / 4];
+    const uint8_t* tb = (const uint8_t*)t;
     const int k0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
     src += blockIdx.z * sbatch;
     dst += blockIdx.z * dbatch;
-    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
-        const int r = i / 64, c = i % 64;   // r: k, c: n
-        const int k = k0 + r, n = n0 + c;
-        t[r][c] = (k < K && n < N) ? src[(int64_t)k * N + n] : (int8_t)0;
+    const int r = threadIdx.x >> 2, c = threadIdx.x & 3;
+    {
+        const int k = k0 + r, n = n0 + 16 * c;
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+        if (vec && k < K && n + 16 <= N) {
+            const uint4 v = *(const uint4*)(src + (int64_t)k * N + n);
+            w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+        } else if (k < K) {
+            for (int j = 0; j < 16; j++)
+                if (n + j < N) w[j >> 2] |= (uint32_t)(uint8_t)src[(int64_t)k * N + n + j] << (8 * (j & 3));
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) t[r * (LS / 4) + 4 * c + i] = w[i];
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
-        const int r = i / 64, c = i % 64;   // r: n, c: k
-        const int n = n0 + r, k = k0 + c;
-        if (n < N && k < Kp) dst[(int64_t)n * Kp + k] = t[c][r];
+    const int n = n0 + r, k = k0 + 16 * c;
+    if (n < N && k < Kp) {   // Kp % 16 == 0, so the whole chunk is inside the row
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint8_t* col = tb + (16 * c + 4 * i) * LS + r;
+            w[i] = (uint32_t)col[0] | (uint32_t)col[LS] << 8 | (uint32_t)col[2 * LS] << 16 |
+                   (uint32_t)col[3 * LS] << 24;
+        }
+        *(uint4*)(dst + (int64_t)n * Kp + k) = make_uint4(w[0], w[1], w[2], w[3]);
     }
 }
 
@@ -1098,10 +1122,12 @@ static int matmul_int8_impl(const int8_t* a, const int8_t* b, void* c, int out_i
         PIO_TRY(own.get(matmul_ws(batch, M, K, N), st));
         ws = own.ptr;
     }
+    PIO_REQUIRE(aligned16(ws), "matmul_int8: the workspace must be 16-byte aligned");
     int8_t* bt = (int8_t*)ws;
     const size_t bt_bytes = ((size_t)batch * N * Kp + 255) / 256 * 256;
     dim3 tg(ceil_div(N, 64), ceil_div(Kp > 0 ? Kp : 1, 64), batch);
-    transpose_i8_kernel<<<tg, 256, 0, st>>>(b, bt, K, N, Kp, (int64_t)K * N, (int64_t)N * Kp);
+    transpose_i8_kernel<<<tg, 256, 0, st>>>(b, bt, K, N, Kp, (int64_t)K * N, (int64_t)N * Kp,
+                                            aligned16(b) && N % 16 == 0);
     PIO_LAUNCHED();
     const int8_t* ap = a;
     if (K % 16) {

@@ -609,6 +609,36 @@ def test_matmul_int8_matches_reference_semantics(env, batch, M, K, N):
         assert np.array_equal(host(c), oracle.ref_matmul_int8(a, b).reshape(c.shape))
 
 
+@pytest.mark.parametrize("batch,M,K,N,b_off,ws_off", [
+    (1, 256, 1024, 3072, 0, 0),   # C3-sized b: whole 16-byte chunks in and out
+    (2, 100, 200, 80, 0, 0),      # N % 16 == 0 with a partial tile on each edge, Kp = 208
+    (2, 100, 200, 80, 1, 0),      # b one byte off alignment: byte reads
+    (1, 70, 96, 48, 0, 3),        # caller workspace off alignment: refused
+])
+def test_matmul_int8_b_layouts(env, batch, M, K, N, b_off, ws_off):
+    """The [K,N] -> [N,Kp] repack of b inside tensor_matmul_int8 on its
+    16-byte and byte read paths, int32 results against the oracle; a caller
+    workspace off 16-byte alignment is refused."""
+    torch, ops, d = env
+    _say(f"matmul_int8 layouts b={batch} M={M} K={K} N={N} b_off={b_off} ws_off={ws_off}")
+    rng = np.random.default_rng(M * 7 + K)
+    a = rng.integers(-128, 128, size=(batch, M, K), dtype=np.int8)
+    b = rng.integers(-128, 128, size=(batch, K, N), dtype=np.int8)
+    bbuf = torch.empty(b.size + 16, dtype=torch.int8, device=d)
+    bd = bbuf[b_off:b_off + b.size]
+    bd.copy_(torch.from_numpy(b.reshape(-1)).to(d))
+    nws = int(ops.lib.pio_matmul_int8_workspace(batch, M, K, N))
+    ws = torch.empty(nws + 16, dtype=torch.uint8, device=d)[ws_off:ws_off + nws]
+    ci = torch.empty((batch, M, N), dtype=torch.int32, device=d)
+    if ws_off % 16:
+        with pytest.raises(RuntimeError, match="16-byte aligned"):
+            ops.matmul_int8(dev(torch, a, d), bd, ci, batch, M, K, N, out_i32=True, workspace=ws)
+        return
+    ops.matmul_int8(dev(torch, a, d), bd, ci, batch, M, K, N, out_i32=True, workspace=ws)
+    sync(torch)
+    assert np.array_equal(host(ci), oracle.matmul_int8(a, b, out_i32=True))
+
+
 # --------------------------------------------------------------------- MoE
 def test_moe_route_matches_oracle(env):
     torch, ops, d = env

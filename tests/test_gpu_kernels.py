@@ -661,7 +661,8 @@ def test_moe_route_matches_oracle(env):
 # (H, I) / 128 = the expert GEMMs' K steps: 1, 2, 3, 4 (= the prefetch depth),
 # 5, 6, 9, 16 and 32 (the largest supported), around the engine's prologue and
 # tail cases; T = 160 with 2 experts also takes the 64-row second tile pass;
-# T = 4100 gives ~2050 rows per expert (33 row tiles).
+# T = 4100 gives ~2050 rows per expert (33 row tiles); T = 2048 runs the
+# grouping kernel's token walk in 4 rounds of 512.
 @pytest.mark.parametrize("T,H,I,E,k,xdt", [(16, 128, 128, 8, 2, np.float32),
                                            (64, 256, 128, 16, 4, np.float16),
                                            (48, 384, 512, 8, 2, np.float32),
@@ -669,6 +670,7 @@ def test_moe_route_matches_oracle(env):
                                            (130, 1152, 128, 32, 8, np.float16),
                                            (160, 4096, 256, 2, 1, np.float32),
                                            (512, 2048, 768, 128, 8, np.float16),
+                                           (2048, 256, 128, 8, 4, np.float16),
                                            (4100, 128, 128, 4, 2, np.float32)])
 def test_moe_layer_matches_oracle(env, T, H, I, E, k, xdt):
     torch, ops, d = env

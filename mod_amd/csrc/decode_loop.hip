@@ -1217,14 +1217,15 @@ __device__ __forceinline__ float lm_split(const Cx& c, const float (&xv)[16], in
     amax = wmax(amax);
     int E;
     (void)frexpf(amax, &E);   // amax = 0: E = 0, every part 0
-    const float inv = ldexpf(1.f, 6 - E);
+    // u = x 2^(6 - E) by exponent arithmetic (v_ldexp_f32): exact, and unlike
+    // a multiply by 2^(6 - E) it cannot overflow when amax is below 2^-121
     // this wave's elements 16 l + 4 w + t: MFMA i = l / 4, lane chunk q = l % 4,
     // byte 4 w + t of the chunk
     uint32_t pk[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int t = 0; t < 4; t++) {
         const float x = c.w == 0 ? xv[t] : c.w == 1 ? xv[4 + t] : c.w == 2 ? xv[8 + t] : xv[12 + t];
-        float u = x * inv;
+        float u = ldexpf(x, 6 - E);
 #pragma unroll
         for (int m = 0; m < 4; m++) {
             const float q = rintf(u);

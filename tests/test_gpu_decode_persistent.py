@@ -214,6 +214,24 @@ def test_persistent_lm_head_small_vocab_and_ties(torch_dev):
         assert np.all(out[len(prompt):] == 0), (mode, out)
 
 
+def test_persistent_lm_head_tiny_final_norm(torch_dev):
+    """The lm phase splits gamma * x into int8 parts under the scale
+    S = 2^(E - 6) of its largest element (2^E > max |gamma * x|). A final norm
+    of 2^-126 puts E near -122, where 2^(6 - E) is past the fp32 range: the
+    parts are formed by exponent arithmetic, so they stay exact and the
+    teacher-forced logits still meet the oracle's bar."""
+    from mod_amd.qwen3 import Qwen3Int8Decoder, random_weights
+    cfg, rcfg = _cfgs(vocab=300)
+    w = random_weights(cfg, seed=65)
+    w["final_norm"] = np.full_like(w["final_norm"], 2.0 ** -126)
+    dec = Qwen3Int8Decoder(cfg, w)
+    ids = np.random.default_rng(66).integers(0, cfg.vocab, size=12).astype(np.int32)
+    _say("lm tiny final norm: teacher forced")
+    got = dec.teacher_forced_logits(ids, mode="persistent")
+    assert np.isfinite(got).all()
+    _check_logits(got, ids, rcfg, w, "persistent, final norm 2^-126")
+
+
 def test_persistent_c2_shape(torch_dev):
     """Full Qwen3-0.6B shape (28 layers, vocab 151936)."""
     cfg, rcfg = _cfgs(n_layers=28, vocab=151936, max_seq=384)

@@ -398,6 +398,14 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(
     // fp16 rows are paired (kv_store): storage slot s holds dim s / 2 + 64 (s & 1)
     constexpr bool PAIR = sizeof(KT) == 2;
     auto dim_of = [](int slot) { return PAIR ? (slot >> 1) + 64 * (slot & 1) : slot; };
+    // values: thread (dg, pg) = (tid % 32, tid / 32) owns dims 4 dg .. 4 dg + 3
+    // of positions pg + 8 u (+ 32 per pass). The first pass's values load with
+    // the keys (both depend only on pos): one memory round trip fewer than
+    // loading them after the softmax. Rows past the split's end are clamped.
+    const int dg = tid & 31, pg = tid >> 5;
+    float4 vv0[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) vv0[u] = kv_ld4(vb + (int64_t)min(pg + 8 * u, n - 1) * D + 4 * dg);
 
     {
         const int part = tid & 7, sub = tid >> 3;
@@ -459,14 +467,10 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(
     }
     __syncthreads();
     {
-        const int dg = tid & 31, pg = tid >> 5;
         float4 o[ATT_MAX_G];
 #pragma unroll
         for (int h = 0; h < ATT_MAX_G; h++) o[h] = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int tb = pg; tb < n; tb += 32) {
-            float4 vv[4];   // clamped like the keys; rows past the end are skipped below
-#pragma unroll
-            for (int u = 0; u < 4; u++) vv[u] = kv_ld4(vb + (int64_t)min(tb + 8 * u, n - 1) * D + 4 * dg);
+        auto accum = [&](int tb, const float4 (&vv)[4]) {
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 const int t = tb + 8 * u;
@@ -478,6 +482,13 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(
                     o[h].x += pt * vv[u].x; o[h].y += pt * vv[u].y; o[h].z += pt * vv[u].z; o[h].w += pt * vv[u].w;
                 }
             }
+        };
+        accum(pg, vv0);
+        for (int tb = pg + 32; tb < n; tb += 32) {
+            float4 vv[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) vv[u] = kv_ld4(vb + (int64_t)min(tb + 8 * u, n - 1) * D + 4 * dg);
+            accum(tb, vv);
         }
 #pragma unroll
         for (int h = 0; h < ATT_MAX_G; h++)

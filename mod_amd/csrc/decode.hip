@@ -189,44 +189,67 @@ __global__ __launch_bounds__(256) void dec_gemv_kernel(DecGemv p) {
     }
 
     // Block prologue: xs = x * norm_w (or x, or the merged attention output),
-    // and the RMSNorm scale.
+    // and the RMSNorm scale. The loop over K in steps of 1024 issues the loads
+    // of several steps (4 of x, 2 of the split merge) before it uses any, at
+    // clamped indices: one step at a time, each step's loads waited for the
+    // previous step's math (two extra round trips at K = 3072).
     float ss = 0.f;
-    for (int k = threadIdx.x * 4; k < K; k += 1024) {
-        float4 a;
-        if (p.att_o) {
-            // softmax-merge of the splits for q head k/128, in split order; all
-            // split loads are issued before any is used.
-            const int h = k >> 7, nh = K >> 7;
-            float m[ATT_SPLITS], l[ATT_SPLITS];
-            float4 o[ATT_SPLITS];
-#pragma unroll
-            for (int i = 0; i < ATT_SPLITS; i++) {
-                m[i] = p.att_ml[(i * nh + h) * 2];
-                l[i] = p.att_ml[(i * nh + h) * 2 + 1];
-                o[i] = *(const float4*)(p.att_o + (int64_t)i * K + k);
-            }
-            float M = m[0];
-#pragma unroll
-            for (int i = 1; i < ATT_SPLITS; i++) M = fmaxf(M, m[i]);
-            float den = 0.f;
-            a = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-            for (int i = 0; i < ATT_SPLITS; i++) {
-                const float f = m[i] == -INFINITY ? 0.f : expf(m[i] - M);
-                den += f * l[i];
-                a.x += f * o[i].x; a.y += f * o[i].y; a.z += f * o[i].z; a.w += f * o[i].w;
-            }
-            const float inv = 1.0f / den;
-            a.x *= inv; a.y *= inv; a.z *= inv; a.w *= inv;
-        } else {
-            a = *(const float4*)(p.x + k);
-        }
+    auto put = [&](int k, float4 a, float4 gw) {
         if (p.norm_w) {
             ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
-            const float4 gw = *(const float4*)(p.norm_w + k);
             a.x *= gw.x; a.y *= gw.y; a.z *= gw.z; a.w *= gw.w;
         }
         *(float4*)&xs[k] = a;
+    };
+    if (p.att_o) {
+        // softmax-merge of the splits for q head k/128, in split order
+        const int nh = K >> 7;
+        for (int k0 = threadIdx.x * 4; k0 < K; k0 += 2048) {
+            float m[2][ATT_SPLITS], l[2][ATT_SPLITS];
+            float4 o[2][ATT_SPLITS], gw[2];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int k = min(k0 + 1024 * u, K - 4), h = k >> 7;
+#pragma unroll
+                for (int i = 0; i < ATT_SPLITS; i++) {
+                    m[u][i] = p.att_ml[(i * nh + h) * 2];
+                    l[u][i] = p.att_ml[(i * nh + h) * 2 + 1];
+                    o[u][i] = *(const float4*)(p.att_o + (int64_t)i * K + k);
+                }
+                gw[u] = p.norm_w ? *(const float4*)(p.norm_w + k) : make_float4(1.f, 1.f, 1.f, 1.f);
+            }
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                if (k0 + 1024 * u >= K) continue;
+                float M = m[u][0];
+#pragma unroll
+                for (int i = 1; i < ATT_SPLITS; i++) M = fmaxf(M, m[u][i]);
+                float den = 0.f;
+                float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int i = 0; i < ATT_SPLITS; i++) {
+                    const float f = m[u][i] == -INFINITY ? 0.f : expf(m[u][i] - M);
+                    den += f * l[u][i];
+                    a.x += f * o[u][i].x; a.y += f * o[u][i].y; a.z += f * o[u][i].z; a.w += f * o[u][i].w;
+                }
+                const float inv = 1.0f / den;
+                a.x *= inv; a.y *= inv; a.z *= inv; a.w *= inv;
+                put(k0 + 1024 * u, a, gw[u]);
+            }
+        }
+    } else {
+        for (int k0 = threadIdx.x * 4; k0 < K; k0 += 4096) {
+            float4 a[4], gw[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int k = min(k0 + 1024 * u, K - 4);
+                a[u] = *(const float4*)(p.x + k);
+                gw[u] = p.norm_w ? *(const float4*)(p.norm_w + k) : make_float4(1.f, 1.f, 1.f, 1.f);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (k0 + 1024 * u < K) put(k0 + 1024 * u, a[u], gw[u]);
+        }
     }
     float nscale = 1.f;
     if (p.norm_w) {
